@@ -1,0 +1,211 @@
+"""Benchmark of the paged KV-cache decode step on one MI355X.
+
+Default workload: Qwen3-0.6B-shaped batched decode in bf16 -- 16 query heads,
+8 KV heads, head_dim 128, 28 layers, 32 sequences with cached lengths drawn
+uniformly from [128, 2048] plus the token appended this step, K/V in 16-token
+pages placed by a seeded random permutation (one table shared by all layers,
+as one block id spans all layers), a distinct pool per layer. One step runs,
+for every layer, the fused q/k RMSNorm + RoPE + append of the new token and
+the split-K GQA decode over the paged pool. Inputs are synthetic N(0, 1)
+values resident in HBM before timing starts.
+
+Printed: one JSON line with tokens/s (decode tokens of all sequences per
+second), the decode kernel's achieved HBM bandwidth against the 8 TB/s peak
+(algorithmic bytes per launch / HIP-event time per launch), and the oracle's
+CPU time on a bounded sample of the same workload.
+
+  python bench.py [--steps K] [--warmup W] [--workload qwen3|qwen25]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mini-serve-rs_amd"))
+
+PEAK_HBM_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (Hq, Hkv, d, layers, batch, len_lo, len_hi, description)
+    "qwen3": (16, 8, 128, 28, 32, 128, 2048,
+              "Qwen3-0.6B batched decode: 16q/8kv heads, d=128, 28 layers, B=32, "
+              "cached U[128,2048] + 1 appended, bf16, 16-token pages"),
+    "qwen25": (14, 2, 64, 24, 64, 4096, 4096,
+               "Qwen2.5-0.5B high-GQA decode: 14q/2kv heads, d=64, 24 layers, B=64, "
+               "4096 cached + 1 appended, bf16, 16-token pages"),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="qwen3", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="wall-clock budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=2)
+    return ap.parse_args()
+
+
+def algorithmic_decode_bytes(lens, hq, hkv, d, es):
+    """HBM bytes one decode launch must move: every attended K and V row once,
+    q in and out once, the used block-table entries and the lengths."""
+    kv = sum(int(n) * 2 * hkv * d * es for n in lens)
+    qo = 2 * len(lens) * hq * d * es
+    tab = sum(((int(n) + 15) // 16) * 4 for n in lens)
+    return kv + qo + tab + 4 * len(lens)
+
+
+def cpu_baseline(args, lens, hq, hkv, d, layers):
+    """The oracle (C restatement of the reference's Candle CPU path: contiguous
+    per-sequence f32 buffers, KvCache append, per-KV-head matmul / softmax /
+    matmul) timed on this host for a bounded number of layer-steps."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    b = len(lens)
+    cap = int(max(lens))
+    rng = np.random.default_rng(7)
+    tile = rng.standard_normal((hkv, 1, d)).astype(np.float32)
+    k = np.ascontiguousarray(np.broadcast_to(tile, (b, hkv, cap, d)), dtype=np.float32)
+    v = k.copy()
+    q = rng.standard_normal((b, hq, d)).astype(np.float32)
+    kn = rng.standard_normal((b, hkv, d)).astype(np.float32)
+    vn = rng.standard_normal((b, hkv, d)).astype(np.float32)
+    lens32 = np.asarray(lens, np.int32)
+    threads = O.max_threads()
+    scale = 1.0 / math.sqrt(d)
+    O.decode_step_f32(q, kn, vn, k, v, lens32, scale, threads)  # warm
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        O.decode_step_f32(q, kn, vn, k, v, lens32, scale, threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or n >= 10 * layers:
+            break
+    steps = n / layers
+    return {"value": b * steps / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} layer-steps (append + decode of all {b} sequences, f32, one "
+                      f"layer's contiguous buffers reused) in {el:.2f} s = {steps:.2f} "
+                      f"decode steps of {layers} layers"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import rlse_kv as kv
+
+    hq, hkv, d, layers, b, lo, hi, desc = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rng = np.random.default_rng(args.seed)
+    cached = rng.integers(lo, hi + 1, b).astype(np.int32)
+    lens = cached + 1  # keys attended: cached + the appended token
+    mbps = int(max((int(n) + 15) // 16 for n in lens))
+    need = int(sum((int(n) + 15) // 16 for n in lens))
+    nb = need + 64
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.zeros((b, mbps), np.int32)
+    used = 0
+    for i, n in enumerate(lens):
+        k = (int(n) + 15) // 16
+        tables[i, :k] = perm[used:used + k]
+        used += k
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    bf = torch.bfloat16
+    k_pools = [torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf)
+               for _ in range(layers)]
+    v_pools = [torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf)
+               for _ in range(layers)]
+    q_in = [torch.randn((b, hq, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
+    k_in = [torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
+    v_in = [torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
+    qw = [(1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf) for _ in range(layers)]
+    kw = [(1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf) for _ in range(layers)]
+    max_pos = int(lens.max()) + 1
+    cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, "bf16")
+    cos_t = torch.frombuffer(bytearray(cos_b), dtype=torch.int16).to(dev).view(bf)
+    sin_t = torch.frombuffer(bytearray(sin_b), dtype=torch.int16).to(dev).view(bf)
+    t_dev = torch.from_numpy(tables).to(dev)
+    pos_dev = torch.from_numpy(cached).to(dev)
+    lens_dev = torch.from_numpy(lens).to(dev)
+    q_rot = torch.empty((b, hq, d), device=dev, dtype=bf)
+    out = torch.empty((b, hq, d), device=dev, dtype=bf)
+    ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    scale = 1.0 / math.sqrt(d)
+    n_events = layers * args.steps
+    ev_a = [torch.cuda.Event(enable_timing=True) for _ in range(n_events)]
+    ev_b = [torch.cuda.Event(enable_timing=True) for _ in range(n_events)]
+
+    def step(timed_index=None):
+        for layer in range(layers):
+            kv.qk_norm_rope_append(q_in[layer], k_in[layer], v_in[layer], qw[layer], kw[layer],
+                                   1e-6, cos_t, sin_t, max_pos, pos_dev, t_dev, b, None, b, hq,
+                                   hkv, d, mbps, nb, q_rot, k_pools[layer], v_pools[layer],
+                                   "bf16", stream)
+            if timed_index is not None:
+                ev_a[timed_index * layers + layer].record(stream)
+            kv.paged_gqa_decode(q_rot, k_pools[layer], v_pools[layer], t_dev, lens_dev, out, b,
+                                hq, hkv, d, mbps, nb, scale, "bf16", ws, ws_bytes, stream)
+            if timed_index is not None:
+                ev_b[timed_index * layers + layer].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(s)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kernel_ms = [a.elapsed_time(e) for a, e in zip(ev_a, ev_b)]
+    avg_ms = float(np.mean(kernel_ms))
+    per_launch = algorithmic_decode_bytes(lens, hq, hkv, d, 2)
+    achieved = per_launch / (avg_ms * 1e-3) / 1e9
+    ms_per_step = elapsed * 1e3 / args.steps
+    result = {
+        "metric": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen3-0.6B shape, 1 GPU",
+        "value": b * args.steps / elapsed,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/q, seeded random page permutation",
+        "config": {"workload": desc, "batch": b, "layers": layers, "q_heads": hq,
+                   "kv_heads": hkv, "head_dim": d, "mean_keys": float(np.mean(lens)),
+                   "pages_per_layer": need, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "kernel": "rlse_paged_gqa_decode (decode_split_kernel + "
+                               "decode_merge_kernel)",
+                     "bytes_per_launch": per_launch, "avg_launch_ms": avg_ms},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args, lens, hq, hkv, d, layers)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

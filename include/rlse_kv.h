@@ -1,0 +1,258 @@
+/*
+ * rlse_kv.h -- C ABI of the MI355X (gfx950) paged KV-cache hot path of the
+ * rlse serving engine (crate `rlse` 0.2.0).
+ *
+ * Conventions (carried over from the reference's FFI precedent,
+ * docs/colab_cuda_kernels/mini_serve_kernels.cu:247-296):
+ *   - every entry point returns an int status: 0 on success, a hipError_t
+ *     value (1 = hipErrorInvalidValue for rejected arguments) or an
+ *     RLSE_ERR_* code >= 10000; nothing ever exits or aborts the process;
+ *   - device buffers are owned by the caller unless a *_create call says
+ *     otherwise; all device work is asynchronous on the given stream
+ *     (NULL = the default stream) and nothing synchronises;
+ *   - arguments are validated before any device work is queued (fail closed);
+ *   - handles are not internally locked: the caller serialises, as the
+ *     reference's backend mutex does (src/backends/candle.rs:385).
+ *
+ * Physical KV pool layout, per layer, for both K and V (the reference
+ * prototype's index formula, mini_serve_kernels.cu:68-70, 93):
+ *     pool[num_blocks][num_kv_heads][16][head_dim]
+ *     elem(block, head, slot, dim) = ((block*Hkv + head)*16 + slot)*head_dim + dim
+ * A sequence's token t lives in block block_table[t / 16], slot t % 16.
+ * Block tables are int32 [batch][max_blocks_per_seq], row-major.
+ */
+#ifndef RLSE_KV_H
+#define RLSE_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* rlse_stream_t; /* a hipStream_t */
+
+enum rlse_dtype { RLSE_DTYPE_F32 = 0, RLSE_DTYPE_BF16 = 1, RLSE_DTYPE_F16 = 2 };
+
+#define RLSE_OK 0
+#define RLSE_ERR_INVALID_VALUE 1 /* == hipErrorInvalidValue */
+#define RLSE_ERR_CACHE_PRESSURE 10001
+#define RLSE_ERR_UNKNOWN_REQUEST 10002
+#define RLSE_ERR_BUFFER_TOO_SMALL 10003
+#define RLSE_BLOCK_SIZE 16 /* src/core/constants.rs:1 DEFAULT_BLOCK_SIZE */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* rlse_last_error(void);
+/* Library ABI version (major*10000 + minor*100 + patch). */
+int rlse_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Physical paged KV pool (device memory owned by the handle).         */
+/* Replaces the per-request contiguous candle_nn KvCache buffers that  */
+/* Attention::append_kv creates (src/backends/qwen2.rs:349-361) and    */
+/* sizes in ModelForCausalLM::set_kv_capacity (qwen2.rs:603-618).      */
+/* One block id spans all layers, as a KVCache id does                 */
+/* (src/cache/kv_cache.rs:15-35). The pool is zero-filled at creation. */
+/* ------------------------------------------------------------------ */
+typedef struct rlse_kv_pool rlse_kv_pool;
+
+int rlse_pool_create(int num_layers, int num_blocks, int num_kv_heads, int head_dim,
+                     int dtype, int block_size, rlse_kv_pool** out_pool);
+int rlse_pool_destroy(rlse_kv_pool* pool);
+/* Device pointers of one layer's K and V pools. */
+int rlse_pool_layer(const rlse_kv_pool* pool, int layer, void** k_pool, void** v_pool);
+/* Elements between consecutive layers' K (and V) pools. */
+int rlse_pool_info(const rlse_kv_pool* pool, int* num_layers, int* num_blocks,
+                   int* num_kv_heads, int* head_dim, int* dtype,
+                   long long* layer_stride_elems);
+
+/* ------------------------------------------------------------------ */
+/* KV data movement (bit-exact).                                       */
+/* ------------------------------------------------------------------ */
+
+/* Append num_tokens new K/V rows ([num_tokens][Hkv][head_dim] each) at
+ * the given positions. Token i belongs to sequence seq_index[i]
+ * (seq_index == NULL: token i belongs to sequence i) and is written to
+ * block block_tables[seq][pos/16], slot pos%16. block_tables has num_seqs
+ * rows; tokens whose sequence is outside [0, num_seqs) are skipped.
+ * Replaces Attention::append_kv -> KvCache::append (src/backends/qwen2.rs:349-361),
+ * i.e. slice_set into the contiguous buffer at cur_len. Tokens whose block
+ * id is outside [0, num_blocks) or whose position is outside
+ * [0, max_blocks_per_seq*16) are skipped. */
+int rlse_kv_append(const void* k_new, const void* v_new, void* k_pool, void* v_pool,
+                   const int32_t* block_tables, int num_seqs, const int32_t* seq_index,
+                   const int32_t* positions, int num_tokens, int num_kv_heads,
+                   int head_dim, int max_blocks_per_seq, int num_blocks, int dtype,
+                   rlse_stream_t stream);
+
+/* Snapshot export: pool pages -> contiguous [num_layers][Hkv][len][head_dim]
+ * K and V, the layout of Attention::get_kv_snapshot views and of the
+ * cumulative prefix snapshots (src/backends/qwen2.rs:363-371;
+ * src/cache/prefix_cache.rs:320-333). Layer l's pools are k_pool/v_pool +
+ * l*layer_stride_elems. block_table is a device int32 array. */
+int rlse_kv_gather(const void* k_pool, const void* v_pool, long long layer_stride_elems,
+                   int num_layers, const int32_t* block_table, int len, void* k_out,
+                   void* v_out, int num_kv_heads, int head_dim, int num_blocks, int dtype,
+                   rlse_stream_t stream);
+
+/* Snapshot restore: contiguous [num_layers][Hkv][len][head_dim] K/V ->
+ * positions start..start+len-1 of the sequence whose table is block_table.
+ * Replaces Attention::set_kv_snapshot (src/backends/qwen2.rs:373-377). */
+int rlse_kv_scatter(const void* k_in, const void* v_in, void* k_pool, void* v_pool,
+                    long long layer_stride_elems, int num_layers,
+                    const int32_t* block_table, int start, int len, int num_kv_heads,
+                    int head_dim, int num_blocks, int dtype, rlse_stream_t stream);
+
+/* Copy-on-write: copy whole blocks src_blocks[i] -> dst_blocks[i] (device
+ * int32 arrays) in every layer's K and V pools. Replaces the per-fork
+ * snapshot copy of Model::set_kv_snapshot (src/backends/qwen2.rs:547-574)
+ * for the last partial block; full blocks are shared by refcount instead. */
+int rlse_kv_copy_blocks(void* k_pool, void* v_pool, long long layer_stride_elems,
+                        int num_layers, const int32_t* src_blocks,
+                        const int32_t* dst_blocks, int num_pairs, int num_kv_heads,
+                        int head_dim, int num_blocks, int dtype, rlse_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* GQA decode attention over the paged pool.                           */
+/* q [batch][num_heads][head_dim], out same shape; query head h uses KV */
+/* head h / (num_heads/num_kv_heads) (src/backends/qwen2.rs:192).       */
+/* seq_lens[b] = keys attended (cached + appended). Result is          */
+/* softmax(q K^T * scale) V per head, as decode_attention_gqa_zero_copy */
+/* (src/backends/qwen2.rs:177-203) computes on contiguous buffers.     */
+/* Rows with seq_len <= 0 produce zeros; seq_len is clamped to          */
+/* max_blocks_per_seq*16; blocks with ids outside [0, num_blocks) are  */
+/* not read and contribute nothing.                                    */
+/* ------------------------------------------------------------------ */
+
+/* Bytes of split-K workspace needed by rlse_paged_gqa_decode on the
+ * current device. */
+int rlse_decode_workspace_size(int batch, int num_heads, int num_kv_heads, int head_dim,
+                               size_t* bytes);
+
+/* Split-K decode. workspace may be NULL, in which case a library-owned
+ * per-device workspace is used (allocated on first need). */
+int rlse_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
+                          const int32_t* block_tables, const int32_t* seq_lens, void* out,
+                          int batch, int num_heads, int num_kv_heads, int head_dim,
+                          int max_blocks_per_seq, int num_blocks, float scale, int dtype,
+                          void* workspace, size_t workspace_bytes, rlse_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Normalisation and rotary embedding.                                 */
+/* ------------------------------------------------------------------ */
+
+/* RMSNorm over the last dim with Candle's cast order
+ * (src/backends/qwen2.rs:68-75): y = dtype(x / sqrt(mean(x^2) + eps)) * w. */
+int rlse_rmsnorm(const void* x, const void* weight, void* out, int rows, int n, float eps,
+                 int dtype, rlse_stream_t stream);
+
+/* Host-side RoPE tables [max_pos][head_dim/2] in dtype, built exactly as
+ * RotaryEmbedding::new (src/backends/qwen2.rs:90-108). cos_out/sin_out are
+ * HOST buffers of max_pos*head_dim/2 elements. */
+int rlse_rope_tables(double theta, int head_dim, int max_pos, int dtype, void* cos_out,
+                     void* sin_out);
+
+/* In-place NeoX RoPE of q [num_tokens][num_heads][head_dim] and
+ * k [num_tokens][num_kv_heads][head_dim] at positions[num_tokens]
+ * (apply_rope / rotate_half, src/backends/qwen2.rs:125-142, 701-719).
+ * Either q or k may be NULL. */
+int rlse_rope(void* q, void* k, const void* cos_table, const void* sin_table,
+              const int32_t* positions, int num_tokens, int num_heads, int num_kv_heads,
+              int head_dim, int max_pos, int dtype, rlse_stream_t stream);
+
+/* Fused Attention::forward front half (src/backends/qwen2.rs:291-313):
+ * q_norm/k_norm RMSNorm (skipped when the weight pointer is NULL, as for
+ * Qwen2), RoPE at positions, then append of the rotated k and raw v into
+ * the pool (as rlse_kv_append), writing the rotated q to q_out.
+ * q [num_tokens][num_heads][head_dim]; k, v [num_tokens][num_kv_heads][head_dim]. */
+int rlse_qk_norm_rope_append(const void* q, const void* k, const void* v,
+                             const void* q_norm_weight, const void* k_norm_weight,
+                             float eps, const void* cos_table, const void* sin_table,
+                             int max_pos, const int32_t* positions,
+                             const int32_t* block_tables, int num_seqs,
+                             const int32_t* seq_index,
+                             int num_tokens, int num_heads, int num_kv_heads,
+                             int head_dim, int max_blocks_per_seq, int num_blocks,
+                             void* q_out, void* k_pool, void* v_pool, int dtype,
+                             rlse_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Prototype-compatible launchers (same signatures and argument meaning */
+/* as mini_serve_kernels.cu:247-296; default stream; head_dim fixed at */
+/* 128; pools in the layout above; no block-id bounds check is possible */
+/* because the signature carries no pool size).                       */
+/* ------------------------------------------------------------------ */
+int launch_rmsnorm_f32(const float* d_x, const float* d_w, float* d_out, int num_rows,
+                       int hidden_size, float eps);
+int launch_rmsnorm_f16(const void* d_x, const void* d_w, void* d_out, int num_rows,
+                       int hidden_size, float eps);
+int launch_rmsnorm_bf16(const void* d_x, const void* d_w, void* d_out, int num_rows,
+                        int hidden_size, float eps);
+int launch_paged_gqa_decode_tiled_f32(const float* d_q, const float* d_k_pool,
+                                      const float* d_v_pool, const int* d_block_tables,
+                                      const int* d_seq_lens, float* d_out, int batch_size,
+                                      int num_heads, int num_kv_heads,
+                                      int max_blocks_per_seq, float scale);
+int launch_paged_gqa_decode_tiled_f16(const void* d_q, const void* d_k_pool,
+                                      const void* d_v_pool, const int* d_block_tables,
+                                      const int* d_seq_lens, void* d_out, int batch_size,
+                                      int num_heads, int num_kv_heads,
+                                      int max_blocks_per_seq, float scale);
+int launch_paged_gqa_decode_tiled_bf16(const void* d_q, const void* d_k_pool,
+                                       const void* d_v_pool, const int* d_block_tables,
+                                       const int* d_seq_lens, void* d_out, int batch_size,
+                                       int num_heads, int num_kv_heads,
+                                       int max_blocks_per_seq, float scale);
+
+/* ------------------------------------------------------------------ */
+/* Host block manager: the physical successor of KVCache               */
+/* (src/cache/kv_cache.rs:15-145) with per-block refcounts for prefix  */
+/* sharing. Ids pop in ascending order from a free stack (kv_cache.rs: */
+/* 23-35); blocks_needed(t) = max(1, ceil(t/block_size)) (:53-59).     */
+/* A block returns to the free stack when its last holder releases it. */
+/* ------------------------------------------------------------------ */
+typedef struct rlse_block_manager rlse_block_manager;
+
+typedef struct rlse_cache_stats {
+  int total_blocks;
+  int allocated_blocks;
+  int free_blocks;
+  float utilization;   /* rounded to 3 decimals, kv_cache.rs:113-145 */
+  float fragmentation; /* (free runs - 1) / free, rounded to 3 decimals */
+} rlse_cache_stats;
+
+int rlse_bm_create(int total_blocks, int block_size, rlse_block_manager** out);
+int rlse_bm_destroy(rlse_block_manager* bm);
+/* KVCache::blocks_needed (kv_cache.rs:53-59). Returns the count (>= 1) or -1. */
+int rlse_bm_blocks_needed(const rlse_block_manager* bm, long long tokens);
+int rlse_bm_free_count(const rlse_block_manager* bm);
+/* KVCache::allocate (kv_cache.rs:61-84): RLSE_ERR_CACHE_PRESSURE with the
+ * reference's message when too few blocks are free. Replaces any previous
+ * allocation list of request_id, as the reference's HashMap insert does. */
+int rlse_bm_allocate(rlse_block_manager* bm, const char* request_id, long long num_tokens,
+                     int32_t* out_blocks, int capacity, int* num_out);
+/* KVCache::allocate_block (kv_cache.rs:86-99). */
+int rlse_bm_allocate_block(rlse_block_manager* bm, const char* request_id,
+                           int32_t* out_block);
+/* KVCache::release (kv_cache.rs:101-111); num_released = blocks the request held. */
+int rlse_bm_release(rlse_block_manager* bm, const char* request_id, int* num_released);
+/* Prefix fork: child_id gets parent_id's first ceil(num_tokens/16) blocks.
+ * Full blocks are shared (refcount + 1); a trailing partial block is
+ * copied-on-write into a fresh block, reported as (cow_src[i], cow_dst[i])
+ * pairs for rlse_kv_copy_blocks. Fails before any change if the child
+ * already holds blocks, the parent holds too few, or no block is free. */
+int rlse_bm_fork(rlse_block_manager* bm, const char* parent_id, const char* child_id,
+                 long long num_tokens, int32_t* cow_src, int32_t* cow_dst,
+                 int cow_capacity, int* num_cow);
+/* The request's block table (physical ids in logical order). */
+int rlse_bm_block_table(const rlse_block_manager* bm, const char* request_id,
+                        int32_t* out_blocks, int capacity, int* num_out);
+int rlse_bm_refcount(const rlse_block_manager* bm, int block);
+int rlse_bm_stats(const rlse_block_manager* bm, rlse_cache_stats* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RLSE_KV_H */

@@ -1,0 +1,400 @@
+"""ctypes binding of librlse_kv.so, the C ABI declared in include/rlse_kv.h.
+
+This is the Python face of the MI355X paged KV-cache hot path. It mirrors the
+reference's operator and cache APIs by name and behaviour:
+
+* ``BlockManager`` -- KVCache (src/cache/kv_cache.rs:15-145): ``allocate``,
+  ``allocate_block``, ``release``, ``blocks_needed``, ``stats`` with the same
+  ids, counts and CachePressure messages, plus ``fork`` for refcounted prefix
+  sharing with copy-on-write of a partial block.
+* ``KVPool`` -- the physical pool that replaces the per-request contiguous
+  candle_nn KvCache buffers (src/backends/qwen2.rs:349-361).
+* ``kv_append`` / ``kv_gather`` / ``kv_scatter`` / ``kv_copy_blocks`` --
+  Attention::append_kv and get/set_kv_snapshot (qwen2.rs:349-377, 547-574).
+* ``paged_gqa_decode`` -- decode_attention_gqa_zero_copy (qwen2.rs:177-203).
+* ``rmsnorm`` / ``rope`` / ``qk_norm_rope_append`` -- RmsNorm::forward,
+  apply_rotary_emb_qkv and the front half of Attention::forward
+  (qwen2.rs:56-142, 291-313).
+
+Device arguments are raw device addresses (ints) or objects with a
+``data_ptr()`` method (torch tensors). Every call raises ``RlseError`` when the
+library returns a non-zero status; nothing here computes on the CPU. Loading
+fails loudly when the shared library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import List, Optional, Sequence, Tuple
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "librlse_kv.so")
+
+DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
+DTYPE_NAMES = {"f32": DTYPE_F32, "float32": DTYPE_F32, "bf16": DTYPE_BF16,
+               "bfloat16": DTYPE_BF16, "f16": DTYPE_F16, "float16": DTYPE_F16}
+DTYPE_SIZE = {DTYPE_F32: 4, DTYPE_BF16: 2, DTYPE_F16: 2}
+
+OK = 0
+ERR_INVALID_VALUE = 1
+ERR_CACHE_PRESSURE = 10001
+ERR_UNKNOWN_REQUEST = 10002
+ERR_BUFFER_TOO_SMALL = 10003
+BLOCK_SIZE = 16
+
+# Every extern "C" symbol of include/rlse_kv.h (checked by the CPU tests).
+EXPORTED = (
+    "rlse_last_error", "rlse_version",
+    "rlse_pool_create", "rlse_pool_destroy", "rlse_pool_layer", "rlse_pool_info",
+    "rlse_kv_append", "rlse_kv_gather", "rlse_kv_scatter", "rlse_kv_copy_blocks",
+    "rlse_decode_workspace_size", "rlse_paged_gqa_decode",
+    "rlse_rmsnorm", "rlse_rope_tables", "rlse_rope", "rlse_qk_norm_rope_append",
+    "launch_rmsnorm_f32", "launch_rmsnorm_f16", "launch_rmsnorm_bf16",
+    "launch_paged_gqa_decode_tiled_f32", "launch_paged_gqa_decode_tiled_f16",
+    "launch_paged_gqa_decode_tiled_bf16",
+    "rlse_bm_create", "rlse_bm_destroy", "rlse_bm_blocks_needed", "rlse_bm_free_count",
+    "rlse_bm_allocate", "rlse_bm_allocate_block", "rlse_bm_release", "rlse_bm_fork",
+    "rlse_bm_block_table", "rlse_bm_refcount", "rlse_bm_stats",
+)
+
+
+class RlseError(RuntimeError):
+    """A non-zero status from librlse_kv; ``status`` holds the code."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"rlse status {status}: {message}")
+        self.status = status
+        self.message = message
+
+
+class CachePressure(RlseError):
+    """RLSE_ERR_CACHE_PRESSURE, the reference's EngineError::CachePressure."""
+
+
+class _CacheStats(ctypes.Structure):
+    _fields_ = [("total_blocks", ctypes.c_int), ("allocated_blocks", ctypes.c_int),
+                ("free_blocks", ctypes.c_int), ("utilization", ctypes.c_float),
+                ("fragmentation", ctypes.c_float)]
+
+
+@dataclass
+class CacheStats:
+    total_blocks: int
+    allocated_blocks: int
+    free_blocks: int
+    utilization: float
+    fragmentation: float
+
+
+_vp, _i, _f, _d, _ll, _sz = (ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_double,
+                             ctypes.c_longlong, ctypes.c_size_t)
+_ip = ctypes.POINTER(ctypes.c_int32)
+_cp = ctypes.c_char_p
+
+_SIGS = {
+    "rlse_last_error": (ctypes.c_char_p, []),
+    "rlse_version": (_i, []),
+    "rlse_pool_create": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_vp)]),
+    "rlse_pool_destroy": (_i, [_vp]),
+    "rlse_pool_layer": (_i, [_vp, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
+    "rlse_pool_info": (_i, [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i),
+                            ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_ll)]),
+    "rlse_kv_append": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "rlse_kv_gather": (_i, [_vp, _vp, _ll, _i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "rlse_kv_scatter": (_i, [_vp, _vp, _vp, _vp, _ll, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "rlse_kv_copy_blocks": (_i, [_vp, _vp, _ll, _i, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "rlse_decode_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
+    "rlse_paged_gqa_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f,
+                                   _i, _vp, _sz, _vp]),
+    "rlse_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp]),
+    "rlse_rope_tables": (_i, [_d, _i, _i, _i, _vp, _vp]),
+    "rlse_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "rlse_qk_norm_rope_append": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _i,
+                                      _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, _vp]),
+    "launch_rmsnorm_f32": (_i, [_vp, _vp, _vp, _i, _i, _f]),
+    "launch_rmsnorm_f16": (_i, [_vp, _vp, _vp, _i, _i, _f]),
+    "launch_rmsnorm_bf16": (_i, [_vp, _vp, _vp, _i, _i, _f]),
+    "launch_paged_gqa_decode_tiled_f32": (_i, [_vp] * 6 + [_i] * 4 + [_f]),
+    "launch_paged_gqa_decode_tiled_f16": (_i, [_vp] * 6 + [_i] * 4 + [_f]),
+    "launch_paged_gqa_decode_tiled_bf16": (_i, [_vp] * 6 + [_i] * 4 + [_f]),
+    "rlse_bm_create": (_i, [_i, _i, ctypes.POINTER(_vp)]),
+    "rlse_bm_destroy": (_i, [_vp]),
+    "rlse_bm_blocks_needed": (_i, [_vp, _ll]),
+    "rlse_bm_free_count": (_i, [_vp]),
+    "rlse_bm_allocate": (_i, [_vp, _cp, _ll, _ip, _i, ctypes.POINTER(_i)]),
+    "rlse_bm_allocate_block": (_i, [_vp, _cp, _ip]),
+    "rlse_bm_release": (_i, [_vp, _cp, ctypes.POINTER(_i)]),
+    "rlse_bm_fork": (_i, [_vp, _cp, _cp, _ll, _ip, _ip, _i, ctypes.POINTER(_i)]),
+    "rlse_bm_block_table": (_i, [_vp, _cp, _ip, _i, ctypes.POINTER(_i)]),
+    "rlse_bm_refcount": (_i, [_vp, _i]),
+    "rlse_bm_stats": (_i, [_vp, ctypes.POINTER(_CacheStats)]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads librlse_kv.so (built in tree next to this file); raises if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; "
+            "g.build()' or make -C mini-serve-rs_amd/csrc)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().rlse_last_error().decode("utf-8", "replace")
+
+
+def _check(status: int) -> None:
+    if status != OK:
+        msg = last_error()
+        if status == ERR_CACHE_PRESSURE:
+            raise CachePressure(status, msg)
+        raise RlseError(status, msg)
+
+
+def _ptr(x) -> Optional[int]:
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return int(x.data_ptr())
+
+
+def _dt(dtype) -> int:
+    if isinstance(dtype, int):
+        return dtype
+    name = str(dtype).replace("torch.", "")
+    return DTYPE_NAMES[name]
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream
+    return int(stream.cuda_stream)
+
+
+# --------------------------------------------------------------------------
+# Block manager (KVCache successor)
+# --------------------------------------------------------------------------
+class BlockManager:
+    """KVCache (src/cache/kv_cache.rs) over physical pool block ids."""
+
+    def __init__(self, total_blocks: int, block_size: int = BLOCK_SIZE):
+        lib = load()
+        h = _vp()
+        _check(lib.rlse_bm_create(total_blocks, block_size, ctypes.byref(h)))
+        self._h = h
+        self._lib = lib
+        self._total = total_blocks
+        self._block_size = block_size
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.rlse_bm_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def block_size(self) -> int:
+        return self._block_size
+
+    def total_blocks(self) -> int:
+        return self._total
+
+    def free_count(self) -> int:
+        return self._lib.rlse_bm_free_count(self._h)
+
+    def allocated_count(self) -> int:
+        return self._total - self.free_count()
+
+    def blocks_needed(self, tokens: int) -> int:
+        return self._lib.rlse_bm_blocks_needed(self._h, tokens)
+
+    def allocate(self, request_id: str, num_tokens: int) -> List[int]:
+        n = self.blocks_needed(num_tokens)
+        buf = (ctypes.c_int32 * max(n, 1))()
+        got = _i()
+        _check(self._lib.rlse_bm_allocate(self._h, request_id.encode(), num_tokens, buf, n,
+                                          ctypes.byref(got)))
+        return list(buf[:got.value])
+
+    def allocate_block(self, request_id: str) -> int:
+        b = ctypes.c_int32()
+        _check(self._lib.rlse_bm_allocate_block(self._h, request_id.encode(), ctypes.byref(b)))
+        return b.value
+
+    def release(self, request_id: str) -> int:
+        n = _i()
+        _check(self._lib.rlse_bm_release(self._h, request_id.encode(), ctypes.byref(n)))
+        return n.value
+
+    def fork(self, parent_id: str, child_id: str, num_tokens: int) -> List[Tuple[int, int]]:
+        src, dst, n = (ctypes.c_int32 * 1)(), (ctypes.c_int32 * 1)(), _i()
+        _check(self._lib.rlse_bm_fork(self._h, parent_id.encode(), child_id.encode(),
+                                      num_tokens, src, dst, 1, ctypes.byref(n)))
+        return [(src[i], dst[i]) for i in range(n.value)]
+
+    def block_table(self, request_id: str) -> List[int]:
+        n = _i()
+        _check(self._lib.rlse_bm_block_table(self._h, request_id.encode(), None, 0,
+                                             ctypes.byref(n)))
+        buf = (ctypes.c_int32 * max(n.value, 1))()
+        _check(self._lib.rlse_bm_block_table(self._h, request_id.encode(), buf, n.value,
+                                             ctypes.byref(n)))
+        return list(buf[:n.value])
+
+    def refcount(self, block: int) -> int:
+        return self._lib.rlse_bm_refcount(self._h, block)
+
+    def stats(self) -> CacheStats:
+        s = _CacheStats()
+        _check(self._lib.rlse_bm_stats(self._h, ctypes.byref(s)))
+        return CacheStats(s.total_blocks, s.allocated_blocks, s.free_blocks, s.utilization,
+                          s.fragmentation)
+
+
+# --------------------------------------------------------------------------
+# Physical pool
+# --------------------------------------------------------------------------
+class KVPool:
+    """Device pool [layers] x {K, V} x [num_blocks][Hkv][16][head_dim]."""
+
+    def __init__(self, num_layers: int, num_blocks: int, num_kv_heads: int, head_dim: int,
+                 dtype, block_size: int = BLOCK_SIZE):
+        lib = load()
+        h = _vp()
+        _check(lib.rlse_pool_create(num_layers, num_blocks, num_kv_heads, head_dim, _dt(dtype),
+                                    block_size, ctypes.byref(h)))
+        self._h = h
+        self._lib = lib
+        self.num_layers, self.num_blocks = num_layers, num_blocks
+        self.num_kv_heads, self.head_dim, self.dtype = num_kv_heads, head_dim, _dt(dtype)
+        stride = _ll()
+        _check(lib.rlse_pool_info(h, None, None, None, None, None, ctypes.byref(stride)))
+        self.layer_stride_elems = stride.value
+
+    def layer(self, layer: int) -> Tuple[int, int]:
+        k, v = _vp(), _vp()
+        _check(self._lib.rlse_pool_layer(self._h, layer, ctypes.byref(k), ctypes.byref(v)))
+        return k.value, v.value
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _check(self._lib.rlse_pool_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# --------------------------------------------------------------------------
+# Kernels
+# --------------------------------------------------------------------------
+def kv_append(k_new, v_new, k_pool, v_pool, block_tables, num_seqs: int, seq_index, positions,
+              num_tokens: int, num_kv_heads: int, head_dim: int, max_blocks_per_seq: int,
+              num_blocks: int, dtype, stream=None) -> None:
+    _check(load().rlse_kv_append(_ptr(k_new), _ptr(v_new), _ptr(k_pool), _ptr(v_pool),
+                                 _ptr(block_tables), num_seqs, _ptr(seq_index), _ptr(positions),
+                                 num_tokens, num_kv_heads, head_dim, max_blocks_per_seq,
+                                 num_blocks, _dt(dtype), _stream(stream)))
+
+
+def kv_gather(k_pool, v_pool, layer_stride_elems: int, num_layers: int, block_table, length: int,
+              k_out, v_out, num_kv_heads: int, head_dim: int, num_blocks: int, dtype,
+              stream=None) -> None:
+    _check(load().rlse_kv_gather(_ptr(k_pool), _ptr(v_pool), layer_stride_elems, num_layers,
+                                 _ptr(block_table), length, _ptr(k_out), _ptr(v_out),
+                                 num_kv_heads, head_dim, num_blocks, _dt(dtype), _stream(stream)))
+
+
+def kv_scatter(k_in, v_in, k_pool, v_pool, layer_stride_elems: int, num_layers: int, block_table,
+               start: int, length: int, num_kv_heads: int, head_dim: int, num_blocks: int, dtype,
+               stream=None) -> None:
+    _check(load().rlse_kv_scatter(_ptr(k_in), _ptr(v_in), _ptr(k_pool), _ptr(v_pool),
+                                  layer_stride_elems, num_layers, _ptr(block_table), start,
+                                  length, num_kv_heads, head_dim, num_blocks, _dt(dtype),
+                                  _stream(stream)))
+
+
+def kv_copy_blocks(k_pool, v_pool, layer_stride_elems: int, num_layers: int, src_blocks,
+                   dst_blocks, num_pairs: int, num_kv_heads: int, head_dim: int,
+                   num_blocks: int, dtype, stream=None) -> None:
+    _check(load().rlse_kv_copy_blocks(_ptr(k_pool), _ptr(v_pool), layer_stride_elems,
+                                      num_layers, _ptr(src_blocks), _ptr(dst_blocks), num_pairs,
+                                      num_kv_heads, head_dim, num_blocks, _dt(dtype),
+                                      _stream(stream)))
+
+
+def decode_workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    n = _sz()
+    _check(load().rlse_decode_workspace_size(batch, num_heads, num_kv_heads, head_dim,
+                                             ctypes.byref(n)))
+    return n.value
+
+
+def paged_gqa_decode(q, k_pool, v_pool, block_tables, seq_lens, out, batch: int, num_heads: int,
+                     num_kv_heads: int, head_dim: int, max_blocks_per_seq: int, num_blocks: int,
+                     scale: float, dtype, workspace=None, workspace_bytes: int = 0,
+                     stream=None) -> None:
+    _check(load().rlse_paged_gqa_decode(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
+                                        _ptr(seq_lens), _ptr(out), batch, num_heads,
+                                        num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
+                                        scale, _dt(dtype), _ptr(workspace), workspace_bytes,
+                                        _stream(stream)))
+
+
+def rmsnorm(x, weight, out, rows: int, n: int, eps: float, dtype, stream=None) -> None:
+    _check(load().rlse_rmsnorm(_ptr(x), _ptr(weight), _ptr(out), rows, n, eps, _dt(dtype),
+                               _stream(stream)))
+
+
+def rope_tables(theta: float, head_dim: int, max_pos: int, dtype):
+    """Host cos/sin tables [max_pos][head_dim/2] as raw bytes (bytearray pair)."""
+    es = DTYPE_SIZE[_dt(dtype)]
+    n = max_pos * (head_dim // 2)
+    cos_b = (ctypes.c_char * (n * es))()
+    sin_b = (ctypes.c_char * (n * es))()
+    _check(load().rlse_rope_tables(theta, head_dim, max_pos, _dt(dtype),
+                                   ctypes.cast(cos_b, _vp), ctypes.cast(sin_b, _vp)))
+    return bytes(cos_b), bytes(sin_b)
+
+
+def rope(q, k, cos_table, sin_table, positions, num_tokens: int, num_heads: int,
+         num_kv_heads: int, head_dim: int, max_pos: int, dtype, stream=None) -> None:
+    _check(load().rlse_rope(_ptr(q), _ptr(k), _ptr(cos_table), _ptr(sin_table), _ptr(positions),
+                            num_tokens, num_heads, num_kv_heads, head_dim, max_pos, _dt(dtype),
+                            _stream(stream)))
+
+
+def qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, eps: float, cos_table, sin_table,
+                        max_pos: int, positions, block_tables, num_seqs: int, seq_index,
+                        num_tokens: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                        max_blocks_per_seq: int, num_blocks: int, q_out, k_pool, v_pool, dtype,
+                        stream=None) -> None:
+    _check(load().rlse_qk_norm_rope_append(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm_weight), _ptr(k_norm_weight), eps,
+        _ptr(cos_table), _ptr(sin_table), max_pos, _ptr(positions), _ptr(block_tables),
+        num_seqs, _ptr(seq_index), num_tokens, num_heads, num_kv_heads, head_dim,
+        max_blocks_per_seq, num_blocks, _ptr(q_out), _ptr(k_pool), _ptr(v_pool), _dt(dtype),
+        _stream(stream)))

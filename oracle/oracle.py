@@ -1,0 +1,361 @@
+"""Oracle for the KV-cache hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use this
+module, and only as the checker (or the timed CPU baseline). The product path
+(librlse_kv.so and its binding) never imports it.
+
+Two layers:
+
+1. ``C`` -- ctypes binding of liboracle.so (oracle/rlse_oracle.c), a C
+   restatement of the reference's Candle CPU path in f32: KvCache
+   append/narrow, the prototype's paged layout, zero-copy GQA decode, masked
+   prefill, RmsNorm with Candle's cast order, RoPE tables and apply_rope.
+2. numpy float64 textbook forms (``*_f64``) of the same math, used to pin the
+   C restatement: softmax(q K^T * scale) V with GQA head mapping h // G,
+   the causal mask with an offset, RMSNorm and NeoX RoPE in exact arithmetic.
+
+Plus ``KVCacheModel``, a pure-Python restatement of the reference block
+allocator (src/cache/kv_cache.rs:15-145) used to cross-check the C++ block
+manager on random operation sequences.
+
+Parity status of each function (how it is pinned) is listed in the module
+docstring of tests/test_oracle.py.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Dict, List, Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} missing: run `make -C oracle`")
+    lib = ctypes.CDLL(LIB_PATH)
+    vp, i, f, d, ll = (ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_double,
+                       ctypes.c_longlong)
+    sigs = {
+        "orc_bf16_to_f32_array": (None, [vp, vp, ll]),
+        "orc_f32_to_bf16_array": (None, [vp, vp, ll]),
+        "orc_kvcache_append": (i, [vp, i, i, i, i, i, vp, i]),
+        "orc_kvcache_narrow": (None, [vp, i, i, i, i, i, vp]),
+        "orc_paged_write_token": (None, [vp, i, i, i, vp, i, vp]),
+        "orc_paged_to_contiguous": (None, [vp, i, i, i, vp, i, vp]),
+        "orc_decode_gqa_f32": (None, [vp, vp, vp, i, i, i, i, i, f, vp]),
+        "orc_decode_batch_f32": (None, [vp, vp, vp, vp, i, i, i, i, i, f, vp, i]),
+        "orc_prefill_f32": (None, [vp, vp, vp, i, i, i, i, i, i, f, vp, i]),
+        "orc_rmsnorm_f32": (None, [vp, vp, vp, i, i, f]),
+        "orc_rmsnorm_bf16": (None, [vp, vp, vp, i, i, f]),
+        "orc_rope_tables_f32": (None, [d, i, i, vp, vp]),
+        "orc_apply_rope_f32": (None, [vp, vp, vp, vp, i, i]),
+        "orc_apply_rope_bf16": (None, [vp, vp, vp, vp, i, i]),
+        "orc_decode_step_f32": (None, [vp, vp, vp, vp, vp, vp, i, i, i, i, i, f, vp, i]),
+        "orc_max_threads": (i, []),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+# ---------------------------------------------------------------------------
+# bf16 helpers (numpy), identical rounding to the C restatement
+# ---------------------------------------------------------------------------
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    load().orc_f32_to_bf16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    return bf16_bits_to_f32(f32_to_bf16_bits(x))
+
+
+# ---------------------------------------------------------------------------
+# C restatement wrappers
+# ---------------------------------------------------------------------------
+class KvCacheC:
+    """candle_nn KvCache over dim 2 of [1, Hkv, cap, d], bytes of any dtype."""
+
+    def __init__(self, hkv: int, cap: int, d: int, np_dtype):
+        self.hkv, self.cap, self.d = hkv, cap, d
+        self.dtype = np.dtype(np_dtype)
+        self.k = np.zeros((hkv, cap, d), dtype=self.dtype)
+        self.v = np.zeros((hkv, cap, d), dtype=self.dtype)
+        self.cur_len = 0
+
+    def append(self, k_new: np.ndarray, v_new: np.ndarray) -> None:
+        """k_new, v_new [Hkv, q, d] (Attention::append_kv, qwen2.rs:349-361)."""
+        k_new = np.ascontiguousarray(k_new, dtype=self.dtype)
+        v_new = np.ascontiguousarray(v_new, dtype=self.dtype)
+        q = k_new.shape[1]
+        es = self.dtype.itemsize
+        lib = load()
+        n1 = lib.orc_kvcache_append(_p(self.k), self.hkv, self.cap, self.d, es, self.cur_len,
+                                    _p(k_new), q)
+        n2 = lib.orc_kvcache_append(_p(self.v), self.hkv, self.cap, self.d, es, self.cur_len,
+                                    _p(v_new), q)
+        if n1 < 0 or n2 < 0:
+            raise ValueError("kv-cache: above max-seq-len")
+        self.cur_len = n1
+
+    def snapshot(self):
+        """get_kv_snapshot: narrow(2, 0, cur_len), contiguous copies."""
+        es = self.dtype.itemsize
+        k = np.empty((self.hkv, self.cur_len, self.d), dtype=self.dtype)
+        v = np.empty_like(k)
+        lib = load()
+        lib.orc_kvcache_narrow(_p(self.k), self.hkv, self.cap, self.d, es, self.cur_len, _p(k))
+        lib.orc_kvcache_narrow(_p(self.v), self.hkv, self.cap, self.d, es, self.cur_len, _p(v))
+        return k, v
+
+
+def paged_write_token(pool: np.ndarray, table: np.ndarray, pos: int, row: np.ndarray) -> None:
+    """pool [nb, Hkv, 16, d]; row [Hkv, d]; prototype index formula."""
+    nb, hkv, bs, d = pool.shape
+    table = np.ascontiguousarray(table, dtype=np.int32)
+    row = np.ascontiguousarray(row, dtype=pool.dtype)
+    load().orc_paged_write_token(_p(pool), hkv, d, pool.dtype.itemsize, _p(table), pos, _p(row))
+
+
+def paged_to_contiguous(pool: np.ndarray, table: np.ndarray, length: int) -> np.ndarray:
+    nb, hkv, bs, d = pool.shape
+    table = np.ascontiguousarray(table, dtype=np.int32)
+    out = np.empty((hkv, length, d), dtype=pool.dtype)
+    load().orc_paged_to_contiguous(_p(pool), hkv, d, pool.dtype.itemsize, _p(table), length,
+                                   _p(out))
+    return out
+
+
+def decode_batch_f32(q: np.ndarray, k: np.ndarray, v: np.ndarray, lens: np.ndarray,
+                     scale: float, threads: int = 0) -> np.ndarray:
+    """q [B, Hq, d]; k, v [B, Hkv, cap, d] f32; returns [B, Hq, d] f32."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    lens = np.ascontiguousarray(lens, dtype=np.int32)
+    b, hq, d = q.shape
+    hkv, cap = k.shape[1], k.shape[2]
+    out = np.empty_like(q)
+    load().orc_decode_batch_f32(_p(q), _p(k), _p(v), _p(lens), b, hq, hkv, cap, d, scale,
+                                _p(out), threads)
+    return out
+
+
+def decode_paged_f32(q: np.ndarray, k_pool: np.ndarray, v_pool: np.ndarray, tables: np.ndarray,
+                     lens: np.ndarray, scale: float, threads: int = 0) -> np.ndarray:
+    """Decode over a paged pool by first laying each sequence out contiguously
+    (the reference's buffer layout) and then running the C restatement."""
+    b = q.shape[0]
+    hkv, d = k_pool.shape[1], k_pool.shape[3]
+    cap = max(int(max(lens)), 1)
+    kc = np.zeros((b, hkv, cap, d), dtype=np.float32)
+    vc = np.zeros_like(kc)
+    for i in range(b):
+        n = int(lens[i])
+        if n > 0:
+            kc[i, :, :n] = paged_to_contiguous(k_pool, tables[i], n).astype(np.float32)
+            vc[i, :, :n] = paged_to_contiguous(v_pool, tables[i], n).astype(np.float32)
+    return decode_batch_f32(q.astype(np.float32), kc, vc, lens, scale, threads)
+
+
+def prefill_f32(q: np.ndarray, k: np.ndarray, v: np.ndarray, offset: int, scale: float,
+                threads: int = 0) -> np.ndarray:
+    """q [Hq, q_len, d]; k, v [Hkv, cap, d]; keys 0..offset+q_len-1 visible."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    hq, ql, d = q.shape
+    hkv, cap = k.shape[0], k.shape[1]
+    out = np.empty_like(q)
+    load().orc_prefill_f32(_p(q), _p(k), _p(v), hq, hkv, cap, ql, offset, d, scale, _p(out),
+                           threads)
+    return out
+
+
+def rmsnorm_f32(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, n = x.reshape(-1, x.shape[-1]).shape
+    out = np.empty_like(x)
+    load().orc_rmsnorm_f32(_p(x), _p(w), _p(out), rows, n, eps)
+    return out
+
+
+def rmsnorm_bf16(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    rows, n = x.reshape(-1, x.shape[-1]).shape
+    out = np.empty_like(x)
+    load().orc_rmsnorm_bf16(_p(x), _p(w), _p(out), rows, n, eps)
+    return out
+
+
+def rope_tables_f32(theta: float, d: int, max_pos: int):
+    c = np.empty((max_pos, d // 2), dtype=np.float32)
+    s = np.empty_like(c)
+    load().orc_rope_tables_f32(theta, d, max_pos, _p(c), _p(s))
+    return c, s
+
+
+def apply_rope_f32(x: np.ndarray, pos: np.ndarray, cos_t: np.ndarray, sin_t: np.ndarray):
+    """x [rows, d] (copied), pos [rows]."""
+    x = np.array(x, dtype=np.float32, order="C")
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    load().orc_apply_rope_f32(_p(x), _p(pos), _p(np.ascontiguousarray(cos_t, np.float32)),
+                              _p(np.ascontiguousarray(sin_t, np.float32)), x.shape[0],
+                              x.shape[1])
+    return x
+
+
+def apply_rope_bf16(x_bits: np.ndarray, pos: np.ndarray, cos_bits: np.ndarray,
+                    sin_bits: np.ndarray):
+    x = np.array(x_bits, dtype=np.uint16, order="C")
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    load().orc_apply_rope_bf16(_p(x), _p(pos), _p(np.ascontiguousarray(cos_bits, np.uint16)),
+                               _p(np.ascontiguousarray(sin_bits, np.uint16)), x.shape[0],
+                               x.shape[1])
+    return x
+
+
+def decode_step_f32(q, k_new, v_new, k, v, lens, scale, threads=0):
+    """Append + decode of one layer on contiguous buffers (timed CPU baseline)."""
+    b, hq, d = q.shape
+    hkv, cap = k.shape[1], k.shape[2]
+    out = np.empty_like(q)
+    load().orc_decode_step_f32(_p(q), _p(k_new), _p(v_new), _p(k), _p(v), _p(lens), b, hq, hkv,
+                               cap, d, scale, _p(out), threads)
+    return out
+
+
+def max_threads() -> int:
+    return load().orc_max_threads()
+
+
+# ---------------------------------------------------------------------------
+# numpy float64 textbook forms
+# ---------------------------------------------------------------------------
+def softmax_f64(s: np.ndarray, axis: int = -1) -> np.ndarray:
+    s = s - np.max(s, axis=axis, keepdims=True)
+    e = np.exp(s)
+    return e / np.sum(e, axis=axis, keepdims=True)
+
+
+def decode_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
+    """One sequence: q [Hq, d]; k, v [Hkv, L, d]; query head h uses KV head h // G."""
+    hq = q.shape[0]
+    hkv = k.shape[0]
+    g = hq // hkv
+    q = q.astype(np.float64)
+    kk = np.repeat(k.astype(np.float64), g, axis=0)  # repeat_kv
+    vv = np.repeat(v.astype(np.float64), g, axis=0)
+    s = np.einsum("hd,hld->hl", q, kk) * scale
+    return np.einsum("hl,hld->hd", softmax_f64(s), vv)
+
+
+def prefill_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, offset: int, scale: float):
+    """q [Hq, q_len, d]; k, v [Hkv, offset+q_len, d]; causal with offset."""
+    hq, ql, d = q.shape
+    hkv, lk = k.shape[0], k.shape[1]
+    g = hq // hkv
+    kk = np.repeat(k.astype(np.float64), g, axis=0)
+    vv = np.repeat(v.astype(np.float64), g, axis=0)
+    s = np.einsum("hid,hjd->hij", q.astype(np.float64), kk) * scale
+    i = np.arange(ql)[:, None]
+    j = np.arange(lk)[None, :]
+    s = np.where(j - offset > i, -np.inf, s)
+    return np.einsum("hij,hjd->hid", softmax_f64(s), vv)
+
+
+def rmsnorm_f64(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = x.astype(np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w.astype(np.float64)
+
+
+def rope_f64(x: np.ndarray, pos: np.ndarray, theta: float) -> np.ndarray:
+    """NeoX rotation in float64: pairs (i, i + d/2) rotated by pos * theta^(-2i/d)."""
+    x = x.astype(np.float64)
+    d = x.shape[-1]
+    half = d // 2
+    inv = theta ** (-(2.0 * np.arange(half)) / d)
+    ang = np.asarray(pos, dtype=np.float64)[:, None] * inv[None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    x1, x2 = x[:, :half], x[:, half:]
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1)
+
+
+# ---------------------------------------------------------------------------
+# KVCache (src/cache/kv_cache.rs:15-145), pure Python
+# ---------------------------------------------------------------------------
+class KVCacheModel:
+    def __init__(self, total_blocks: int, block_size: int = 16):
+        self.total = total_blocks
+        self.block_size = block_size
+        self.free = list(range(total_blocks - 1, -1, -1))  # pop() yields 0, 1, 2, ...
+        self.allocations: Dict[str, List[int]] = {}
+
+    def blocks_needed(self, tokens: int) -> int:
+        return 1 if tokens == 0 else -(-tokens // self.block_size)
+
+    def allocate(self, rid: str, num_tokens: int) -> List[int]:
+        needed = self.blocks_needed(num_tokens)
+        if needed > len(self.free):
+            raise MemoryError(f"Requested {needed} blocks ({num_tokens} tokens), but only "
+                              f"{len(self.free)} free blocks remain")
+        blocks = [self.free.pop() for _ in range(needed)]
+        self.allocations[rid] = list(blocks)
+        return blocks
+
+    def allocate_block(self, rid: str) -> int:
+        if not self.free:
+            raise MemoryError("KV cache pressure: no free blocks remaining for incremental "
+                              "allocation")
+        b = self.free.pop()
+        self.allocations.setdefault(rid, []).append(b)
+        return b
+
+    def release(self, rid: str) -> int:
+        blocks = self.allocations.pop(rid, None)
+        if blocks is None:
+            return 0
+        self.free.extend(blocks)
+        return len(blocks)
+
+    def stats(self):
+        free = len(self.free)
+        allocated = self.total - free
+        util = np.float32(allocated) / np.float32(self.total) if self.total > 0 else np.float32(0)
+        fs = set(self.free)
+        runs = sum(1 for i in range(self.total) if i in fs and (i == 0 or (i - 1) not in fs))
+        frag = (np.float32(runs) - np.float32(1)) / np.float32(free) if (free > 0 and runs > 1) \
+            else np.float32(0)
+
+        def r3(x):
+            x = np.float32(x) * np.float32(1000.0)
+            return np.float32(math.floor(abs(float(x)) + 0.5) * (1 if x >= 0 else -1)) \
+                / np.float32(1000.0)
+        return (self.total, allocated, free, float(r3(util)), float(r3(min(frag, 1.0))))

@@ -1,0 +1,229 @@
+"""Paged GQA decode attention on the GPU against the oracle.
+
+Reference: decode_attention_gqa_zero_copy (src/backends/qwen2.rs:177-203) over
+the buffers KvCache::append builds (:349-361), batched as in
+step_decode_batch (:723-744). The oracle is the C restatement of that Candle
+CPU path (oracle/rlse_oracle.c), itself pinned against float64 forms in
+tests/test_oracle.py. Bars: max-abs 2e-3 for f32, 2e-2 for bf16/f16; the
+relative error (max-abs / max |reference|) is printed beside it.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import (DEV, TOL, as_f32, build_tables, err_report, random_values, to_dev,
+                         to_host)
+
+pytestmark = pytest.mark.gpu
+
+
+def run_decode(kv, q, kp, vp, tables, lens, hq, hkv, d, dtype, scale, workspace=None):
+    b, mbps, nb = q.shape[0], tables.shape[1], kp.shape[0]
+    out = torch.empty_like(q)
+    ws, wsb = None, 0
+    if workspace is not None:
+        ws, wsb = workspace, workspace.numel()
+    kv.paged_gqa_decode(q, kp, vp, to_dev(tables), to_dev(lens), out, b, hq, hkv, d, mbps, nb,
+                        scale, dtype, ws, wsb)
+    return to_host(out)
+
+
+def check(name, got, want, dtype):
+    mx, rel = err_report(got, want)
+    print(f"[{name}] dtype={dtype} max_abs={mx:.3e} rel={rel:.3e}")
+    assert np.isfinite(got).all()
+    assert mx <= TOL[dtype], (name, mx)
+    return mx, rel
+
+
+def make_case(rng, lens, hq, hkv, d, dtype, extra_blocks=7):
+    lens = np.asarray(lens, np.int32)
+    mbps = max(1, int(max((int(n) + 15) // 16 for n in lens)))
+    nb = int(sum((int(n) + 15) // 16 for n in lens)) + extra_blocks
+    tables = build_tables(rng, lens, nb, mbps)
+    kpool = random_values(rng, (nb, hkv, 16, d), dtype)
+    vpool = random_values(rng, (nb, hkv, 16, d), dtype)
+    q = random_values(rng, (len(lens), hq, d), dtype)
+    return q, kpool, vpool, tables, lens
+
+
+def oracle_decode(q, kpool, vpool, tables, lens, dtype, scale):
+    return O.decode_paged_f32(as_f32(q, dtype), as_f32(kpool, dtype), as_f32(vpool, dtype),
+                              tables, lens, scale)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("fixture", ["decode_f32.npz", "decode_gqa7_f32.npz"])
+def test_golden_case_matrix(kv, dtype, fixture):
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", fixture))
+    q, kpool, vpool = g["q"], g["k_pool"], g["v_pool"]
+    if dtype == "f32":
+        q, kpool, vpool = (O.bf16_bits_to_f32(x) for x in (q, kpool, vpool))
+    hq, d = q.shape[1], q.shape[2]
+    hkv = kpool.shape[1]
+    got = run_decode(kv, to_dev(q, dtype), to_dev(kpool, dtype), to_dev(vpool, dtype),
+                     g["tables"], g["lens"], hq, hkv, d, dtype, float(g["scale"]))
+    check(f"golden {fixture}", as_f32(got, dtype), g["out_f64"], dtype)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (14, 2, 64), (32, 8, 128), (8, 8, 64),
+                                      (24, 3, 128), (40, 5, 64), (48, 8, 128), (64, 8, 64)])
+def test_group_sizes_and_ragged_lengths(kv, dtype, hq, hkv, d):
+    rng = np.random.default_rng(hq * 131 + d)
+    lens = [1, 2, 15, 16, 17, 33, 64, 127, 300, 513]
+    q, kp, vp, tables, lens = make_case(rng, lens, hq, hkv, d, dtype)
+    scale = 1.0 / math.sqrt(d)
+    got = run_decode(kv, to_dev(q, dtype), to_dev(kp, dtype), to_dev(vp, dtype), tables, lens,
+                     hq, hkv, d, dtype, scale)
+    want = oracle_decode(q, kp, vp, tables, lens, dtype, scale)
+    check(f"G={hq // hkv} d={d}", as_f32(got, dtype), want, dtype)
+
+
+def test_config1_qwen3_f32_decode_step(kv):
+    """Single-layer Qwen3-0.6B decode step, f32, batch 1: 16 query heads, 8 KV
+    heads, head_dim 128, 512 cached tokens; q and the new k go through
+    q_norm/k_norm (eps 1e-6, weights 1 + 0.1 N(0,1)) and RoPE (theta 1e6) at
+    position 512; the new k/v are appended and attention runs over 513 keys
+    (Attention::forward order, src/backends/qwen2.rs:291-328)."""
+    rng = np.random.default_rng(1)
+    hq, hkv, d, cached, theta, eps = 16, 8, 128, 512, 1e6, 1e-6
+    nb, mbps = 48, 33
+    tables = build_tables(rng, [cached + 1], nb, mbps)
+    k_cache = rng.standard_normal((hkv, cached, d)).astype(np.float32)
+    v_cache = rng.standard_normal((hkv, cached, d)).astype(np.float32)
+    q_raw = rng.standard_normal((1, hq, d)).astype(np.float32)
+    k_raw = rng.standard_normal((1, hkv, d)).astype(np.float32)
+    v_raw = rng.standard_normal((1, hkv, d)).astype(np.float32)
+    qw = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    kw = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    scale = 1.0 / math.sqrt(d)
+
+    # oracle: the reference's Candle CPU op sequence
+    cos_t, sin_t = O.rope_tables_f32(theta, d, cached + 1)
+    pos = np.full(hq, cached, np.int32)
+    q_o = O.apply_rope_f32(O.rmsnorm_f32(q_raw[0], qw, eps), pos, cos_t, sin_t)
+    k_o = O.apply_rope_f32(O.rmsnorm_f32(k_raw[0], kw, eps), pos[:hkv], cos_t, sin_t)
+    cache_k = O.KvCacheC(hkv, cached + 1, d, np.float32)
+    cache_v = O.KvCacheC(hkv, cached + 1, d, np.float32)
+    cache_k.append(k_cache, k_cache)
+    cache_v.append(v_cache, v_cache)
+    cache_k.append(k_o[:, None], k_o[:, None])
+    cache_v.append(v_raw[0][:, None], v_raw[0][:, None])
+    want = O.decode_batch_f32(q_o[None], cache_k.snapshot()[0][None], cache_v.snapshot()[0][None],
+                              np.array([cached + 1], np.int32), scale)
+
+    # device: restore the cached tokens, fused norm + RoPE + append, decode
+    kp = torch.zeros((nb, hkv, 16, d), dtype=torch.float32, device=DEV)
+    vp = torch.zeros_like(kp)
+    t_dev = to_dev(tables)
+    kv.kv_scatter(to_dev(k_cache), to_dev(v_cache), kp, vp, 0, 1, t_dev, 0, cached, hkv, d, nb,
+                  "f32")
+    cos_b, sin_b = kv.rope_tables(theta, d, cached + 1, "f32")
+    cos_d = to_dev(np.frombuffer(cos_b, np.float32).copy())
+    sin_d = to_dev(np.frombuffer(sin_b, np.float32).copy())
+    q_rot = torch.empty((1, hq, d), dtype=torch.float32, device=DEV)
+    kv.qk_norm_rope_append(to_dev(q_raw), to_dev(k_raw), to_dev(v_raw), to_dev(qw), to_dev(kw),
+                           eps, cos_d, sin_d, cached + 1, to_dev(np.array([cached], np.int32)),
+                           t_dev, 1, None, 1, hq, hkv, d, mbps, nb, q_rot, kp, vp, "f32")
+    np.testing.assert_allclose(to_host(q_rot)[0], q_o, rtol=2e-6, atol=2e-6)
+    got = run_decode(kv, q_rot, kp, vp, tables, np.array([cached + 1], np.int32), hq, hkv, d,
+                     "f32", scale)
+    check("config1", got, want, "f32")
+
+
+@pytest.mark.parametrize("hq,hkv,d,batch,lmin,lmax", [
+    (16, 8, 128, 32, 128, 2048),   # Qwen3-0.6B batched decode, one layer
+    (14, 2, 64, 64, 4096, 4096),   # Qwen2.5-0.5B, 4096 cached tokens
+])
+def test_full_batch_one_layer_bf16(kv, hq, hkv, d, batch, lmin, lmax):
+    """One layer of the batched-decode workloads at their full batch and
+    length mix: ragged lengths + 1 appended token, 16-token blocks drawn
+    from a seeded random permutation."""
+    rng = np.random.default_rng(2 if hq == 16 else 3)
+    lens = rng.integers(lmin, lmax + 1, batch) + 1
+    q, kp, vp, tables, lens = make_case(rng, lens, hq, hkv, d, "bf16")
+    scale = 1.0 / math.sqrt(d)
+    got = run_decode(kv, to_dev(q, "bf16"), to_dev(kp, "bf16"), to_dev(vp, "bf16"), tables, lens,
+                     hq, hkv, d, "bf16", scale)
+    want = oracle_decode(q, kp, vp, tables, lens, "bf16", scale)
+    check(f"batch{batch} G={hq // hkv}", as_f32(got, "bf16"), want, "bf16")
+
+
+def test_edge_lengths_and_invalid_blocks(kv):
+    rng = np.random.default_rng(9)
+    hq, hkv, d, dtype = 16, 8, 128, "bf16"
+    q, kp, vp, tables, _ = make_case(rng, [48, 48, 48, 48], hq, hkv, d, dtype)
+    nb = kp.shape[0]
+    tables = tables.copy()
+    tables[2, 1] = nb + 5  # middle page outside the pool: skipped
+    lens = np.array([0, 48, 48, 1000], np.int32)  # empty row; clamp to 3 pages * 16
+    got = as_f32(run_decode(kv, to_dev(q, dtype), to_dev(kp, dtype), to_dev(vp, dtype), tables,
+                            lens, hq, hkv, d, dtype, 0.088), dtype)
+    assert np.all(got[0] == 0.0)
+    want1 = oracle_decode(q[1:2], kp, vp, tables[1:2], np.array([48], np.int32), dtype, 0.088)
+    check("plain row", got[1:2], want1, dtype)
+    # row 2 without its second page: keys 0-15 and 32-47
+    kf, vf = as_f32(kp, dtype), as_f32(vp, dtype)
+    t2 = tables[2]
+    k2 = np.concatenate([O.paged_to_contiguous(kf, t2[:1], 16),
+                         O.paged_to_contiguous(kf, t2[2:3], 16)], axis=1)
+    v2 = np.concatenate([O.paged_to_contiguous(vf, t2[:1], 16),
+                         O.paged_to_contiguous(vf, t2[2:3], 16)], axis=1)
+    want2 = O.decode_batch_f32(as_f32(q[2:3], dtype), k2[None], v2[None],
+                               np.array([32], np.int32), 0.088)
+    check("skipped page", got[2:3], want2, dtype)
+    want3 = oracle_decode(q[3:4], kp, vp, tables[3:4], np.array([48], np.int32), dtype, 0.088)
+    check("clamped length", got[3:4], want3, dtype)
+
+
+def test_workspace_paths_and_prototype_launcher_agree(kv):
+    rng = np.random.default_rng(10)
+    hq, hkv, d, dtype = 16, 8, 128, "bf16"
+    lens = rng.integers(100, 900, 12) + 1
+    q, kp, vp, tables, lens = make_case(rng, lens, hq, hkv, d, dtype)
+    qd, kd, vd = to_dev(q, dtype), to_dev(kp, dtype), to_dev(vp, dtype)
+    a = run_decode(kv, qd, kd, vd, tables, lens, hq, hkv, d, dtype, 0.0883)
+    ws = torch.empty(kv.decode_workspace_size(len(lens), hq, hkv, d), dtype=torch.uint8,
+                     device=DEV)
+    b = run_decode(kv, qd, kd, vd, tables, lens, hq, hkv, d, dtype, 0.0883, workspace=ws)
+    out = torch.empty_like(qd)
+    t_dev, l_dev = to_dev(tables), to_dev(lens)  # keep the buffers alive until the kernel ran
+    rc = kv.load().launch_paged_gqa_decode_tiled_bf16(
+        qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), t_dev.data_ptr(), l_dev.data_ptr(),
+        out.data_ptr(), len(lens), hq, hkv, tables.shape[1], 0.0883)
+    assert rc == 0
+    c = to_host(out)
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(a, c)
+    # repeated launches are deterministic
+    np.testing.assert_array_equal(a, run_decode(kv, qd, kd, vd, tables, lens, hq, hkv, d, dtype,
+                                                0.0883))
+    with pytest.raises(kv.RlseError):
+        small = torch.empty(16, dtype=torch.uint8, device=DEV)
+        run_decode(kv, qd, kd, vd, tables, lens, hq, hkv, d, dtype, 0.0883, workspace=small)
+
+
+def test_physical_placement_does_not_change_result(kv):
+    """Moving every page to a different physical block (and rewriting the
+    table) must give bit-identical output: the kernel sees only the table."""
+    rng = np.random.default_rng(11)
+    hq, hkv, d, dtype = 16, 8, 128, "bf16"
+    lens = rng.integers(1, 700, 9) + 1
+    q, kp, vp, tables, lens = make_case(rng, lens, hq, hkv, d, dtype)
+    nb = kp.shape[0]
+    perm = rng.permutation(nb)
+    kp2, vp2 = np.empty_like(kp), np.empty_like(vp)
+    kp2[perm], vp2[perm] = kp, vp
+    t2 = perm[tables].astype(np.int32)
+    for i, n in enumerate(lens):
+        t2[i, (int(n) + 15) // 16:] = 0
+    a = run_decode(kv, to_dev(q, dtype), to_dev(kp, dtype), to_dev(vp, dtype), tables, lens, hq,
+                   hkv, d, dtype, 0.0883)
+    b = run_decode(kv, to_dev(q, dtype), to_dev(kp2, dtype), to_dev(vp2, dtype), t2, lens, hq,
+                   hkv, d, dtype, 0.0883)
+    np.testing.assert_array_equal(a, b)

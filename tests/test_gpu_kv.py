@@ -1,0 +1,184 @@
+"""KV data movement on the GPU, bit-exact against the reference layout.
+
+The reference keeps each request's K/V in a contiguous [1, Hkv, cap, d] buffer
+written by KvCache::append (src/backends/qwen2.rs:349-361), restores prefix
+snapshots by copying (set_kv_snapshot, :373-377, 547-574) and requires the
+cached snapshot bytes to be unchanged after reuse (src/backends/candle.rs:
+1281-1292). Here the same bytes must come out of the paged pool.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import DEV, NP_OF, build_tables, random_values, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = ["bf16", "f32", "f16"]
+SHAPES = [(8, 128), (2, 64)]  # (Hkv, head_dim): Qwen3-0.6B, Qwen2.5-0.5B
+
+
+def _pool(num_blocks, hkv, d, dtype):
+    return torch.zeros((num_blocks, hkv, 16, d), dtype={"bf16": torch.bfloat16,
+                                                        "f32": torch.float32,
+                                                        "f16": torch.float16}[dtype], device=DEV)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("hkv,d", SHAPES)
+def test_append_is_bit_exact(kv, dtype, hkv, d):
+    rng = np.random.default_rng(100)
+    nb, mbps = 64, 8
+    prompts = [1, 15, 16, 17, 40]
+    steps = 20
+    b = len(prompts)
+    tables = build_tables(rng, [p + steps for p in prompts], nb, mbps)
+    t_dev = to_dev(tables)
+    kp, vp = _pool(nb, hkv, d, dtype), _pool(nb, hkv, d, dtype)
+    np_dt = NP_OF[dtype]
+    pool_k = np.zeros((nb, hkv, 16, d), np_dt)
+    pool_v = np.zeros_like(pool_k)
+    caches = [(O.KvCacheC(hkv, 128, d, np_dt), O.KvCacheC(hkv, 128, d, np_dt)) for _ in range(b)]
+
+    # prefill-style multi-token append: every prompt token of every sequence
+    seq_index = np.concatenate([np.full(p, i, np.int32) for i, p in enumerate(prompts)])
+    positions = np.concatenate([np.arange(p, dtype=np.int32) for p in prompts])
+    n = len(positions)
+    k_new = random_values(rng, (n, hkv, d), dtype)
+    v_new = random_values(rng, (n, hkv, d), dtype)
+    kv.kv_append(to_dev(k_new, dtype), to_dev(v_new, dtype), kp, vp, t_dev, b,
+                 to_dev(seq_index), to_dev(positions), n, hkv, d, mbps, nb, dtype)
+    for t in range(n):
+        s, p = seq_index[t], positions[t]
+        O.paged_write_token(pool_k, tables[s], p, k_new[t])
+        O.paged_write_token(pool_v, tables[s], p, v_new[t])
+        caches[s][0].append(k_new[t][:, None], k_new[t][:, None])
+        caches[s][1].append(v_new[t][:, None], v_new[t][:, None])
+
+    # decode-style appends: one token per sequence per step
+    lens = np.array(prompts, np.int32)
+    for _ in range(steps):
+        k1 = random_values(rng, (b, hkv, d), dtype)
+        v1 = random_values(rng, (b, hkv, d), dtype)
+        kv.kv_append(to_dev(k1, dtype), to_dev(v1, dtype), kp, vp, t_dev, b, None,
+                     to_dev(lens), b, hkv, d, mbps, nb, dtype)
+        for s in range(b):
+            O.paged_write_token(pool_k, tables[s], int(lens[s]), k1[s])
+            O.paged_write_token(pool_v, tables[s], int(lens[s]), v1[s])
+            caches[s][0].append(k1[s][:, None], k1[s][:, None])
+            caches[s][1].append(v1[s][:, None], v1[s][:, None])
+        lens += 1
+
+    np.testing.assert_array_equal(to_host(kp), pool_k)
+    np.testing.assert_array_equal(to_host(vp), pool_v)
+    for s in range(b):
+        length = int(lens[s])
+        ko = torch.empty((hkv, length, d), dtype=kp.dtype, device=DEV)
+        vo = torch.empty_like(ko)
+        kv.kv_gather(kp, vp, 0, 1, to_dev(tables[s]), length, ko, vo, hkv, d, nb, dtype)
+        np.testing.assert_array_equal(to_host(ko), caches[s][0].snapshot()[0])
+        np.testing.assert_array_equal(to_host(vo), caches[s][1].snapshot()[0])
+
+
+def test_append_skips_out_of_range_slots(kv):
+    rng = np.random.default_rng(101)
+    nb, mbps, hkv, d = 8, 2, 2, 64
+    tables = np.array([[3, 99], [5, -1]], np.int32)  # invalid ids in the second page
+    kp, vp = _pool(nb, hkv, d, "bf16"), _pool(nb, hkv, d, "bf16")
+    k = random_values(rng, (4, hkv, d), "bf16")
+    # positions: valid, invalid block id, beyond max_blocks_per_seq*16, negative
+    pos = np.array([2, 20, 40, -1], np.int32)
+    seq = np.array([0, 1, 0, 1], np.int32)
+    kv.kv_append(to_dev(k, "bf16"), to_dev(k, "bf16"), kp, vp, to_dev(tables), 2, to_dev(seq),
+                 to_dev(pos), 4, hkv, d, mbps, nb, "bf16")
+    got = to_host(kp)
+    want = np.zeros_like(got)
+    want[3, :, 2] = k[0]
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_pool_handle_scatter_gather_round_trip(kv, dtype):
+    rng = np.random.default_rng(102)
+    layers, nb, hkv, d = 3, 40, 8, 128
+    pool = kv.KVPool(layers, nb, hkv, d, dtype)
+    k0, v0 = pool.layer(0)
+    k2, _ = pool.layer(2)
+    es = {"bf16": 2, "f32": 4}[dtype]
+    assert k2 - k0 == 2 * pool.layer_stride_elems * es
+    table = rng.permutation(nb)[:5].astype(np.int32)
+    snap_k = random_values(rng, (layers, hkv, 70, d), dtype)
+    snap_v = random_values(rng, (layers, hkv, 70, d), dtype)
+    t_dev = to_dev(table)
+    kv.kv_scatter(to_dev(snap_k, dtype), to_dev(snap_v, dtype), k0, v0, pool.layer_stride_elems,
+                  layers, t_dev, 0, 70, hkv, d, nb, dtype)
+    tail = random_values(rng, (layers, hkv, 9, d), dtype)
+    kv.kv_scatter(to_dev(tail, dtype), to_dev(tail, dtype), k0, v0, pool.layer_stride_elems,
+                  layers, t_dev, 70, 9, hkv, d, nb, dtype)
+    tdt = {"bf16": torch.bfloat16, "f32": torch.float32}[dtype]
+    ko = torch.empty((layers, hkv, 79, d), dtype=tdt, device=DEV)
+    vo = torch.empty_like(ko)
+    kv.kv_gather(k0, v0, pool.layer_stride_elems, layers, t_dev, 79, ko, vo, hkv, d, nb, dtype)
+    np.testing.assert_array_equal(to_host(ko), np.concatenate([snap_k, tail], axis=2))
+    np.testing.assert_array_equal(to_host(vo), np.concatenate([snap_v, tail], axis=2))
+    pool.close()
+
+
+@pytest.mark.parametrize("prefix_len", [1024, 1030])
+def test_prefix_fork_copy_on_write_is_bit_exact(kv, prefix_len):
+    """Config-4 semantics at reduced size: a shared prefix held by refcounted
+    blocks, forks with copy-on-write of the trailing partial block, per-fork
+    suffix appends; every fork must read back exactly "copy the prefix snapshot
+    into a fresh buffer, then append" and the prefix must stay untouched."""
+    rng = np.random.default_rng(103)
+    layers, nb, hkv, d, dtype = 2, 256, 8, 128, "bf16"
+    pool = kv.KVPool(layers, nb, hkv, d, dtype)
+    k0, v0 = pool.layer(0)
+    stride = pool.layer_stride_elems
+    bm = kv.BlockManager(nb, 16)
+    bm.allocate("prefix", prefix_len)
+    ptable = np.array(bm.block_table("prefix"), np.int32)
+    pk = random_values(rng, (layers, hkv, prefix_len, d), dtype)
+    pv = random_values(rng, (layers, hkv, prefix_len, d), dtype)
+    kv.kv_scatter(to_dev(pk, dtype), to_dev(pv, dtype), k0, v0, stride, layers, to_dev(ptable),
+                  0, prefix_len, hkv, d, nb, dtype)
+    suffix = [64, 77, 100, 5]
+    expect = {}
+    for i, s in enumerate(suffix):
+        rid = f"seq{i}"
+        pairs = bm.fork("prefix", rid, prefix_len)
+        assert len(pairs) == (1 if prefix_len % 16 else 0)
+        if pairs:
+            src = to_dev(np.array([p[0] for p in pairs], np.int32))
+            dst = to_dev(np.array([p[1] for p in pairs], np.int32))
+            kv.kv_copy_blocks(k0, v0, stride, layers, src, dst, len(pairs), hkv, d, nb, dtype)
+        sk = random_values(rng, (layers, s, hkv, d), dtype)
+        sv = random_values(rng, (layers, s, hkv, d), dtype)
+        while len(bm.block_table(rid)) * 16 < prefix_len + s:
+            bm.allocate_block(rid)
+        table = np.array(bm.block_table(rid), np.int32)
+        t_dev = to_dev(table)
+        pos = to_dev(np.arange(prefix_len, prefix_len + s, dtype=np.int32))
+        seq = to_dev(np.zeros(s, np.int32))
+        for layer in range(layers):
+            kl = k0 + layer * stride * 2
+            vl = v0 + layer * stride * 2
+            kv.kv_append(to_dev(sk[layer], dtype), to_dev(sv[layer], dtype), kl, vl, t_dev, 1,
+                         seq, pos, s, hkv, d, len(table), nb, dtype)
+        expect[rid] = (table, np.concatenate([pk, sk.transpose(0, 2, 1, 3)], axis=2),
+                       np.concatenate([pv, sv.transpose(0, 2, 1, 3)], axis=2))
+    for rid, (table, ek, ev) in expect.items():
+        length = ek.shape[2]
+        ko = torch.empty((layers, hkv, length, d), dtype=torch.bfloat16, device=DEV)
+        vo = torch.empty_like(ko)
+        kv.kv_gather(k0, v0, stride, layers, to_dev(table), length, ko, vo, hkv, d, nb, dtype)
+        np.testing.assert_array_equal(to_host(ko), ek)
+        np.testing.assert_array_equal(to_host(vo), ev)
+    # the cached prefix snapshot is unchanged after reuse
+    ko = torch.empty((layers, hkv, prefix_len, d), dtype=torch.bfloat16, device=DEV)
+    vo = torch.empty_like(ko)
+    kv.kv_gather(k0, v0, stride, layers, to_dev(ptable), prefix_len, ko, vo, hkv, d, nb, dtype)
+    np.testing.assert_array_equal(to_host(ko), pk)
+    np.testing.assert_array_equal(to_host(vo), pv)
+    pool.close()
