@@ -87,7 +87,7 @@ def cpu_baseline(args, lens, hq, hkv, d, layers):
         O.decode_step_f32(q, kn, vn, k, v, lens32, scale, threads)
         n += 1
         el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or n >= 10 * layers:
+        if el >= args.cpu_seconds or n >= 200 * layers:
             break
     steps = n / layers
     return {"value": b * steps / el, "unit": "tokens/s", "cores": threads, "kind": "port",
@@ -146,7 +146,7 @@ def main():
     q_rot = torch.empty((b, hq, d), device=dev, dtype=bf)
     out = torch.empty((b, hq, d), device=dev, dtype=bf)
     ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # zero-filled before first use
     stream = torch.cuda.current_stream()
     scale = 1.0 / math.sqrt(d)
     n_events = layers * args.steps
@@ -197,8 +197,7 @@ def main():
                    "pages_per_layer": need, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
-                     "kernel": "rlse_paged_gqa_decode (decode_split_kernel + "
-                               "decode_merge_kernel)",
+                     "kernel": "decode_split_kernel (rlse_paged_gqa_decode)",
                      "bytes_per_launch": per_launch, "avg_launch_ms": avg_ms},
         "cpu_baseline": None,
     }

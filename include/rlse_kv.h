@@ -130,8 +130,11 @@ int rlse_kv_copy_blocks(void* k_pool, void* v_pool, long long layer_stride_elems
 int rlse_decode_workspace_size(int batch, int num_heads, int num_kv_heads, int head_dim,
                                size_t* bytes);
 
-/* Split-K decode. workspace may be NULL, in which case a library-owned
- * per-device workspace is used (allocated on first need). */
+/* Split-K decode in one launch. workspace may be NULL, in which case a
+ * library-owned per-device workspace is used (allocated and zero-filled on
+ * first need). A caller workspace must be zero-filled once before its first
+ * use; every launch leaves it zero-filled again (per-row arrival counters).
+ * Launches that share a workspace must be ordered (same stream). */
 int rlse_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                           const int32_t* block_tables, const int32_t* seq_lens, void* out,
                           int batch, int num_heads, int num_kv_heads, int head_dim,

@@ -5,24 +5,29 @@
 // h*G .. h*G+G-1 attend to that head's K/V with softmax(q K^T * scale) V --
 // evaluated on the paged pool instead of a contiguous [Hkv, L, d] buffer.
 //
-// Work decomposition. The (sequence, KV head) rows are laid end to end as a
-// single stream of 16-token blocks (row r = b*Hkv + h holds ceil(L_b/16)
-// blocks). Worker w (one wave) takes the contiguous range
-// [w*T/W, (w+1)*T/W) of that stream, so every worker streams the same number
-// of bytes whatever the length mix. A worker walks its range one row segment
-// at a time; all G query heads of the row are kept in registers so each K/V
-// block is read from HBM exactly once (no repeat_kv). A row that lies wholly
-// inside one worker is finished in place; a row cut by a range boundary
-// leaves (m, l, acc) partials in the workspace and a second small kernel
-// merges them with a log-sum-exp combine.
+// Work decomposition. The (sequence, KV head) rows are laid end to end as one
+// stream of 16-token blocks (row r = b*Hkv + h holds ceil(L_b/16) blocks).
+// Workgroup w -- a group of kWaves wavefronts -- takes the contiguous range
+// [w*T/W, (w+1)*T/W) of that stream, so every workgroup streams the same number
+// of bytes whatever the length mix. The group walks its range one row segment
+// at a time; inside a segment its waves take interleaved blocks, each wave
+// keeping all G query heads of the KV head in registers, so every K/V block
+// is read from HBM exactly once (no repeat_kv) and shared by the G heads. The
+// waves' online-softmax states (running max m in log2 units, sum l, acc) are
+// combined through LDS. A row that lies wholly inside one group's range is
+// finished there; a row cut by a range boundary leaves one (m, l, acc)
+// partial per group in the workspace, and the group that finishes the row
+// last (a per-row arrival counter) merges the partials with a log-sum-exp
+// combine in the same launch. The counters return to zero after every
+// launch, so a workspace only needs zero-filling once, before first use.
 //
 // Inside a wave a K/V block is read as 16-byte packets: LPR lanes cover one
 // 16-token row's head_dim, RPL = 64/LPR rows are read per instruction and each
 // lane owns NR = 16/RPL rows of the block. Scores are reduced over the LPR
-// lanes of a row with DPP adds; each lane group keeps its own online-softmax
-// state (running max m in log2 units, sum l, acc over its head_dim slice) and
-// the groups are merged once per segment. Blocks are double-buffered in
-// registers so the next block's loads are in flight during the math.
+// lanes of a row with DPP adds (bf16/f16 dot products with v_dot2); each lane
+// group keeps its own online-softmax state and the groups are merged once per
+// segment. Blocks are double-buffered in registers so the next block's loads
+// are in flight during the math.
 #include <math.h>
 
 #include "common.cuh"
@@ -30,13 +35,13 @@
 
 namespace rlse {
 
-// Smallest number of blocks a worker is given (caps the number of partials
-// when the batch is small).
-constexpr int kMinBlocksPerWorker = 4;
-// Largest batch handled per launch (prefix table lives in LDS).
-constexpr int kMaxDecodeBatch = 16384;
-// Workers launched per compute unit.
-constexpr int kWorkersPerCU = 8;
+constexpr int kWaves = 4;               // wavefronts per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kGroupsPerCU = 2;         // workgroups launched per compute unit
+constexpr int kMinBlocksPerGroup = 8;   // smallest share of blocks per workgroup
+constexpr int kMaxDecodeBatch = 8192;   // prefix table lives in LDS
+constexpr int kMaxDecodeRows = 65536;   // batch * num_kv_heads (arrival counters)
+constexpr int kMergeChunk = 8;          // partials loaded per batch in a merge
 
 template <typename T, int D>
 struct DecodeShape {
@@ -56,11 +61,9 @@ __device__ __forceinline__ int clamp_len(int L, int mbps) {
   return L > cap ? cap : L;
 }
 
-// Exclusive prefix of per-sequence block counts into s_pref[0..B]; returns
-// the blocks of one KV head summed over the batch.
-__device__ int block_prefix(const int* __restrict__ seq_lens, int B, int mbps,
-                            int* s_pref) {
-  const int lane = threadIdx.x;
+// Exclusive prefix of per-sequence block counts into s_pref[0..B] (one wave).
+__device__ void block_prefix(const int* __restrict__ seq_lens, int B, int mbps, int* s_pref) {
+  const int lane = threadIdx.x & 63;
   int carry = 0;
   for (int base = 0; base < B; base += 64) {
     const int b = base + lane;
@@ -76,12 +79,10 @@ __device__ int block_prefix(const int* __restrict__ seq_lens, int B, int mbps,
     carry += __shfl(x, 63, 64);
   }
   if (lane == 0) s_pref[0] = 0;
-  __syncthreads();
-  return carry;
 }
 
-__device__ __forceinline__ long long effective_workers(long long total, int W) {
-  long long we = total / kMinBlocksPerWorker;
+__device__ __forceinline__ long long effective_groups(long long total, int W) {
+  long long we = total / kMinBlocksPerGroup;
   if (we < 1) we = 1;
   return we < W ? we : W;
 }
@@ -107,6 +108,27 @@ __device__ __forceinline__ int locate_seq(const int* s_pref, int B, int Hkv, lon
 // records stay 16-byte aligned.
 __host__ __device__ constexpr int rec_floats(int G, int D) { return G * D + ((2 * G + 3) & ~3); }
 
+// Partial records and arrival counters are accessed with device-scope
+// (agent) atomic loads and stores: on gfx950 these carry the sc1 bit, so each
+// access is coherent across the XCDs' L2 caches by itself. A group's record
+// stores are therefore visible device-wide once they complete, and waiting for
+// them (vmcnt(0)) before the counter increment orders them ahead of it -- no
+// whole-L2 writeback or invalidate is needed (a __threadfence() would emit
+// both, once per partial).
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima), fenced
+// against compiler reordering on both sides.
+__device__ __forceinline__ void wait_vm_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 struct DecodeParams {
   const void* q;
   const void* k_pool;
@@ -114,39 +136,65 @@ struct DecodeParams {
   const int* tables;
   const int* seq_lens;
   void* out;
-  float* ws;
+  float* ws;      // partial records, two slots per workgroup
+  int* counters;  // per-row arrival counters, zero between launches
   int B;
   int Hkv;
   int mbps;
   int num_blocks;
-  int W;
+  int W;    // workgroups launched
   float c;  // scale * log2(e)
 };
 
-template <typename T, int D, int G>
+// Combines (m, l, a) with (mo, lo, ao), all in log2 units; -inf maxima mean
+// "empty" and never produce NaN.
+__device__ __forceinline__ void lse_combine(float& m, float& l, float& a, float mo, float lo,
+                                            float ao) {
+  const float M = fmaxf(m, mo);
+  const float Ms = (M == -INFINITY) ? 0.f : M;
+  const float sa = __builtin_amdgcn_exp2f(m - Ms);
+  const float sb = __builtin_amdgcn_exp2f(mo - Ms);
+  l = l * sa + lo * sb;
+  a = a * sa + ao * sb;
+  m = M;
+}
+
+template <typename T, int D>
 struct Buf {
   uint4 k[DecodeShape<T, D>::NR];
   uint4 v[DecodeShape<T, D>::NR];
-  int nvalid;  // valid rows (0 = block skipped)
+  int nvalid;  // valid rows of the block (0 = block skipped)
 };
 
 template <typename T, int D, int G>
-__global__ __launch_bounds__(64) void decode_split_kernel(DecodeParams p) {
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   using S = DecodeShape<T, D>;
   constexpr int EPL = S::EPL, LPR = S::LPR, RPL = S::RPL, NR = S::NR;
-  extern __shared__ int s_pref[];
+  constexpr int REC = rec_floats(G, D);
+  extern __shared__ int s_pref[];           // [B + 1]
+  __shared__ float s_st[kWaves][G][D + 2];  // per wave: acc[D], m, l for each head
+  __shared__ int s_last;
 
-  const int lane = threadIdx.x;
-  const int col = lane % LPR;
-  const int rsub = lane / LPR;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int col = lane % LPR, rsub = lane / LPR;
   const int B = p.B, Hkv = p.Hkv, mbps = p.mbps;
   const int Hq = Hkv * G;
+  T* __restrict__ ob = reinterpret_cast<T*>(p.out);
 
-  const int per_head = block_prefix(p.seq_lens, B, mbps, s_pref);
-  const long long total = (long long)Hkv * per_head;
-  if (total == 0) return;
-  const long long we = effective_workers(total, p.W);
+  if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref);
+  __syncthreads();
   const long long w = blockIdx.x;
+  if (w == 0) {  // rows of sequences without keys produce zeros
+    for (int b = 0; b < B; ++b) {
+      if (s_pref[b + 1] != s_pref[b]) continue;
+      for (int i = tid; i < Hq * D; i += kThreads)
+        ob[(size_t)b * Hq * D + i] = Elem<T>::from_f32(0.f);
+    }
+  }
+  const long long total = (long long)Hkv * s_pref[B];
+  if (total == 0) return;
+  const long long we = effective_groups(total, p.W);
   if (w >= we) return;
   long long lo = range_lo(w, total, we);
   const long long hi = range_lo(w + 1, total, we);
@@ -169,13 +217,6 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeParams p) {
     const int L = clamp_len(p.seq_lens[b], mbps);
     const int* __restrict__ trow = p.tables + (size_t)b * mbps + blk0;
 
-    // Query packets of the G heads that share this KV head.
-    uint4 qv[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-      qv[g] = *reinterpret_cast<const uint4*>(
-          qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
-
     float m[G], l[G], acc[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -185,222 +226,224 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeParams p) {
       for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
     }
 
-    // Physical ids of the segment's blocks, 64 at a time.
-    int id_base = 0;
-    int ids = lane < cnt ? trow[lane] : 0;
-    auto issue = [&](Buf<T, D, G>& bf, int j) {
-      if (j - id_base >= 64) {
-        id_base += 64;
-        ids = (id_base + lane) < cnt ? trow[id_base + lane] : 0;
-      }
-      const int id = __builtin_amdgcn_readlane(ids, j - id_base);
-      int nv = L - (blk0 + j) * 16;
-      nv = nv > 16 ? 16 : nv;
-      if ((unsigned)id >= (unsigned)p.num_blocks) nv = 0;
-      bf.nvalid = nv;
-      if (nv > 0) {
-        const size_t base = ((size_t)id * Hkv + kvh) * tile + lane_off;
-#pragma unroll
-        for (int i = 0; i < NR; ++i) {
-          bf.k[i] = *reinterpret_cast<const uint4*>(kp + base + (size_t)i * RPL * D);
-          bf.v[i] = *reinterpret_cast<const uint4*>(vp + base + (size_t)i * RPL * D);
-        }
-      }
-    };
-    auto compute = [&](const Buf<T, D, G>& bf) {
-      const int nv = bf.nvalid;
-      if (nv <= 0) return;
-      float s[G][NR];
+    // This wave's blocks of the segment: j = wave, wave + kWaves, ...
+    const int mine = cnt > wave ? (cnt - wave + kWaves - 1) / kWaves : 0;
+    if (mine > 0) {
+      uint4 qv[G];  // query packets of the G heads sharing this KV head
 #pragma unroll
       for (int g = 0; g < G; ++g)
+        qv[g] = *reinterpret_cast<const uint4*>(
+            qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
+      int id_base = 0;
+      int ids = lane < mine ? trow[wave + lane * kWaves] : 0;
+      auto issue = [&](Buf<T, D>& bf, int i) {
+        if (i - id_base >= 64) {
+          id_base += 64;
+          ids = (id_base + lane) < mine ? trow[wave + (id_base + lane) * kWaves] : 0;
+        }
+        const int id = __builtin_amdgcn_readlane(ids, i - id_base);
+        int nv = L - (blk0 + wave + i * kWaves) * 16;
+        nv = nv > 16 ? 16 : nv;
+        if ((unsigned)id >= (unsigned)p.num_blocks) nv = 0;
+        bf.nvalid = nv;
+        if (nv > 0) {
+          const size_t base = ((size_t)id * Hkv + kvh) * tile + lane_off;
 #pragma unroll
-        for (int i = 0; i < NR; ++i)
-          s[g][i] = group_sum<LPR>(Packet<T>::dot(qv[g], bf.k[i], 0.f)) * p.c;
-      float vf[NR][EPL];
-#pragma unroll
-      for (int i = 0; i < NR; ++i) Packet<T>::unpack(bf.v[i], vf[i]);
-      if (nv < 16) {
-#pragma unroll
-        for (int i = 0; i < NR; ++i) {
-          if (i * RPL + rsub >= nv) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) s[g][i] = -INFINITY;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) vf[i][e] = 0.f;
+          for (int r = 0; r < NR; ++r) {
+            bf.k[r] = *reinterpret_cast<const uint4*>(kp + base + (size_t)r * RPL * D);
+            bf.v[r] = *reinterpret_cast<const uint4*>(vp + base + (size_t)r * RPL * D);
           }
         }
-      }
+      };
+      auto compute = [&](const Buf<T, D>& bf) {
+        const int nv = bf.nvalid;
+        if (nv <= 0) return;
+        float s[G][NR];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float mx = m[g];
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int i = 0; i < NR; ++i) mx = fmaxf(mx, s[g][i]);
-        const float ms = (mx == -INFINITY) ? 0.f : mx;
-        const float alpha = __builtin_amdgcn_exp2f(m[g] - ms);
-        float pr[NR];
-        float psum = 0.f;
+          for (int r = 0; r < NR; ++r)
+            s[g][r] = group_sum<LPR>(Packet<T>::dot(qv[g], bf.k[r], 0.f)) * p.c;
+        float vf[NR][EPL];
 #pragma unroll
-        for (int i = 0; i < NR; ++i) {
-          pr[i] = __builtin_amdgcn_exp2f(s[g][i] - ms);
-          psum += pr[i];
+        for (int r = 0; r < NR; ++r) Packet<T>::unpack(bf.v[r], vf[r]);
+        if (nv < 16) {  // tail block: mask rows past the sequence end
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            if (r * RPL + rsub >= nv) {
+#pragma unroll
+              for (int g = 0; g < G; ++g) s[g][r] = -INFINITY;
+#pragma unroll
+              for (int e = 0; e < EPL; ++e) vf[r][e] = 0.f;
+            }
+          }
         }
-        l[g] = fmaf(l[g], alpha, psum);
-        m[g] = mx;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-          float a = acc[g][e] * alpha;
+        for (int g = 0; g < G; ++g) {
+          float mx = m[g];
 #pragma unroll
-          for (int i = 0; i < NR; ++i) a = fmaf(pr[i], vf[i][e], a);
-          acc[g][e] = a;
+          for (int r = 0; r < NR; ++r) mx = fmaxf(mx, s[g][r]);
+          const float ms = (mx == -INFINITY) ? 0.f : mx;
+          const float alpha = __builtin_amdgcn_exp2f(m[g] - ms);
+          float pr[NR];
+          float psum = 0.f;
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            pr[r] = __builtin_amdgcn_exp2f(s[g][r] - ms);
+            psum += pr[r];
+          }
+          l[g] = fmaf(l[g], alpha, psum);
+          m[g] = mx;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) {
+            float a = acc[g][e] * alpha;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) a = fmaf(pr[r], vf[r][e], a);
+            acc[g][e] = a;
+          }
         }
-      }
-    };
+      };
 
-    Buf<T, D, G> bA, bB;
-    issue(bA, 0);
-    for (int j = 0;;) {
-      issue(bB, j + 1 < cnt ? j + 1 : j);
-      compute(bA);
-      if (++j == cnt) break;
-      issue(bA, j + 1 < cnt ? j + 1 : j);
-      compute(bB);
-      if (++j == cnt) break;
+      Buf<T, D> bA, bB;
+      issue(bA, 0);
+      for (int i = 0;;) {
+        issue(bB, i + 1 < mine ? i + 1 : i);
+        compute(bA);
+        if (++i == mine) break;
+        issue(bA, i + 1 < mine ? i + 1 : i);
+        compute(bB);
+        if (++i == mine) break;
+      }
+
+      // Merge the RPL lane groups of the wave (each saw different rows).
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float mo = __shfl_xor(m[g], off, 64);
+          const float lo_ = __shfl_xor(l[g], off, 64);
+          const float M = fmaxf(m[g], mo);
+          const float Ms = (M == -INFINITY) ? 0.f : M;
+          const float sa = __builtin_amdgcn_exp2f(m[g] - Ms);
+          const float sb = __builtin_amdgcn_exp2f(mo - Ms);
+          l[g] = l[g] * sa + lo_ * sb;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) {
+            const float ao = __shfl_xor(acc[g][e], off, 64);
+            acc[g][e] = acc[g][e] * sa + ao * sb;
+          }
+          m[g] = M;
+        }
+      }
     }
-
-    // Merge the RPL lane groups (each saw different rows of every block).
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float mo = __shfl_xor(m[g], off, 64);
-        const float lo_ = __shfl_xor(l[g], off, 64);
-        const float M = fmaxf(m[g], mo);
-        const float Ms = (M == -INFINITY) ? 0.f : M;
-        const float a = __builtin_amdgcn_exp2f(m[g] - Ms);
-        const float bsc = __builtin_amdgcn_exp2f(mo - Ms);
-        l[g] = l[g] * a + lo_ * bsc;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-          const float ao = __shfl_xor(acc[g][e], off, 64);
-          acc[g][e] = acc[g][e] * a + ao * bsc;
-        }
-        m[g] = M;
-      }
-    }
-
-    const bool full_row = (blk0 == 0) && (cnt == nb);
     if (rsub == 0) {
-      if (full_row) {
-        T* ob = reinterpret_cast<T*>(p.out);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;  // all pages skipped -> zeros
-          T* dst = ob + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL;
+      for (int g = 0; g < G; ++g) {
 #pragma unroll
-          for (int e = 0; e < EPL; ++e) dst[e] = Elem<T>::from_f32(acc[g][e] * inv);
-        }
-      } else {
-        const int slot = first_seg ? 0 : 1;
-        float* rec = p.ws + ((size_t)w * 2 + slot) * (size_t)rec_floats(G, D);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float4* dst = reinterpret_cast<float4*>(rec + (size_t)g * D + (size_t)col * EPL);
-#pragma unroll
-          for (int e = 0; e < EPL; e += 4)
-            dst[e / 4] = make_float4(acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]);
-          if (col == 0) {
-            rec[G * D + g] = m[g];
-            rec[G * D + G + g] = l[g];
-          }
+        for (int e = 0; e < EPL; ++e) s_st[wave][g][col * EPL + e] = acc[g][e];
+        if (col == 0) {
+          s_st[wave][g][D] = m[g];
+          s_st[wave][g][D + 1] = l[g];
         }
       }
     }
+    __syncthreads();
+
+    // Combine the waves: one thread per (head, dim) output element.
+    const bool full_row = (blk0 == 0) && (cnt == nb);
+    float* rec = p.ws + ((size_t)w * 2 + (first_seg ? 0 : 1)) * (size_t)REC;
+    for (int idx = tid; idx < G * D; idx += kThreads) {
+      const int g = idx / D, d = idx - g * D;
+      float M = -INFINITY, ls = 0.f, a = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < kWaves; ++wv)
+        lse_combine(M, ls, a, s_st[wv][g][D], s_st[wv][g][D + 1], s_st[wv][g][d]);
+      if (full_row) {
+        const float inv = ls > 0.f ? 1.f / ls : 0.f;  // all pages skipped -> zeros
+        ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(a * inv);
+      } else {
+        st_dev(rec + (size_t)g * D + d, a);
+        if (d == 0) {
+          st_dev(rec + G * D + g, M);
+          st_dev(rec + G * D + G + g, ls);
+        }
+      }
+    }
+
+    if (!full_row) {
+      // Publish the partial and count the arrival; the last of the row's np
+      // groups merges. Records of group w: slot 0 = its first segment, slot 1
+      // = a later one; group wa (holding the row's first block) used slot 0
+      // only if its range starts exactly at the row start.
+      const int row = b * Hkv + kvh;
+      const long long R = (long long)Hkv * s_pref[b] + (long long)kvh * nb;
+      const long long wa = ((R + 1) * we - 1) / total;
+      const long long wb = ((R + nb) * we - 1) / total;
+      const int np = (int)(wb - wa + 1);
+      const bool wa_slot1 = range_lo(wa, total, we) != R;
+      wait_vm_stores();
+      __syncthreads();
+      if (tid == 0)
+        s_last = __hip_atomic_fetch_add(p.counters + row, 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == np - 1;
+      __syncthreads();
+      if (s_last) {
+        for (int idx = tid; idx < G * D; idx += kThreads) {
+          const int g = idx / D, d = idx - g * D;
+          float M = -INFINITY, ls = 0.f, a = 0.f;
+          for (int c = 0; c < np; c += kMergeChunk) {
+            float mv[kMergeChunk], lv[kMergeChunk], av[kMergeChunk];
+#pragma unroll
+            for (int i = 0; i < kMergeChunk; ++i) {  // issue the chunk's loads together
+              const int j = c + i < np ? c + i : np - 1;
+              const int slot = (j == 0 && wa_slot1) ? 1 : 0;
+              const float* r = p.ws + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
+              mv[i] = ld_dev(r + G * D + g);
+              lv[i] = ld_dev(r + G * D + G + g);
+              av[i] = ld_dev(r + (size_t)g * D + d);
+            }
+#pragma unroll
+            for (int i = 0; i < kMergeChunk; ++i)
+              if (c + i < np) lse_combine(M, ls, a, mv[i], lv[i], av[i]);
+          }
+          const float inv = ls > 0.f ? 1.f / ls : 0.f;
+          ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(a * inv);
+        }
+        if (tid == 0)
+          __hip_atomic_store(p.counters + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();  // s_st and s_last are reused by the next segment
     first_seg = false;
     lo += cnt;
-  }
-}
-
-// One wave per (sequence, KV head) row: combine the partials of rows that
-// were cut by worker boundaries, and zero the rows of empty sequences.
-template <typename T, int D, int G>
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeParams p) {
-  extern __shared__ int s_pref[];
-  const int lane = threadIdx.x;
-  const int B = p.B, Hkv = p.Hkv;
-  const int Hq = Hkv * G;
-  const int r = blockIdx.x;
-  const int b = r / Hkv, kvh = r % Hkv;
-  const int per_head = block_prefix(p.seq_lens, B, p.mbps, s_pref);
-  const int nb = s_pref[b + 1] - s_pref[b];
-  T* ob = reinterpret_cast<T*>(p.out) + ((size_t)b * Hq + (size_t)kvh * G) * D;
-  if (nb == 0) {
-    for (int i = lane; i < G * D; i += 64) ob[i] = Elem<T>::from_f32(0.f);
-    return;
-  }
-  const long long total = (long long)Hkv * per_head;
-  const long long we = effective_workers(total, p.W);
-  const long long R = (long long)Hkv * s_pref[b] + (long long)kvh * nb;
-  const long long wa = ((R + 1) * we - 1) / total;
-  const long long wb = ((R + nb) * we - 1) / total;
-  if (wa == wb) return;  // finished in place by the split kernel
-  const long long lo_a = range_lo(wa, total, we);
-  const size_t rec_stride = (size_t)rec_floats(G, D);
-  for (int g = 0; g < G; ++g) {
-    float M = -INFINITY;
-    for (long long w = wa; w <= wb; ++w) {
-      const int slot = (w == wa && lo_a != R) ? 1 : 0;
-      const float* rec = p.ws + ((size_t)w * 2 + slot) * rec_stride;
-      M = fmaxf(M, rec[G * D + g]);
-    }
-    const float Ms = (M == -INFINITY) ? 0.f : M;
-    float lsum = 0.f;
-    float acc[(D + 63) / 64];
-#pragma unroll
-    for (int k = 0; k < (D + 63) / 64; ++k) acc[k] = 0.f;
-    for (long long w = wa; w <= wb; ++w) {
-      const int slot = (w == wa && lo_a != R) ? 1 : 0;
-      const float* rec = p.ws + ((size_t)w * 2 + slot) * rec_stride;
-      const float sc = __builtin_amdgcn_exp2f(rec[G * D + g] - Ms);
-      lsum = fmaf(rec[G * D + G + g], sc, lsum);
-#pragma unroll
-      for (int k = 0; k < (D + 63) / 64; ++k) {
-        const int d = lane + 64 * k;
-        if (d < D) acc[k] = fmaf(rec[(size_t)g * D + d], sc, acc[k]);
-      }
-    }
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-#pragma unroll
-    for (int k = 0; k < (D + 63) / 64; ++k) {
-      const int d = lane + 64 * k;
-      if (d < D) ob[(size_t)g * D + d] = Elem<T>::from_f32(acc[k] * inv);
-    }
   }
 }
 
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
-static int decode_workers(int* W) {
+static int decode_groups(int* W) {
   int cus = 0;
   int st = device_cu_count(&cus);
   if (st) return st;
-  *W = cus * kWorkersPerCU;
+  *W = cus * kGroupsPerCU;
   return RLSE_OK;
 }
 
+// Workspace: a fixed region of kMaxDecodeRows arrival counters, then two
+// partial records per workgroup. The counter region does not depend on the
+// call's shape, so one zero-filled workspace stays valid across calls of any
+// batch.
+static size_t decode_counter_bytes() { return (size_t)kMaxDecodeRows * sizeof(int); }
 static size_t decode_ws_bytes(int W, int G, int D) {
-  return (size_t)W * 2 * (size_t)rec_floats(G, D) * sizeof(float);
+  return decode_counter_bytes() + (size_t)W * 2 * (size_t)rec_floats(G, D) * sizeof(float);
 }
 
 template <typename T, int D, int G>
 static int launch_decode_t(const DecodeParams& p, hipStream_t stream) {
   const size_t lds = (size_t)(p.B + 1) * sizeof(int);
-  hipLaunchKernelGGL((decode_split_kernel<T, D, G>), dim3(p.W), dim3(64), lds, stream, p);
-  int st = launch_status("decode_split_kernel");
-  if (st) return st;
-  hipLaunchKernelGGL((decode_merge_kernel<T, D, G>), dim3(p.B * p.Hkv), dim3(64), lds, stream,
-                     p);
-  return launch_status("decode_merge_kernel");
+  hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3(p.W), dim3(kThreads), lds, stream, p);
+  return launch_status("decode_kernel");
 }
 
 template <typename T, int D>
@@ -441,14 +484,16 @@ static int validate_decode(int batch, int num_heads, int num_kv_heads, int head_
                 num_heads, num_kv_heads);
   const int G = num_heads / num_kv_heads;
   if (G > 8) return fail(RLSE_ERR_INVALID_VALUE, "decode: group size %d > 8", G);
+  if ((long long)batch * num_kv_heads > kMaxDecodeRows)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode: batch * num_kv_heads > %d", kMaxDecodeRows);
   if (head_dim != 64 && head_dim != 128)
     return fail(RLSE_ERR_INVALID_VALUE, "decode: head_dim %d not in {64, 128}", head_dim);
   if (max_blocks_per_seq <= 0 || num_blocks <= 0)
     return fail(RLSE_ERR_INVALID_VALUE, "decode: max_blocks_per_seq %d / num_blocks %d",
                 max_blocks_per_seq, num_blocks);
   if (dtype_size(dtype) == 0) return fail(RLSE_ERR_INVALID_VALUE, "decode: bad dtype %d", dtype);
-  if ((long long)batch * num_heads * head_dim > (1LL << 40))
-    return fail(RLSE_ERR_INVALID_VALUE, "decode: problem too large");
+  if ((long long)max_blocks_per_seq * 16 > 0x7fffffffLL)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode: max_blocks_per_seq too large");
   return RLSE_OK;
 }
 
@@ -463,7 +508,7 @@ extern "C" int rlse_decode_workspace_size(int batch, int num_heads, int num_kv_h
       head_dim <= 0)
     return fail(RLSE_ERR_INVALID_VALUE, "decode_workspace_size: bad shape");
   int W = 0;
-  int st = decode_workers(&W);
+  int st = decode_groups(&W);
   if (st) return st;
   *bytes = decode_ws_bytes(W, num_heads / num_kv_heads, head_dim);
   return RLSE_OK;
@@ -483,7 +528,7 @@ extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const vo
   if (!(scale > 0.f) || !isfinite(scale))
     return fail(RLSE_ERR_INVALID_VALUE, "decode: scale must be finite and positive");
   int W = 0;
-  st = decode_workers(&W);
+  st = decode_groups(&W);
   if (st) return st;
   const int G = num_heads / num_kv_heads;
   const size_t need = decode_ws_bytes(W, G, head_dim);
@@ -498,6 +543,8 @@ extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const vo
       g_ws_size[dev] = 0;
       e = hipMalloc(&g_ws_ptr[dev], need);
       if (e != hipSuccess) return fail((int)e, "decode: workspace hipMalloc failed");
+      e = hipMemset(g_ws_ptr[dev], 0, need);
+      if (e != hipSuccess) return fail((int)e, "decode: workspace hipMemset failed");
       g_ws_size[dev] = need;
     }
     workspace = g_ws_ptr[dev];
@@ -512,7 +559,8 @@ extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const vo
   p.tables = block_tables;
   p.seq_lens = seq_lens;
   p.out = out;
-  p.ws = reinterpret_cast<float*>(workspace);
+  p.counters = reinterpret_cast<int*>(workspace);
+  p.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + decode_counter_bytes());
   p.B = batch;
   p.Hkv = num_kv_heads;
   p.mbps = max_blocks_per_seq;

@@ -188,7 +188,7 @@ def test_workspace_paths_and_prototype_launcher_agree(kv):
     q, kp, vp, tables, lens = make_case(rng, lens, hq, hkv, d, dtype)
     qd, kd, vd = to_dev(q, dtype), to_dev(kp, dtype), to_dev(vp, dtype)
     a = run_decode(kv, qd, kd, vd, tables, lens, hq, hkv, d, dtype, 0.0883)
-    ws = torch.empty(kv.decode_workspace_size(len(lens), hq, hkv, d), dtype=torch.uint8,
+    ws = torch.zeros(kv.decode_workspace_size(len(lens), hq, hkv, d), dtype=torch.uint8,
                      device=DEV)
     b = run_decode(kv, qd, kd, vd, tables, lens, hq, hkv, d, dtype, 0.0883, workspace=ws)
     out = torch.empty_like(qd)
@@ -227,3 +227,30 @@ def test_physical_placement_does_not_change_result(kv):
     b = run_decode(kv, to_dev(q, dtype), to_dev(kp2, dtype), to_dev(vp2, dtype), t2, lens, hq,
                    hkv, d, dtype, 0.0883)
     np.testing.assert_array_equal(a, b)
+
+
+def test_workspace_counters_reset_between_launches(kv):
+    """Rows cut between workers are merged by the last arriving worker through a
+    per-row counter in the workspace; the counters must be back at zero after
+    every launch so one zero-filled workspace serves any sequence of calls."""
+    rng = np.random.default_rng(12)
+    hq, hkv, d, dtype = 16, 8, 128, "bf16"
+    cases = []
+    for lens in ([2049, 1500, 17, 800], [5, 4096, 300], [1] * 20 + [3000]):
+        q, kp, vp, tables, lens = make_case(rng, lens, hq, hkv, d, dtype)
+        cases.append((to_dev(q, dtype), to_dev(kp, dtype), to_dev(vp, dtype), tables, lens,
+                      oracle_decode(q, kp, vp, tables, lens, dtype, 0.0883)))
+    size = max(kv.decode_workspace_size(len(c[4]), hq, hkv, d) for c in cases)
+    ws = torch.zeros(size, dtype=torch.uint8, device=DEV)
+    first = []
+    for rep in range(2):
+        for i, (qd, kd, vd, tables, lens, want) in enumerate(cases):
+            got = run_decode(kv, qd, kd, vd, tables, lens, hq, hkv, d, dtype, 0.0883,
+                             workspace=ws)
+            check(f"case{i} rep{rep}", as_f32(got, dtype), want, dtype)
+            if rep == 0:
+                first.append(got)
+            else:
+                np.testing.assert_array_equal(got, first[i])
+    counters = to_host(ws[: 4 * 65536].view(torch.int32))  # the fixed counter region
+    assert np.all(counters == 0)
