@@ -108,6 +108,11 @@ struct Packet<bf16> {
     c = dot2(a.w, b.w, c);
     return c;
   }
+  // Two floats rounded to nearest-even bf16, lo in the low half.
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
 };
 
 template <>
@@ -125,6 +130,11 @@ struct Packet<f16> {
   static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a),
                                   __builtin_bit_cast(f16x2_t, b), c, false);
+  }
+  // Two floats rounded to nearest-even f16, lo in the low half.
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    const f16x2_t v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
   }
   static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float c) {
     c = dot2(a.x, b.x, c);

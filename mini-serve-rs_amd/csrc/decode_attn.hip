@@ -8,26 +8,28 @@
 // Work decomposition. The (sequence, KV head) rows are laid end to end as one
 // stream of 16-token blocks (row r = b*Hkv + h holds ceil(L_b/16) blocks).
 // Workgroup w -- a group of kWaves wavefronts -- takes the contiguous range
-// [w*T/W, (w+1)*T/W) of that stream, so every workgroup streams the same number
-// of bytes whatever the length mix. The group walks its range one row segment
-// at a time; inside a segment its waves take interleaved blocks, each wave
-// keeping all G query heads of the KV head in registers, so every K/V block
-// is read from HBM exactly once (no repeat_kv) and shared by the G heads. The
-// waves' online-softmax states (running max m in log2 units, sum l, acc) are
-// combined through LDS. A row that lies wholly inside one group's range is
-// finished there; a row cut by a range boundary leaves one (m, l, acc)
-// partial per group in the workspace, and the group that finishes the row
-// last (a per-row arrival counter) merges the partials with a log-sum-exp
-// combine in the same launch. The counters return to zero after every
-// launch, so a workspace only needs zero-filling once, before first use.
+// [w*T/W, (w+1)*T/W) of that stream and each of its waves a contiguous quarter
+// of it, so every wave streams the same number of bytes whatever the length
+// mix. A wave keeps all G query heads of the current KV head in registers, so
+// every K/V block is read from HBM exactly once (no repeat_kv) and shared by
+// the G heads. A row that lies wholly inside a wave's share is finished by the
+// wave; pieces of rows cut between waves are parked in LDS and combined after
+// one barrier at the end; rows cut by the group's range boundary leave one
+// (m, l, acc) partial per group in the workspace, and the group that finishes
+// such a row last (a per-row arrival counter) merges the partials with a
+// log-sum-exp combine in the same launch. The counters return to zero after
+// every launch, so a workspace only needs zero-filling once, before first use.
 //
 // Inside a wave a K/V block is read as 16-byte packets: LPR lanes cover one
 // 16-token row's head_dim, RPL = 64/LPR rows are read per instruction and each
 // lane owns NR = 16/RPL rows of the block. Scores are reduced over the LPR
 // lanes of a row with DPP adds (bf16/f16 dot products with v_dot2); each lane
-// group keeps its own online-softmax state and the groups are merged once per
-// segment. Blocks are double-buffered in registers so the next block's loads
-// are in flight during the math.
+// group keeps its own online-softmax state (running max m in log2 units, sum
+// l, acc) and the groups are merged when the wave's part of a row ends. The
+// page ids of 64 blocks are fetched at once (one per lane), blocks are
+// double-buffered in registers so the next block's loads -- and the query of
+// a new row -- are in flight during the math, and no barrier is taken while
+// streaming.
 #include <math.h>
 
 #include "common.cuh"
@@ -42,6 +44,9 @@ constexpr int kMinBlocksPerGroup = 8;   // smallest share of blocks per workgrou
 constexpr int kMaxDecodeBatch = 8192;   // prefix table lives in LDS
 constexpr int kMaxDecodeRows = 65536;   // batch * num_kv_heads (arrival counters)
 constexpr int kMergeChunk = 8;          // partials loaded per batch in a merge
+// The running max of a softmax moves only when a score exceeds it by more
+// than this many powers of two.
+constexpr float kLazyLog2 = 8.f;
 
 template <typename T, int D>
 struct DecodeShape {
@@ -159,11 +164,14 @@ __device__ __forceinline__ void lse_combine(float& m, float& l, float& a, float 
   m = M;
 }
 
-template <typename T, int D>
+template <typename T, int D, int G>
 struct Buf {
   uint4 k[DecodeShape<T, D>::NR];
   uint4 v[DecodeShape<T, D>::NR];
-  int nvalid;  // valid rows of the block (0 = block skipped)
+  uint4 q[G];   // query packets, loaded with the first block of a row
+  int nvalid;   // valid rows of the block (0 = block skipped)
+  int row;      // b * Hkv + kvh
+  bool newrow;  // first block of its row in this wave's range
 };
 
 template <typename T, int D, int G>
@@ -171,9 +179,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   using S = DecodeShape<T, D>;
   constexpr int EPL = S::EPL, LPR = S::LPR, RPL = S::RPL, NR = S::NR;
   constexpr int REC = rec_floats(G, D);
-  extern __shared__ int s_pref[];           // [B + 1]
-  __shared__ float s_st[kWaves][G][D + 2];  // per wave: acc[D], m, l for each head
-  __shared__ int s_last;
+  constexpr int NPART = 2 * kWaves;
+  constexpr int DPL = (D + 63) / 64;  // output dims per lane in the row epilogue
+  // Register buffers per wave: three when the block and query packets fit
+  // beside two waves per SIMD, else two.
+  constexpr int kNumBufs = (sizeof(T) == 2 && G <= 2) ? 3 : 2;
+  extern __shared__ int s_pref[];             // [B + 1]
+  __shared__ float s_part[NPART][G][D + 2];   // wave partials: acc[D], m, l per head
+  __shared__ int s_part_row[NPART];           // their rows (-1 = unused)
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -183,6 +196,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   T* __restrict__ ob = reinterpret_cast<T*>(p.out);
 
   if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref);
+  if (tid < NPART) s_part_row[tid] = -1;
   __syncthreads();
   const long long w = blockIdx.x;
   if (w == 0) {  // rows of sequences without keys produce zeros
@@ -196,126 +210,93 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   if (total == 0) return;
   const long long we = effective_groups(total, p.W);
   if (w >= we) return;
-  long long lo = range_lo(w, total, we);
-  const long long hi = range_lo(w + 1, total, we);
+  const long long glo = range_lo(w, total, we);
+  const long long ghi = range_lo(w + 1, total, we);
+  // This wave's contiguous share of the group's range.
+  const long long wlo = glo + (ghi - glo) * wave / kWaves;
+  const long long whi = glo + (ghi - glo) * (wave + 1) / kWaves;
+  const int nblk = (int)(whi - wlo);
 
-  const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
-  const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
-  const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
-  const size_t tile = (size_t)16 * D;  // elements of one (block, head) tile
-  const size_t lane_off = (size_t)rsub * D + (size_t)col * EPL;
+  // Row start in the block stream and its block count.
+  auto row_extent = [&](int row, long long& R, int& nb) __attribute__((always_inline)) {
+    const int b = row / Hkv, kvh = row - b * Hkv;
+    nb = s_pref[b + 1] - s_pref[b];
+    R = (long long)Hkv * s_pref[b] + (long long)kvh * nb;
+  };
 
-  bool first_seg = true;
-  while (lo < hi) {
-    const int b = locate_seq(s_pref, B, Hkv, lo);
-    const int nb = s_pref[b + 1] - s_pref[b];
-    const long long o = lo - (long long)Hkv * s_pref[b];
-    const int kvh = (int)(o / nb);
-    const int blk0 = (int)(o % nb);
-    const long long rem_row = nb - blk0;
-    const int cnt = (int)((hi - lo) < rem_row ? (hi - lo) : rem_row);
-    const int L = clamp_len(p.seq_lens[b], mbps);
-    const int* __restrict__ trow = p.tables + (size_t)b * mbps + blk0;
+  if (nblk > 0) {
+    const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
+    const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
+    const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
+    const size_t tile = (size_t)16 * D;  // elements of one (block, head) tile
+    const size_t lane_off = (size_t)rsub * D + (size_t)col * EPL;
 
-    float m[G], l[G], acc[G][EPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m[g] = -INFINITY;
-      l[g] = 0.f;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
-    }
+    // Descriptors of 64 consecutive blocks, one per lane: page id, valid
+    // rows and row, read back with readlane when the block is issued.
+    int d_id = 0, d_nv = 0, d_row = -1, cbase = 0;
+    auto load_chunk = [&](int base) __attribute__((always_inline)) {
+      cbase = base;
+      const long long f = wlo + base + lane;
+      d_id = 0;
+      d_nv = 0;
+      d_row = -1;
+      if (f < whi) {
+        const int b = locate_seq(s_pref, B, Hkv, f);
+        const int nb = s_pref[b + 1] - s_pref[b];
+        const long long o = f - (long long)Hkv * s_pref[b];
+        const int kvh = (int)(o / nb), blk = (int)(o % nb);
+        d_row = b * Hkv + kvh;
+        d_id = p.tables[(size_t)b * mbps + blk];
+        int nv = clamp_len(p.seq_lens[b], mbps) - blk * 16;
+        d_nv = nv > 16 ? 16 : nv;
+        if ((unsigned)d_id >= (unsigned)p.num_blocks) d_nv = 0;
+      }
+    };
+    load_chunk(0);
 
-    // This wave's blocks of the segment: j = wave, wave + kWaves, ...
-    const int mine = cnt > wave ? (cnt - wave + kWaves - 1) / kWaves : 0;
-    if (mine > 0) {
-      uint4 qv[G];  // query packets of the G heads sharing this KV head
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-        qv[g] = *reinterpret_cast<const uint4*>(
-            qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
-      int id_base = 0;
-      int ids = lane < mine ? trow[wave + lane * kWaves] : 0;
-      auto issue = [&](Buf<T, D>& bf, int i) {
-        if (i - id_base >= 64) {
-          id_base += 64;
-          ids = (id_base + lane) < mine ? trow[wave + (id_base + lane) * kWaves] : 0;
-        }
-        const int id = __builtin_amdgcn_readlane(ids, i - id_base);
-        int nv = L - (blk0 + wave + i * kWaves) * 16;
-        nv = nv > 16 ? 16 : nv;
-        if ((unsigned)id >= (unsigned)p.num_blocks) nv = 0;
-        bf.nvalid = nv;
-        if (nv > 0) {
-          const size_t base = ((size_t)id * Hkv + kvh) * tile + lane_off;
-#pragma unroll
-          for (int r = 0; r < NR; ++r) {
-            bf.k[r] = *reinterpret_cast<const uint4*>(kp + base + (size_t)r * RPL * D);
-            bf.v[r] = *reinterpret_cast<const uint4*>(vp + base + (size_t)r * RPL * D);
-          }
-        }
-      };
-      auto compute = [&](const Buf<T, D>& bf) {
-        const int nv = bf.nvalid;
-        if (nv <= 0) return;
-        float s[G][NR];
+    int issued_row = -1;
+    auto issue = [&](Buf<T, D, G>& bf, int j) __attribute__((always_inline)) {
+      if (j - cbase >= 64) load_chunk(cbase + 64);
+      const int k = j - cbase;
+      const int id = __builtin_amdgcn_readlane(d_id, k);
+      const int nv = __builtin_amdgcn_readlane(d_nv, k);
+      const int row = __builtin_amdgcn_readlane(d_row, k);
+      const int b = row / Hkv, kvh = row - b * Hkv;
+      bf.nvalid = nv;
+      bf.row = row;
+      bf.newrow = row != issued_row;
+      if (bf.newrow) {
+        issued_row = row;
 #pragma unroll
         for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int r = 0; r < NR; ++r)
-            s[g][r] = group_sum<LPR>(Packet<T>::dot(qv[g], bf.k[r], 0.f)) * p.c;
-        float vf[NR][EPL];
-#pragma unroll
-        for (int r = 0; r < NR; ++r) Packet<T>::unpack(bf.v[r], vf[r]);
-        if (nv < 16) {  // tail block: mask rows past the sequence end
-#pragma unroll
-          for (int r = 0; r < NR; ++r) {
-            if (r * RPL + rsub >= nv) {
-#pragma unroll
-              for (int g = 0; g < G; ++g) s[g][r] = -INFINITY;
-#pragma unroll
-              for (int e = 0; e < EPL; ++e) vf[r][e] = 0.f;
-            }
-          }
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float mx = m[g];
-#pragma unroll
-          for (int r = 0; r < NR; ++r) mx = fmaxf(mx, s[g][r]);
-          const float ms = (mx == -INFINITY) ? 0.f : mx;
-          const float alpha = __builtin_amdgcn_exp2f(m[g] - ms);
-          float pr[NR];
-          float psum = 0.f;
-#pragma unroll
-          for (int r = 0; r < NR; ++r) {
-            pr[r] = __builtin_amdgcn_exp2f(s[g][r] - ms);
-            psum += pr[r];
-          }
-          l[g] = fmaf(l[g], alpha, psum);
-          m[g] = mx;
-#pragma unroll
-          for (int e = 0; e < EPL; ++e) {
-            float a = acc[g][e] * alpha;
-#pragma unroll
-            for (int r = 0; r < NR; ++r) a = fmaf(pr[r], vf[r][e], a);
-            acc[g][e] = a;
-          }
-        }
-      };
-
-      Buf<T, D> bA, bB;
-      issue(bA, 0);
-      for (int i = 0;;) {
-        issue(bB, i + 1 < mine ? i + 1 : i);
-        compute(bA);
-        if (++i == mine) break;
-        issue(bA, i + 1 < mine ? i + 1 : i);
-        compute(bB);
-        if (++i == mine) break;
+          bf.q[g] = *reinterpret_cast<const uint4*>(
+              qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
       }
+      if (nv > 0) {
+        const size_t base = ((size_t)id * Hkv + kvh) * tile + lane_off;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          bf.k[r] = *reinterpret_cast<const uint4*>(kp + base + (size_t)r * RPL * D);
+          bf.v[r] = *reinterpret_cast<const uint4*>(vp + base + (size_t)r * RPL * D);
+        }
+      }
+    };
 
-      // Merge the RPL lane groups of the wave (each saw different rows).
+    float m[G], l[G], acc[G][EPL];
+    uint4 qv[G];
+    int cur_row = -1;
+    auto reset = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+      }
+    };
+    // Ends the wave's part of cur_row: merge the lane groups, then write the
+    // output (row wholly inside this wave) or park the state in LDS.
+    auto finalize = [&]() __attribute__((always_inline)) {
 #pragma unroll
       for (int off = LPR; off < 64; off <<= 1) {
 #pragma unroll
@@ -335,87 +316,295 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
           m[g] = M;
         }
       }
-    }
-    if (rsub == 0) {
+      long long R;
+      int nb;
+      row_extent(cur_row, R, nb);
+      const int b = cur_row / Hkv, kvh = cur_row - b * Hkv;
+      if (R >= wlo && R + nb <= whi) {
+        if (rsub == 0) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;  // all pages skipped -> zeros
+            T* dst = ob + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) dst[e] = Elem<T>::from_f32(acc[g][e] * inv);
+          }
+        }
+      } else {
+        const int slot = 2 * wave + (R < wlo ? 0 : 1);
+        if (rsub == 0) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) s_part[slot][g][col * EPL + e] = acc[g][e];
+            if (col == 0) {
+              s_part[slot][g][D] = m[g];
+              s_part[slot][g][D + 1] = l[g];
+            }
+          }
+        }
+        if (lane == 0) s_part_row[slot] = cur_row;
+      }
+    };
+    auto compute = [&](const Buf<T, D, G>& bf) __attribute__((always_inline)) {
+      if (bf.newrow) {
+        if (cur_row >= 0) finalize();
+        reset();
+        cur_row = bf.row;
+#pragma unroll
+        for (int g = 0; g < G; ++g) qv[g] = bf.q[g];
+      }
+      const int nv = bf.nvalid;
+      if (nv <= 0) return;
+      // Raw scores q.k, summed over the LPR lanes of each row.
+      float s[G][NR];
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          s[g][r] = group_sum<LPR>(Packet<T>::dot(qv[g], bf.k[r], 0.f));
+      uint4 vr[NR];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) vr[r] = bf.v[r];
+      if (nv < 16) {  // tail block: rows past the sequence end get p = 0 and V = 0
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          if (r * RPL + rsub >= nv) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) s[g][r] = -INFINITY;
+            vr[r] = make_uint4(0, 0, 0, 0);
+          }
+        }
+      }
+      // 16-bit V: pair rows (r, r+1) element-wise so one v_dot2 applies two
+      // probabilities; the pairing is shared by all G heads.
+      constexpr bool kPacked = sizeof(T) == 2;
+      uint32_t vpair[kPacked ? NR / 2 : 1][4][2];
+      float vf[kPacked ? 1 : NR][EPL];
+      if constexpr (kPacked) {
+#pragma unroll
+        for (int r = 0; r < NR; r += 2) {
+          const uint32_t w0[4] = {vr[r].x, vr[r].y, vr[r].z, vr[r].w};
+          const uint32_t w1[4] = {vr[r + 1].x, vr[r + 1].y, vr[r + 1].z, vr[r + 1].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            vpair[r / 2][k][0] = __builtin_amdgcn_perm(w1[k], w0[k], 0x05040100u);  // low halves
+            vpair[r / 2][k][1] = __builtin_amdgcn_perm(w1[k], w0[k], 0x07060302u);  // high halves
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) Packet<T>::unpack(vr[r], vf[r]);
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
+        float mx = s[g][0];
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) s_st[wave][g][col * EPL + e] = acc[g][e];
-        if (col == 0) {
-          s_st[wave][g][D] = m[g];
-          s_st[wave][g][D + 1] = l[g];
+        for (int r = 1; r < NR; ++r) mx = fmaxf(mx, s[g][r]);
+        const float cand = mx * p.c;
+        // Lazy rescaling: the running max moves only when a score exceeds it
+        // by more than kLazyLog2 (probabilities then stay below 2^kLazyLog2).
+        if (__any(cand > m[g] + kLazyLog2)) {
+          const float mn = fmaxf(m[g], cand);
+          const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m[g] - mn);
+          l[g] *= alpha;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
+          m[g] = mn;
         }
-      }
-    }
-    __syncthreads();
-
-    // Combine the waves: one thread per (head, dim) output element.
-    const bool full_row = (blk0 == 0) && (cnt == nb);
-    float* rec = p.ws + ((size_t)w * 2 + (first_seg ? 0 : 1)) * (size_t)REC;
-    for (int idx = tid; idx < G * D; idx += kThreads) {
-      const int g = idx / D, d = idx - g * D;
-      float M = -INFINITY, ls = 0.f, a = 0.f;
+        const float nms = (m[g] == -INFINITY) ? 0.f : -m[g];
+        float pr[NR];
 #pragma unroll
-      for (int wv = 0; wv < kWaves; ++wv)
-        lse_combine(M, ls, a, s_st[wv][g][D], s_st[wv][g][D + 1], s_st[wv][g][d]);
-      if (full_row) {
-        const float inv = ls > 0.f ? 1.f / ls : 0.f;  // all pages skipped -> zeros
-        ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(a * inv);
-      } else {
-        st_dev(rec + (size_t)g * D + d, a);
-        if (d == 0) {
-          st_dev(rec + G * D + g, M);
-          st_dev(rec + G * D + G + g, ls);
+        for (int r = 0; r < NR; ++r) {
+          pr[r] = __builtin_amdgcn_exp2f(fmaf(s[g][r], p.c, nms));
+          l[g] += pr[r];
         }
-      }
-    }
-
-    if (!full_row) {
-      // Publish the partial and count the arrival; the last of the row's np
-      // groups merges. Records of group w: slot 0 = its first segment, slot 1
-      // = a later one; group wa (holding the row's first block) used slot 0
-      // only if its range starts exactly at the row start.
-      const int row = b * Hkv + kvh;
-      const long long R = (long long)Hkv * s_pref[b] + (long long)kvh * nb;
-      const long long wa = ((R + 1) * we - 1) / total;
-      const long long wb = ((R + nb) * we - 1) / total;
-      const int np = (int)(wb - wa + 1);
-      const bool wa_slot1 = range_lo(wa, total, we) != R;
-      wait_vm_stores();
-      __syncthreads();
-      if (tid == 0)
-        s_last = __hip_atomic_fetch_add(p.counters + row, 1, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT) == np - 1;
-      __syncthreads();
-      if (s_last) {
-        for (int idx = tid; idx < G * D; idx += kThreads) {
-          const int g = idx / D, d = idx - g * D;
-          float M = -INFINITY, ls = 0.f, a = 0.f;
-          for (int c = 0; c < np; c += kMergeChunk) {
-            float mv[kMergeChunk], lv[kMergeChunk], av[kMergeChunk];
+        if constexpr (kPacked) {
 #pragma unroll
-            for (int i = 0; i < kMergeChunk; ++i) {  // issue the chunk's loads together
-              const int j = c + i < np ? c + i : np - 1;
-              const int slot = (j == 0 && wa_slot1) ? 1 : 0;
-              const float* r = p.ws + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
-              mv[i] = ld_dev(r + G * D + g);
-              lv[i] = ld_dev(r + G * D + G + g);
-              av[i] = ld_dev(r + (size_t)g * D + d);
+          for (int r = 0; r < NR; r += 2) {
+            const uint32_t pp = Packet<T>::pack2(pr[r], pr[r + 1]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              acc[g][2 * k] = Packet<T>::dot2(vpair[r / 2][k][0], pp, acc[g][2 * k]);
+              acc[g][2 * k + 1] = Packet<T>::dot2(vpair[r / 2][k][1], pp, acc[g][2 * k + 1]);
             }
-#pragma unroll
-            for (int i = 0; i < kMergeChunk; ++i)
-              if (c + i < np) lse_combine(M, ls, a, mv[i], lv[i], av[i]);
           }
-          const float inv = ls > 0.f ? 1.f / ls : 0.f;
-          ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(a * inv);
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) {
+            float a = acc[g][e];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) a = fmaf(pr[r], vf[r][e], a);
+            acc[g][e] = a;
+          }
         }
-        if (tid == 0)
-          __hip_atomic_store(p.counters + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    };
+
+    // kNumBufs blocks in flight: kNumBufs-1 are loading while one is
+    // computed (indices past the end re-load the last block, never computed).
+    const int last = nblk - 1;
+    if constexpr (kNumBufs == 3) {
+      Buf<T, D, G> b0, b1, b2;
+      issue(b0, 0);
+      issue(b1, last < 1 ? last : 1);
+      for (int i = 0;;) {
+        issue(b2, i + 2 < last ? i + 2 : last);
+        compute(b0);
+        if (++i == nblk) break;
+        issue(b0, i + 2 < last ? i + 2 : last);
+        compute(b1);
+        if (++i == nblk) break;
+        issue(b1, i + 2 < last ? i + 2 : last);
+        compute(b2);
+        if (++i == nblk) break;
+      }
+    } else {
+      Buf<T, D, G> b0, b1;
+      issue(b0, 0);
+      for (int i = 0;;) {
+        issue(b1, i + 1 < last ? i + 1 : last);
+        compute(b0);
+        if (++i == nblk) break;
+        issue(b0, i + 1 < last ? i + 1 : last);
+        compute(b1);
+        if (++i == nblk) break;
       }
     }
-    __syncthreads();  // s_st and s_last are reused by the next segment
-    first_seg = false;
-    lo += cnt;
+    finalize();
+  }
+  __syncthreads();
+
+  // Rows this group holds in pieces. The wave holding the group's last piece
+  // of a row finishes it: it combines the pieces parked by earlier waves
+  // (waves own consecutive ranges, so a row's pieces sit in consecutive
+  // waves), then writes the output (row inside the group's range) or
+  // publishes one group partial and merges the row if it arrives last. Waves
+  // handle their rows independently, so the publication chains overlap.
+  for (int s = 0; s < 2; ++s) {
+    const int row = s_part_row[2 * wave + s];
+    if (row < 0) continue;
+    long long R;
+    int nb;
+    row_extent(row, R, nb);
+    if (R + nb > whi && whi < ghi) continue;  // a later wave holds more of the row
+    const int b = row / Hkv, kvh = row - b * Hkv;
+    const bool inside = R >= glo && R + nb <= ghi;
+    float M[G][DPL], Ls[G][DPL], A[G][DPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        M[g][k] = -INFINITY;
+        Ls[g][k] = 0.f;
+        A[g][k] = 0.f;
+      }
+    for (int wv = wave; wv >= 0; --wv) {
+      bool any = false;
+      for (int s2 = 1; s2 >= 0; --s2) {
+        const int slot = 2 * wv + s2;
+        if ((wv == wave && s2 != s) || s_part_row[slot] != row) continue;
+        any = true;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) {
+            const int d = lane + 64 * k;
+            if (d < D)
+              lse_combine(M[g][k], Ls[g][k], A[g][k], s_part[slot][g][D], s_part[slot][g][D + 1],
+                          s_part[slot][g][d]);
+          }
+      }
+      if (!any) break;
+    }
+    if (inside) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) {
+          const int d = lane + 64 * k;
+          if (d < D) {
+            const float inv = Ls[g][k] > 0.f ? 1.f / Ls[g][k] : 0.f;
+            ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(A[g][k] * inv);
+          }
+        }
+      continue;
+    }
+    // Group partial: slot 0 = the group's first segment, 1 = a later one.
+    float* rec = p.ws + ((size_t)w * 2 + (R <= glo ? 0 : 1)) * (size_t)REC;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        const int d = lane + 64 * k;
+        if (d < D) st_dev(rec + (size_t)g * D + d, A[g][k]);
+      }
+      if (lane == 0) {
+        st_dev(rec + G * D + g, M[g][0]);
+        st_dev(rec + G * D + G + g, Ls[g][0]);
+      }
+    }
+    // Count the arrival; the last of the row's np groups merges. Group wa
+    // (holding the row's first block) used slot 0 only if its range starts
+    // exactly at the row start.
+    const long long wa = ((R + 1) * we - 1) / total;
+    const long long wb = ((R + nb) * we - 1) / total;
+    const int np = (int)(wb - wa + 1);
+    const bool wa_slot1 = range_lo(wa, total, we) != R;
+    wait_vm_stores();
+    int prev = 0;
+    if (lane == 0)
+      prev = __hip_atomic_fetch_add(p.counters + row, 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0, 64);
+    if (prev != np - 1) continue;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        M[g][k] = -INFINITY;
+        Ls[g][k] = 0.f;
+        A[g][k] = 0.f;
+      }
+    for (int c = 0; c < np; c += kMergeChunk) {
+      float mv[kMergeChunk][G], lv[kMergeChunk][G], av[kMergeChunk][G][DPL];
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i) {  // issue the chunk's loads together
+        const int j = c + i < np ? c + i : np - 1;
+        const int slot = (j == 0 && wa_slot1) ? 1 : 0;
+        const float* r = p.ws + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          mv[i][g] = ld_dev(r + G * D + g);
+          lv[i][g] = ld_dev(r + G * D + G + g);
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) {
+            const int d = lane + 64 * k;
+            av[i][g][k] = d < D ? ld_dev(r + (size_t)g * D + d) : 0.f;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i)
+        if (c + i < np)
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int k = 0; k < DPL; ++k)
+              lse_combine(M[g][k], Ls[g][k], A[g][k], mv[i][g], lv[i][g], av[i][g][k]);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        const int d = lane + 64 * k;
+        if (d < D) {
+          const float inv = Ls[g][k] > 0.f ? 1.f / Ls[g][k] : 0.f;
+          ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(A[g][k] * inv);
+        }
+      }
+    if (lane == 0)
+      __hip_atomic_store(p.counters + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
