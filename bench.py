@@ -5,9 +5,11 @@ Default workload: Qwen3-0.6B-shaped batched decode in bf16 -- 16 query heads,
 uniformly from [128, 2048] plus the token appended this step, K/V in 16-token
 pages placed by a seeded random permutation (one table shared by all layers,
 as one block id spans all layers), a distinct pool per layer. One step runs,
-for every layer, the fused q/k RMSNorm + RoPE + append of the new token and
-the split-K GQA decode over the paged pool. Inputs are synthetic N(0, 1)
-values resident in HBM before timing starts.
+for every layer, one rlse_decode_step launch: q/k RMSNorm + RoPE of the new
+token, its K/V append into the pool, and the split-K GQA decode over the
+paged pool (--unfused runs rlse_qk_norm_rope_append + rlse_paged_gqa_decode
+instead). Inputs are synthetic N(0, 1) values resident in HBM before timing
+starts.
 
 Printed: one JSON line with tokens/s (decode tokens of all sequences per
 second), the decode kernel's achieved HBM bandwidth against the 8 TB/s peak
@@ -49,16 +51,20 @@ def parse():
                     help="wall-clock budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--unfused", action="store_true",
+                    help="norm/RoPE/append and decode as two launches per layer")
     return ap.parse_args()
 
 
-def algorithmic_decode_bytes(lens, hq, hkv, d, es):
+def algorithmic_decode_bytes(lens, hq, hkv, d, es, fused):
     """HBM bytes one decode launch must move: every attended K and V row once,
-    q in and out once, the used block-table entries and the lengths."""
+    q in and out once, the used block-table entries and the lengths; the fused
+    step also writes the appended K/V row of every sequence."""
     kv = sum(int(n) * 2 * hkv * d * es for n in lens)
     qo = 2 * len(lens) * hq * d * es
     tab = sum(((int(n) + 15) // 16) * 4 for n in lens)
-    return kv + qo + tab + 4 * len(lens)
+    app = len(lens) * 2 * hkv * d * es if fused else 0
+    return kv + qo + tab + 4 * len(lens) + app
 
 
 def cpu_baseline(args, lens, hq, hkv, d, layers):
@@ -136,7 +142,7 @@ def main():
     v_in = [torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
     qw = [(1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf) for _ in range(layers)]
     kw = [(1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf) for _ in range(layers)]
-    max_pos = int(lens.max()) + 1
+    max_pos = mbps * 16  # every position the block tables can hold
     cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, "bf16")
     cos_t = torch.frombuffer(bytearray(cos_b), dtype=torch.int16).to(dev).view(bf)
     sin_t = torch.frombuffer(bytearray(sin_b), dtype=torch.int16).to(dev).view(bf)
@@ -155,14 +161,21 @@ def main():
 
     def step(timed_index=None):
         for layer in range(layers):
-            kv.qk_norm_rope_append(q_in[layer], k_in[layer], v_in[layer], qw[layer], kw[layer],
-                                   1e-6, cos_t, sin_t, max_pos, pos_dev, t_dev, b, None, b, hq,
-                                   hkv, d, mbps, nb, q_rot, k_pools[layer], v_pools[layer],
-                                   "bf16", stream)
+            if args.unfused:
+                kv.qk_norm_rope_append(q_in[layer], k_in[layer], v_in[layer], qw[layer],
+                                       kw[layer], 1e-6, cos_t, sin_t, max_pos, pos_dev, t_dev, b,
+                                       None, b, hq, hkv, d, mbps, nb, q_rot, k_pools[layer],
+                                       v_pools[layer], "bf16", stream)
             if timed_index is not None:
                 ev_a[timed_index * layers + layer].record(stream)
-            kv.paged_gqa_decode(q_rot, k_pools[layer], v_pools[layer], t_dev, lens_dev, out, b,
-                                hq, hkv, d, mbps, nb, scale, "bf16", ws, ws_bytes, stream)
+            if args.unfused:
+                kv.paged_gqa_decode(q_rot, k_pools[layer], v_pools[layer], t_dev, lens_dev, out,
+                                    b, hq, hkv, d, mbps, nb, scale, "bf16", ws, ws_bytes, stream)
+            else:
+                kv.decode_step(q_in[layer], k_in[layer], v_in[layer], qw[layer], kw[layer], 1e-6,
+                               cos_t, sin_t, max_pos, k_pools[layer], v_pools[layer], t_dev,
+                               lens_dev, out, b, hq, hkv, d, mbps, nb, scale, "bf16", ws,
+                               ws_bytes, stream)
             if timed_index is not None:
                 ev_b[timed_index * layers + layer].record(stream)
 
@@ -176,7 +189,7 @@ def main():
     elapsed = time.perf_counter() - t0
     kernel_ms = [a.elapsed_time(e) for a, e in zip(ev_a, ev_b)]
     avg_ms = float(np.mean(kernel_ms))
-    per_launch = algorithmic_decode_bytes(lens, hq, hkv, d, 2)
+    per_launch = algorithmic_decode_bytes(lens, hq, hkv, d, 2, not args.unfused)
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
     ms_per_step = elapsed * 1e3 / args.steps
     result = {
@@ -197,7 +210,8 @@ def main():
                    "pages_per_layer": need, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
-                     "kernel": "decode_split_kernel (rlse_paged_gqa_decode)",
+                     "kernel": ("decode_kernel (rlse_paged_gqa_decode)" if args.unfused else
+                                "decode_kernel fused step (rlse_decode_step)"),
                      "bytes_per_launch": per_launch, "avg_launch_ms": avg_ms},
         "cpu_baseline": None,
     }

@@ -141,6 +141,25 @@ int rlse_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                           int max_blocks_per_seq, int num_blocks, float scale, int dtype,
                           void* workspace, size_t workspace_bytes, rlse_stream_t stream);
 
+/* Fused decode step of one layer: the front half of Attention::forward
+ * and its decode branch (src/backends/qwen2.rs:291-328) in one launch.
+ * For every sequence b the new token sits at position p = seq_lens[b]-1:
+ * q [batch][num_heads][head_dim] and k_new/v_new [batch][num_kv_heads]
+ * [head_dim] are the raw projections; q and k get q_norm/k_norm RMSNorm
+ * (skipped when the weight is NULL, as for Qwen2) and NeoX RoPE at p; the
+ * rotated k and raw v are appended to the pool at p; out receives the
+ * attention over the seq_lens[b] keys, as rlse_paged_gqa_decode would give
+ * after rlse_qk_norm_rope_append. cos/sin tables are [max_pos][head_dim/2]
+ * with max_pos >= max_blocks_per_seq*16. Workspace rules as for
+ * rlse_paged_gqa_decode. */
+int rlse_decode_step(const void* q, const void* k_new, const void* v_new,
+                     const void* q_norm_weight, const void* k_norm_weight, float eps,
+                     const void* cos_table, const void* sin_table, int max_pos, void* k_pool,
+                     void* v_pool, const int32_t* block_tables, const int32_t* seq_lens,
+                     void* out, int batch, int num_heads, int num_kv_heads, int head_dim,
+                     int max_blocks_per_seq, int num_blocks, float scale, int dtype,
+                     void* workspace, size_t workspace_bytes, rlse_stream_t stream);
+
 /* ------------------------------------------------------------------ */
 /* Normalisation and rotary embedding.                                 */
 /* ------------------------------------------------------------------ */

@@ -149,6 +149,17 @@ struct DecodeParams {
   int num_blocks;
   int W;    // workgroups launched
   float c;  // scale * log2(e)
+  // Fused decode step only (rlse_decode_step): raw new-token k/v
+  // [B][Hkv][D], q/k RMSNorm weights [D] (null: no norm), RoPE tables
+  // [max_pos][D/2]. The new token of sequence b sits at seq_lens[b] - 1.
+  const void* k_new;
+  const void* v_new;
+  const void* qw;
+  const void* kw;
+  const void* cos_t;
+  const void* sin_t;
+  float eps;
+  float inv_d;
 };
 
 // Combines (m, l, a) with (mo, lo, ao), all in log2 units; -inf maxima mean
@@ -169,12 +180,73 @@ struct Buf {
   uint4 k[DecodeShape<T, D>::NR];
   uint4 v[DecodeShape<T, D>::NR];
   uint4 q[G];   // query packets, loaded with the first block of a row
+  uint4 cs, sn; // fused step: RoPE cos/sin packets of the row's new token
+  uint4 kn, vn; // fused step: raw new-token k/v packets (last block of a row)
   int nvalid;   // valid rows of the block (0 = block skipped)
   int row;      // b * Hkv + kvh
+  int id;       // physical block
   bool newrow;  // first block of its row in this wave's range
+  bool last;    // last block of its row (holds the new token)
 };
 
-template <typename T, int D, int G>
+// Packs EPL floats of a row slice into a 16-byte packet of T.
+template <typename T>
+__device__ __forceinline__ uint4 pack_packet(const float* y) {
+  if constexpr (sizeof(T) == 4) {
+    return make_uint4(__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]),
+                      __float_as_uint(y[3]));
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const T a = Elem<T>::from_f32(y[2 * i]), b = Elem<T>::from_f32(y[2 * i + 1]);
+      uint16_t ua, ub;
+      __builtin_memcpy(&ua, &a, 2);
+      __builtin_memcpy(&ub, &b, 2);
+      w[i] = (uint32_t)ua | ((uint32_t)ub << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// RMSNorm (optional) then NeoX RoPE of one row held as packets: lane col of
+// an LPR-lane group holds elements [col*EPL, col*EPL + EPL); rotate_half
+// pairs element i with i + D/2, held by lane col ^ LPR/2. Rounding follows
+// Candle's op sequence (RmsNorm::forward, apply_rope; src/backends/qwen2.rs:
+// 68-75, 133-142): x/norm and *w rounded to T, x*cos and rot*sin rounded,
+// then the sum rounded; no fused multiply-adds.
+template <typename T, int D>
+__device__ __forceinline__ uint4 norm_rope_packet(uint4 x, bool norm, uint4 w, float inv_d,
+                                                  float eps, uint4 cs, uint4 sn, int col) {
+  using S = DecodeShape<T, D>;
+  constexpr int EPL = S::EPL, LPR = S::LPR;
+  float xf[EPL], wf[EPL], cf[EPL], sf[EPL];
+  Packet<T>::unpack(x, xf);
+  if (norm) {
+    Packet<T>::unpack(w, wf);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) ss = __fadd_rn(ss, __fmul_rn(xf[e], xf[e]));
+    ss = group_sum<LPR>(ss);
+    const float nrm = sqrtf(__fadd_rn(__fmul_rn(ss, inv_d), eps));
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) xf[e] = round_to<T>(__fmul_rn(round_to<T>(xf[e] / nrm), wf[e]));
+  }
+  Packet<T>::unpack(cs, cf);
+  Packet<T>::unpack(sn, sf);
+  const bool upper = col >= LPR / 2;
+  float y[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float pf = __shfl_xor(xf[e], LPR / 2, 64);
+    const float a = round_to<T>(__fmul_rn(xf[e], cf[e]));
+    const float bb = round_to<T>(__fmul_rn(upper ? pf : -pf, sf[e]));
+    y[e] = __fadd_rn(a, bb);
+  }
+  return pack_packet<T>(y);
+}
+
+template <typename T, int D, int G, bool FUSED>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   using S = DecodeShape<T, D>;
   constexpr int EPL = S::EPL, LPR = S::LPR, RPL = S::RPL, NR = S::NR;
@@ -183,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   constexpr int DPL = (D + 63) / 64;  // output dims per lane in the row epilogue
   // Register buffers per wave: three when the block and query packets fit
   // beside two waves per SIMD, else two.
-  constexpr int kNumBufs = (sizeof(T) == 2 && G <= 2) ? 3 : 2;
+  constexpr int kNumBufs = (sizeof(T) == 2 && G <= 2 && !FUSED) ? 3 : 2;
   extern __shared__ int s_pref[];             // [B + 1]
   __shared__ float s_part[NPART][G][D + 2];   // wave partials: acc[D], m, l per head
   __shared__ int s_part_row[NPART];           // their rows (-1 = unused)
@@ -233,13 +305,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
 
     // Descriptors of 64 consecutive blocks, one per lane: page id, valid
     // rows and row, read back with readlane when the block is issued.
-    int d_id = 0, d_nv = 0, d_row = -1, cbase = 0;
+    // d_nv holds the valid rows in bits 0-7 and "last block of its row" in
+    // bit 8; d_pos is the row's new-token position (fused step).
+    int d_id = 0, d_nv = 0, d_row = -1, d_pos = 0, cbase = 0;
     auto load_chunk = [&](int base) __attribute__((always_inline)) {
       cbase = base;
       const long long f = wlo + base + lane;
       d_id = 0;
       d_nv = 0;
       d_row = -1;
+      d_pos = 0;
       if (f < whi) {
         const int b = locate_seq(s_pref, B, Hkv, f);
         const int nb = s_pref[b + 1] - s_pref[b];
@@ -247,9 +322,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
         const int kvh = (int)(o / nb), blk = (int)(o % nb);
         d_row = b * Hkv + kvh;
         d_id = p.tables[(size_t)b * mbps + blk];
-        int nv = clamp_len(p.seq_lens[b], mbps) - blk * 16;
+        const int L = clamp_len(p.seq_lens[b], mbps);
+        const int nv = L - blk * 16;
         d_nv = nv > 16 ? 16 : nv;
-        if ((unsigned)d_id >= (unsigned)p.num_blocks) d_nv = 0;
+        d_pos = L - 1;
+        if ((unsigned)d_id >= (unsigned)p.num_blocks)
+          d_nv = 0;
+        else if (blk == nb - 1)
+          d_nv |= 256;
       }
     };
     load_chunk(0);
@@ -259,18 +339,34 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       if (j - cbase >= 64) load_chunk(cbase + 64);
       const int k = j - cbase;
       const int id = __builtin_amdgcn_readlane(d_id, k);
-      const int nv = __builtin_amdgcn_readlane(d_nv, k);
+      const int nvf = __builtin_amdgcn_readlane(d_nv, k);
       const int row = __builtin_amdgcn_readlane(d_row, k);
       const int b = row / Hkv, kvh = row - b * Hkv;
+      const int nv = nvf & 255;
       bf.nvalid = nv;
       bf.row = row;
+      bf.id = id;
       bf.newrow = row != issued_row;
+      bf.last = (nvf >> 8) != 0;
       if (bf.newrow) {
         issued_row = row;
 #pragma unroll
         for (int g = 0; g < G; ++g)
           bf.q[g] = *reinterpret_cast<const uint4*>(
               qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
+        if constexpr (FUSED) {
+          const int pos = __builtin_amdgcn_readlane(d_pos, k);
+          const size_t to = (size_t)pos * (D / 2) + (size_t)(col % (LPR / 2)) * EPL;
+          bf.cs = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.cos_t) + to);
+          bf.sn = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.sin_t) + to);
+        }
+      }
+      if constexpr (FUSED) {
+        if (bf.last) {
+          const size_t no = ((size_t)b * Hkv + kvh) * D + (size_t)col * EPL;
+          bf.kn = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.k_new) + no);
+          bf.vn = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.v_new) + no);
+        }
       }
       if (nv > 0) {
         const size_t base = ((size_t)id * Hkv + kvh) * tile + lane_off;
@@ -284,6 +380,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
 
     float m[G], l[G], acc[G][EPL];
     uint4 qv[G];
+    uint4 cs_cur = make_uint4(0, 0, 0, 0), sn_cur = make_uint4(0, 0, 0, 0);
+    uint4 qw_pk = make_uint4(0, 0, 0, 0), kw_pk = make_uint4(0, 0, 0, 0);
+    if constexpr (FUSED) {
+      if (p.qw) qw_pk = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.qw) + col * EPL);
+      if (p.kw) kw_pk = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.kw) + col * EPL);
+    }
     int cur_row = -1;
     auto reset = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -351,21 +453,55 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
         if (cur_row >= 0) finalize();
         reset();
         cur_row = bf.row;
+        if constexpr (FUSED) {  // q_norm + RoPE of the row's query heads
+          cs_cur = bf.cs;
+          sn_cur = bf.sn;
 #pragma unroll
-        for (int g = 0; g < G; ++g) qv[g] = bf.q[g];
+          for (int g = 0; g < G; ++g)
+            qv[g] = norm_rope_packet<T, D>(bf.q[g], p.qw != nullptr, qw_pk, p.inv_d, p.eps,
+                                           cs_cur, sn_cur, col);
+        } else {
+#pragma unroll
+          for (int g = 0; g < G; ++g) qv[g] = bf.q[g];
+        }
       }
       const int nv = bf.nvalid;
       if (nv <= 0) return;
+      uint4 kr[NR], vr[NR];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        kr[r] = bf.k[r];
+        vr[r] = bf.v[r];
+      }
+      if constexpr (FUSED) {
+        if (bf.last) {
+          // The new token is the row's last key (slot nv-1 of this block):
+          // k_norm + RoPE it, append k and raw v to the pool, and use them in
+          // place of whatever the slot held.
+          const uint4 kn = norm_rope_packet<T, D>(bf.kn, p.kw != nullptr, kw_pk, p.inv_d,
+                                                  p.eps, cs_cur, sn_cur, col);
+          const int slot = nv - 1;
+          const int kvh = bf.row % Hkv;
+          if (rsub == slot % RPL) {
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+              if (r == slot / RPL) {
+                kr[r] = kn;
+                vr[r] = bf.vn;
+              }
+            const size_t dst = (((size_t)bf.id * Hkv + kvh) * 16 + slot) * D + (size_t)col * EPL;
+            *reinterpret_cast<uint4*>(const_cast<T*>(kp) + dst) = kn;
+            *reinterpret_cast<uint4*>(const_cast<T*>(vp) + dst) = bf.vn;
+          }
+        }
+      }
       // Raw scores q.k, summed over the LPR lanes of each row.
       float s[G][NR];
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int r = 0; r < NR; ++r)
-          s[g][r] = group_sum<LPR>(Packet<T>::dot(qv[g], bf.k[r], 0.f));
-      uint4 vr[NR];
-#pragma unroll
-      for (int r = 0; r < NR; ++r) vr[r] = bf.v[r];
+          s[g][r] = group_sum<LPR>(Packet<T>::dot(qv[g], kr[r], 0.f));
       if (nv < 16) {  // tail block: rows past the sequence end get p = 0 and V = 0
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
@@ -628,35 +764,46 @@ static size_t decode_ws_bytes(int W, int G, int D) {
   return decode_counter_bytes() + (size_t)W * 2 * (size_t)rec_floats(G, D) * sizeof(float);
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, bool FUSED>
 static int launch_decode_t(const DecodeParams& p, hipStream_t stream) {
   const size_t lds = (size_t)(p.B + 1) * sizeof(int);
-  hipLaunchKernelGGL((decode_kernel<T, D, G>), dim3(p.W), dim3(kThreads), lds, stream, p);
+  hipLaunchKernelGGL((decode_kernel<T, D, G, FUSED>), dim3(p.W), dim3(kThreads), lds, stream,
+                     p);
   return launch_status("decode_kernel");
 }
 
-template <typename T, int D>
+template <typename T, int D, bool FUSED>
 static int launch_decode_g(int G, const DecodeParams& p, hipStream_t s) {
   switch (G) {
-    case 1: return launch_decode_t<T, D, 1>(p, s);
-    case 2: return launch_decode_t<T, D, 2>(p, s);
-    case 3: return launch_decode_t<T, D, 3>(p, s);
-    case 4: return launch_decode_t<T, D, 4>(p, s);
-    case 5: return launch_decode_t<T, D, 5>(p, s);
-    case 6: return launch_decode_t<T, D, 6>(p, s);
-    case 7: return launch_decode_t<T, D, 7>(p, s);
-    case 8: return launch_decode_t<T, D, 8>(p, s);
+    case 1: return launch_decode_t<T, D, 1, FUSED>(p, s);
+    case 2: return launch_decode_t<T, D, 2, FUSED>(p, s);
+    case 3: return launch_decode_t<T, D, 3, FUSED>(p, s);
+    case 4: return launch_decode_t<T, D, 4, FUSED>(p, s);
+    case 5: return launch_decode_t<T, D, 5, FUSED>(p, s);
+    case 6: return launch_decode_t<T, D, 6, FUSED>(p, s);
+    case 7: return launch_decode_t<T, D, 7, FUSED>(p, s);
+    case 8: return launch_decode_t<T, D, 8, FUSED>(p, s);
   }
   return fail(RLSE_ERR_INVALID_VALUE, "decode: unsupported group size %d", G);
 }
 
-template <typename T>
+template <typename T, bool FUSED>
 static int launch_decode_d(int D, int G, const DecodeParams& p, hipStream_t s) {
   switch (D) {
-    case 64: return launch_decode_g<T, 64>(G, p, s);
-    case 128: return launch_decode_g<T, 128>(G, p, s);
+    case 64: return launch_decode_g<T, 64, FUSED>(G, p, s);
+    case 128: return launch_decode_g<T, 128, FUSED>(G, p, s);
   }
   return fail(RLSE_ERR_INVALID_VALUE, "decode: unsupported head_dim %d", D);
+}
+
+template <bool FUSED>
+static int launch_decode_dtype(int dtype, int D, int G, const DecodeParams& p, hipStream_t s) {
+  switch (dtype) {
+    case RLSE_DTYPE_F32: return launch_decode_d<float, FUSED>(D, G, p, s);
+    case RLSE_DTYPE_BF16: return launch_decode_d<bf16, FUSED>(D, G, p, s);
+    case RLSE_DTYPE_F16: return launch_decode_d<f16, FUSED>(D, G, p, s);
+  }
+  return fail(RLSE_ERR_INVALID_VALUE, "decode: bad dtype %d", dtype);
 }
 
 // Library-owned workspace per device, for callers that pass none.
@@ -703,12 +850,12 @@ extern "C" int rlse_decode_workspace_size(int batch, int num_heads, int num_kv_h
   return RLSE_OK;
 }
 
-extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
-                                     const int32_t* block_tables, const int32_t* seq_lens,
-                                     void* out, int batch, int num_heads, int num_kv_heads,
-                                     int head_dim, int max_blocks_per_seq, int num_blocks,
-                                     float scale, int dtype, void* workspace,
-                                     size_t workspace_bytes, rlse_stream_t stream) {
+// Validates the shared decode arguments and fills p (workspace included).
+static int prepare_decode(DecodeParams& p, const void* q, const void* k_pool,
+                          const void* v_pool, const int32_t* block_tables,
+                          const int32_t* seq_lens, void* out, int batch, int num_heads,
+                          int num_kv_heads, int head_dim, int max_blocks_per_seq, int num_blocks,
+                          float scale, int dtype, void* workspace, size_t workspace_bytes) {
   int st = validate_decode(batch, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
                            num_blocks, dtype);
   if (st) return st;
@@ -741,7 +888,7 @@ extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const vo
     return fail(RLSE_ERR_BUFFER_TOO_SMALL, "decode: workspace %zu bytes < %zu needed",
                 workspace_bytes, need);
   }
-  DecodeParams p;
+  p = DecodeParams{};
   p.q = q;
   p.k_pool = k_pool;
   p.v_pool = v_pool;
@@ -756,13 +903,55 @@ extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const vo
   p.num_blocks = num_blocks;
   p.W = W;
   p.c = scale * 1.4426950408889634f;
-  hipStream_t s = as_stream(stream);
-  switch (dtype) {
-    case RLSE_DTYPE_F32: return launch_decode_d<float>(head_dim, G, p, s);
-    case RLSE_DTYPE_BF16: return launch_decode_d<bf16>(head_dim, G, p, s);
-    case RLSE_DTYPE_F16: return launch_decode_d<f16>(head_dim, G, p, s);
-  }
-  return fail(RLSE_ERR_INVALID_VALUE, "decode: bad dtype %d", dtype);
+  return RLSE_OK;
+}
+
+extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
+                                     const int32_t* block_tables, const int32_t* seq_lens,
+                                     void* out, int batch, int num_heads, int num_kv_heads,
+                                     int head_dim, int max_blocks_per_seq, int num_blocks,
+                                     float scale, int dtype, void* workspace,
+                                     size_t workspace_bytes, rlse_stream_t stream) {
+  DecodeParams p;
+  const int st = prepare_decode(p, q, k_pool, v_pool, block_tables, seq_lens, out, batch,
+                                num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                                num_blocks, scale, dtype, workspace, workspace_bytes);
+  if (st) return st;
+  return launch_decode_dtype<false>(dtype, head_dim, num_heads / num_kv_heads, p,
+                                    as_stream(stream));
+}
+
+extern "C" int rlse_decode_step(const void* q, const void* k_new, const void* v_new,
+                                const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                const void* cos_table, const void* sin_table, int max_pos,
+                                void* k_pool, void* v_pool, const int32_t* block_tables,
+                                const int32_t* seq_lens, void* out, int batch, int num_heads,
+                                int num_kv_heads, int head_dim, int max_blocks_per_seq,
+                                int num_blocks, float scale, int dtype, void* workspace,
+                                size_t workspace_bytes, rlse_stream_t stream) {
+  DecodeParams p;
+  const int st = prepare_decode(p, q, k_pool, v_pool, block_tables, seq_lens, out, batch,
+                                num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                                num_blocks, scale, dtype, workspace, workspace_bytes);
+  if (st) return st;
+  if (!k_new || !v_new || !cos_table || !sin_table)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_step: null pointer argument");
+  if (!(eps >= 0.f)) return fail(RLSE_ERR_INVALID_VALUE, "decode_step: eps must be >= 0");
+  if ((long long)max_pos < (long long)max_blocks_per_seq * 16)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "decode_step: max_pos %d < max_blocks_per_seq * 16 (%lld): every position the "
+                "block table can hold needs a RoPE table row",
+                max_pos, (long long)max_blocks_per_seq * 16);
+  p.k_new = k_new;
+  p.v_new = v_new;
+  p.qw = q_norm_weight;
+  p.kw = k_norm_weight;
+  p.cos_t = cos_table;
+  p.sin_t = sin_table;
+  p.eps = eps;
+  p.inv_d = (float)(1.0 / (double)head_dim);
+  return launch_decode_dtype<true>(dtype, head_dim, num_heads / num_kv_heads, p,
+                                   as_stream(stream));
 }
 
 static int compat_decode(const void* q, const void* k, const void* v, const int* tables,

@@ -48,7 +48,7 @@ EXPORTED = (
     "rlse_last_error", "rlse_version",
     "rlse_pool_create", "rlse_pool_destroy", "rlse_pool_layer", "rlse_pool_info",
     "rlse_kv_append", "rlse_kv_gather", "rlse_kv_scatter", "rlse_kv_copy_blocks",
-    "rlse_decode_workspace_size", "rlse_paged_gqa_decode",
+    "rlse_decode_workspace_size", "rlse_paged_gqa_decode", "rlse_decode_step",
     "rlse_rmsnorm", "rlse_rope_tables", "rlse_rope", "rlse_qk_norm_rope_append",
     "launch_rmsnorm_f32", "launch_rmsnorm_f16", "launch_rmsnorm_bf16",
     "launch_paged_gqa_decode_tiled_f32", "launch_paged_gqa_decode_tiled_f16",
@@ -107,6 +107,8 @@ _SIGS = {
     "rlse_decode_workspace_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
     "rlse_paged_gqa_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f,
                                    _i, _vp, _sz, _vp]),
+    "rlse_decode_step": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp,
+                              _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp]),
     "rlse_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp]),
     "rlse_rope_tables": (_i, [_d, _i, _i, _i, _vp, _vp]),
     "rlse_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
@@ -365,6 +367,21 @@ def paged_gqa_decode(q, k_pool, v_pool, block_tables, seq_lens, out, batch: int,
                                         num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
                                         scale, _dt(dtype), _ptr(workspace), workspace_bytes,
                                         _stream(stream)))
+
+
+def decode_step(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: float, cos_table, sin_table,
+                max_pos: int, k_pool, v_pool, block_tables, seq_lens, out, batch: int,
+                num_heads: int, num_kv_heads: int, head_dim: int, max_blocks_per_seq: int,
+                num_blocks: int, scale: float, dtype, workspace=None, workspace_bytes: int = 0,
+                stream=None) -> None:
+    """One layer's fused q/k-norm + RoPE + append + paged decode (new token of
+    sequence b at position seq_lens[b] - 1)."""
+    _check(load().rlse_decode_step(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(q_norm_weight), _ptr(k_norm_weight), eps,
+        _ptr(cos_table), _ptr(sin_table), max_pos, _ptr(k_pool), _ptr(v_pool),
+        _ptr(block_tables), _ptr(seq_lens), _ptr(out), batch, num_heads, num_kv_heads, head_dim,
+        max_blocks_per_seq, num_blocks, scale, _dt(dtype), _ptr(workspace), workspace_bytes,
+        _stream(stream)))
 
 
 def rmsnorm(x, weight, out, rows: int, n: int, eps: float, dtype, stream=None) -> None:

@@ -254,3 +254,82 @@ def test_workspace_counters_reset_between_launches(kv):
                 np.testing.assert_array_equal(got, first[i])
     counters = to_host(ws[: 4 * 65536].view(torch.int32))  # the fixed counter region
     assert np.all(counters == 0)
+
+
+# ------------------------------------------------------------- fused step ----
+def _rope_tables_dev(kv, theta, d, max_pos, dtype):
+    np_dt = {"f32": np.float32, "bf16": np.uint16, "f16": np.float16}[dtype]
+    cb, sb = kv.rope_tables(theta, d, max_pos, dtype)
+    c = np.frombuffer(cb, np_dt).reshape(max_pos, d // 2).copy()
+    s = np.frombuffer(sb, np_dt).reshape(max_pos, d // 2).copy()
+    return c, s
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d,norm,lens", [
+    ("bf16", 16, 8, 128, True, [1, 2, 16, 17, 300, 513, 2049, 1000, 31]),   # Qwen3-0.6B
+    ("bf16", 14, 2, 64, False, [5, 4097, 100, 16, 33]),                       # Qwen2.5, no qk-norm
+    ("f32", 16, 8, 128, True, [513]),                                          # config-1 shape
+    ("f16", 32, 8, 128, True, [70, 1, 900]),                                   # Qwen3-8B heads
+])
+def test_fused_decode_step_matches_two_kernel_path_and_oracle(kv, dtype, hq, hkv, d, norm, lens):
+    """rlse_decode_step (norm + RoPE + append + decode in one launch) against
+    rlse_qk_norm_rope_append followed by rlse_paged_gqa_decode, and against
+    the oracle's Candle op chain (RmsNorm, apply_rope, KvCache append, zero-copy
+    GQA decode; src/backends/qwen2.rs:291-328)."""
+    rng = np.random.default_rng(31 + d + hq)
+    lens = np.asarray(lens, np.int32)
+    q, kp, vp, tables, lens = make_case(rng, lens, hq, hkv, d, dtype)
+    b, mbps, nb = len(lens), tables.shape[1], kp.shape[0]
+    k_new = random_values(rng, (b, hkv, d), dtype)
+    v_new = random_values(rng, (b, hkv, d), dtype)
+    w = lambda: random_values(rng, (d,), dtype) if norm else None  # noqa: E731
+    qw, kw = w(), w()
+    if norm and dtype != "bf16":
+        qw = (1 + 0.1 * rng.standard_normal(d)).astype(qw.dtype)
+        kw = (1 + 0.1 * rng.standard_normal(d)).astype(kw.dtype)
+    elif norm:
+        qw = O.f32_to_bf16_bits(1 + 0.1 * rng.standard_normal(d))
+        kw = O.f32_to_bf16_bits(1 + 0.1 * rng.standard_normal(d))
+    max_pos = mbps * 16
+    c, s = _rope_tables_dev(kv, 1e6, d, max_pos, dtype)
+    scale = 1.0 / math.sqrt(d)
+    dev = lambda a: None if a is None else to_dev(a, dtype)  # noqa: E731
+    t_dev, l_dev = to_dev(tables), to_dev(lens)
+    c_dev, s_dev = to_dev(c, dtype), to_dev(s, dtype)
+
+    # fused
+    kp1, vp1 = to_dev(kp, dtype), to_dev(vp, dtype)
+    out1 = torch.empty_like(to_dev(q, dtype))
+    kv.decode_step(dev(q), dev(k_new), dev(v_new), dev(qw), dev(kw), 1e-6, c_dev, s_dev, max_pos,
+                   kp1, vp1, t_dev, l_dev, out1, b, hq, hkv, d, mbps, nb, scale, dtype)
+    # two kernels
+    kp2, vp2 = to_dev(kp, dtype), to_dev(vp, dtype)
+    qrot = torch.empty_like(out1)
+    pos = lens - 1
+    kv.qk_norm_rope_append(dev(q), dev(k_new), dev(v_new), dev(qw), dev(kw), 1e-6, c_dev, s_dev,
+                           max_pos, to_dev(pos), t_dev, b, None, b, hq, hkv, d, mbps, nb, qrot,
+                           kp2, vp2, dtype)
+    out2 = run_decode(kv, qrot, kp2, vp2, tables, lens, hq, hkv, d, dtype, scale)
+    got = as_f32(to_host(out1), dtype)
+    check(f"fused vs two-kernel {dtype} G={hq // hkv}", got, as_f32(out2, dtype), dtype)
+    # appended V is bit-exact, appended K within an ulp, untouched pages unchanged
+    pk1, pv1, pk2, pv2 = (to_host(x) for x in (kp1, vp1, kp2, vp2))
+    np.testing.assert_array_equal(pv1, pv2)
+    rel = {"f32": 4e-6, "bf16": 2.0 ** -7, "f16": 2.0 ** -10}[dtype]
+    np.testing.assert_allclose(as_f32(pk1, dtype), as_f32(pk2, dtype), rtol=rel,
+                               atol=rel * float(np.mean(np.abs(as_f32(pk2, dtype)))))
+    # oracle chain on the appended pool
+    norm_f = (O.rmsnorm_bf16 if dtype == "bf16" else None)
+    if dtype == "bf16":
+        qn = q.reshape(-1, d) if not norm else norm_f(q.reshape(-1, d), qw, 1e-6)
+        q_ref = O.bf16_bits_to_f32(O.apply_rope_bf16(qn, np.repeat(pos, hq), c, s))
+    else:
+        qf = q.astype(np.float32).reshape(-1, d)
+        qn = O.rmsnorm_f32(qf, qw.astype(np.float32), 1e-6) if norm else qf
+        q_ref = O.apply_rope_f32(qn, np.repeat(pos, hq), c.astype(np.float32),
+                                 s.astype(np.float32))
+        if dtype == "f16":
+            q_ref = q_ref.astype(np.float16).astype(np.float32)
+    want = O.decode_paged_f32(q_ref.reshape(b, hq, d), as_f32(pk1, dtype), as_f32(pv1, dtype),
+                              tables, lens, scale)
+    check(f"fused vs oracle {dtype} G={hq // hkv}", got, want, dtype)
