@@ -1,0 +1,957 @@
+// Split-K GQA decode attention over the paged KV pool (gfx950, wave64).
+//
+// Reference semantics: decode_attention_gqa_zero_copy
+// (src/backends/qwen2.rs:177-203) -- for every KV head h, the G query heads
+// h*G .. h*G+G-1 attend to that head's K/V with softmax(q K^T * scale) V --
+// evaluated on the paged pool instead of a contiguous [Hkv, L, d] buffer.
+//
+// Work decomposition. The (sequence, KV head) rows are laid end to end as one
+// stream of 16-token blocks (row r = b*Hkv + h holds ceil(L_b/16) blocks).
+// Workgroup w -- a group of kWaves wavefronts -- takes the contiguous range
+// [w*T/W, (w+1)*T/W) of that stream and each of its waves a contiguous quarter
+// of it, so every wave streams the same number of bytes whatever the length
+// mix. A wave keeps all G query heads of the current KV head in registers, so
+// every K/V block is read from HBM exactly once (no repeat_kv) and shared by
+// the G heads. A row that lies wholly inside a wave's share is finished by the
+// wave; pieces of rows cut between waves are parked in LDS and combined after
+// one barrier at the end; rows cut by the group's range boundary leave one
+// (m, l, acc) partial per group in the workspace, and the group that finishes
+// such a row last (a per-row arrival counter) merges the partials with a
+// log-sum-exp combine in the same launch. The counters return to zero after
+// every launch, so a workspace only needs zero-filling once, before first use.
+//
+// Inside a wave a K/V block is read as 16-byte packets: LPR lanes cover one
+// 16-token row's head_dim, RPL = 64/LPR rows are read per instruction and each
+// lane owns NR = 16/RPL rows of the block. Scores are reduced over the LPR
+// lanes of a row with DPP adds (bf16/f16 dot products with v_dot2); each lane
+// group keeps its own online-softmax state (running max m in log2 units, sum
+// l, acc) and the groups are merged when the wave's part of a row ends. The
+// page ids of 64 blocks are fetched at once (one per lane), blocks are
+// double-buffered in registers so the next block's loads -- and the query of
+// a new row -- are in flight during the math, and no barrier is taken while
+// streaming.
+#pragma once
+
+#include <math.h>
+
+#include "common.cuh"
+#include "host_common.h"
+
+namespace rlse {
+
+constexpr int kWaves = 4;               // wavefronts per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kGroupsPerCU = 2;         // workgroups launched per compute unit
+constexpr int kMinBlocksPerGroup = 8;   // smallest share of blocks per workgroup
+constexpr int kMaxDecodeBatch = 8192;   // prefix table lives in LDS
+constexpr int kMaxDecodeRows = 65536;   // batch * num_kv_heads (arrival counters)
+constexpr int kMergeChunk = 8;          // partials loaded per batch in a merge
+// The running max of a softmax moves only when a score exceeds it by more
+// than this many powers of two.
+constexpr float kLazyLog2 = 8.f;
+
+template <typename T, int D>
+struct DecodeShape {
+  static constexpr int ES = sizeof(T);
+  static constexpr int EPL = 16 / ES;   // elements per 16-byte packet
+  static constexpr int LPR = D / EPL;   // lanes covering one K/V row
+  static constexpr int RPL = 64 / LPR;  // rows per wave-wide packet load
+  static constexpr int NR = 16 / RPL;   // packets per lane per 16-row block
+  static_assert(D % EPL == 0, "head_dim must be a multiple of the packet size");
+  static_assert(LPR >= 1 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "bad lanes per row");
+  static_assert(RPL >= 1 && RPL <= 16, "bad rows per load");
+};
+
+__device__ __forceinline__ int clamp_len(int L, int mbps) {
+  L = L < 0 ? 0 : L;
+  const int cap = mbps * 16;
+  return L > cap ? cap : L;
+}
+
+// Exclusive prefix of per-sequence block counts into s_pref[0..B] (one wave).
+__device__ void block_prefix(const int* __restrict__ seq_lens, int B, int mbps, int* s_pref) {
+  const int lane = threadIdx.x & 63;
+  int carry = 0;
+  for (int base = 0; base < B; base += 64) {
+    const int b = base + lane;
+    int nb = 0;
+    if (b < B) nb = (clamp_len(seq_lens[b], mbps) + 15) >> 4;
+    int x = nb;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (b < B) s_pref[b + 1] = carry + x;
+    carry += __shfl(x, 63, 64);
+  }
+  if (lane == 0) s_pref[0] = 0;
+}
+
+__device__ __forceinline__ long long effective_groups(long long total, int W) {
+  long long we = total / kMinBlocksPerGroup;
+  if (we < 1) we = 1;
+  return we < W ? we : W;
+}
+
+__device__ __forceinline__ long long range_lo(long long w, long long total, long long we) {
+  return (w * total) / we;
+}
+
+// Largest b in [0, B) with Hkv*s_pref[b] <= g (that sequence is non-empty).
+__device__ __forceinline__ int locate_seq(const int* s_pref, int B, int Hkv, long long g) {
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((long long)Hkv * s_pref[mid] <= g)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+// Floats of one partial record: acc[G][D], then m[G] and l[G], padded so
+// records stay 16-byte aligned.
+__host__ __device__ constexpr int rec_floats(int G, int D) { return G * D + ((2 * G + 3) & ~3); }
+
+// Partial records and arrival counters are accessed with device-scope
+// (agent) atomic loads and stores: on gfx950 these carry the sc1 bit, so each
+// access is coherent across the XCDs' L2 caches by itself. A group's record
+// stores are therefore visible device-wide once they complete, and waiting for
+// them (vmcnt(0)) before the counter increment orders them ahead of it -- no
+// whole-L2 writeback or invalidate is needed (a __threadfence() would emit
+// both, once per partial).
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima), fenced
+// against compiler reordering on both sides.
+__device__ __forceinline__ void wait_vm_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+struct DecodeParams {
+  const void* q;
+  const void* k_pool;
+  const void* v_pool;
+  const int* tables;
+  const int* seq_lens;
+  void* out;
+  float* ws;      // partial records, two slots per workgroup
+  int* counters;  // per-row arrival counters, zero between launches
+  int B;
+  int Hkv;
+  int mbps;
+  int num_blocks;
+  int W;    // workgroups launched
+  float c;  // scale * log2(e)
+  // Fused decode step only (rlse_decode_step): raw new-token k/v
+  // [B][Hkv][D], q/k RMSNorm weights [D] (null: no norm), RoPE tables
+  // [max_pos][D/2]. The new token of sequence b sits at seq_lens[b] - 1.
+  const void* k_new;
+  const void* v_new;
+  const void* qw;
+  const void* kw;
+  const void* cos_t;
+  const void* sin_t;
+  float eps;
+  float inv_d;
+};
+
+// Combines (m, l, a) with (mo, lo, ao), all in log2 units; -inf maxima mean
+// "empty" and never produce NaN.
+__device__ __forceinline__ void lse_combine(float& m, float& l, float& a, float mo, float lo,
+                                            float ao) {
+  const float M = fmaxf(m, mo);
+  const float Ms = (M == -INFINITY) ? 0.f : M;
+  const float sa = __builtin_amdgcn_exp2f(m - Ms);
+  const float sb = __builtin_amdgcn_exp2f(mo - Ms);
+  l = l * sa + lo * sb;
+  a = a * sa + ao * sb;
+  m = M;
+}
+
+template <typename T, int D>
+struct Buf {
+  uint4 k[DecodeShape<T, D>::NR];
+  uint4 v[DecodeShape<T, D>::NR];
+  int nvalid;   // valid rows of the block (0 = block skipped)
+  int row;      // b * Hkv + kvh
+  int sub;      // fused step: s_new entry holding the block's new row (-1: none)
+  bool newrow;  // first block of its row in this wave's range
+};
+
+// LDS bytes per wave for staged query packets: the queries of QR consecutive
+// rows are staged at once (QR = kQStageBytes / (G * D * sizeof(T)), at least 1).
+constexpr int kQStageBytes = 4096;
+template <typename T, int D, int G>
+__host__ __device__ constexpr int q_stage_rows() {
+  return kQStageBytes / (G * D * (int)sizeof(T)) > 0 ? kQStageBytes / (G * D * (int)sizeof(T))
+                                                      : 1;
+}
+
+// Rounding to T for the prologue's element-wise math: bf16 uses the
+// select-form conversion (same result as round_to).
+template <typename T>
+__device__ __forceinline__ uint16_t bits_sel(float v) {
+  if constexpr (sizeof(T) == 2 && !__is_same(T, f16)) {
+    return f32_to_bf16_bits_sel(v);
+  } else {
+    const T h = Elem<T>::from_f32(v);
+    uint16_t u;
+    __builtin_memcpy(&u, &h, 2);
+    return u;
+  }
+}
+template <typename T>
+__device__ __forceinline__ float round_sel(float v) {
+  if constexpr (sizeof(T) == 4) {
+    return v;
+  } else if constexpr (!__is_same(T, f16)) {
+    return bf16_bits_to_f32(f32_to_bf16_bits_sel(v));
+  } else {
+    return round_to<T>(v);
+  }
+}
+
+// Packs EPL floats of a row slice into a 16-byte packet of T.
+template <typename T>
+__device__ __forceinline__ uint4 pack_packet(const float* y) {
+  if constexpr (sizeof(T) == 4) {
+    return make_uint4(__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]),
+                      __float_as_uint(y[3]));
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)bits_sel<T>(y[2 * i]) | ((uint32_t)bits_sel<T>(y[2 * i + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// RMSNorm (optional) then NeoX RoPE of one row held as packets: lane col of
+// an LPR-lane group holds elements [col*EPL, col*EPL + EPL); rotate_half
+// pairs element i with i + D/2, held by lane col ^ LPR/2. Rounding follows
+// Candle's op sequence (RmsNorm::forward, apply_rope; src/backends/qwen2.rs:
+// 68-75, 133-142): x/norm and *w rounded to T, x*cos and rot*sin rounded,
+// then the sum rounded; no fused multiply-adds.
+template <typename T, int D>
+__device__ __forceinline__ uint4 norm_rope_packet(uint4 x, bool norm, uint4 w, float inv_d,
+                                                  float eps, uint4 cs, uint4 sn, int col) {
+  using S = DecodeShape<T, D>;
+  constexpr int EPL = S::EPL, LPR = S::LPR;
+  float xf[EPL], wf[EPL], cf[EPL], sf[EPL];
+  Packet<T>::unpack(x, xf);
+  if (norm) {
+    Packet<T>::unpack(w, wf);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) ss = __fadd_rn(ss, __fmul_rn(xf[e], xf[e]));
+    ss = group_sum<LPR>(ss);
+    const float nrm = sqrtf(__fadd_rn(__fmul_rn(ss, inv_d), eps));
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) xf[e] = round_sel<T>(__fmul_rn(round_sel<T>(xf[e] / nrm), wf[e]));
+  }
+  Packet<T>::unpack(cs, cf);
+  Packet<T>::unpack(sn, sf);
+  const bool upper = col >= LPR / 2;
+  float y[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float pf = __shfl_xor(xf[e], LPR / 2, 64);
+    const float a = round_sel<T>(__fmul_rn(xf[e], cf[e]));
+    const float bb = round_sel<T>(__fmul_rn(upper ? pf : -pf, sf[e]));
+    y[e] = __fadd_rn(a, bb);
+  }
+  return pack_packet<T>(y);
+}
+
+template <typename T, int D, int G, bool FUSED>
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
+  using S = DecodeShape<T, D>;
+  constexpr int EPL = S::EPL, LPR = S::LPR, RPL = S::RPL, NR = S::NR;
+  constexpr int REC = rec_floats(G, D);
+  constexpr int NPART = 2 * kWaves;
+  constexpr int DPL = (D + 63) / 64;  // output dims per lane in the row epilogue
+  constexpr int QR = q_stage_rows<T, D, G>();
+  // Register buffers per wave: three blocks in flight for 16-bit K/V, two
+  // for f32 (whose blocks take twice the registers).
+  constexpr int kNumBufs = sizeof(T) == 2 ? 3 : 2;
+  constexpr int kPreIssued = kNumBufs - 1;  // blocks issued before the prologue's appends
+  extern __shared__ int s_pref[];             // [B + 1]; fused step: then s_len[B]
+  __shared__ float s_part[NPART][G][D + 2];   // wave partials: acc[D], m, l per head
+  __shared__ int s_part_row[NPART];           // their rows (-1 = unused)
+  __shared__ uint4 s_q[kWaves][QR][G][LPR];   // staged query packets per wave
+  __shared__ uint4 s_new[FUSED ? kWaves : 1][kPreIssued][2][LPR];  // appended k, v rows
+
+  const int tid = threadIdx.x;
+  // The wave index and everything derived from LDS-held prefixes below are
+  // wave-uniform; readfirstlane tells the compiler so, which keeps the
+  // streaming loop a scalar loop (a divergent trip count would make it an
+  // exec-masked loop, with conservative waits on the loads in flight).
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int col = lane % LPR, rsub = lane / LPR;
+  const int B = p.B, Hkv = p.Hkv, mbps = p.mbps;
+  const int Hq = Hkv * G;
+  T* __restrict__ ob = reinterpret_cast<T*>(p.out);
+
+  int* s_len = s_pref + B + 1;  // fused step: clamped sequence lengths
+  if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref);
+  if constexpr (FUSED) {
+    for (int b = tid; b < B; b += kThreads) s_len[b] = clamp_len(p.seq_lens[b], mbps);
+  }
+  if (tid < NPART) s_part_row[tid] = -1;
+  __syncthreads();
+  const long long w = blockIdx.x;
+  if (w == 0) {  // rows of sequences without keys produce zeros
+    for (int b = 0; b < B; ++b) {
+      if (s_pref[b + 1] != s_pref[b]) continue;
+      for (int i = tid; i < Hq * D; i += kThreads)
+        ob[(size_t)b * Hq * D + i] = Elem<T>::from_f32(0.f);
+    }
+  }
+  const long long total = (long long)Hkv * __builtin_amdgcn_readfirstlane(s_pref[B]);
+  if (total == 0) return;
+  const long long we = effective_groups(total, p.W);
+  if (w >= we) return;
+  const long long glo = range_lo(w, total, we);
+  const long long ghi = range_lo(w + 1, total, we);
+  // This wave's contiguous share of the group's range.
+  const long long wlo = glo + (ghi - glo) * wave / kWaves;
+  const long long whi = glo + (ghi - glo) * (wave + 1) / kWaves;
+  const int nblk = (int)(whi - wlo);
+
+  // Row start in the block stream and its block count.
+  auto row_extent = [&](int row, long long& R, int& nb) __attribute__((always_inline)) {
+    const int b = row / Hkv, kvh = row - b * Hkv;
+    nb = s_pref[b + 1] - s_pref[b];
+    R = (long long)Hkv * s_pref[b] + (long long)kvh * nb;
+  };
+
+  if (nblk > 0) {
+    const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
+    const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
+    const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
+    const size_t tile = (size_t)16 * D;  // elements of one (block, head) tile
+    const size_t lane_off = (size_t)rsub * D + (size_t)col * EPL;
+
+    // Descriptors of 64 consecutive blocks, one per lane: page id, valid
+    // rows and row, read back with readlane when the block is issued.
+    // d_nv holds the valid rows in bits 0-7 and "last block of its row" in
+    // bit 8; d_pos is the row's new-token position (fused step).
+    int d_id = 0, d_nv = 0, d_row = -1, d_pos = 0, cbase = 0;
+    auto load_chunk = [&](int base) __attribute__((always_inline)) {
+      cbase = base;
+      const long long f = wlo + base + lane;
+      d_id = 0;
+      d_nv = 0;
+      d_row = -1;
+      d_pos = 0;
+      if (f < whi) {
+        const int b = locate_seq(s_pref, B, Hkv, f);
+        const int nb = s_pref[b + 1] - s_pref[b];
+        const long long o = f - (long long)Hkv * s_pref[b];
+        const int kvh = (int)(o / nb), blk = (int)(o % nb);
+        d_row = b * Hkv + kvh;
+        d_id = p.tables[(size_t)b * mbps + blk];
+        const int L = clamp_len(p.seq_lens[b], mbps);
+        const int nv = L - blk * 16;
+        d_nv = nv > 16 ? 16 : nv;
+        d_pos = L - 1;
+        if ((unsigned)d_id >= (unsigned)p.num_blocks)
+          d_nv = 0;
+        else if (blk == nb - 1)
+          d_nv |= 256;
+      }
+    };
+    load_chunk(0);
+
+    // RoPE cos/sin packets of position pos for lane column col: rotate_half
+    // pairs element i with i + D/2, so both halves use table columns
+    // (col % (LPR/2)) * EPL onwards.
+    auto rope_packets = [&](int pos, uint4& cs, uint4& sn) __attribute__((always_inline)) {
+      const size_t to = (size_t)pos * (D / 2) + (size_t)(col % (LPR / 2)) * EPL;
+      cs = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.cos_t) + to);
+      sn = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.sin_t) + to);
+    };
+    // RMSNorm weight packet of lane column col (zeros when w is null), read
+    // where it is used (an L1 hit) rather than held across the streaming loop.
+    // RMSNorm weight packet of lane column col, read where it is used (an L1
+    // hit) rather than held across the streaming loop. A null weight (no
+    // norm) reads q instead, which norm_rope_packet then ignores.
+    auto load_weight = [&](const void* w) __attribute__((always_inline)) {
+      const T* wp = reinterpret_cast<const T*>(w ? w : p.q);
+      return *reinterpret_cast<const uint4*>(wp + col * EPL);
+    };
+    // Query packets of QR consecutive rows from q_base on, staged in this
+    // wave's LDS slice (fused step: q_norm + RoPE at the row's new position).
+    // Staging is split into loads and then math + LDS stores, so the first
+    // stage's loads are in flight together with the first blocks' loads.
+    constexpr int QITEMS = QR * G;
+    constexpr int QPASSES = (QITEMS + RPL - 1) / RPL;
+    int q_base = 0, q_top = 0;  // staged rows [q_base, q_top)
+    uint4 sq_q[QPASSES], sq_c[QPASSES], sq_s[QPASSES], sq_w;
+    // Every staging load is unconditional, with its indices clamped into
+    // range (items past the end re-read a valid row and are never used): a
+    // load under a branch with a zero default would make the compiler copy
+    // its result at the join and wait for it right after issue.
+    // The wave's last row; staging never goes past it.
+    int last_row;
+    {
+      const long long f = whi - 1;
+      const int b = locate_seq(s_pref, B, Hkv, f);
+      const int nb = s_pref[b + 1] - s_pref[b];
+      last_row = __builtin_amdgcn_readfirstlane(b * Hkv + (int)((f - (long long)Hkv * s_pref[b]) / nb));
+    }
+    int q_items = 0;  // staged (row, head) items: (q_top - q_base) * G
+    auto stage_bounds = [&](int row0) __attribute__((always_inline)) {
+      q_base = row0;
+      q_top = row0 + QR < last_row + 1 ? row0 + QR : last_row + 1;
+      q_items = (q_top - q_base) * G;
+    };
+    auto stage_q_load = [&](int row0) __attribute__((always_inline)) {
+      const int nrows = B * Hkv;
+      stage_bounds(row0);
+      if constexpr (FUSED) sq_w = load_weight(p.qw);
+#pragma unroll
+      for (int ps = 0; ps < QPASSES; ++ps) {
+        const int item = ps * RPL + rsub;
+        const int t = item / G, g = item - t * G;
+        const int r = row0 + t < nrows ? row0 + t : nrows - 1;
+        const int b = r / Hkv, kvh = r - b * Hkv;
+        sq_q[ps] = *reinterpret_cast<const uint4*>(
+            qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
+        if constexpr (FUSED) {
+          const int pos = s_len[b] - 1;
+          rope_packets(pos > 0 ? pos : 0, sq_c[ps], sq_s[ps]);
+        }
+      }
+    };
+    // In-loop restaging (a wave whose range holds more than QR rows): one
+    // pass at a time in a rolled loop, which keeps the streaming loop's code
+    // (unrolled over the block buffers) small.
+    auto stage_q_refill = [&](int row0) __attribute__((always_inline)) {
+      const int nrows = B * Hkv;
+      stage_bounds(row0);
+      const uint4 w = FUSED ? load_weight(p.qw) : make_uint4(0, 0, 0, 0);
+#pragma unroll 1
+      for (int ps = 0; ps * RPL < q_items; ++ps) {
+        const int item = ps * RPL + rsub;
+        const int t = item / G, g = item - t * G;
+        const int r = row0 + t < nrows ? row0 + t : nrows - 1;
+        const int b = r / Hkv, kvh = r - b * Hkv;
+        uint4 x = *reinterpret_cast<const uint4*>(
+            qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
+        if constexpr (FUSED) {
+          const int pos = s_len[b] - 1;
+          uint4 cs, sn;
+          rope_packets(pos > 0 ? pos : 0, cs, sn);
+          x = norm_rope_packet<T, D>(x, p.qw != nullptr, w, p.inv_d, p.eps, cs, sn, col);
+        }
+        if (item < q_items) s_q[wave][t][g][col] = x;
+      }
+    };
+    // Passes past the staged items skip their math (the loads above were
+    // issued for every pass, clamped, so no wait depends on the item count).
+    auto stage_q_store = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int ps = 0; ps < QPASSES; ++ps) {
+        if (ps > 0 && ps * RPL >= q_items) break;
+        const int item = ps * RPL + rsub;
+        const int t = item / G, g = item - t * G;
+        uint4 y = sq_q[ps];
+        if constexpr (FUSED)
+          y = norm_rope_packet<T, D>(sq_q[ps], p.qw != nullptr, sq_w, p.inv_d, p.eps, sq_c[ps],
+                                     sq_s[ps], col);
+        if (item < q_items) s_q[wave][t][g][col] = y;
+      }
+    };
+
+    // Fused step: the new token of every row whose last block lies in this
+    // wave's range is appended by this wave (k_norm + RoPE of k, raw v), as
+    // that block is read by this wave only. The first kPreIssued blocks are
+    // issued before the appends are stored and take the new row from LDS
+    // (s_new); the appends have completed (vmcnt(0)) before any later block
+    // is issued, and the compute unit's write-through L1 shows them to its
+    // loads. A pass appends up to RPL rows, one per lane group.
+    uint64_t amask = 0;
+    int a_src = -1;
+    uint4 a_k, a_v, a_c, a_s, a_w;  // one pass's loads (append_load)
+    auto append_load = [&]() __attribute__((always_inline)) {
+      int src = -1;
+#pragma unroll
+      for (int i = 0; i < RPL; ++i) {
+        if (amask) {
+          const int k = __builtin_ctzll(amask);
+          amask &= amask - 1;
+          if (rsub == i) src = k;
+        }
+      }
+      a_src = src;
+      // Lane groups without a row load lane 0's (a valid block of the chunk)
+      // and store nothing.
+      const int sl = src >= 0 ? src : 0;
+      const int row = __shfl(d_row, sl, 64), pos = __shfl(d_pos, sl, 64);
+      a_w = load_weight(p.kw);
+      const size_t no = (size_t)row * D + (size_t)col * EPL;
+      a_k = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.k_new) + no);
+      a_v = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.v_new) + no);
+      rope_packets(pos, a_c, a_s);
+    };
+    auto append_store = [&]() __attribute__((always_inline)) {
+      const int sl = a_src >= 0 ? a_src : 0;
+      const int row = __shfl(d_row, sl, 64), pos = __shfl(d_pos, sl, 64);
+      const int id = __shfl(d_id, sl, 64);
+      const uint4 kr = norm_rope_packet<T, D>(a_k, p.kw != nullptr, a_w, p.inv_d, p.eps, a_c, a_s,
+                                              col);
+      if (a_src >= 0) {
+        const int kvh = row % Hkv;
+        const size_t dst = (((size_t)id * Hkv + kvh) * 16 + (pos & 15)) * D + (size_t)col * EPL;
+        *reinterpret_cast<uint4*>(const_cast<T*>(kp) + dst) = kr;
+        *reinterpret_cast<uint4*>(const_cast<T*>(vp) + dst) = a_v;
+        if (cbase == 0 && a_src < kPreIssued) {
+          s_new[wave][a_src][0][col] = kr;
+          s_new[wave][a_src][1][col] = a_v;
+        }
+      }
+    };
+
+    // Before the first blocks are issued: the first row's query loads and
+    // the first append pass's loads.
+    stage_q_load(__builtin_amdgcn_readfirstlane(d_row));
+    if constexpr (FUSED) {
+      amask = __ballot((d_nv & 256) != 0);
+      append_load();
+    }
+    // Keep these loads ahead of the block loads: the math after the first
+    // issues waits for them, and a wait for a load issued after the blocks
+    // would wait for the blocks too (loads complete in order).
+    __builtin_amdgcn_sched_barrier(0);
+    // After the first kPreIssued blocks are issued: finish the query stage
+    // and every append.
+    auto after_pre_issue = [&]() __attribute__((always_inline)) {
+      stage_q_store();
+      if constexpr (FUSED) {
+        append_store();
+        for (int base = 0; base < nblk; base += 64) {
+          if (base) {
+            load_chunk(base);
+            amask = __ballot((d_nv & 256) != 0);
+          }
+          while (amask) {
+            append_load();
+            append_store();
+          }
+        }
+        if (nblk > 64) load_chunk(0);
+        wait_vm_stores();
+      }
+    };
+
+    int issued_row = -1;
+    auto issue = [&](Buf<T, D>& bf, int j) __attribute__((always_inline)) {
+      if (j - cbase >= 64) load_chunk(cbase + 64);
+      const int k = j - cbase;
+      const int id = __builtin_amdgcn_readlane(d_id, k);
+      const int nvf = __builtin_amdgcn_readlane(d_nv, k);
+      const int row = __builtin_amdgcn_readlane(d_row, k);
+      const int kvh = row % Hkv;
+      const int nv = nvf & 255;
+      bf.nvalid = nv;
+      bf.row = row;
+      bf.newrow = row != issued_row;
+      bf.sub = (FUSED && (nvf & 256) && j < kPreIssued) ? j : -1;
+      issued_row = row;
+      // The loads are issued for every block, a skipped one (invalid page id)
+      // reading page 0 instead: with loads under a branch the compiler cannot
+      // count the loads in flight and waits for every earlier block before
+      // reusing a buffer's registers, which would serialize the pipeline.
+      const size_t base = ((size_t)(nv > 0 ? id : 0) * Hkv + kvh) * tile + lane_off;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        bf.k[r] = *reinterpret_cast<const uint4*>(kp + base + (size_t)r * RPL * D);
+        bf.v[r] = *reinterpret_cast<const uint4*>(vp + base + (size_t)r * RPL * D);
+      }
+    };
+
+    float m[G], l[G], acc[G][EPL];
+    uint4 qv[G];
+    int cur_row = -1;
+    auto reset = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+      }
+    };
+    // Ends the wave's part of cur_row: merge the lane groups, then write the
+    // output (row wholly inside this wave) or park the state in LDS.
+    auto finalize = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float mo = __shfl_xor(m[g], off, 64);
+          const float lo_ = __shfl_xor(l[g], off, 64);
+          const float M = fmaxf(m[g], mo);
+          const float Ms = (M == -INFINITY) ? 0.f : M;
+          const float sa = __builtin_amdgcn_exp2f(m[g] - Ms);
+          const float sb = __builtin_amdgcn_exp2f(mo - Ms);
+          l[g] = l[g] * sa + lo_ * sb;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) {
+            const float ao = __shfl_xor(acc[g][e], off, 64);
+            acc[g][e] = acc[g][e] * sa + ao * sb;
+          }
+          m[g] = M;
+        }
+      }
+      long long R;
+      int nb;
+      row_extent(cur_row, R, nb);
+      const int b = cur_row / Hkv, kvh = cur_row - b * Hkv;
+      if (R >= wlo && R + nb <= whi) {
+        if (rsub == 0) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;  // all pages skipped -> zeros
+            T* dst = ob + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) dst[e] = Elem<T>::from_f32(acc[g][e] * inv);
+          }
+        }
+      } else {
+        const int slot = 2 * wave + (R < wlo ? 0 : 1);
+        if (rsub == 0) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) s_part[slot][g][col * EPL + e] = acc[g][e];
+            if (col == 0) {
+              s_part[slot][g][D] = m[g];
+              s_part[slot][g][D + 1] = l[g];
+            }
+          }
+        }
+        if (lane == 0) s_part_row[slot] = cur_row;
+      }
+    };
+    auto compute = [&](const Buf<T, D>& bf) __attribute__((always_inline)) {
+      if (bf.newrow) {
+        if (cur_row >= 0) finalize();
+        reset();
+        cur_row = bf.row;
+        if (cur_row < q_base || cur_row >= q_top) stage_q_refill(cur_row);
+#pragma unroll
+        for (int g = 0; g < G; ++g) qv[g] = s_q[wave][cur_row - q_base][g][col];
+      }
+      // A skipped block (nv = 0) runs the same math with every row masked,
+      // which leaves m, l and acc unchanged; consuming its registers on every
+      // path keeps the compiler's count of loads in flight exact.
+      const int nv = bf.nvalid;
+      uint4 kr[NR], vr[NR];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        kr[r] = bf.k[r];
+        vr[r] = bf.v[r];
+      }
+      if constexpr (FUSED) {
+        if (bf.sub >= 0) {  // the new token (slot nv-1) was appended after this load issued
+          const int slot = nv - 1;
+          if (rsub == slot % RPL) {
+            const uint4 kn = s_new[wave][bf.sub][0][col], vn = s_new[wave][bf.sub][1][col];
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+              if (r == slot / RPL) {
+                kr[r] = kn;
+                vr[r] = vn;
+              }
+          }
+        }
+      }
+      // Raw scores q.k, summed over the LPR lanes of each row.
+      float s[G][NR];
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          s[g][r] = group_sum<LPR>(Packet<T>::dot(qv[g], kr[r], 0.f));
+      if (nv < 16) {  // tail block: rows past the sequence end get p = 0 and V = 0
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          if (r * RPL + rsub >= nv) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) s[g][r] = -INFINITY;
+            vr[r] = make_uint4(0, 0, 0, 0);
+          }
+        }
+      }
+      // 16-bit V: pair rows (r, r+1) element-wise so one v_dot2 applies two
+      // probabilities; the pairing is shared by all G heads.
+      constexpr bool kPacked = sizeof(T) == 2;
+      uint32_t vpair[kPacked ? NR / 2 : 1][4][2];
+      float vf[kPacked ? 1 : NR][EPL];
+      if constexpr (kPacked) {
+#pragma unroll
+        for (int r = 0; r < NR; r += 2) {
+          const uint32_t w0[4] = {vr[r].x, vr[r].y, vr[r].z, vr[r].w};
+          const uint32_t w1[4] = {vr[r + 1].x, vr[r + 1].y, vr[r + 1].z, vr[r + 1].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            vpair[r / 2][k][0] = __builtin_amdgcn_perm(w1[k], w0[k], 0x05040100u);  // low halves
+            vpair[r / 2][k][1] = __builtin_amdgcn_perm(w1[k], w0[k], 0x07060302u);  // high halves
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) Packet<T>::unpack(vr[r], vf[r]);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float mx = s[g][0];
+#pragma unroll
+        for (int r = 1; r < NR; ++r) mx = fmaxf(mx, s[g][r]);
+        const float cand = mx * p.c;
+        // Lazy rescaling: the running max moves only when a score exceeds it
+        // by more than kLazyLog2 (probabilities then stay below 2^kLazyLog2).
+        if (__any(cand > m[g] + kLazyLog2)) {
+          const float mn = fmaxf(m[g], cand);
+          const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m[g] - mn);
+          l[g] *= alpha;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
+          m[g] = mn;
+        }
+        const float nms = (m[g] == -INFINITY) ? 0.f : -m[g];
+        float pr[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          pr[r] = __builtin_amdgcn_exp2f(fmaf(s[g][r], p.c, nms));
+          l[g] += pr[r];
+        }
+        if constexpr (kPacked) {
+#pragma unroll
+          for (int r = 0; r < NR; r += 2) {
+            const uint32_t pp = Packet<T>::pack2(pr[r], pr[r + 1]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              acc[g][2 * k] = Packet<T>::dot2(vpair[r / 2][k][0], pp, acc[g][2 * k]);
+              acc[g][2 * k + 1] = Packet<T>::dot2(vpair[r / 2][k][1], pp, acc[g][2 * k + 1]);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) {
+            float a = acc[g][e];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) a = fmaf(pr[r], vf[r][e], a);
+            acc[g][e] = a;
+          }
+        }
+      }
+    };
+
+    // kNumBufs blocks in flight: kNumBufs-1 are loading while one is
+    // computed (indices past the end re-load the last block, never computed).
+    const int last = nblk - 1;
+    if constexpr (kNumBufs == 3) {
+      Buf<T, D> b0, b1, b2;
+      issue(b0, 0);
+      issue(b1, last < 1 ? last : 1);
+      after_pre_issue();
+      for (int i = 0;;) {
+        issue(b2, i + 2 < last ? i + 2 : last);
+        compute(b0);
+        if (++i == nblk) break;
+        issue(b0, i + 2 < last ? i + 2 : last);
+        compute(b1);
+        if (++i == nblk) break;
+        issue(b1, i + 2 < last ? i + 2 : last);
+        compute(b2);
+        if (++i == nblk) break;
+      }
+    } else {
+      Buf<T, D> b0, b1;
+      issue(b0, 0);
+      after_pre_issue();
+      for (int i = 0;;) {
+        issue(b1, i + 1 < last ? i + 1 : last);
+        compute(b0);
+        if (++i == nblk) break;
+        issue(b0, i + 1 < last ? i + 1 : last);
+        compute(b1);
+        if (++i == nblk) break;
+      }
+    }
+    finalize();
+  }
+  __syncthreads();
+
+  // Rows this group holds in pieces. The wave holding the group's last piece
+  // of a row finishes it: it combines the pieces parked by earlier waves
+  // (waves own consecutive ranges, so a row's pieces sit in consecutive
+  // waves), then writes the output (row inside the group's range) or
+  // publishes one group partial and merges the row if it arrives last. Waves
+  // handle their rows independently, so the publication chains overlap.
+  for (int s = 0; s < 2; ++s) {
+    const int row = s_part_row[2 * wave + s];
+    if (row < 0) continue;
+    long long R;
+    int nb;
+    row_extent(row, R, nb);
+    if (R + nb > whi && whi < ghi) continue;  // a later wave holds more of the row
+    const int b = row / Hkv, kvh = row - b * Hkv;
+    const bool inside = R >= glo && R + nb <= ghi;
+    float M[G][DPL], Ls[G][DPL], A[G][DPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        M[g][k] = -INFINITY;
+        Ls[g][k] = 0.f;
+        A[g][k] = 0.f;
+      }
+    for (int wv = wave; wv >= 0; --wv) {
+      bool any = false;
+      for (int s2 = 1; s2 >= 0; --s2) {
+        const int slot = 2 * wv + s2;
+        if ((wv == wave && s2 != s) || s_part_row[slot] != row) continue;
+        any = true;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) {
+            const int d = lane + 64 * k;
+            if (d < D)
+              lse_combine(M[g][k], Ls[g][k], A[g][k], s_part[slot][g][D], s_part[slot][g][D + 1],
+                          s_part[slot][g][d]);
+          }
+      }
+      if (!any) break;
+    }
+    if (inside) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) {
+          const int d = lane + 64 * k;
+          if (d < D) {
+            const float inv = Ls[g][k] > 0.f ? 1.f / Ls[g][k] : 0.f;
+            ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(A[g][k] * inv);
+          }
+        }
+      continue;
+    }
+    // Group partial: slot 0 = the group's first segment, 1 = a later one.
+    float* rec = p.ws + ((size_t)w * 2 + (R <= glo ? 0 : 1)) * (size_t)REC;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        const int d = lane + 64 * k;
+        if (d < D) st_dev(rec + (size_t)g * D + d, A[g][k]);
+      }
+      if (lane == 0) {
+        st_dev(rec + G * D + g, M[g][0]);
+        st_dev(rec + G * D + G + g, Ls[g][0]);
+      }
+    }
+    // Count the arrival; the last of the row's np groups merges. Group wa
+    // (holding the row's first block) used slot 0 only if its range starts
+    // exactly at the row start.
+    const long long wa = ((R + 1) * we - 1) / total;
+    const long long wb = ((R + nb) * we - 1) / total;
+    const int np = (int)(wb - wa + 1);
+    const bool wa_slot1 = range_lo(wa, total, we) != R;
+    wait_vm_stores();
+    int prev = 0;
+    if (lane == 0)
+      prev = __hip_atomic_fetch_add(p.counters + row, 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0, 64);
+    if (prev != np - 1) continue;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        M[g][k] = -INFINITY;
+        Ls[g][k] = 0.f;
+        A[g][k] = 0.f;
+      }
+    for (int c = 0; c < np; c += kMergeChunk) {
+      float mv[kMergeChunk][G], lv[kMergeChunk][G], av[kMergeChunk][G][DPL];
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i) {  // issue the chunk's loads together
+        const int j = c + i < np ? c + i : np - 1;
+        const int slot = (j == 0 && wa_slot1) ? 1 : 0;
+        const float* r = p.ws + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          mv[i][g] = ld_dev(r + G * D + g);
+          lv[i][g] = ld_dev(r + G * D + G + g);
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) {
+            const int d = lane + 64 * k;
+            av[i][g][k] = d < D ? ld_dev(r + (size_t)g * D + d) : 0.f;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i)
+        if (c + i < np)
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int k = 0; k < DPL; ++k)
+              lse_combine(M[g][k], Ls[g][k], A[g][k], mv[i][g], lv[i][g], av[i][g][k]);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        const int d = lane + 64 * k;
+        if (d < D) {
+          const float inv = Ls[g][k] > 0.f ? 1.f / Ls[g][k] : 0.f;
+          ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(A[g][k] * inv);
+        }
+      }
+    if (lane == 0)
+      __hip_atomic_store(p.counters + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Launches one instantiation of the kernel on stream (defined here, instantiated
+// explicitly per element type and mode in the decode_inst_*.hip units so they
+// compile in parallel).
+template <typename T, int D, int G, bool FUSED>
+int launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+  // Dynamic LDS: block prefix [B + 1], then (fused step) lengths [B].
+  const size_t lds = (size_t)(p.B + 1 + (FUSED ? p.B : 0)) * sizeof(int);
+  hipLaunchKernelGGL((decode_kernel<T, D, G, FUSED>), dim3(p.W), dim3(kThreads), lds, stream,
+                     p);
+  return launch_status("decode_kernel");
+}
+
+#define RLSE_DECODE_INST_G(PREFIX, T, D, FUSED)                              \
+  PREFIX int launch_decode_t<T, D, 1, FUSED>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 2, FUSED>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 3, FUSED>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 4, FUSED>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 5, FUSED>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 6, FUSED>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 7, FUSED>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 8, FUSED>(const DecodeParams&, hipStream_t);
+// Every supported (head_dim, group size) of one element type and mode.
+#define RLSE_DECODE_INSTANCES(PREFIX, T, FUSED) \
+  RLSE_DECODE_INST_G(PREFIX, T, 64, FUSED)      \
+  RLSE_DECODE_INST_G(PREFIX, T, 128, FUSED)
+
+}  // namespace rlse
