@@ -53,18 +53,54 @@ def parse():
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--unfused", action="store_true",
                     help="norm/RoPE/append and decode as two launches per layer")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of 1 GiB (HBM counter calibration)")
     return ap.parse_args()
+
+
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration():
+    """A plain device-to-device copy of COPY_BYTES, three times: reads and
+    writes exactly COPY_BYTES per dispatch, so the FETCH_SIZE / WRITE_SIZE
+    counters of one dispatch give the counters' scale for HBM bytes."""
+    import torch
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "dispatches": 3}))
 
 
 def algorithmic_decode_bytes(lens, hq, hkv, d, es, fused):
     """HBM bytes one decode launch must move: every attended K and V row once,
-    q in and out once, the used block-table entries and the lengths; the fused
-    step also writes the appended K/V row of every sequence."""
+    q in and out once, the used block-table entries and the lengths. The fused
+    step also reads each sequence's new K/V rows and writes them into the pool
+    (2 x B x 2 x Hkv x d elements), reads one cos and one sin row of d/2
+    elements per sequence and the two RMSNorm weights."""
+    b = len(lens)
     kv = sum(int(n) * 2 * hkv * d * es for n in lens)
-    qo = 2 * len(lens) * hq * d * es
+    qo = 2 * b * hq * d * es
     tab = sum(((int(n) + 15) // 16) * 4 for n in lens)
-    app = len(lens) * 2 * hkv * d * es if fused else 0
-    return kv + qo + tab + 4 * len(lens) + app
+    app = (2 * b * 2 * hkv * d * es + b * d * es + 2 * d * es) if fused else 0
+    return kv + qo + tab + 4 * b + app
+
+
+def measured_traffic(workload, fused):
+    """HBM bytes per launch of the fused decode kernel for this workload, from
+    the committed rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs (scaled by the
+    copy calibration recorded beside them), or None when none is recorded."""
+    if not fused:
+        return None, None
+    path = os.path.join(ROOT, "profiles", f"decode_step_{workload}_hbm_counters.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        rec = json.load(f)
+    return rec["traffic_bytes_per_launch"], os.path.relpath(path, ROOT)
 
 
 def cpu_baseline(args, lens, hq, hkv, d, layers):
@@ -104,6 +140,9 @@ def cpu_baseline(args, lens, hq, hkv, d, layers):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
@@ -201,6 +240,7 @@ def main():
     per_launch = algorithmic_decode_bytes(lens, hq, hkv, d, 2, not args.unfused)
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
     ms_per_step = elapsed * 1e3 / args.steps
+    traffic, traffic_src = measured_traffic(args.workload, not args.unfused)
     result = {
         "metric": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen3-0.6B shape, 1 GPU",
         "value": b * args.steps / elapsed,
@@ -218,7 +258,8 @@ def main():
                    "kv_heads": hkv, "head_dim": d, "mean_keys": float(np.mean(lens)),
                    "pages_per_layer": need, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": ("decode_kernel (rlse_paged_gqa_decode)" if args.unfused else
                                 "decode_kernel fused step (rlse_decode_step)"),
                      "bytes_per_launch": per_launch, "avg_launch_ms": avg_ms,
