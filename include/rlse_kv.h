@@ -160,6 +160,27 @@ int rlse_decode_step(const void* q, const void* k_new, const void* v_new,
                      int max_blocks_per_seq, int num_blocks, float scale, int dtype,
                      void* workspace, size_t workspace_bytes, rlse_stream_t stream);
 
+/* Chunked-prefill attention of one sequence: the prefill branch of
+ * Attention::forward (src/backends/qwen2.rs:329-345) with the causal mask
+ * of prepare_causal_attention_mask (src/backends/qwen2.rs:476-503), read
+ * from the paged pool with GQA head mapping hq / (num_heads/num_kv_heads)
+ * instead of repeat_kv. The chunk's num_tokens queries q [num_tokens]
+ * [num_heads][head_dim] sit at positions ctx_len-num_tokens .. ctx_len-1;
+ * their K/V must already be in the pool (appended as the reference appends
+ * before attending). Query t sees keys 0 .. ctx_len-num_tokens+t of the
+ * page list block_table[max_blocks] (ctx_len <= max_blocks*16); keys in
+ * pages with ids outside [0, num_blocks) are skipped. out [num_tokens]
+ * [num_heads][head_dim]. bf16 and f16 only (MFMA tiles), head_dim 64 or
+ * 128. workspace: rlse_prefill_workspace_size bytes (may be 0), or NULL
+ * for a library-owned one per device. */
+int rlse_prefill_workspace_size(int num_tokens, int ctx_len, int num_heads, int num_kv_heads,
+                                int head_dim, size_t* bytes);
+int rlse_prefill_attn(const void* q, const void* k_pool, const void* v_pool,
+                      const int32_t* block_table, int ctx_len, int num_tokens, void* out,
+                      int num_heads, int num_kv_heads, int head_dim, int max_blocks,
+                      int num_blocks, float scale, int dtype, void* workspace,
+                      size_t workspace_bytes, rlse_stream_t stream);
+
 /* ------------------------------------------------------------------ */
 /* Normalisation and rotary embedding.                                 */
 /* ------------------------------------------------------------------ */

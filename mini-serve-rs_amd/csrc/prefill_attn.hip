@@ -1,0 +1,505 @@
+// Chunked-prefill attention over the paged KV pool, on MFMA tiles (gfx950).
+//
+// Reference semantics: the prefill branch of Attention::forward
+// (src/backends/qwen2.rs:329-345) with prepare_causal_attention_mask
+// (src/backends/qwen2.rs:476-503). A chunk of Tq query tokens sits at
+// positions offset .. offset+Tq-1 of its sequence (offset = ctx_len - Tq, the
+// chunk's own K/V already appended); query token t attends to keys
+// 0 .. offset+t with softmax(q K^T * scale) V, query head hq reading KV head
+// hq / G -- evaluated here on the paged pool, without repeat_kv and without
+// materialising the score matrix.
+//
+// Work decomposition. For KV head h the (token, head-in-group) pairs form
+// Tq*G rows (row = t*G + g). A workgroup of 4 waves takes 128 rows of one KV
+// head, each wave 32 of them, and streams that head's keys in tiles of 64:
+// the tile's K rows and V (transposed) are staged in LDS once and shared by
+// the 4 waves. When there are too few row tiles to fill the chip, the keys
+// are also split across workgroups and a second kernel merges the per-split
+// (m, l, acc) partials with a log-sum-exp combine. Workgroups are mapped to
+// work so that consecutive work items -- the row tiles reading the same K/V
+// range -- run on one XCD and share its L2.
+//
+// Per wave and tile (v_mfma_f32_32x32x16_{bf16,f16}; lane l holds
+// A[l%32][8*(l/32)+j], B[8*(l/32)+j][l%32] and accumulator element i at
+// [8*(i/4) + 4*(l/32) + i%4][l%32]):
+//   S^T (keys x queries) = K (keys x d) . Q^T (d x queries)
+// so each lane owns one query column: the softmax max and sum are 16 values
+// in the lane plus one exchange with lane l^32. The probabilities stay in the
+// accumulator layout and feed
+//   O^T (d x queries) += V^T (d x keys) . P^T (keys x queries)
+// directly as the B operand; the keys of each 16-key MFMA block are taken in
+// the order the accumulator holds them, and V^T is laid out in LDS in that
+// same order so its A operand is one 16-byte read.
+#include <math.h>
+
+#include "common.cuh"
+#include "host_common.h"
+
+namespace rlse {
+namespace {
+
+constexpr int kPWaves = 4;
+constexpr int kPThreads = 64 * kPWaves;
+constexpr int kBM = 32 * kPWaves;  // rows per workgroup
+constexpr int kBN = 64;            // keys per tile
+constexpr int kPad = 8;            // LDS row padding (elements): conflict-free 16-byte reads
+constexpr int kMinKeysPerSplit = 512;
+constexpr int kMaxSplits = 16;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+// Staging type for 16-byte packets: a native vector, so copies are vector
+// loads and stores (HIP's uint4 struct is copied with memcpy, which keeps an
+// array of them in scratch memory when it is later written to LDS).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<bf16> {
+  static __device__ __forceinline__ f32x16_t mma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<f16> {
+  static __device__ __forceinline__ f32x16_t mma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+struct PrefillParams {
+  const void* q;       // [Tq][Hq][D]
+  const void* k_pool;  // [num_blocks][Hkv][16][D]
+  const void* v_pool;
+  const int* table;    // [mbps] page ids of the sequence
+  void* out;           // [Tq][Hq][D]
+  float* part;         // [S][Tq*Hq][D + 2] partials (S > 1)
+  int Tq, L, offset, Hq, Hkv, G, num_blocks, mbps;
+  int row_tiles, splits, split_keys;
+  float c;  // scale * log2(e)
+};
+
+// Position of actual key a (0..15) of a 16-key MFMA block in the order the
+// S^T accumulator holds it: lane half h owns keys 4h..4h+3 and 8+4h..11+4h.
+__device__ __forceinline__ int key_slot(int a) {
+  return ((a >> 2) & 1) * 8 + (a >> 3) * 4 + (a & 3);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) {
+  constexpr int KB = D / 16;                  // 16-wide k-blocks of q.k
+  constexpr int DB = D / 32;                  // 32-row blocks of O^T
+  constexpr int CPR = D / 8;                  // 16-byte chunks per key row
+  constexpr int KPK = kBN * CPR;              // K packets per tile
+  constexpr int KPT = KPK / kPThreads;        // per thread
+  constexpr int VIT = (kBN / 4) * CPR;        // V items (4 keys x 8 dims) per tile
+  constexpr int VPT = (VIT + kPThreads - 1) / kPThreads;
+  static_assert(KPK % kPThreads == 0, "K tile must split evenly");
+  __shared__ __align__(16) uint16_t s_k[2][kBN][D + kPad];   // K rows
+  __shared__ __align__(16) uint16_t s_v[2][D][kBN + kPad];   // V^T, keys in MFMA order
+  __shared__ int s_valid[2];                                 // page-valid bits of the tile
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int half = lane >> 5, col = lane & 31;
+
+  // XCD-aware work index: workgroup b runs on XCD b % 8; give each XCD a
+  // contiguous run of work items.
+  const int nwg = gridDim.x;
+  const int b = blockIdx.x;
+  const int wid = (nwg % 8 == 0) ? (b % 8) * (nwg / 8) + b / 8 : b;
+  const int rt = wid % p.row_tiles;
+  const int h = (wid / p.row_tiles) % p.Hkv;
+  const int split = wid / (p.row_tiles * p.Hkv);
+
+  const int G = p.G, Hq = p.Hq, Hkv = p.Hkv;
+  const int rows = p.Tq * G;
+  const int myrow = rt * kBM + wave * 32 + col;
+  const int row_c = myrow < rows ? myrow : rows - 1;
+  const int t = row_c / G, g = row_c - t * G, qh = h * G + g;
+  const int kmax = p.offset + t;  // last key this query sees
+
+  // Keys of this workgroup: up to the last query's diagonal, this split's share.
+  const int last_row = min(rows - 1, rt * kBM + kBM - 1);
+  const int wg_keys = min(p.L, p.offset + last_row / G + 1);
+  const int k_begin = split * p.split_keys;
+  const int k_end = min(wg_keys, k_begin + p.split_keys);
+
+  const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
+  const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
+  const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
+
+  f32x16_t o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+  float m = -INFINITY, lsum = 0.f;
+
+  if (k_begin < k_end) {
+    uint4 qreg[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+      qreg[kb] = *reinterpret_cast<const uint4*>(qb + ((size_t)t * Hq + qh) * D + kb * 16 +
+                                                 half * 8);
+
+    const int last_tile = k_begin + ((k_end - 1 - k_begin) / kBN) * kBN;
+    static_assert(kBN == 64, "a tile spans the 4 pages held in pid");
+    u32x4_t kst[KPT], vst[VPT][4];
+    int4 pid;  // page ids of the tile's 4 pages (-1: invalid)
+    // Page id of tile page i, invalid ones replaced by page 0 (selects on a
+    // vector value: an indexed register array would live in scratch memory).
+    auto page_of = [&](int i) __attribute__((always_inline)) {
+      const int r = i == 0 ? pid.x : i == 1 ? pid.y : i == 2 ? pid.z : pid.w;
+      return r < 0 ? 0 : r;
+    };
+    // Global loads of the tile at kt (keys past L clamp to L-1 and are masked
+    // later; invalid page ids read page 0 and are masked).
+    auto load_tile = [&](int kt) __attribute__((always_inline)) {
+      auto table_id = [&](int pg) __attribute__((always_inline)) {
+        int pi = (kt >> 4) + pg;
+        const int plast = (p.L - 1) >> 4;
+        pi = pi < plast ? pi : plast;
+        const int id = p.table[pi];
+        return ((unsigned)id < (unsigned)p.num_blocks) ? id : -1;
+      };
+      pid = make_int4(table_id(0), table_id(1), table_id(2), table_id(3));
+#pragma unroll
+      for (int u = 0; u < KPT; ++u) {
+        const int pk = tid + u * kPThreads;
+        const int kk = pk / CPR, dc = pk - kk * CPR;
+        const int ka = min(kt + kk, p.L - 1);
+        const int id = page_of((ka - kt) >> 4);
+        kst[u] = *reinterpret_cast<const u32x4_t*>(
+            kp + (((size_t)id * Hkv + h) * 16 + (ka & 15)) * D + dc * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < VPT; ++u) {
+        int it = tid + u * kPThreads;
+        it = it < VIT ? it : VIT - 1;
+        const int kg = it % (kBN / 4), dc = it / (kBN / 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int ka = min(kt + kg * 4 + j, p.L - 1);
+          const int id = page_of((ka - kt) >> 4);
+          vst[u][j] = *reinterpret_cast<const u32x4_t*>(
+              vp + (((size_t)id * Hkv + h) * 16 + (ka & 15)) * D + dc * 8);
+        }
+      }
+    };
+    // Staged registers -> LDS buffer bf: K rows as they are, V transposed
+    // with each 16-key block's keys in accumulator order.
+    auto store_tile = [&](int bf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < KPT; ++u) {
+        const int pk = tid + u * kPThreads;
+        const int kk = pk / CPR, dc = pk - kk * CPR;
+        *reinterpret_cast<u32x4_t*>(&s_k[bf][kk][dc * 8]) = kst[u];
+      }
+#pragma unroll
+      for (int u = 0; u < VPT; ++u) {
+        const int it = tid + u * kPThreads;
+        if (it < VIT) {
+          const int kg = it % (kBN / 4), dc = it / (kBN / 4);
+          const int a0 = kg * 4;  // first key of the group, 4-aligned
+          const int slot = (a0 & ~15) + key_slot(a0 & 15);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            // Element e of each of the 4 keys: the low or high half of word e/2.
+            const int wi = e >> 1;
+            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+            const uint32_t k01 = __builtin_amdgcn_perm(vst[u][1][wi], vst[u][0][wi], sel);
+            const uint32_t k23 = __builtin_amdgcn_perm(vst[u][3][wi], vst[u][2][wi], sel);
+            *reinterpret_cast<uint2*>(&s_v[bf][dc * 8 + e][slot]) = make_uint2(k01, k23);
+          }
+        }
+      }
+      if (tid == 0) {
+        s_valid[bf] = (pid.x >= 0 ? 1 : 0) | (pid.y >= 0 ? 2 : 0) | (pid.z >= 0 ? 4 : 0) |
+                      (pid.w >= 0 ? 8 : 0);
+      }
+    };
+
+    load_tile(k_begin);
+    store_tile(0);
+    __syncthreads();
+    int bf = 0;
+    for (int kt = k_begin;; kt += kBN) {
+      const bool more = kt < last_tile;
+      load_tile(more ? kt + kBN : kt);  // in flight during this tile's math
+      const int vbits = s_valid[bf];
+
+      // S^T for the two 32-key halves of the tile.
+      f32x16_t s[2];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const uint4 a =
+              *reinterpret_cast<const uint4*>(&s_k[bf][sb * 32 + col][kb * 16 + half * 8]);
+          s[sb] = Mfma<T>::mma(a, qreg[kb], s[sb]);
+        }
+      }
+      // Scale (log2 units) and mask: causal, past the context, invalid pages,
+      // past this split.
+      float mx = -INFINITY;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kk = sb * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+          const int ka = kt + kk;
+          const bool ok = ka <= kmax && ka < k_end && ((vbits >> (kk >> 4)) & 1);
+          const float x = ok ? s[sb][i] * p.c : -INFINITY;
+          s[sb][i] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m, mx);
+      const float ms = mn == -INFINITY ? 0.f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m - ms);
+      float rs = 0.f;
+      uint4 pk[4];  // P^T operands of the four 16-key blocks
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        float pr[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          pr[i] = __builtin_amdgcn_exp2f(s[sb][i] - ms);
+          rs += pr[i];
+        }
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2) {
+          const float* v8 = pr + kb2 * 8;
+          pk[sb * 2 + kb2] = make_uint4(Packet<T>::pack2(v8[0], v8[1]), Packet<T>::pack2(v8[2], v8[3]),
+                                        Packet<T>::pack2(v8[4], v8[5]), Packet<T>::pack2(v8[6], v8[7]));
+        }
+      }
+      rs += __shfl_xor(rs, 32, 64);
+      lsum = lsum * alpha + rs;
+      m = mn;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      // O^T += V^T . P^T
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int kq = 0; kq < 4; ++kq) {
+          const uint4 a =
+              *reinterpret_cast<const uint4*>(&s_v[bf][db * 32 + col][kq * 16 + half * 8]);
+          o[db] = Mfma<T>::mma(a, pk[kq], o[db]);
+        }
+
+      if (!more) break;
+      store_tile(bf ^ 1);
+      __syncthreads();
+      bf ^= 1;
+    }
+  }
+
+  if (myrow >= rows) return;
+  // Lane holds O^T rows d = 32*db + 8*(i/4) + 4*half + i%4 of its query.
+  if (p.splits == 1) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    T* dst = reinterpret_cast<T*>(p.out) + ((size_t)t * Hq + qh) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int d0 = db * 32 + i4 * 8 + half * 4;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = o[db][i4 * 4 + e] * inv;
+        if constexpr (sizeof(T) == 2) {
+          uint2 w = make_uint2(Packet<T>::pack2(y[0], y[1]), Packet<T>::pack2(y[2], y[3]));
+          *reinterpret_cast<uint2*>(dst + d0) = w;
+        }
+      }
+  } else {
+    float* rec = p.part + ((size_t)split * p.Tq * Hq + (size_t)t * Hq + qh) * (D + 2);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int d0 = db * 32 + i4 * 8 + half * 4;
+        *reinterpret_cast<float2*>(rec + d0) = make_float2(o[db][i4 * 4], o[db][i4 * 4 + 1]);
+        *reinterpret_cast<float2*>(rec + d0 + 2) =
+            make_float2(o[db][i4 * 4 + 2], o[db][i4 * 4 + 3]);
+      }
+    if (half == 0) {
+      rec[D] = m;
+      rec[D + 1] = lsum;
+    }
+  }
+}
+
+// Log-sum-exp merge of the per-split partials: one thread per output element.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long total = (long long)p.Tq * p.Hq * D;
+  if (idx >= total) return;
+  const long long r = idx / D;
+  const int d = (int)(idx - r * D);
+  const size_t stride = (size_t)p.Tq * p.Hq * (D + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < p.splits; ++s) M = fmaxf(M, p.part[s * stride + r * (D + 2) + D]);
+  const float Ms = M == -INFINITY ? 0.f : M;
+  float L = 0.f, A = 0.f;
+  for (int s = 0; s < p.splits; ++s) {
+    const float* rec = p.part + s * stride + r * (D + 2);
+    const float w = __builtin_amdgcn_exp2f(rec[D] - Ms);
+    L += rec[D + 1] * w;
+    A += rec[d] * w;
+  }
+  reinterpret_cast<T*>(p.out)[idx] = Elem<T>::from_f32(L > 0.f ? A / L : 0.f);
+}
+
+struct PrefillPlan {
+  int row_tiles, splits, split_keys;
+  size_t ws_bytes;
+};
+
+int plan_prefill(int Tq, int ctx_len, int Hq, int Hkv, int D, PrefillPlan* plan) {
+  int cus = 0;
+  const int st = device_cu_count(&cus);
+  if (st) return st;
+  const int G = Hq / Hkv;
+  plan->row_tiles = (Tq * G + kBM - 1) / kBM;
+  const long long base = (long long)plan->row_tiles * Hkv;
+  int s = (int)((2LL * cus + base - 1) / base);
+  const int by_len = (ctx_len + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
+  s = s < by_len ? s : by_len;
+  s = s < kMaxSplits ? s : kMaxSplits;
+  s = s < 1 ? 1 : s;
+  int per = (ctx_len + s - 1) / s;
+  per = (per + kBN - 1) / kBN * kBN;
+  s = (ctx_len + per - 1) / per;  // drop splits left empty by the rounding
+  plan->splits = s;
+  plan->split_keys = per;
+  plan->ws_bytes = s > 1 ? (size_t)s * Tq * Hq * (D + 2) * sizeof(float) : 0;
+  return RLSE_OK;
+}
+
+template <typename T, int D>
+int launch_prefill(PrefillParams& pp, hipStream_t stream) {
+  const int nwg = pp.row_tiles * pp.Hkv * pp.splits;
+  hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(nwg), dim3(kPThreads), 0, stream, pp);
+  int st = launch_status("prefill_kernel");
+  if (st || pp.splits == 1) return st;
+  const long long total = (long long)pp.Tq * pp.Hq * D;
+  hipLaunchKernelGGL((prefill_merge_kernel<T, D>), dim3((unsigned)((total + 255) / 256)),
+                     dim3(256), 0, stream, pp);
+  return launch_status("prefill_merge_kernel");
+}
+
+void* g_pws_ptr[64] = {nullptr};
+size_t g_pws_size[64] = {0};
+
+int validate_prefill(int num_tokens, int ctx_len, int Hq, int Hkv, int D, int mbps,
+                     int num_blocks, int dtype) {
+  if (num_tokens <= 0 || ctx_len < num_tokens)
+    return fail(RLSE_ERR_INVALID_VALUE, "prefill: need 1 <= num_tokens (%d) <= ctx_len (%d)",
+                num_tokens, ctx_len);
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
+    return fail(RLSE_ERR_INVALID_VALUE, "prefill: num_heads %d not a multiple of num_kv_heads %d",
+                Hq, Hkv);
+  if (D != 64 && D != 128)
+    return fail(RLSE_ERR_INVALID_VALUE, "prefill: head_dim %d not in {64, 128}", D);
+  if (dtype != RLSE_DTYPE_BF16 && dtype != RLSE_DTYPE_F16)
+    return fail(RLSE_ERR_INVALID_VALUE, "prefill: dtype %d unsupported (bf16 and f16 only)",
+                dtype);
+  if (mbps <= 0 || num_blocks <= 0 || (long long)mbps * 16 < ctx_len)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "prefill: ctx_len %d exceeds the table's %d blocks of 16 (num_blocks %d)",
+                ctx_len, mbps, num_blocks);
+  if ((long long)num_tokens * Hq > 0x7fffffffLL / 256)
+    return fail(RLSE_ERR_INVALID_VALUE, "prefill: num_tokens * num_heads too large");
+  return RLSE_OK;
+}
+
+}  // namespace
+}  // namespace rlse
+
+using namespace rlse;
+
+extern "C" int rlse_prefill_workspace_size(int num_tokens, int ctx_len, int num_heads,
+                                           int num_kv_heads, int head_dim, size_t* bytes) {
+  if (!bytes) return fail(RLSE_ERR_INVALID_VALUE, "prefill_workspace_size: null output");
+  if (num_tokens <= 0 || ctx_len < num_tokens || num_heads <= 0 || num_kv_heads <= 0 ||
+      num_heads % num_kv_heads != 0 || (head_dim != 64 && head_dim != 128))
+    return fail(RLSE_ERR_INVALID_VALUE, "prefill_workspace_size: bad shape");
+  PrefillPlan plan;
+  const int st = plan_prefill(num_tokens, ctx_len, num_heads, num_kv_heads, head_dim, &plan);
+  if (st) return st;
+  *bytes = plan.ws_bytes;
+  return RLSE_OK;
+}
+
+extern "C" int rlse_prefill_attn(const void* q, const void* k_pool, const void* v_pool,
+                                 const int32_t* block_table, int ctx_len, int num_tokens,
+                                 void* out, int num_heads, int num_kv_heads, int head_dim,
+                                 int max_blocks, int num_blocks, float scale, int dtype,
+                                 void* workspace, size_t workspace_bytes, rlse_stream_t stream) {
+  int st = validate_prefill(num_tokens, ctx_len, num_heads, num_kv_heads, head_dim, max_blocks,
+                            num_blocks, dtype);
+  if (st) return st;
+  if (!q || !k_pool || !v_pool || !block_table || !out)
+    return fail(RLSE_ERR_INVALID_VALUE, "prefill: null pointer argument");
+  if (!(scale > 0.f) || !isfinite(scale))
+    return fail(RLSE_ERR_INVALID_VALUE, "prefill: scale must be finite and positive");
+  PrefillPlan plan;
+  st = plan_prefill(num_tokens, ctx_len, num_heads, num_kv_heads, head_dim, &plan);
+  if (st) return st;
+  if (plan.ws_bytes > 0) {
+    if (workspace == nullptr) {
+      int dev = 0;
+      hipError_t e = hipGetDevice(&dev);
+      if (e != hipSuccess || dev < 0 || dev >= 64)
+        return fail(RLSE_ERR_INVALID_VALUE, "prefill: no current device");
+      if (g_pws_size[dev] < plan.ws_bytes) {
+        if (g_pws_ptr[dev]) (void)hipFree(g_pws_ptr[dev]);
+        g_pws_ptr[dev] = nullptr;
+        g_pws_size[dev] = 0;
+        e = hipMalloc(&g_pws_ptr[dev], plan.ws_bytes);
+        if (e != hipSuccess) return fail((int)e, "prefill: workspace hipMalloc failed");
+        g_pws_size[dev] = plan.ws_bytes;
+      }
+      workspace = g_pws_ptr[dev];
+    } else if (workspace_bytes < plan.ws_bytes) {
+      return fail(RLSE_ERR_BUFFER_TOO_SMALL, "prefill: workspace %zu bytes < %zu needed",
+                  workspace_bytes, plan.ws_bytes);
+    }
+  }
+  PrefillParams pp{};
+  pp.q = q;
+  pp.k_pool = k_pool;
+  pp.v_pool = v_pool;
+  pp.table = block_table;
+  pp.out = out;
+  pp.part = reinterpret_cast<float*>(workspace);
+  pp.Tq = num_tokens;
+  pp.L = ctx_len;
+  pp.offset = ctx_len - num_tokens;
+  pp.Hq = num_heads;
+  pp.Hkv = num_kv_heads;
+  pp.G = num_heads / num_kv_heads;
+  pp.num_blocks = num_blocks;
+  pp.mbps = max_blocks;
+  pp.row_tiles = plan.row_tiles;
+  pp.splits = plan.splits;
+  pp.split_keys = plan.split_keys;
+  pp.c = scale * 1.4426950408889634f;
+  const hipStream_t s = as_stream(stream);
+  if (dtype == RLSE_DTYPE_BF16)
+    return head_dim == 128 ? launch_prefill<bf16, 128>(pp, s) : launch_prefill<bf16, 64>(pp, s);
+  return head_dim == 128 ? launch_prefill<f16, 128>(pp, s) : launch_prefill<f16, 64>(pp, s);
+}

@@ -49,6 +49,7 @@ EXPORTED = (
     "rlse_pool_create", "rlse_pool_destroy", "rlse_pool_layer", "rlse_pool_info",
     "rlse_kv_append", "rlse_kv_gather", "rlse_kv_scatter", "rlse_kv_copy_blocks",
     "rlse_decode_workspace_size", "rlse_paged_gqa_decode", "rlse_decode_step",
+    "rlse_prefill_workspace_size", "rlse_prefill_attn",
     "rlse_rmsnorm", "rlse_rope_tables", "rlse_rope", "rlse_qk_norm_rope_append",
     "launch_rmsnorm_f32", "launch_rmsnorm_f16", "launch_rmsnorm_bf16",
     "launch_paged_gqa_decode_tiled_f32", "launch_paged_gqa_decode_tiled_f16",
@@ -109,6 +110,9 @@ _SIGS = {
                                    _i, _vp, _sz, _vp]),
     "rlse_decode_step": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                               _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp]),
+    "rlse_prefill_workspace_size": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz)]),
+    "rlse_prefill_attn": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp,
+                               _sz, _vp]),
     "rlse_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp]),
     "rlse_rope_tables": (_i, [_d, _i, _i, _i, _vp, _vp]),
     "rlse_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
@@ -382,6 +386,26 @@ def decode_step(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: float, cos_t
         _ptr(block_tables), _ptr(seq_lens), _ptr(out), batch, num_heads, num_kv_heads, head_dim,
         max_blocks_per_seq, num_blocks, scale, _dt(dtype), _ptr(workspace), workspace_bytes,
         _stream(stream)))
+
+
+def prefill_workspace_size(num_tokens: int, ctx_len: int, num_heads: int, num_kv_heads: int,
+                           head_dim: int) -> int:
+    n = _sz(0)
+    _check(load().rlse_prefill_workspace_size(num_tokens, ctx_len, num_heads, num_kv_heads,
+                                              head_dim, ctypes.byref(n)))
+    return n.value
+
+
+def prefill_attn(q, k_pool, v_pool, block_table, ctx_len: int, num_tokens: int, out,
+                 num_heads: int, num_kv_heads: int, head_dim: int, max_blocks: int,
+                 num_blocks: int, scale: float, dtype, workspace=None, workspace_bytes: int = 0,
+                 stream=None) -> None:
+    """Causal attention of a chunk of num_tokens queries (positions
+    ctx_len-num_tokens .. ctx_len-1) over one sequence's paged K/V."""
+    _check(load().rlse_prefill_attn(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_table),
+                                    ctx_len, num_tokens, _ptr(out), num_heads, num_kv_heads,
+                                    head_dim, max_blocks, num_blocks, scale, _dt(dtype),
+                                    _ptr(workspace), workspace_bytes, _stream(stream)))
 
 
 def rmsnorm(x, weight, out, rows: int, n: int, eps: float, dtype, stream=None) -> None:

@@ -51,6 +51,22 @@ def test_decode_rejects_bad_shapes(kv, args):
     assert rc == kv.ERR_INVALID_VALUE
 
 
+@pytest.mark.parametrize("case", [
+    dict(tq=0, L=10, hq=8, hkv=8, d=128, mb=1, dt="bf16"),     # empty chunk
+    dict(tq=20, L=10, hq=8, hkv=8, d=128, mb=1, dt="bf16"),    # chunk longer than context
+    dict(tq=4, L=40, hq=8, hkv=8, d=128, mb=2, dt="bf16"),     # table too short for ctx_len
+    dict(tq=4, L=10, hq=12, hkv=8, d=128, mb=1, dt="bf16"),    # Hq not a multiple of Hkv
+    dict(tq=4, L=10, hq=8, hkv=8, d=96, mb=1, dt="bf16"),      # unsupported head_dim
+    dict(tq=4, L=10, hq=8, hkv=8, d=128, mb=1, dt="f32"),      # MFMA path: bf16/f16 only
+])
+def test_prefill_rejects_bad_arguments(kv, case):
+    lib = kv.load()
+    rc = lib.rlse_prefill_attn(1, 1, 1, 1, case["L"], case["tq"], 1, case["hq"], case["hkv"],
+                               case["d"], case["mb"], 64, 0.088, kv.DTYPE_NAMES[case["dt"]],
+                               None, 0, None)
+    assert rc == kv.ERR_INVALID_VALUE, kv.last_error()
+
+
 def test_prototype_launchers_fail_closed(kv):
     lib = kv.load()
     assert lib.launch_rmsnorm_f32(None, None, None, 0, 1024, 1e-6) != 0
