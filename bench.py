@@ -38,7 +38,23 @@ WORKLOADS = {
     "qwen25": (14, 2, 64, 24, 64, 4096, 4096,
                "Qwen2.5-0.5B high-GQA decode: 14q/2kv heads, d=64, 24 layers, B=64, "
                "4096 cached + 1 appended, bf16, 16-token pages"),
+    "qwen3_8b": (32, 8, 128, 1, 128, 8192, 32768,
+                 "Qwen3-8B long-context decode: 32q/8kv heads, d=128, 1 layer, B=128, "
+                 "cached U[8192,32768] + 1 appended, bf16, 16-token pages"),
 }
+METRIC_NAME = {
+    "qwen3": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen3-0.6B shape, 1 GPU",
+    "qwen25": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen2.5-0.5B shape, 1 GPU",
+    "qwen3_8b": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen3-8B long-context "
+                "shape, 1 GPU",
+}
+# Chunked prefill: (Hq, Hkv, d, chunk tokens, cached tokens before the chunk, description)
+PREFILL = {
+    "qwen3_8b_prefill": (32, 8, 128, 512, 8192,
+                         "Qwen3-8B chunked prefill: 512-token chunk after 8192 cached tokens, "
+                         "32q/8kv heads, d=128, causal, bf16, one layer"),
+}
+PEAK_BF16_TFLOPS = 2500.0  # dense MFMA
 
 
 def parse():
@@ -46,7 +62,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="qwen3", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="qwen3", choices=sorted(WORKLOADS) + sorted(PREFILL))
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -138,6 +154,112 @@ def cpu_baseline(args, lens, hq, hkv, d, layers):
                       f"decode steps of {layers} layers"}
 
 
+def prefill_flops(hq, d, tq, offset):
+    """Algorithmic FLOPs of one causal chunk: query t attends offset+t+1 keys;
+    q.k and p.v are 2*d FLOPs each per (query head, key)."""
+    pairs = tq * offset + tq * (tq + 1) // 2
+    return 4 * d * hq * pairs
+
+
+def prefill_bench(args):
+    """One step = one rlse_prefill_attn call (its merge launch included) for
+    the chunk, inputs resident in HBM; value = algorithmic TFLOP/s."""
+    import numpy as np
+    import torch
+
+    import rlse_kv as kv
+
+    hq, hkv, d, tq, offset, desc = PREFILL[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = offset + tq
+    npages = (L + 15) // 16
+    nb = npages + 64
+    rng = np.random.default_rng(args.seed)
+    table = torch.from_numpy(rng.permutation(nb)[:npages].astype(np.int32)).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    bf = torch.bfloat16
+    kp = torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf)
+    vp = torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf)
+    q = torch.randn((tq, hq, d), generator=g, device=dev, dtype=bf)
+    out = torch.empty_like(q)
+    ws_bytes = kv.prefill_workspace_size(tq, L, hq, hkv, d)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    scale = 1.0 / math.sqrt(d)
+
+    def step():
+        kv.prefill_attn(q, kp, vp, table, L, tq, out, hq, hkv, d, npages, nb, scale, "bf16", ws,
+                        ws_bytes, stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(min(args.steps, 50))]
+    for a, e in ev:
+        a.record(stream)
+        step()
+        e.record(stream)
+    torch.cuda.synchronize()
+    avg_ms = float(np.mean([a.elapsed_time(e) for a, e in ev]))
+    flops = prefill_flops(hq, d, tq, offset)
+    achieved = flops / (avg_ms * 1e-3) / 1e12
+    result = {
+        "metric": "prefill-attn TFLOP/s (% of dense bf16 MFMA peak) at Qwen3-8B chunk, 1 GPU",
+        "value": flops * args.steps / elapsed / 1e12, "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": elapsed * 1e3 / args.steps, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1) q/K/V, seeded random page permutation",
+        "config": {"workload": desc, "chunk": tq, "cached": offset, "q_heads": hq,
+                   "kv_heads": hkv, "head_dim": d, "splits_workspace_bytes": ws_bytes,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "kernel": "prefill_kernel + prefill_merge_kernel (rlse_prefill_attn)",
+                     "flops_per_launch": flops, "avg_launch_ms": avg_ms,
+                     "timed_launches": len(ev)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = prefill_cpu_baseline(args, hq, hkv, d, tq, offset)
+    print(json.dumps(result))
+
+
+def prefill_cpu_baseline(args, hq, hkv, d, tq, offset):
+    """The oracle's orc_prefill_f32 (Candle's CPU op order: per query, dot
+    products, mask, softmax, weighted V sum; OpenMP over all host threads) on
+    the same chunk shape, for a bounded number of KV heads."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    g = hq // hkv
+    L = offset + tq
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((g, tq, d)).astype(np.float32)
+    k = rng.standard_normal((1, L, d)).astype(np.float32)
+    v = rng.standard_normal((1, L, d)).astype(np.float32)
+    threads = O.max_threads()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        O.prefill_f32(q, k, v, offset, 1.0 / math.sqrt(d), threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or n >= hkv:
+            break
+    flops = prefill_flops(g, d, tq, offset) * n
+    return {"value": flops / el / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{n} KV head(s) of the chunk ({g} query heads each, f32) in {el:.2f} s"}
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -147,6 +269,9 @@ def main():
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
+    if args.workload in PREFILL:
+        prefill_bench(args)
+        return
     import numpy as np
     import torch
 
@@ -242,7 +367,7 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     traffic, traffic_src = measured_traffic(args.workload, not args.unfused)
     result = {
-        "metric": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen3-0.6B shape, 1 GPU",
+        "metric": METRIC_NAME[args.workload],
         "value": b * args.steps / elapsed,
         "unit": "tokens/s",
         "n_gpus": 1,
