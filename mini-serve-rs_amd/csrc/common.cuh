@@ -193,4 +193,29 @@ __device__ __forceinline__ float wave_max(float x) {
 
 __device__ __forceinline__ int wave_lane() { return __lane_id(); }
 
+// ---------------------------------------------------------------------------
+// Cross-workgroup hand-off of partial results within one launch.
+// ---------------------------------------------------------------------------
+// Partial records and arrival counters are accessed with device-scope
+// (agent) atomic loads and stores: on gfx950 these carry the sc1 bit, so each
+// access is coherent across the XCDs' L2 caches by itself. A group's record
+// stores are therefore visible device-wide once they complete, and waiting for
+// them (vmcnt(0)) before the counter increment orders them ahead of it -- no
+// whole-L2 writeback or invalidate is needed (a __threadfence() would emit
+// both, once per partial).
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima), fenced
+// against compiler reordering on both sides.
+__device__ __forceinline__ void wait_vm_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+
 }  // namespace rlse

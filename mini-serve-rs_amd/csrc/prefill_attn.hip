@@ -14,8 +14,9 @@
 // head, each wave 32 of them, and streams that head's keys in tiles of 64:
 // the tile's K rows and V (transposed) are staged in LDS once and shared by
 // the 4 waves. When there are too few row tiles to fill the chip, the keys
-// are also split across workgroups and a second kernel merges the per-split
-// (m, l, acc) partials with a log-sum-exp combine. Workgroups are mapped to
+// are also split across workgroups: each publishes its (m, l, acc) partial,
+// and the workgroup arriving last for a row tile merges them with a
+// log-sum-exp combine in the same launch. Workgroups are mapped to
 // work so that consecutive work items -- the row tiles reading the same K/V
 // range -- run on one XCD and share its L2.
 //
@@ -45,6 +46,10 @@ constexpr int kBN = 64;            // keys per tile
 constexpr int kPad = 8;            // LDS row padding (elements): conflict-free 16-byte reads
 constexpr int kMinKeysPerSplit = 512;
 constexpr int kMaxSplits = 16;
+constexpr int kMaxSplitPages = 1024;  // page ids of a split staged in LDS (16384 keys)
+// The running max of a query's softmax moves only when a score exceeds it by
+// more than this many powers of two (probabilities stay below 2^kLazyLog2).
+constexpr float kLazyLog2 = 8.f;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -77,7 +82,8 @@ struct PrefillParams {
   const void* v_pool;
   const int* table;    // [mbps] page ids of the sequence
   void* out;           // [Tq][Hq][D]
-  float* part;         // [S][Tq*Hq][D + 2] partials (S > 1)
+  float* part;         // per-workgroup partial blocks (S > 1), see the kernel's tail
+  int* counters;       // [row_tiles*Hkv] arrivals per (row tile, KV head), zero between launches
   int Tq, L, offset, Hq, Hkv, G, num_blocks, mbps;
   int row_tiles, splits, split_keys;
   float c;  // scale * log2(e)
@@ -96,12 +102,11 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
   constexpr int CPR = D / 8;                  // 16-byte chunks per key row
   constexpr int KPK = kBN * CPR;              // K packets per tile
   constexpr int KPT = KPK / kPThreads;        // per thread
-  constexpr int VIT = (kBN / 4) * CPR;        // V items (4 keys x 8 dims) per tile
-  constexpr int VPT = (VIT + kPThreads - 1) / kPThreads;
   static_assert(KPK % kPThreads == 0, "K tile must split evenly");
   __shared__ __align__(16) uint16_t s_k[2][kBN][D + kPad];   // K rows
   __shared__ __align__(16) uint16_t s_v[2][D][kBN + kPad];   // V^T, keys in MFMA order
   __shared__ int s_valid[2];                                 // page-valid bits of the tile
+  __shared__ __align__(16) int s_pages[kMaxSplitPages];      // the split's page ids (-1: invalid)
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -122,6 +127,8 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
   const int row_c = myrow < rows ? myrow : rows - 1;
   const int t = row_c / G, g = row_c - t * G, qh = h * G + g;
   const int kmax = p.offset + t;  // last key this query sees
+  // Last key every query of this wave sees (its first row has the smallest t).
+  const int kmin_wave = p.offset + min(rt * kBM + wave * 32, rows - 1) / G;
 
   // Keys of this workgroup: up to the last query's diagonal, this split's share.
   const int last_row = min(rows - 1, rt * kBM + kBM - 1);
@@ -132,6 +139,19 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
   const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
   const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
   const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
+
+  // Page ids of this split's keys, staged once (whole 4-page tiles, indices
+  // past the context clamped to its last page).
+  {
+    const int npg = k_begin < k_end ? (((k_end - k_begin + 15) >> 4) + 3) & ~3 : 0;
+    const int plast = (p.L - 1) >> 4;
+    for (int i = tid; i < npg; i += kPThreads) {
+      const int pi = min((k_begin >> 4) + i, plast);
+      const int id = p.table[pi];
+      s_pages[i] = ((unsigned)id < (unsigned)p.num_blocks) ? id : -1;
+    }
+    __syncthreads();
+  }
 
   f32x16_t o[DB];
 #pragma unroll
@@ -148,48 +168,40 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
                                                  half * 8);
 
     const int last_tile = k_begin + ((k_end - 1 - k_begin) / kBN) * kBN;
-    static_assert(kBN == 64, "a tile spans the 4 pages held in pid");
-    u32x4_t kst[KPT], vst[VPT][4];
+    static_assert(kBN == 64 && kPWaves == 4, "a tile spans 4 pages, one per wave");
+    u32x4_t kst[KPT], vst[4];
     int4 pid;  // page ids of the tile's 4 pages (-1: invalid)
-    // Page id of tile page i, invalid ones replaced by page 0 (selects on a
-    // vector value: an indexed register array would live in scratch memory).
+    // Page id of tile page i (wave-uniform i), invalid ones read page 0.
     auto page_of = [&](int i) __attribute__((always_inline)) {
+      i = __builtin_amdgcn_readfirstlane(i);
       const int r = i == 0 ? pid.x : i == 1 ? pid.y : i == 2 ? pid.z : pid.w;
       return r < 0 ? 0 : r;
     };
-    // Global loads of the tile at kt (keys past L clamp to L-1 and are masked
-    // later; invalid page ids read page 0 and are masked).
+    // V copy: wave w copies page w of the tile; lane = (dims chunk dc, group
+    // of 4 keys kgl). Lanes past the row (d = 64) repeat the last chunk and
+    // skip the LDS write.
+    const int v_kgl = lane & 3, v_dc = lane >> 2;
+    const int v_dcl = v_dc < CPR ? v_dc : CPR - 1;
+    // Global loads of the tile at kt. Every address is in bounds: page
+    // indices past the context read the last page and invalid page ids read
+    // page 0; those keys are masked in the math.
     auto load_tile = [&](int kt) __attribute__((always_inline)) {
-      auto table_id = [&](int pg) __attribute__((always_inline)) {
-        int pi = (kt >> 4) + pg;
-        const int plast = (p.L - 1) >> 4;
-        pi = pi < plast ? pi : plast;
-        const int id = p.table[pi];
-        return ((unsigned)id < (unsigned)p.num_blocks) ? id : -1;
-      };
-      pid = make_int4(table_id(0), table_id(1), table_id(2), table_id(3));
+      pid = *reinterpret_cast<const int4*>(&s_pages[(kt - k_begin) >> 4]);
 #pragma unroll
       for (int u = 0; u < KPT; ++u) {
+        // Packet u of this thread: key kk of the tile (its page is
+        // wave-uniform: kk >> 4 = (tid + 256u) / (16 * CPR)), chunk dc.
         const int pk = tid + u * kPThreads;
         const int kk = pk / CPR, dc = pk - kk * CPR;
-        const int ka = min(kt + kk, p.L - 1);
-        const int id = page_of((ka - kt) >> 4);
+        const int id = page_of(kk >> 4);
         kst[u] = *reinterpret_cast<const u32x4_t*>(
-            kp + (((size_t)id * Hkv + h) * 16 + (ka & 15)) * D + dc * 8);
+            kp + (((size_t)id * Hkv + h) * 16 + (kk & 15)) * D + dc * 8);
       }
+      const int vid = page_of(wave);
 #pragma unroll
-      for (int u = 0; u < VPT; ++u) {
-        int it = tid + u * kPThreads;
-        it = it < VIT ? it : VIT - 1;
-        const int kg = it % (kBN / 4), dc = it / (kBN / 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int ka = min(kt + kg * 4 + j, p.L - 1);
-          const int id = page_of((ka - kt) >> 4);
-          vst[u][j] = *reinterpret_cast<const u32x4_t*>(
-              vp + (((size_t)id * Hkv + h) * 16 + (ka & 15)) * D + dc * 8);
-        }
-      }
+      for (int j = 0; j < 4; ++j)
+        vst[j] = *reinterpret_cast<const u32x4_t*>(
+            vp + (((size_t)vid * Hkv + h) * 16 + v_kgl * 4 + j) * D + v_dcl * 8);
     };
     // Staged registers -> LDS buffer bf: K rows as they are, V transposed
     // with each 16-key block's keys in accumulator order.
@@ -200,22 +212,16 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
         const int kk = pk / CPR, dc = pk - kk * CPR;
         *reinterpret_cast<u32x4_t*>(&s_k[bf][kk][dc * 8]) = kst[u];
       }
+      if (v_dc < CPR) {
+        const int slot = wave * 16 + key_slot(v_kgl * 4);
 #pragma unroll
-      for (int u = 0; u < VPT; ++u) {
-        const int it = tid + u * kPThreads;
-        if (it < VIT) {
-          const int kg = it % (kBN / 4), dc = it / (kBN / 4);
-          const int a0 = kg * 4;  // first key of the group, 4-aligned
-          const int slot = (a0 & ~15) + key_slot(a0 & 15);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            // Element e of each of the 4 keys: the low or high half of word e/2.
-            const int wi = e >> 1;
-            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            const uint32_t k01 = __builtin_amdgcn_perm(vst[u][1][wi], vst[u][0][wi], sel);
-            const uint32_t k23 = __builtin_amdgcn_perm(vst[u][3][wi], vst[u][2][wi], sel);
-            *reinterpret_cast<uint2*>(&s_v[bf][dc * 8 + e][slot]) = make_uint2(k01, k23);
-          }
+        for (int e = 0; e < 8; ++e) {
+          // Element e of each of the 4 keys: the low or high half of word e/2.
+          const int wi = e >> 1;
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          const uint32_t k01 = __builtin_amdgcn_perm(vst[1][wi], vst[0][wi], sel);
+          const uint32_t k23 = __builtin_amdgcn_perm(vst[3][wi], vst[2][wi], sel);
+          *reinterpret_cast<uint2*>(&s_v[bf][v_dc * 8 + e][slot]) = make_uint2(k01, k23);
         }
       }
       if (tid == 0) {
@@ -234,36 +240,54 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
       const int vbits = s_valid[bf];
 
       // S^T for the two 32-key halves of the tile.
+      // (The two halves' MFMA chains are interleaved: consecutive MFMAs then
+      // never wait on each other's accumulator.)
       f32x16_t s[2];
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
+      for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
           const uint4 a =
               *reinterpret_cast<const uint4*>(&s_k[bf][sb * 32 + col][kb * 16 + half * 8]);
           s[sb] = Mfma<T>::mma(a, qreg[kb], s[sb]);
         }
+      // Mask (causal, past the split's end, invalid pages) only on tiles that
+      // need it: the test is wave-uniform and most tiles are fully visible.
+      if (!(kt + kBN - 1 <= kmin_wave && kt + kBN <= k_end && vbits == 15)) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kk = sb * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+            const int ka = kt + kk;
+            if (!(ka <= kmax && ka < k_end && ((vbits >> (kk >> 4)) & 1))) s[sb][i] = -INFINITY;
+          }
       }
-      // Scale (log2 units) and mask: causal, past the context, invalid pages,
-      // past this split.
       float mx = -INFINITY;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kk = sb * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-          const int ka = kt + kk;
-          const bool ok = ka <= kmax && ka < k_end && ((vbits >> (kk >> 4)) & 1);
-          const float x = ok ? s[sb][i] * p.c : -INFINITY;
-          s[sb][i] = x;
-          mx = fmaxf(mx, x);
-        }
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sb][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(m, mx);
-      const float ms = mn == -INFINITY ? 0.f : mn;
-      const float alpha = __builtin_amdgcn_exp2f(m - ms);
+      // Online softmax in log2 units (the scale folded into the exponent's
+      // FMA). The running max moves only when a score exceeds it by more
+      // than kLazyLog2, so the accumulator rescale is rare.
+      const float cand = mx * p.c;
+      if (__any(cand > m + kLazyLog2)) {
+        const float mn = fmaxf(m, cand);
+        const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+        lsum *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        m = mn;
+      }
+      const float nms = m == -INFINITY ? 0.f : -m;
       float rs = 0.f;
       uint4 pk[4];  // P^T operands of the four 16-key blocks
 #pragma unroll
@@ -271,7 +295,7 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
         float pr[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          pr[i] = __builtin_amdgcn_exp2f(s[sb][i] - ms);
+          pr[i] = __builtin_amdgcn_exp2f(fmaf(s[sb][i], p.c, nms));
           rs += pr[i];
         }
 #pragma unroll
@@ -282,17 +306,12 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
         }
       }
       rs += __shfl_xor(rs, 32, 64);
-      lsum = lsum * alpha + rs;
-      m = mn;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      lsum += rs;
       // O^T += V^T . P^T
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
+      for (int kq = 0; kq < 4; ++kq)
 #pragma unroll
-        for (int kq = 0; kq < 4; ++kq) {
+        for (int db = 0; db < DB; ++db) {
           const uint4 a =
               *reinterpret_cast<const uint4*>(&s_v[bf][db * 32 + col][kq * 16 + half * 8]);
           o[db] = Mfma<T>::mma(a, pk[kq], o[db]);
@@ -305,67 +324,96 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
     }
   }
 
-  if (myrow >= rows) return;
   // Lane holds O^T rows d = 32*db + 8*(i/4) + 4*half + i%4 of its query.
+  T* dst = reinterpret_cast<T*>(p.out) + ((size_t)t * Hq + qh) * D;
+  auto write_out = [&](const f32x16_t* acc, float inv) __attribute__((always_inline)) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int d0 = db * 32 + i4 * 8 + half * 4;
+        const f32x16_t& y = acc[db];
+        *reinterpret_cast<uint2*>(dst + d0) =
+            make_uint2(Packet<T>::pack2(y[i4 * 4] * inv, y[i4 * 4 + 1] * inv),
+                       Packet<T>::pack2(y[i4 * 4 + 2] * inv, y[i4 * 4 + 3] * inv));
+      }
+  };
   if (p.splits == 1) {
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    T* dst = reinterpret_cast<T*>(p.out) + ((size_t)t * Hq + qh) * D;
+    if (myrow < rows) write_out(o, lsum > 0.f ? 1.f / lsum : 0.f);
+    return;
+  }
+  // Key splits: publish this split's (acc, m, l) for the workgroup's rows;
+  // the workgroup arriving last for this (row tile, KV head) merges them.
+  // Publication is plain vector stores, then one agent-scope release fence
+  // (L2 writeback) ahead of the arrival count; the merging workgroup takes an
+  // agent-scope acquire fence (L1/L2 invalidate) before its plain loads.
+  // A workgroup's partial is stored in its register layout: float4 slot k of
+  // thread tid at blk + (k*256 + tid)*4 floats -- slots 0..4*DB-1 hold acc,
+  // slot 4*DB holds (m, l) -- so every store and load covers 1 KB of
+  // consecutive bytes. All splits of a (row tile, KV head) use the same
+  // thread-to-row map, so the merging workgroup reads its own rows' slots.
+  constexpr int SLOTS = 4 * DB + 1;
+  auto blk_of = [&](int sp) __attribute__((always_inline)) {
+    const size_t wgi = ((size_t)sp * Hkv + h) * p.row_tiles + rt;
+    return reinterpret_cast<float4*>(p.part) + wgi * SLOTS * kPThreads + tid;
+  };
+  {
+    float4* blk = blk_of(split);
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int d0 = db * 32 + i4 * 8 + half * 4;
-        float y[4];
+      for (int i4 = 0; i4 < 4; ++i4)
+        blk[(db * 4 + i4) * kPThreads] =
+            make_float4(o[db][i4 * 4], o[db][i4 * 4 + 1], o[db][i4 * 4 + 2], o[db][i4 * 4 + 3]);
+    blk[4 * DB * kPThreads] = make_float4(m, lsum, 0.f, 0.f);
+  }
+  __syncthreads();
+  __shared__ int s_last;
+  int* counter = p.counters + rt * Hkv + h;
+  if (tid == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             p.splits - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  {
+    float M = -INFINITY;
+    for (int sp = 0; sp < p.splits; ++sp) M = fmaxf(M, blk_of(sp)[4 * DB * kPThreads].x);
+    const float Ms = M == -INFINITY ? 0.f : M;
+    float Lw = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = o[db][i4 * 4 + e] * inv;
-        if constexpr (sizeof(T) == 2) {
-          uint2 w = make_uint2(Packet<T>::pack2(y[0], y[1]), Packet<T>::pack2(y[2], y[3]));
-          *reinterpret_cast<uint2*>(dst + d0) = w;
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+    for (int sp = 0; sp < p.splits; ++sp) {
+      const float4* blk = blk_of(sp);
+      const float4 ml = blk[4 * DB * kPThreads];
+      const float w = __builtin_amdgcn_exp2f(ml.x - Ms);
+      Lw += w * ml.y;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const float4 a = blk[(db * 4 + i4) * kPThreads];
+          o[db][i4 * 4] += w * a.x;
+          o[db][i4 * 4 + 1] += w * a.y;
+          o[db][i4 * 4 + 2] += w * a.z;
+          o[db][i4 * 4 + 3] += w * a.w;
         }
-      }
-  } else {
-    float* rec = p.part + ((size_t)split * p.Tq * Hq + (size_t)t * Hq + qh) * (D + 2);
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int d0 = db * 32 + i4 * 8 + half * 4;
-        *reinterpret_cast<float2*>(rec + d0) = make_float2(o[db][i4 * 4], o[db][i4 * 4 + 1]);
-        *reinterpret_cast<float2*>(rec + d0 + 2) =
-            make_float2(o[db][i4 * 4 + 2], o[db][i4 * 4 + 3]);
-      }
-    if (half == 0) {
-      rec[D] = m;
-      rec[D + 1] = lsum;
     }
+    if (myrow < rows) write_out(o, Lw > 0.f ? 1.f / Lw : 0.f);
   }
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Log-sum-exp merge of the per-split partials: one thread per output element.
-template <typename T, int D>
-__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
-  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long total = (long long)p.Tq * p.Hq * D;
-  if (idx >= total) return;
-  const long long r = idx / D;
-  const int d = (int)(idx - r * D);
-  const size_t stride = (size_t)p.Tq * p.Hq * (D + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < p.splits; ++s) M = fmaxf(M, p.part[s * stride + r * (D + 2) + D]);
-  const float Ms = M == -INFINITY ? 0.f : M;
-  float L = 0.f, A = 0.f;
-  for (int s = 0; s < p.splits; ++s) {
-    const float* rec = p.part + s * stride + r * (D + 2);
-    const float w = __builtin_amdgcn_exp2f(rec[D] - Ms);
-    L += rec[D + 1] * w;
-    A += rec[d] * w;
-  }
-  reinterpret_cast<T*>(p.out)[idx] = Elem<T>::from_f32(L > 0.f ? A / L : 0.f);
-}
-
+// Workspace (key splits only): arrival counters [row_tiles*Hkv] padded to
+// 256 bytes, then the partial records. The counters return to zero at the
+// end of every launch, so a workspace is zero-filled once before first use.
 struct PrefillPlan {
   int row_tiles, splits, split_keys;
-  size_t ws_bytes;
+  size_t counter_bytes, ws_bytes;
 };
 
 int plan_prefill(int Tq, int ctx_len, int Hq, int Hkv, int D, PrefillPlan* plan) {
@@ -379,13 +427,19 @@ int plan_prefill(int Tq, int ctx_len, int Hq, int Hkv, int D, PrefillPlan* plan)
   const int by_len = (ctx_len + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
   s = s < by_len ? s : by_len;
   s = s < kMaxSplits ? s : kMaxSplits;
+  const int by_pages = (ctx_len + kMaxSplitPages * 16 - 1) / (kMaxSplitPages * 16);
+  s = s > by_pages ? s : by_pages;  // a split's page ids must fit the LDS stage
   s = s < 1 ? 1 : s;
   int per = (ctx_len + s - 1) / s;
   per = (per + kBN - 1) / kBN * kBN;
   s = (ctx_len + per - 1) / per;  // drop splits left empty by the rounding
   plan->splits = s;
   plan->split_keys = per;
-  plan->ws_bytes = s > 1 ? (size_t)s * Tq * Hq * (D + 2) * sizeof(float) : 0;
+  plan->counter_bytes = ((size_t)plan->row_tiles * Hkv * sizeof(int) + 255) / 256 * 256;
+  plan->ws_bytes =
+      s > 1 ? plan->counter_bytes + (size_t)s * Hkv * plan->row_tiles * (4 * (D / 32) + 1) *
+                                  kPThreads * 4 * sizeof(float)
+            : 0;
   return RLSE_OK;
 }
 
@@ -393,12 +447,7 @@ template <typename T, int D>
 int launch_prefill(PrefillParams& pp, hipStream_t stream) {
   const int nwg = pp.row_tiles * pp.Hkv * pp.splits;
   hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(nwg), dim3(kPThreads), 0, stream, pp);
-  int st = launch_status("prefill_kernel");
-  if (st || pp.splits == 1) return st;
-  const long long total = (long long)pp.Tq * pp.Hq * D;
-  hipLaunchKernelGGL((prefill_merge_kernel<T, D>), dim3((unsigned)((total + 255) / 256)),
-                     dim3(256), 0, stream, pp);
-  return launch_status("prefill_merge_kernel");
+  return launch_status("prefill_kernel");
 }
 
 void* g_pws_ptr[64] = {nullptr};
@@ -471,6 +520,8 @@ extern "C" int rlse_prefill_attn(const void* q, const void* k_pool, const void* 
         g_pws_size[dev] = 0;
         e = hipMalloc(&g_pws_ptr[dev], plan.ws_bytes);
         if (e != hipSuccess) return fail((int)e, "prefill: workspace hipMalloc failed");
+        e = hipMemset(g_pws_ptr[dev], 0, plan.ws_bytes);
+        if (e != hipSuccess) return fail((int)e, "prefill: workspace hipMemset failed");
         g_pws_size[dev] = plan.ws_bytes;
       }
       workspace = g_pws_ptr[dev];
@@ -485,7 +536,8 @@ extern "C" int rlse_prefill_attn(const void* q, const void* k_pool, const void* 
   pp.v_pool = v_pool;
   pp.table = block_table;
   pp.out = out;
-  pp.part = reinterpret_cast<float*>(workspace);
+  pp.counters = reinterpret_cast<int*>(workspace);
+  pp.part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + plan.counter_bytes);
   pp.Tq = num_tokens;
   pp.L = ctx_len;
   pp.offset = ctx_len - num_tokens;
