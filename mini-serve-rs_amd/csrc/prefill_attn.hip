@@ -170,11 +170,11 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
     const int last_tile = k_begin + ((k_end - 1 - k_begin) / kBN) * kBN;
     static_assert(kBN == 64 && kPWaves == 4, "a tile spans 4 pages, one per wave");
     u32x4_t kst[KPT], vst[4];
-    int4 pid;  // page ids of the tile's 4 pages (-1: invalid)
-    // Page id of tile page i (wave-uniform i), invalid ones read page 0.
-    auto page_of = [&](int i) __attribute__((always_inline)) {
-      i = __builtin_amdgcn_readfirstlane(i);
-      const int r = i == 0 ? pid.x : i == 1 ? pid.y : i == 2 ? pid.z : pid.w;
+    int4 pid;  // page ids of the tile's 4 pages (-1: invalid), for the valid bits
+    // Page id of page i of the tile at kt, read per lane from the staged
+    // table (no branches), invalid ids replaced by page 0.
+    auto page_of = [&](int kt, int i) __attribute__((always_inline)) {
+      const int r = s_pages[((kt - k_begin) >> 4) + i];
       return r < 0 ? 0 : r;
     };
     // V copy: wave w copies page w of the tile; lane = (dims chunk dc, group
@@ -193,11 +193,11 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
         // wave-uniform: kk >> 4 = (tid + 256u) / (16 * CPR)), chunk dc.
         const int pk = tid + u * kPThreads;
         const int kk = pk / CPR, dc = pk - kk * CPR;
-        const int id = page_of(kk >> 4);
+        const int id = page_of(kt, kk >> 4);
         kst[u] = *reinterpret_cast<const u32x4_t*>(
             kp + (((size_t)id * Hkv + h) * 16 + (kk & 15)) * D + dc * 8);
       }
-      const int vid = page_of(wave);
+      const int vid = page_of(kt, wave);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         vst[j] = *reinterpret_cast<const u32x4_t*>(
