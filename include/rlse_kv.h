@@ -171,9 +171,8 @@ int rlse_decode_step(const void* q, const void* k_new, const void* v_new,
  * page list block_table[max_blocks] (ctx_len <= max_blocks*16); keys in
  * pages with ids outside [0, num_blocks) are skipped. out [num_tokens]
  * [num_heads][head_dim]. bf16 and f16 only (MFMA tiles), head_dim 64 or
- * 128. workspace: rlse_prefill_workspace_size bytes (may be 0), zero-filled
- * once before its first use (the kernel leaves its counters at zero), or
- * NULL for a library-owned one per device. */
+ * 128. workspace: rlse_prefill_workspace_size bytes (may be 0), or NULL
+ * for a library-owned one per device. */
 int rlse_prefill_workspace_size(int num_tokens, int ctx_len, int num_heads, int num_kv_heads,
                                 int head_dim, size_t* bytes);
 int rlse_prefill_attn(const void* q, const void* k_pool, const void* v_pool,

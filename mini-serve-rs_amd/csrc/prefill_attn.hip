@@ -14,9 +14,8 @@
 // head, each wave 32 of them, and streams that head's keys in tiles of 64:
 // the tile's K rows and V (transposed) are staged in LDS once and shared by
 // the 4 waves. When there are too few row tiles to fill the chip, the keys
-// are also split across workgroups: each publishes its (m, l, acc) partial,
-// and the workgroup arriving last for a row tile merges them with a
-// log-sum-exp combine in the same launch. Workgroups are mapped to
+// are also split across workgroups: each stores its (m, l, acc) partial and
+// a second launch merges them with a log-sum-exp combine. Workgroups are mapped to
 // work so that consecutive work items -- the row tiles reading the same K/V
 // range -- run on one XCD and share its L2.
 //
@@ -83,11 +82,18 @@ struct PrefillParams {
   const int* table;    // [mbps] page ids of the sequence
   void* out;           // [Tq][Hq][D]
   float* part;         // per-workgroup partial blocks (S > 1), see the kernel's tail
-  int* counters;       // [row_tiles*Hkv] arrivals per (row tile, KV head), zero between launches
   int Tq, L, offset, Hq, Hkv, G, num_blocks, mbps;
   int row_tiles, splits, split_keys;
   float c;  // scale * log2(e)
 };
+
+// The partial block of split sp for (KV head h, row tile rt): (4*D/32 + 1)
+// float4 slots per thread of the workgroup.
+template <int D>
+__device__ __forceinline__ float4* part_block(const PrefillParams& p, int sp, int h, int rt) {
+  const size_t wgi = ((size_t)sp * p.Hkv + h) * p.row_tiles + rt;
+  return reinterpret_cast<float4*>(p.part) + wgi * (4 * (D / 32) + 1) * kPThreads;
+}
 
 // Position of actual key a (0..15) of a 16-key MFMA block in the order the
 // S^T accumulator holds it: lane half h owns keys 4h..4h+3 and 8+4h..11+4h.
@@ -342,78 +348,72 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
     if (myrow < rows) write_out(o, lsum > 0.f ? 1.f / lsum : 0.f);
     return;
   }
-  // Key splits: publish this split's (acc, m, l) for the workgroup's rows;
-  // the workgroup arriving last for this (row tile, KV head) merges them.
-  // Publication is plain vector stores, then one agent-scope release fence
-  // (L2 writeback) ahead of the arrival count; the merging workgroup takes an
-  // agent-scope acquire fence (L1/L2 invalidate) before its plain loads.
-  // A workgroup's partial is stored in its register layout: float4 slot k of
-  // thread tid at blk + (k*256 + tid)*4 floats -- slots 0..4*DB-1 hold acc,
-  // slot 4*DB holds (m, l) -- so every store and load covers 1 KB of
-  // consecutive bytes. All splits of a (row tile, KV head) use the same
-  // thread-to-row map, so the merging workgroup reads its own rows' slots.
-  constexpr int SLOTS = 4 * DB + 1;
-  auto blk_of = [&](int sp) __attribute__((always_inline)) {
-    const size_t wgi = ((size_t)sp * Hkv + h) * p.row_tiles + rt;
-    return reinterpret_cast<float4*>(p.part) + wgi * SLOTS * kPThreads + tid;
-  };
-  {
-    float4* blk = blk_of(split);
+  // Key splits: store this split's (acc, m, l) for the workgroup's rows in
+  // its register layout -- float4 slot k of thread tid at
+  // blk + (k*256 + tid)*4 floats, slots 0..4*DB-1 holding acc and slot 4*DB
+  // (m, l) -- so every store covers 1 KB of consecutive bytes. The merge
+  // launch reads them back with the same thread-to-row map.
+  float4* blk = part_block<D>(p, split, h, rt) + tid;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4)
-        blk[(db * 4 + i4) * kPThreads] =
-            make_float4(o[db][i4 * 4], o[db][i4 * 4 + 1], o[db][i4 * 4 + 2], o[db][i4 * 4 + 3]);
-    blk[4 * DB * kPThreads] = make_float4(m, lsum, 0.f, 0.f);
-  }
-  __syncthreads();
-  __shared__ int s_last;
-  int* counter = p.counters + rt * Hkv + h;
-  if (tid == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             p.splits - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  {
-    float M = -INFINITY;
-    for (int sp = 0; sp < p.splits; ++sp) M = fmaxf(M, blk_of(sp)[4 * DB * kPThreads].x);
-    const float Ms = M == -INFINITY ? 0.f : M;
-    float Lw = 0.f;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-    for (int sp = 0; sp < p.splits; ++sp) {
-      const float4* blk = blk_of(sp);
-      const float4 ml = blk[4 * DB * kPThreads];
-      const float w = __builtin_amdgcn_exp2f(ml.x - Ms);
-      Lw += w * ml.y;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const float4 a = blk[(db * 4 + i4) * kPThreads];
-          o[db][i4 * 4] += w * a.x;
-          o[db][i4 * 4 + 1] += w * a.y;
-          o[db][i4 * 4 + 2] += w * a.z;
-          o[db][i4 * 4 + 3] += w * a.w;
-        }
-    }
-    if (myrow < rows) write_out(o, Lw > 0.f ? 1.f / Lw : 0.f);
-  }
-  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i4 = 0; i4 < 4; ++i4)
+      blk[(db * 4 + i4) * kPThreads] =
+          make_float4(o[db][i4 * 4], o[db][i4 * 4 + 1], o[db][i4 * 4 + 2], o[db][i4 * 4 + 3]);
+  blk[4 * DB * kPThreads] = make_float4(m, lsum, 0.f, 0.f);
 }
 
-// Workspace (key splits only): arrival counters [row_tiles*Hkv] padded to
-// 256 bytes, then the partial records. The counters return to zero at the
-// end of every launch, so a workspace is zero-filled once before first use.
+// Log-sum-exp merge of the key splits: one workgroup per (row tile, KV
+// head), thread tid combining the slots thread tid of every split stored.
+template <typename T, int D>
+__global__ __launch_bounds__(kPThreads) void prefill_merge_kernel(PrefillParams p) {
+  constexpr int DB = D / 32;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, half = lane >> 5, col = lane & 31;
+  const int rt = blockIdx.x % p.row_tiles, h = blockIdx.x / p.row_tiles;
+  const int G = p.G, Hq = p.Hq;
+  const int rows = p.Tq * G;
+  const int myrow = rt * kBM + wave * 32 + col;
+  if (myrow >= rows) return;
+  const int t = myrow / G, qh = h * G + (myrow - (myrow / G) * G);
+  float M = -INFINITY;
+  for (int sp = 0; sp < p.splits; ++sp)
+    M = fmaxf(M, (part_block<D>(p, sp, h, rt) + tid)[4 * DB * kPThreads].x);
+  const float Ms = M == -INFINITY ? 0.f : M;
+  float Lw = 0.f;
+  float acc[DB * 16];
+#pragma unroll
+  for (int i = 0; i < DB * 16; ++i) acc[i] = 0.f;
+  for (int sp = 0; sp < p.splits; ++sp) {
+    const float4* blk = part_block<D>(p, sp, h, rt) + tid;
+    const float4 ml = blk[4 * DB * kPThreads];
+    const float w = __builtin_amdgcn_exp2f(ml.x - Ms);
+    Lw += w * ml.y;
+#pragma unroll
+    for (int k = 0; k < 4 * DB; ++k) {
+      const float4 a = blk[k * kPThreads];
+      acc[k * 4] += w * a.x;
+      acc[k * 4 + 1] += w * a.y;
+      acc[k * 4 + 2] += w * a.z;
+      acc[k * 4 + 3] += w * a.w;
+    }
+  }
+  const float inv = Lw > 0.f ? 1.f / Lw : 0.f;
+  T* dst = reinterpret_cast<T*>(p.out) + ((size_t)t * Hq + qh) * D;
+#pragma unroll
+  for (int k = 0; k < 4 * DB; ++k) {
+    // slot k = (db, i4): dims 32*db + 8*i4 + 4*half .. +3
+    const int d0 = (k >> 2) * 32 + (k & 3) * 8 + half * 4;
+    *reinterpret_cast<uint2*>(dst + d0) =
+        make_uint2(Packet<T>::pack2(acc[k * 4] * inv, acc[k * 4 + 1] * inv),
+                   Packet<T>::pack2(acc[k * 4 + 2] * inv, acc[k * 4 + 3] * inv));
+  }
+}
+
+// Workspace (key splits only): the partial blocks of every workgroup.
 struct PrefillPlan {
   int row_tiles, splits, split_keys;
-  size_t counter_bytes, ws_bytes;
+  size_t ws_bytes;
 };
 
 int plan_prefill(int Tq, int ctx_len, int Hq, int Hkv, int D, PrefillPlan* plan) {
@@ -435,11 +435,9 @@ int plan_prefill(int Tq, int ctx_len, int Hq, int Hkv, int D, PrefillPlan* plan)
   s = (ctx_len + per - 1) / per;  // drop splits left empty by the rounding
   plan->splits = s;
   plan->split_keys = per;
-  plan->counter_bytes = ((size_t)plan->row_tiles * Hkv * sizeof(int) + 255) / 256 * 256;
-  plan->ws_bytes =
-      s > 1 ? plan->counter_bytes + (size_t)s * Hkv * plan->row_tiles * (4 * (D / 32) + 1) *
-                                  kPThreads * 4 * sizeof(float)
-            : 0;
+  plan->ws_bytes = s > 1 ? (size_t)s * Hkv * plan->row_tiles * (4 * (D / 32) + 1) * kPThreads *
+                               4 * sizeof(float)
+                         : 0;
   return RLSE_OK;
 }
 
@@ -447,7 +445,11 @@ template <typename T, int D>
 int launch_prefill(PrefillParams& pp, hipStream_t stream) {
   const int nwg = pp.row_tiles * pp.Hkv * pp.splits;
   hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(nwg), dim3(kPThreads), 0, stream, pp);
-  return launch_status("prefill_kernel");
+  const int st = launch_status("prefill_kernel");
+  if (st || pp.splits == 1) return st;
+  hipLaunchKernelGGL((prefill_merge_kernel<T, D>), dim3(pp.row_tiles * pp.Hkv), dim3(kPThreads),
+                     0, stream, pp);
+  return launch_status("prefill_merge_kernel");
 }
 
 void* g_pws_ptr[64] = {nullptr};
@@ -520,8 +522,6 @@ extern "C" int rlse_prefill_attn(const void* q, const void* k_pool, const void* 
         g_pws_size[dev] = 0;
         e = hipMalloc(&g_pws_ptr[dev], plan.ws_bytes);
         if (e != hipSuccess) return fail((int)e, "prefill: workspace hipMalloc failed");
-        e = hipMemset(g_pws_ptr[dev], 0, plan.ws_bytes);
-        if (e != hipSuccess) return fail((int)e, "prefill: workspace hipMemset failed");
         g_pws_size[dev] = plan.ws_bytes;
       }
       workspace = g_pws_ptr[dev];
@@ -536,8 +536,7 @@ extern "C" int rlse_prefill_attn(const void* q, const void* k_pool, const void* 
   pp.v_pool = v_pool;
   pp.table = block_table;
   pp.out = out;
-  pp.counters = reinterpret_cast<int*>(workspace);
-  pp.part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + plan.counter_bytes);
+  pp.part = reinterpret_cast<float*>(workspace);
   pp.Tq = num_tokens;
   pp.L = ctx_len;
   pp.offset = ctx_len - num_tokens;
