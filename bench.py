@@ -55,6 +55,17 @@ PREFILL = {
                          "32q/8kv heads, d=128, causal, bf16, one layer"),
 }
 PEAK_BF16_TFLOPS = 2500.0  # dense MFMA
+# Prefix fork: (Hq, Hkv, d, layers, batch, prefix tokens, suffix lo, suffix hi, description)
+FORK = {
+    "qwen3_fork": (16, 8, 128, 28, 64, 1024, 64, 512,
+                   "Qwen3-0.6B prefix-fork decode: 64 sequences forked from one 1024-token "
+                   "prefix (refcounted pages), private suffixes U[64,512] + 1 appended, 16q/8kv "
+                   "heads, d=128, 28 layers, bf16"),
+    "qwen3_fork1030": (16, 8, 128, 28, 64, 1030, 64, 512,
+                       "Qwen3-0.6B prefix-fork decode: 64 sequences forked from one 1030-token "
+                       "prefix (refcounted pages + copy-on-write of the partial page), private "
+                       "suffixes U[64,512] + 1 appended, 16q/8kv heads, d=128, 28 layers, bf16"),
+}
 
 
 def parse():
@@ -62,7 +73,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="qwen3", choices=sorted(WORKLOADS) + sorted(PREFILL))
+    ap.add_argument("--workload", default="qwen3",
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(FORK))
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -260,6 +272,139 @@ def prefill_cpu_baseline(args, hq, hkv, d, tq, offset):
             "sample": f"{n} KV head(s) of the chunk ({g} query heads each, f32) in {el:.2f} s"}
 
 
+def fork_bench(args):
+    """Prefix fork: one prefix held in refcounted pages of a pool handle (all
+    layers in one allocation, one block id spanning the layers), 64 requests
+    forked from it by the block manager (full pages shared, the trailing
+    partial page copied on write), each with a private suffix. The fork runs
+    once per request and is timed on its own; one step = one rlse_decode_step
+    per layer for the 64 forked sequences (append of the new token + decode
+    over shared prefix pages and private suffix pages)."""
+    import numpy as np
+    import torch
+
+    import rlse_kv as kv
+
+    hq, hkv, d, layers, b, plen, lo, hi, desc = FORK[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rng = np.random.default_rng(args.seed)
+    suffix = rng.integers(lo, hi + 1, b).astype(np.int32)
+    lens = plen + suffix + 1  # keys after this step's append
+    nb = (plen + 15) // 16 + int(sum((int(n) + 15) // 16 - plen // 16 for n in lens)) + 64
+    bf = torch.bfloat16
+    pool = kv.KVPool(layers, nb, hkv, d, "bf16")
+    stride = pool.layer_stride_elems
+    k0, v0 = pool.layer(0)
+    bm = kv.BlockManager(nb)
+    bm.allocate("prefix", plen)
+    ptable = torch.tensor(bm.block_table("prefix"), dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    pk = torch.randn((layers, hkv, plen, d), generator=g, device=dev, dtype=bf)
+    pv = torch.randn((layers, hkv, plen, d), generator=g, device=dev, dtype=bf)
+    kv.kv_scatter(pk, pv, k0, v0, stride, layers, ptable, 0, plen, hkv, d, nb, "bf16")
+    del pk, pv
+    torch.cuda.synchronize()
+    # Fork every request from the prefix (host block manager + one device
+    # copy of the partial pages), timed.
+    t0 = time.perf_counter()
+    src, dst = [], []
+    for i in range(b):
+        for sp, dp in bm.fork("prefix", f"r{i}", plen):
+            src.append(sp)
+            dst.append(dp)
+    if src:
+        kv.kv_copy_blocks(k0, v0, stride, layers, torch.tensor(src, dtype=torch.int32, device=dev),
+                          torch.tensor(dst, dtype=torch.int32, device=dev), len(src), hkv, d, nb,
+                          "bf16")
+    torch.cuda.synchronize()
+    fork_ms = (time.perf_counter() - t0) * 1e3
+    # Private suffix pages and their cached K/V.
+    for i in range(b):
+        while len(bm.block_table(f"r{i}")) * 16 < int(lens[i]):
+            bm.allocate_block(f"r{i}")
+    mbps = max(len(bm.block_table(f"r{i}")) for i in range(b))
+    tables = np.zeros((b, mbps), np.int32)
+    for i in range(b):
+        t = bm.block_table(f"r{i}")
+        tables[i, :len(t)] = t
+    t_dev = torch.from_numpy(tables).to(dev)
+    for i in range(b):
+        n = int(suffix[i])
+        sk = torch.randn((layers, hkv, n, d), generator=g, device=dev, dtype=bf)
+        sv = torch.randn((layers, hkv, n, d), generator=g, device=dev, dtype=bf)
+        kv.kv_scatter(sk, sv, k0, v0, stride, layers, t_dev[i], plen, n, hkv, d, nb, "bf16")
+    q_in = [torch.randn((b, hq, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
+    k_in = [torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
+    v_in = [torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
+    qw = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf)
+    kw = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf)
+    max_pos = mbps * 16
+    cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, "bf16")
+    cos_t = torch.frombuffer(bytearray(cos_b), dtype=torch.int16).to(dev).view(bf)
+    sin_t = torch.frombuffer(bytearray(sin_b), dtype=torch.int16).to(dev).view(bf)
+    lens_dev = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    out = torch.empty((b, hq, d), device=dev, dtype=bf)
+    ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    scale = 1.0 / math.sqrt(d)
+    ptrs = [pool.layer(layer) for layer in range(layers)]
+
+    def step(evs=None):
+        for layer in range(layers):
+            if evs is not None:
+                evs[layer][0].record(stream)
+            kv.decode_step(q_in[layer], k_in[layer], v_in[layer], qw, kw, 1e-6, cos_t, sin_t,
+                           max_pos, ptrs[layer][0], ptrs[layer][1], t_dev, lens_dev, out, b, hq,
+                           hkv, d, mbps, nb, scale, "bf16", ws, ws_bytes, stream)
+            if evs is not None:
+                evs[layer][1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ev_steps = min(args.steps, 50)
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(layers)] for _ in range(ev_steps)]
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    avg_ms = float(np.mean([a.elapsed_time(z) for e in evs for a, z in e]))
+    row = 2 * hkv * d * 2  # K+V bytes of one token
+    extra = 2 * b * hq * d * 2 + sum(((int(n) + 15) // 16) * 4 for n in lens) + 4 * b + \
+        2 * b * row + b * d * 2 + 2 * d * 2
+    compulsory = plen * row + int(sum(int(n) - plen for n in lens)) * row + extra
+    logical = int(sum(int(n) for n in lens)) * row + extra
+    achieved = compulsory / (avg_ms * 1e-3) / 1e9
+    result = {
+        "metric": "prefix-fork decode tokens/sec and compulsory HBM GB/s at Qwen3-0.6B shape, "
+                  "1 GPU",
+        "value": b * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": elapsed * 1e3 / args.steps,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1) prefix/suffix K/V and q, block-manager page placement",
+        "config": {"workload": desc, "batch": b, "layers": layers, "prefix": plen,
+                   "mean_keys": float(np.mean(lens)), "fork_ms": fork_ms,
+                   "cow_pages_per_layer": len(src), "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "kernel": "decode_kernel fused step (rlse_decode_step)",
+                     "bytes_per_launch": compulsory, "logical_bytes_per_launch": logical,
+                     "effective_GBps": logical / (avg_ms * 1e-3) / 1e9,
+                     "avg_launch_ms": avg_ms, "timed_launches": ev_steps * layers},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result))
+    pool.close()
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -271,6 +416,9 @@ def main():
         sys.exit(2)
     if args.workload in PREFILL:
         prefill_bench(args)
+        return
+    if args.workload in FORK:
+        fork_bench(args)
         return
     import numpy as np
     import torch

@@ -182,3 +182,101 @@ def test_prefix_fork_copy_on_write_is_bit_exact(kv, prefix_len):
     np.testing.assert_array_equal(to_host(ko), pk)
     np.testing.assert_array_equal(to_host(vo), pv)
     pool.close()
+
+
+@pytest.mark.parametrize("prefix_len", [1024, 1030])
+def test_forked_decode_step_equals_private_copies(kv, prefix_len):
+    """Config-4 step at reduced batch: decode steps over forked sequences
+    (prefix pages shared by refcount, partial page copied on write) give
+    bit-for-bit the output of the same step over private copies of every
+    sequence, the appended tokens land in private pages, and the shared
+    prefix bytes stay unchanged."""
+    import math
+    rng = np.random.default_rng(404)
+    layers, hq, hkv, d, dtype, b = 2, 16, 8, 128, "bf16", 6
+    suffix = rng.integers(20, 90, b).astype(np.int32)
+    lens = prefix_len + suffix + 1
+    nb = 600  # the private-copy layout alone needs b * ceil(lens/16) pages
+    bf = torch.bfloat16
+    pa = kv.KVPool(layers, nb, hkv, d, dtype)   # forked layout
+    pb = kv.KVPool(layers, nb, hkv, d, dtype)   # private copies
+    stride = pa.layer_stride_elems
+    ka0, va0 = pa.layer(0)
+    kb0, vb0 = pb.layer(0)
+    bma, bmb = kv.BlockManager(nb), kv.BlockManager(nb)
+    pk = random_values(rng, (layers, hkv, prefix_len, d), dtype)
+    pv = random_values(rng, (layers, hkv, prefix_len, d), dtype)
+    bma.allocate("prefix", prefix_len)
+    ptab = np.array(bma.block_table("prefix"), np.int32)
+    kv.kv_scatter(to_dev(pk, dtype), to_dev(pv, dtype), ka0, va0, stride, layers, to_dev(ptab), 0,
+                  prefix_len, hkv, d, nb, dtype)
+    pairs = []
+    for i in range(b):
+        pairs += bma.fork("prefix", f"r{i}", prefix_len)
+        while len(bma.block_table(f"r{i}")) * 16 < int(lens[i]):
+            bma.allocate_block(f"r{i}")
+        bmb.allocate(f"r{i}", int(lens[i]))
+    assert len(pairs) == (b if prefix_len % 16 else 0)
+    if pairs:
+        kv.kv_copy_blocks(ka0, va0, stride, layers, to_dev(np.array([p[0] for p in pairs], np.int32)),
+                          to_dev(np.array([p[1] for p in pairs], np.int32)), len(pairs), hkv, d,
+                          nb, dtype)
+    mbps = max(len(bma.block_table(f"r{i}")) for i in range(b))
+    ta = np.zeros((b, mbps), np.int32)
+    tb = np.zeros((b, mbps), np.int32)
+    sks, svs = [], []
+    for i in range(b):
+        a_t, b_t = bma.block_table(f"r{i}"), bmb.block_table(f"r{i}")
+        ta[i, :len(a_t)] = a_t
+        tb[i, :len(b_t)] = b_t
+        n = int(suffix[i])
+        sk = random_values(rng, (layers, hkv, n, d), dtype)
+        sv = random_values(rng, (layers, hkv, n, d), dtype)
+        sks.append(sk)
+        svs.append(sv)
+        kv.kv_scatter(to_dev(sk, dtype), to_dev(sv, dtype), ka0, va0, stride, layers,
+                      to_dev(ta[i]), prefix_len, n, hkv, d, nb, dtype)
+        kv.kv_scatter(to_dev(np.concatenate([pk, sk], axis=2), dtype),
+                      to_dev(np.concatenate([pv, sv], axis=2), dtype), kb0, vb0, stride, layers,
+                      to_dev(tb[i]), 0, prefix_len + n, hkv, d, nb, dtype)
+    max_pos = mbps * 16
+    cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, dtype)
+    cos_t = torch.frombuffer(bytearray(cos_b), dtype=torch.int16).to(DEV).view(bf)
+    sin_t = torch.frombuffer(bytearray(sin_b), dtype=torch.int16).to(DEV).view(bf)
+    lens_dev = to_dev(lens.astype(np.int32))
+    qw = to_dev(random_values(rng, (d,), dtype), dtype)
+    kw = to_dev(random_values(rng, (d,), dtype), dtype)
+    scale = 1 / math.sqrt(d)
+    tad, tbd = to_dev(ta), to_dev(tb)
+    for layer in range(layers):
+        q = to_dev(random_values(rng, (b, hq, d), dtype), dtype)
+        kn = to_dev(random_values(rng, (b, hkv, d), dtype), dtype)
+        vn = to_dev(random_values(rng, (b, hkv, d), dtype), dtype)
+        outs = []
+        for (k0, v0), tab in (((ka0, va0), tad), ((kb0, vb0), tbd)):
+            kl, vl = k0 + layer * stride * 2, v0 + layer * stride * 2
+            out = torch.empty((b, hq, d), dtype=bf, device=DEV)
+            print(f"fork decode step layer {layer} prefix {prefix_len}", flush=True)
+            kv.decode_step(q, kn, vn, qw, kw, 1e-6, cos_t, sin_t, max_pos, kl, vl, tab, lens_dev,
+                           out, b, hq, hkv, d, mbps, nb, scale, dtype)
+            outs.append(to_host(out))
+        np.testing.assert_array_equal(outs[0], outs[1])
+    # every sequence reads back identically from both layouts
+    for i in range(b):
+        n = int(lens[i])
+        got = []
+        for (k0, v0), tab in (((ka0, va0), ta), ((kb0, vb0), tb)):
+            ko = torch.empty((layers, hkv, n, d), dtype=bf, device=DEV)
+            vo = torch.empty_like(ko)
+            kv.kv_gather(k0, v0, stride, layers, to_dev(tab[i]), n, ko, vo, hkv, d, nb, dtype)
+            got.append((to_host(ko), to_host(vo)))
+        np.testing.assert_array_equal(got[0][0], got[1][0])
+        np.testing.assert_array_equal(got[0][1], got[1][1])
+    # the shared prefix is untouched by the forks' appends
+    ko = torch.empty((layers, hkv, prefix_len, d), dtype=bf, device=DEV)
+    vo = torch.empty_like(ko)
+    kv.kv_gather(ka0, va0, stride, layers, to_dev(ptab), prefix_len, ko, vo, hkv, d, nb, dtype)
+    np.testing.assert_array_equal(to_host(ko), pk)
+    np.testing.assert_array_equal(to_host(vo), pv)
+    pa.close()
+    pb.close()
