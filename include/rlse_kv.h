@@ -294,6 +294,62 @@ int rlse_bm_block_table(const rlse_block_manager* bm, const char* request_id,
 int rlse_bm_refcount(const rlse_block_manager* bm, int block);
 int rlse_bm_stats(const rlse_block_manager* bm, rlse_cache_stats* out);
 
+/* ------------------------------------------------------------------ */
+/* Prefix cache over refcounted pages: successor of PrefixCache        */
+/* (src/cache/prefix_cache.rs:58-394). Same chained SHA-256 chunk keys */
+/* (:98-124), LRU refresh and eviction, lookup / lookup_kv / insert /  */
+/* insert_kv rules and counters; a chunk holding KV keeps references  */
+/* on its prefix's pages instead of a contiguous copy. Destroy the     */
+/* cache before its block manager. Host only.                          */
+/* ------------------------------------------------------------------ */
+typedef struct rlse_prefix_cache rlse_prefix_cache;
+typedef struct rlse_prefix_stats {
+  long long hits, misses, tokens_saved; /* record_reuse counters (:368-380) */
+  long long kv_evictions;               /* evicted chunks that held KV      */
+  long long chunks, held_pages;         /* cached chunks, page references   */
+  float hit_rate;                       /* percent, as hit_rate (:382-389)  */
+} rlse_prefix_stats;
+
+/* chunk_size: tokens per chunk, a multiple of the block manager's block size. */
+int rlse_pc_create(rlse_block_manager* bm, int chunk_size, int max_chunks,
+                   rlse_prefix_cache** out);
+/* Releases every page reference the cache holds. */
+int rlse_pc_destroy(rlse_prefix_cache* pc);
+/* compute_chunk_hashes (:98-124): 64 hex digits + NUL per whole chunk. */
+int rlse_pc_chunk_hashes(const uint32_t* tokens, long long num_tokens, int chunk_size,
+                         char* out_hex, int capacity, int* num_chunks);
+/* lookup (:126-155): matched tokens of the leading cached chunks. */
+int rlse_pc_lookup(rlse_prefix_cache* pc, const uint32_t* tokens, long long num_tokens,
+                   long long* matched_tokens);
+/* insert (:198-203): metadata-only chunks. */
+int rlse_pc_insert(rlse_prefix_cache* pc, const uint32_t* tokens, long long num_tokens);
+/* insert_kv (:250-345): KV for every chunk boundary of tokens, from the
+ * pages request_id holds (its first chunk_end/block_size pages); the chunk
+ * ending exactly at num_tokens records the caller's logits handle when
+ * has_logits. No bytes are copied. */
+int rlse_pc_insert_kv(rlse_prefix_cache* pc, const uint32_t* tokens, long long num_tokens,
+                      const char* request_id, int has_logits, long long logits_handle);
+/* lookup_kv (:157-196): tokens covered by the longest cached chunk with KV;
+ * has_logits / logits_handle only when that chunk ends at num_tokens. */
+int rlse_pc_lookup_kv(rlse_prefix_cache* pc, const uint32_t* tokens, long long num_tokens,
+                      long long* matched_tokens, int* has_logits, long long* logits_handle);
+/* Restore of a prefix into child_id (the snapshot copy of set_kv_snapshot,
+ * src/backends/candle.rs:437-478, 557-574): the child receives the cached
+ * pages of the first restore_tokens tokens (<= the lookup_kv match), full
+ * pages shared by refcount; a trailing partial page is copied on write --
+ * one (src, dst) pair for rlse_kv_copy_blocks. */
+int rlse_pc_fork(rlse_prefix_cache* pc, const uint32_t* tokens, long long num_tokens,
+                 long long restore_tokens, const char* child_id, int32_t* cow_src,
+                 int32_t* cow_dst, int cow_capacity, int* num_cow);
+/* Evicts least recently used chunks until the block manager has at least
+ * min_free_blocks free (the memory-pressure eviction of reserve_memory,
+ * :216-232); RLSE_ERR_CACHE_PRESSURE if the cache empties first. */
+int rlse_pc_reclaim(rlse_prefix_cache* pc, int min_free_blocks, int* evicted);
+int rlse_pc_clear(rlse_prefix_cache* pc);
+/* record_reuse (:368-376). */
+int rlse_pc_record_reuse(rlse_prefix_cache* pc, long long skipped_tokens);
+int rlse_pc_stats(const rlse_prefix_cache* pc, rlse_prefix_stats* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,9 @@ EXPORTED = (
     "rlse_bm_create", "rlse_bm_destroy", "rlse_bm_blocks_needed", "rlse_bm_free_count",
     "rlse_bm_allocate", "rlse_bm_allocate_block", "rlse_bm_release", "rlse_bm_fork",
     "rlse_bm_block_table", "rlse_bm_refcount", "rlse_bm_stats",
+    "rlse_pc_create", "rlse_pc_destroy", "rlse_pc_chunk_hashes", "rlse_pc_lookup",
+    "rlse_pc_insert", "rlse_pc_insert_kv", "rlse_pc_lookup_kv", "rlse_pc_fork",
+    "rlse_pc_reclaim", "rlse_pc_clear", "rlse_pc_record_reuse", "rlse_pc_stats",
 )
 
 
@@ -77,6 +80,24 @@ class _CacheStats(ctypes.Structure):
     _fields_ = [("total_blocks", ctypes.c_int), ("allocated_blocks", ctypes.c_int),
                 ("free_blocks", ctypes.c_int), ("utilization", ctypes.c_float),
                 ("fragmentation", ctypes.c_float)]
+
+
+class _PrefixStats(ctypes.Structure):
+    _fields_ = [("hits", ctypes.c_longlong), ("misses", ctypes.c_longlong),
+                ("tokens_saved", ctypes.c_longlong), ("kv_evictions", ctypes.c_longlong),
+                ("chunks", ctypes.c_longlong), ("held_pages", ctypes.c_longlong),
+                ("hit_rate", ctypes.c_float)]
+
+
+@dataclass
+class PrefixStats:
+    hits: int
+    misses: int
+    tokens_saved: int
+    kv_evictions: int
+    chunks: int
+    held_pages: int
+    hit_rate: float
 
 
 @dataclass
@@ -135,6 +156,19 @@ _SIGS = {
     "rlse_bm_block_table": (_i, [_vp, _cp, _ip, _i, ctypes.POINTER(_i)]),
     "rlse_bm_refcount": (_i, [_vp, _i]),
     "rlse_bm_stats": (_i, [_vp, ctypes.POINTER(_CacheStats)]),
+    "rlse_pc_create": (_i, [_vp, _i, _i, ctypes.POINTER(_vp)]),
+    "rlse_pc_destroy": (_i, [_vp]),
+    "rlse_pc_chunk_hashes": (_i, [_vp, _ll, _i, ctypes.c_char_p, _i, ctypes.POINTER(_i)]),
+    "rlse_pc_lookup": (_i, [_vp, _vp, _ll, ctypes.POINTER(_ll)]),
+    "rlse_pc_insert": (_i, [_vp, _vp, _ll]),
+    "rlse_pc_insert_kv": (_i, [_vp, _vp, _ll, _cp, _i, _ll]),
+    "rlse_pc_lookup_kv": (_i, [_vp, _vp, _ll, ctypes.POINTER(_ll), ctypes.POINTER(_i),
+                               ctypes.POINTER(_ll)]),
+    "rlse_pc_fork": (_i, [_vp, _vp, _ll, _ll, _cp, _ip, _ip, _i, ctypes.POINTER(_i)]),
+    "rlse_pc_reclaim": (_i, [_vp, _i, ctypes.POINTER(_i)]),
+    "rlse_pc_clear": (_i, [_vp]),
+    "rlse_pc_record_reuse": (_i, [_vp, _ll]),
+    "rlse_pc_stats": (_i, [_vp, ctypes.POINTER(_PrefixStats)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -275,6 +309,94 @@ class BlockManager:
         _check(self._lib.rlse_bm_stats(self._h, ctypes.byref(s)))
         return CacheStats(s.total_blocks, s.allocated_blocks, s.free_blocks, s.utilization,
                           s.fragmentation)
+
+
+def _tokens(tokens):
+    arr = (ctypes.c_uint32 * max(len(tokens), 1))(*[int(t) & 0xffffffff for t in tokens])
+    return arr, len(tokens)
+
+
+class PrefixCache:
+    """PrefixCache (src/cache/prefix_cache.rs) over refcounted pages of a
+    BlockManager: chained SHA-256 chunk keys and LRU as the reference; a
+    chunk with KV holds references on its prefix's pages (no copies)."""
+
+    def __init__(self, bm: BlockManager, chunk_size: int = BLOCK_SIZE, max_chunks: int = 512):
+        lib = load()
+        h = _vp()
+        _check(lib.rlse_pc_create(bm._h, chunk_size, max_chunks, ctypes.byref(h)))
+        self._h, self._lib, self._bm = h, lib, bm
+        self.chunk_size = chunk_size
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.rlse_pc_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def compute_chunk_hashes(tokens, chunk_size: int) -> List[str]:
+        arr, n = _tokens(tokens)
+        cnt = _i()
+        _check(load().rlse_pc_chunk_hashes(arr, n, chunk_size, None, 0, ctypes.byref(cnt)))
+        buf = ctypes.create_string_buffer(65 * max(cnt.value, 1))
+        _check(load().rlse_pc_chunk_hashes(arr, n, chunk_size, buf, cnt.value, ctypes.byref(cnt)))
+        return [buf.raw[65 * i:65 * i + 64].decode() for i in range(cnt.value)]
+
+    def lookup(self, tokens) -> int:
+        arr, n = _tokens(tokens)
+        m = _ll()
+        _check(self._lib.rlse_pc_lookup(self._h, arr, n, ctypes.byref(m)))
+        return m.value
+
+    def insert(self, tokens) -> None:
+        arr, n = _tokens(tokens)
+        _check(self._lib.rlse_pc_insert(self._h, arr, n))
+
+    def insert_kv(self, tokens, request_id: str, logits_handle: Optional[int] = None) -> None:
+        arr, n = _tokens(tokens)
+        _check(self._lib.rlse_pc_insert_kv(self._h, arr, n, request_id.encode(),
+                                           0 if logits_handle is None else 1,
+                                           0 if logits_handle is None else logits_handle))
+
+    def lookup_kv(self, tokens) -> Tuple[int, Optional[int]]:
+        """(matched tokens, logits handle or None)."""
+        arr, n = _tokens(tokens)
+        m, has, handle = _ll(), _i(), _ll()
+        _check(self._lib.rlse_pc_lookup_kv(self._h, arr, n, ctypes.byref(m), ctypes.byref(has),
+                                           ctypes.byref(handle)))
+        return m.value, (handle.value if has.value else None)
+
+    def fork(self, tokens, restore_tokens: int, child_id: str) -> List[Tuple[int, int]]:
+        """Restores restore_tokens cached tokens into child_id; returns the
+        copy-on-write (src, dst) page pairs for rlse_kv_copy_blocks."""
+        arr, n = _tokens(tokens)
+        src, dst, cnt = (ctypes.c_int32 * 1)(), (ctypes.c_int32 * 1)(), _i()
+        _check(self._lib.rlse_pc_fork(self._h, arr, n, restore_tokens, child_id.encode(), src,
+                                      dst, 1, ctypes.byref(cnt)))
+        return [(src[i], dst[i]) for i in range(cnt.value)]
+
+    def reclaim(self, min_free_blocks: int) -> int:
+        n = _i()
+        _check(self._lib.rlse_pc_reclaim(self._h, min_free_blocks, ctypes.byref(n)))
+        return n.value
+
+    def clear(self) -> None:
+        _check(self._lib.rlse_pc_clear(self._h))
+
+    def record_reuse(self, skipped_tokens: int) -> None:
+        _check(self._lib.rlse_pc_record_reuse(self._h, skipped_tokens))
+
+    def stats(self) -> PrefixStats:
+        st = _PrefixStats()
+        _check(self._lib.rlse_pc_stats(self._h, ctypes.byref(st)))
+        return PrefixStats(st.hits, st.misses, st.tokens_saved, st.kv_evictions, st.chunks,
+                           st.held_pages, st.hit_rate)
 
 
 # --------------------------------------------------------------------------

@@ -359,3 +359,97 @@ class KVCacheModel:
             return np.float32(math.floor(abs(float(x)) + 0.5) * (1 if x >= 0 else -1)) \
                 / np.float32(1000.0)
         return (self.total, allocated, free, float(r3(util)), float(r3(min(frag, 1.0))))
+
+
+# ---------------------------------------------------------------------------
+# PrefixCache (src/cache/prefix_cache.rs:58-394), pure Python
+# ---------------------------------------------------------------------------
+class PrefixCacheModel:
+    """Chunk keys, LRU order and the lookup / insert / insert_kv / lookup_kv
+    rules of the reference's PrefixCache, with a chunk's KV reduced to a flag
+    and an optional logits handle (the memory budget is not modelled: page
+    references need no new memory)."""
+
+    def __init__(self, chunk_size: int, max_chunks: int):
+        self.cs = chunk_size
+        self.max = max_chunks
+        self.chunks = {}  # key -> {"kv": bool, "logits": handle or None}
+        self.lru = []     # keys, least recently used first
+        self.hits = self.misses = self.tokens_saved = self.kv_evictions = 0
+
+    @staticmethod
+    def chunk_hashes(tokens, chunk_size):
+        """compute_chunk_hashes (:98-124): key_i = sha256(key_{i-1} hex ||
+        tokens of chunk i as little-endian u32), hex encoded."""
+        import hashlib
+        out, prev = [], ""
+        for i in range(len(tokens) // chunk_size):
+            h = hashlib.sha256()
+            if prev:
+                h.update(prev.encode())
+            for t in tokens[i * chunk_size:(i + 1) * chunk_size]:
+                h.update(int(t).to_bytes(4, "little"))
+            prev = h.hexdigest()
+            out.append(prev)
+        return out
+
+    def _touch(self, k):
+        self.lru.remove(k)
+        self.lru.append(k)
+
+    def _evict_oldest(self):
+        k = self.lru.pop(0)
+        if self.chunks.pop(k)["kv"]:
+            self.kv_evictions += 1
+
+    def _add(self, k, kv, logits):
+        while len(self.chunks) >= self.max:
+            self._evict_oldest()
+        self.chunks[k] = {"kv": kv, "logits": logits}
+        self.lru.append(k)
+
+    def lookup(self, tokens):
+        m = 0
+        for k in self.chunk_hashes(tokens, self.cs):
+            if k not in self.chunks:
+                break
+            m += 1
+            self._touch(k)
+        return m * self.cs
+
+    def insert(self, tokens):
+        if self.max == 0:
+            return
+        for k in self.chunk_hashes(tokens, self.cs):
+            if k not in self.chunks:
+                self._add(k, False, None)
+
+    def insert_kv(self, tokens, logits=None):
+        if self.max == 0:
+            return
+        for i, k in enumerate(self.chunk_hashes(tokens, self.cs)):
+            offer = logits is not None and (i + 1) * self.cs == len(tokens)
+            c = self.chunks.get(k)
+            if c is not None and c["kv"] and (not offer or c["logits"] is not None):
+                continue
+            if c is not None:
+                del self.chunks[k]
+                self.lru.remove(k)
+            self._add(k, True, logits if offer else None)
+
+    def lookup_kv(self, tokens):
+        best, best_key = 0, None
+        for i, k in enumerate(self.chunk_hashes(tokens, self.cs)):
+            if k in self.chunks:
+                if self.chunks[k]["kv"]:
+                    best, best_key = (i + 1) * self.cs, k
+                self._touch(k)
+        logits = self.chunks[best_key]["logits"] if best_key and best == len(tokens) else None
+        return best, logits
+
+    def record_reuse(self, skipped):
+        if skipped == 0:
+            self.misses += 1
+        else:
+            self.hits += 1
+            self.tokens_saved += skipped

@@ -280,3 +280,60 @@ def test_forked_decode_step_equals_private_copies(kv, prefix_len):
     np.testing.assert_array_equal(to_host(vo), pv)
     pa.close()
     pb.close()
+
+
+def test_prefix_cache_restore_reads_back_the_cached_prefix(kv):
+    """A prompt's KV cached through the prefix cache (page references, no
+    copy) and restored into a new request after the original request is gone:
+    the restored tokens read back byte for byte, a restore ending mid-page
+    copies that page, and appends to the restored request leave the cached
+    pages untouched."""
+    rng = np.random.default_rng(77)
+    layers, nb, hkv, d, dtype = 3, 64, 8, 128, "bf16"
+    pool = kv.KVPool(layers, nb, hkv, d, dtype)
+    k0, v0 = pool.layer(0)
+    stride = pool.layer_stride_elems
+    bm = kv.BlockManager(nb)
+    cache = kv.PrefixCache(bm, 16, 64)
+    prompt = rng.integers(0, 30000, 70).tolist()
+    table = np.array(bm.allocate("a", 70), np.int32)
+    ka = random_values(rng, (layers, hkv, 70, d), dtype)
+    va = random_values(rng, (layers, hkv, 70, d), dtype)
+    kv.kv_scatter(to_dev(ka, dtype), to_dev(va, dtype), k0, v0, stride, layers, to_dev(table), 0,
+                  70, hkv, d, nb, dtype)
+    cache.insert_kv(prompt, "a")
+    bm.release("a")
+    assert cache.lookup_kv(prompt)[0] == 64
+    for child, restore in [("b", 64), ("c", 63), ("d", 40)]:
+        print(f"restore {restore} tokens into {child}", flush=True)
+        cow = cache.fork(prompt, restore, child)
+        assert len(cow) == (1 if restore % 16 else 0)
+        if cow:
+            kv.kv_copy_blocks(k0, v0, stride, layers, to_dev(np.array([cow[0][0]], np.int32)),
+                              to_dev(np.array([cow[0][1]], np.int32)), 1, hkv, d, nb, dtype)
+        ctab = np.array(bm.block_table(child), np.int32)
+        ko = torch.empty((layers, hkv, restore, d), dtype=torch.bfloat16, device=DEV)
+        vo = torch.empty_like(ko)
+        kv.kv_gather(k0, v0, stride, layers, to_dev(ctab), restore, ko, vo, hkv, d, nb, dtype)
+        np.testing.assert_array_equal(to_host(ko), ka[:, :, :restore])
+        np.testing.assert_array_equal(to_host(vo), va[:, :, :restore])
+        # the restored request appends its next token into its own page
+        while len(bm.block_table(child)) * 16 < restore + 1:
+            bm.allocate_block(child)
+        ctab = np.array(bm.block_table(child), np.int32)
+        nk = random_values(rng, (1, hkv, d), dtype)
+        for layer in range(layers):
+            kv.kv_append(to_dev(nk, dtype), to_dev(nk, dtype), k0 + layer * stride * 2,
+                         v0 + layer * stride * 2, to_dev(ctab), 1,
+                         to_dev(np.zeros(1, np.int32)), to_dev(np.array([restore], np.int32)), 1,
+                         hkv, d, len(ctab), nb, dtype)
+    # the cached pages still hold the original prompt
+    cow = cache.fork(prompt, 64, "z")
+    ztab = np.array(bm.block_table("z"), np.int32)
+    ko = torch.empty((layers, hkv, 64, d), dtype=torch.bfloat16, device=DEV)
+    vo = torch.empty_like(ko)
+    kv.kv_gather(k0, v0, stride, layers, to_dev(ztab), 64, ko, vo, hkv, d, nb, dtype)
+    np.testing.assert_array_equal(to_host(ko), ka[:, :, :64])
+    np.testing.assert_array_equal(to_host(vo), va[:, :, :64])
+    cache.close()
+    pool.close()
