@@ -411,7 +411,7 @@ def main():
         copy_calibration()
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+        print(f"bench.py measures one GPU only (the library has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
     if args.workload in PREFILL:

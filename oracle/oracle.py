@@ -1,8 +1,9 @@
 """Oracle for the KV-cache hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use this
-module, and only as the checker (or the timed CPU baseline). The product path
-(librlse_kv.so and its binding) never imports it.
+module, and only as the reference results are compared with (or the timed
+CPU baseline). The product path (librlse_kv.so and its binding) never
+imports it.
 
 Two layers:
 

@@ -2,8 +2,9 @@
  * rlse_oracle.c -- CPU restatement of the reference's KV-cache hot path, as
  * its Candle CPU backend evaluates it.
  *
- * TEST INFRASTRUCTURE ONLY. This file is the checker for the HIP kernels and
- * the timed CPU baseline of bench.py; no product code links or calls it.
+ * TEST INFRASTRUCTURE ONLY. The tests compare the HIP kernels with this
+ * file, which is also the timed CPU baseline of bench.py; no product code
+ * links or calls it.
  *
  * Every function cites the reference code it restates. Arithmetic is f32 in
  * the reference's op order (matmul as a sequential dot product, then the

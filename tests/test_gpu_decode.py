@@ -84,7 +84,7 @@ def test_group_sizes_and_ragged_lengths(kv, dtype, hq, hkv, d):
     check(f"G={hq // hkv} d={d}", as_f32(got, dtype), want, dtype)
 
 
-def test_config1_qwen3_f32_decode_step(kv):
+def test_qwen3_f32_single_sequence_decode_step(kv):
     """Single-layer Qwen3-0.6B decode step, f32, batch 1: 16 query heads, 8 KV
     heads, head_dim 128, 512 cached tokens; q and the new k go through
     q_norm/k_norm (eps 1e-6, weights 1 + 0.1 N(0,1)) and RoPE (theta 1e6) at
@@ -133,7 +133,7 @@ def test_config1_qwen3_f32_decode_step(kv):
     np.testing.assert_allclose(to_host(q_rot)[0], q_o, rtol=2e-6, atol=2e-6)
     got = run_decode(kv, q_rot, kp, vp, tables, np.array([cached + 1], np.int32), hq, hkv, d,
                      "f32", scale)
-    check("config1", got, want, "f32")
+    check("qwen3 f32 B=1 L=513", got, want, "f32")
 
 
 @pytest.mark.parametrize("hq,hkv,d,batch,lmin,lmax", [
@@ -268,7 +268,7 @@ def _rope_tables_dev(kv, theta, d, max_pos, dtype):
 @pytest.mark.parametrize("dtype,hq,hkv,d,norm,lens", [
     ("bf16", 16, 8, 128, True, [1, 2, 16, 17, 300, 513, 2049, 1000, 31]),   # Qwen3-0.6B
     ("bf16", 14, 2, 64, False, [5, 4097, 100, 16, 33]),                       # Qwen2.5, no qk-norm
-    ("f32", 16, 8, 128, True, [513]),                                          # config-1 shape
+    ("f32", 16, 8, 128, True, [513]),                                          # Qwen3 f32, one sequence of 513 keys
     ("f16", 32, 8, 128, True, [70, 1, 900]),                                   # Qwen3-8B heads
 ])
 def test_fused_decode_step_matches_two_kernel_path_and_oracle(kv, dtype, hq, hkv, d, norm, lens):

@@ -127,7 +127,7 @@ def test_pool_handle_scatter_gather_round_trip(kv, dtype):
 
 @pytest.mark.parametrize("prefix_len", [1024, 1030])
 def test_prefix_fork_copy_on_write_is_bit_exact(kv, prefix_len):
-    """Config-4 semantics at reduced size: a shared prefix held by refcounted
+    """Prefix-fork semantics at reduced size: a shared prefix held by refcounted
     blocks, forks with copy-on-write of the trailing partial block, per-fork
     suffix appends; every fork must read back exactly "copy the prefix snapshot
     into a fresh buffer, then append" and the prefix must stay untouched."""
@@ -186,7 +186,7 @@ def test_prefix_fork_copy_on_write_is_bit_exact(kv, prefix_len):
 
 @pytest.mark.parametrize("prefix_len", [1024, 1030])
 def test_forked_decode_step_equals_private_copies(kv, prefix_len):
-    """Config-4 step at reduced batch: decode steps over forked sequences
+    """Prefix-fork decode step at reduced batch: decode steps over forked sequences
     (prefix pages shared by refcount, partial page copied on write) give
     bit-for-bit the output of the same step over private copies of every
     sequence, the appended tokens land in private pages, and the shared
