@@ -209,6 +209,14 @@ __device__ __forceinline__ void st_dev(float* p, float v) {
 __device__ __forceinline__ float ld_dev(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Four dwords as a native vector (element-wise copies, no memcpy).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+// Word 3 of a raw buffer descriptor on gfx9-family targets: 32-bit data
+// format, no swizzle, no index stride. A raw buffer load whose byte offset
+// is at or past the descriptor's record count returns zeros without
+// accessing memory.
+constexpr int kBufferWord3 = 0x00020000;
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima), fenced
 // against compiler reordering on both sides.
 __device__ __forceinline__ void wait_vm_stores() {

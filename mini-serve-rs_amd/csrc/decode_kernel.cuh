@@ -259,15 +259,21 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   constexpr int NPART = 2 * kWaves;
   constexpr int DPL = (D + 63) / 64;  // output dims per lane in the row epilogue
   constexpr int QR = q_stage_rows<T, D, G>();
-  // Register buffers per wave: three blocks in flight for 16-bit K/V, two
-  // for f32 (whose blocks take twice the registers).
-  constexpr int kNumBufs = sizeof(T) == 2 ? 3 : 2;
-  constexpr int kPreIssued = kNumBufs - 1;  // blocks issued before the prologue's appends
+  // Two register buffers per wave: one block loading while one is computed.
+  // With 2 * kWaves waves per compute unit that is enough bytes in flight to
+  // keep HBM streaming; deeper buffering only lengthens the memory queues,
+  // which the publication chain at the end of the launch then waits behind.
+  constexpr int kPreIssued = 1;  // blocks issued before the prologue's appends
+  // Appended rows per wave kept in LDS: the blocks of a wave's first kNewCap
+  // appends take the new row from there, so their loads never wait for the
+  // append stores.
+  constexpr int kNewCap = sizeof(T) == 2 ? 4 : 2;
+  static_assert(kNewCap >= kPreIssued, "pre-issued blocks must find their new rows in LDS");
   extern __shared__ int s_pref[];             // [B + 1]; fused step: then s_len[B]
   __shared__ float s_part[NPART][G][D + 2];   // wave partials: acc[D], m, l per head
   __shared__ int s_part_row[NPART];           // their rows (-1 = unused)
   __shared__ uint4 s_q[kWaves][QR][G][LPR];   // staged query packets per wave
-  __shared__ uint4 s_new[FUSED ? kWaves : 1][kPreIssued][2][LPR];  // appended k, v rows
+  __shared__ uint4 s_new[FUSED ? kWaves : 1][FUSED ? kNewCap : 1][2][LPR];  // appended k, v rows
 
   const int tid = threadIdx.x;
   // The wave index and everything derived from LDS-held prefixes below are
@@ -455,24 +461,34 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     // Fused step: the new token of every row whose last block lies in this
     // wave's range is appended by this wave (k_norm + RoPE of k, raw v), as
     // that block is read by this wave only. The first kPreIssued blocks are
-    // issued before the appends are stored and take the new row from LDS
-    // (s_new); the appends have completed (vmcnt(0)) before any later block
-    // is issued, and the compute unit's write-through L1 shows them to its
-    // loads. A pass appends up to RPL rows, one per lane group.
+    // issued before the appends are stored. The wave's first kNewCap appends
+    // (in stream order) also go to LDS (s_new) and their blocks take the new
+    // row from there whenever they are loaded, so no load waits for an append
+    // store. A wave with more appends waits for its stores (vmcnt(0)) before
+    // issuing any later block -- the compute unit's write-through L1 then shows
+    // them to its loads -- and only blocks issued after that wait can hold an
+    // append past the first kNewCap. A pass appends up to RPL rows, one per
+    // lane group.
     uint64_t amask = 0;
-    int a_src = -1;
+    int a_src = -1, a_slot = -1;
+    int a_ord = 0;  // appends started so far (wave-uniform)
     uint4 a_k, a_v, a_c, a_s, a_w;  // one pass's loads (append_load)
     auto append_load = [&]() __attribute__((always_inline)) {
-      int src = -1;
+      int src = -1, ord = -1;
 #pragma unroll
       for (int i = 0; i < RPL; ++i) {
         if (amask) {
           const int k = __builtin_ctzll(amask);
           amask &= amask - 1;
-          if (rsub == i) src = k;
+          if (rsub == i) {
+            src = k;
+            ord = a_ord;
+          }
+          ++a_ord;
         }
       }
       a_src = src;
+      a_slot = ord;
       // Lane groups without a row load lane 0's (a valid block of the chunk)
       // and store nothing.
       const int sl = src >= 0 ? src : 0;
@@ -494,9 +510,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
         const size_t dst = (((size_t)id * Hkv + kvh) * 16 + (pos & 15)) * D + (size_t)col * EPL;
         *reinterpret_cast<uint4*>(const_cast<T*>(kp) + dst) = kr;
         *reinterpret_cast<uint4*>(const_cast<T*>(vp) + dst) = a_v;
-        if (cbase == 0 && a_src < kPreIssued) {
-          s_new[wave][a_src][0][col] = kr;
-          s_new[wave][a_src][1][col] = a_v;
+        if (a_slot < kNewCap) {
+          s_new[wave][a_slot][0][col] = kr;
+          s_new[wave][a_slot][1][col] = a_v;
         }
       }
     };
@@ -529,12 +545,23 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
           }
         }
         if (nblk > 64) load_chunk(0);
-        wait_vm_stores();
+        if (a_ord > kNewCap) wait_vm_stores();
       }
     };
 
     int issued_row = -1;
+    int n_last = 0;  // last blocks of rows issued so far = their append ordinal
+    const int voff = (int)(lane_off * sizeof(T));
+    // Block j of the wave's range (j >= nblk: past the end, never computed).
+    // The loads are issued for every j, as raw buffer loads through a
+    // descriptor of the block's tile: a block past the end or on an invalid
+    // page gets a descriptor of zero records, which returns zeros without a
+    // memory access. With loads under a branch instead the compiler cannot
+    // count the loads in flight and waits for every earlier block before
+    // reusing a buffer's registers, which would serialize the pipeline.
     auto issue = [&](Buf<T, D>& bf, int j) __attribute__((always_inline)) {
+      const bool real = j < nblk;
+      j = real ? j : nblk - 1;
       if (j - cbase >= 64) load_chunk(cbase + 64);
       const int k = j - cbase;
       const int id = __builtin_amdgcn_readlane(d_id, k);
@@ -545,17 +572,26 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       bf.nvalid = nv;
       bf.row = row;
       bf.newrow = row != issued_row;
-      bf.sub = (FUSED && (nvf & 256) && j < kPreIssued) ? j : -1;
-      issued_row = row;
-      // The loads are issued for every block, a skipped one (invalid page id)
-      // reading page 0 instead: with loads under a branch the compiler cannot
-      // count the loads in flight and waits for every earlier block before
-      // reusing a buffer's registers, which would serialize the pipeline.
-      const size_t base = ((size_t)(nv > 0 ? id : 0) * Hkv + kvh) * tile + lane_off;
+      const bool row_end = FUSED && (nvf & 256);
+      bf.sub = (row_end && n_last < kNewCap) ? n_last : -1;
+      if (real) {
+        if (row_end) ++n_last;
+        issued_row = row;
+      }
+      const bool fetch = real && nv > 0;
+      const size_t tb = ((size_t)(fetch ? id : 0) * Hkv + kvh) * tile;
+      const int nrec = fetch ? (int)(tile * sizeof(T)) : 0;
+      const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kp + tb), 0, nrec,
+                                                        kBufferWord3);
+      const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vp + tb), 0, nrec,
+                                                        kBufferWord3);
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        bf.k[r] = *reinterpret_cast<const uint4*>(kp + base + (size_t)r * RPL * D);
-        bf.v[r] = *reinterpret_cast<const uint4*>(vp + base + (size_t)r * RPL * D);
+        const int o = voff + r * RPL * D * (int)sizeof(T);
+        const u32x4_t kx = __builtin_amdgcn_raw_buffer_load_b128(rk, o, 0, 0);
+        const u32x4_t vx = __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, 0);
+        bf.k[r] = make_uint4(kx.x, kx.y, kx.z, kx.w);
+        bf.v[r] = make_uint4(vx.x, vx.y, vx.z, vx.w);
       }
     };
 
@@ -643,7 +679,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
         vr[r] = bf.v[r];
       }
       if constexpr (FUSED) {
-        if (bf.sub >= 0) {  // the new token (slot nv-1) was appended after this load issued
+        if (bf.sub >= 0) {  // the new token (slot nv-1) may not be stored yet: take it from LDS
           const int slot = nv - 1;
           if (rsub == slot % RPL) {
             const uint4 kn = s_new[wave][bf.sub][0][col], vn = s_new[wave][bf.sub][1][col];
@@ -738,37 +774,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       }
     };
 
-    // kNumBufs blocks in flight: kNumBufs-1 are loading while one is
-    // computed (indices past the end re-load the last block, never computed).
-    const int last = nblk - 1;
-    if constexpr (kNumBufs == 3) {
-      Buf<T, D> b0, b1, b2;
-      issue(b0, 0);
-      issue(b1, last < 1 ? last : 1);
-      after_pre_issue();
-      for (int i = 0;;) {
-        issue(b2, i + 2 < last ? i + 2 : last);
-        compute(b0);
-        if (++i == nblk) break;
-        issue(b0, i + 2 < last ? i + 2 : last);
-        compute(b1);
-        if (++i == nblk) break;
-        issue(b1, i + 2 < last ? i + 2 : last);
-        compute(b2);
-        if (++i == nblk) break;
-      }
-    } else {
-      Buf<T, D> b0, b1;
-      issue(b0, 0);
-      after_pre_issue();
-      for (int i = 0;;) {
-        issue(b1, i + 1 < last ? i + 1 : last);
-        compute(b0);
-        if (++i == nblk) break;
-        issue(b0, i + 1 < last ? i + 1 : last);
-        compute(b1);
-        if (++i == nblk) break;
-      }
+    // The next block is issued before the current one is computed (an index
+    // past the end loads nothing and is never computed).
+    Buf<T, D> b0, b1;
+    issue(b0, 0);
+    after_pre_issue();
+    for (int i = 0;;) {
+      issue(b1, i + 1);
+      compute(b0);
+      if (++i == nblk) break;
+      issue(b0, i + 1);
+      compute(b1);
+      if (++i == nblk) break;
     }
     finalize();
   }

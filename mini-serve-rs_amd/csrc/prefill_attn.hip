@@ -53,10 +53,9 @@ constexpr float kLazyLog2 = 8.f;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-// Staging type for 16-byte packets: a native vector, so copies are vector
-// loads and stores (HIP's uint4 struct is copied with memcpy, which keeps an
-// array of them in scratch memory when it is later written to LDS).
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+// 16-byte packets are staged as u32x4_t, a native vector, so copies are
+// vector loads and stores (HIP's uint4 struct is copied with memcpy, which
+// keeps an array of them in scratch memory when it is later written to LDS).
 
 template <typename T>
 struct Mfma;
