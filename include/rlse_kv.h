@@ -133,7 +133,8 @@ int rlse_decode_workspace_size(int batch, int num_heads, int num_kv_heads, int h
 /* Split-K decode in one launch. workspace may be NULL, in which case a
  * library-owned per-device workspace is used (allocated and zero-filled on
  * first need). A caller workspace must be zero-filled once before its first
- * use; every launch leaves it zero-filled again (per-row arrival counters).
+ * use; every launch leaves it zero-filled again (the group that merges a
+ * partial record clears it).
  * Launches that share a workspace must be ordered (same stream). */
 int rlse_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                           const int32_t* block_tables, const int32_t* seq_lens, void* out,

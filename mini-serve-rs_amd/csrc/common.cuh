@@ -196,17 +196,15 @@ __device__ __forceinline__ int wave_lane() { return __lane_id(); }
 // ---------------------------------------------------------------------------
 // Cross-workgroup hand-off of partial results within one launch.
 // ---------------------------------------------------------------------------
-// Partial records and arrival counters are accessed with device-scope
-// (agent) atomic loads and stores: on gfx950 these carry the sc1 bit, so each
-// access is coherent across the XCDs' L2 caches by itself. A group's record
-// stores are therefore visible device-wide once they complete, and waiting for
-// them (vmcnt(0)) before the counter increment orders them ahead of it -- no
-// whole-L2 writeback or invalidate is needed (a __threadfence() would emit
-// both, once per partial).
-__device__ __forceinline__ void st_dev(float* p, float v) {
+// Partial records are written and read as single 32-bit words with
+// device-scope (agent) atomic stores and loads: on gfx950 these carry the sc1
+// bit, so each access is coherent across the XCDs' L2 caches by itself and a
+// word is seen whole or not at all -- no whole-L2 writeback or invalidate is
+// needed (a __threadfence() would emit both).
+__device__ __forceinline__ void st_word(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_dev(const float* p) {
+__device__ __forceinline__ uint32_t ld_word(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Four dwords as a native vector (element-wise copies, no memcpy).

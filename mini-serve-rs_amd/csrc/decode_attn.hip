@@ -22,13 +22,11 @@ static int decode_groups(int* W) {
   return RLSE_OK;
 }
 
-// Workspace: a fixed region of kMaxDecodeRows arrival counters, then two
-// partial records per workgroup. The counter region does not depend on the
-// call's shape, so one zero-filled workspace stays valid across calls of any
-// batch.
-static size_t decode_counter_bytes() { return (size_t)kMaxDecodeRows * sizeof(int); }
+// Workspace: two partial records per workgroup. Every launch leaves the
+// records zero (each is cleared by the group that reads it), so one
+// zero-filled workspace stays valid across calls of any shape.
 static size_t decode_ws_bytes(int W, int G, int D) {
-  return decode_counter_bytes() + (size_t)W * 2 * (size_t)rec_floats(G, D) * sizeof(float);
+  return (size_t)W * 2 * (size_t)rec_floats(G, D) * sizeof(uint32_t);
 }
 
 template <typename T, int D, bool FUSED>
@@ -154,8 +152,7 @@ static int prepare_decode(DecodeParams& p, const void* q, const void* k_pool,
   p.tables = block_tables;
   p.seq_lens = seq_lens;
   p.out = out;
-  p.counters = reinterpret_cast<int*>(workspace);
-  p.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + decode_counter_bytes());
+  p.ws = reinterpret_cast<uint32_t*>(workspace);
   p.B = batch;
   p.Hkv = num_kv_heads;
   p.mbps = max_blocks_per_seq;

@@ -15,10 +15,14 @@
 // the G heads. A row that lies wholly inside a wave's share is finished by the
 // wave; pieces of rows cut between waves are parked in LDS and combined after
 // one barrier at the end; rows cut by the group's range boundary leave one
-// (m, l, acc) partial per group in the workspace, and the group that finishes
-// such a row last (a per-row arrival counter) merges the partials with a
-// log-sum-exp combine in the same launch. The counters return to zero after
-// every launch, so a workspace only needs zero-filling once, before first use.
+// (m, l, acc) partial per earlier group in the workspace, and the group
+// holding the row's last block merges them with a log-sum-exp combine in the
+// same launch, taking each partial as soon as all of its words have arrived
+// (record words are self-validating: 0 = not written). Groups are dispatched
+// in index order and the grid never exceeds two groups per compute unit, so a
+// merging group only ever waits for groups that are running or done. The
+// merging group clears the records it read, so a workspace only needs
+// zero-filling once, before first use.
 //
 // Inside a wave a K/V block is read as 16-byte packets: LPR lanes cover one
 // 16-token row's head_dim, RPL = 64/LPR rows are read per instruction and each
@@ -44,8 +48,10 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kGroupsPerCU = 2;         // workgroups launched per compute unit
 constexpr int kMinBlocksPerGroup = 8;   // smallest share of blocks per workgroup
 constexpr int kMaxDecodeBatch = 8192;   // prefix table lives in LDS
-constexpr int kMaxDecodeRows = 65536;   // batch * num_kv_heads (arrival counters)
-constexpr int kMergeChunk = 8;          // partials loaded per batch in a merge
+constexpr int kMaxDecodeRows = 65536;   // batch * num_kv_heads
+// A merge waits at most this long (wall clock ticks, 100 MHz: 100 ms) for a
+// partial of an earlier group before it gives up and writes NaN.
+constexpr unsigned long long kMergeWaitTicks = 10000000ull;
 // The running max of a softmax moves only when a score exceeds it by more
 // than this many powers of two.
 constexpr float kLazyLog2 = 8.f;
@@ -111,9 +117,20 @@ __device__ __forceinline__ int locate_seq(const int* s_pref, int B, int Hkv, lon
   return lo;
 }
 
-// Floats of one partial record: acc[G][D], then m[G] and l[G], padded so
+// Words of one partial record: acc[G][D], then m[G] and l[G], padded so
 // records stay 16-byte aligned.
 __host__ __device__ constexpr int rec_floats(int G, int D) { return G * D + ((2 * G + 3) & ~3); }
+
+// Record words hold the complement of a float's bits, so a stored word is
+// never 0 (the bits 0xFFFFFFFF, a NaN, are stored as another NaN) and 0 marks
+// a word not yet written in this launch. Each word is stored once per launch
+// with a single 32-bit agent-scope store, so a reader that sees it non-zero
+// sees the whole value; the merging group clears the words it read.
+__device__ __forceinline__ uint32_t rec_encode(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return ~(u == 0xFFFFFFFFu ? 0x7FFFFFFFu : u);
+}
+__device__ __forceinline__ float rec_decode(uint32_t x) { return __uint_as_float(~x); }
 
 struct DecodeParams {
   const void* q;
@@ -122,8 +139,7 @@ struct DecodeParams {
   const int* tables;
   const int* seq_lens;
   void* out;
-  float* ws;      // partial records, two slots per workgroup
-  int* counters;  // per-row arrival counters, zero between launches
+  uint32_t* ws;  // partial records (encoded words), two slots per workgroup; zero between launches
   int B;
   int Hkv;
   int mbps;
@@ -259,6 +275,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   constexpr int NPART = 2 * kWaves;
   constexpr int DPL = (D + 63) / 64;  // output dims per lane in the row epilogue
   constexpr int QR = q_stage_rows<T, D, G>();
+  constexpr int MC = 16 / G > 2 ? 16 / G : 2;  // partial records loaded per batch in a merge
   // Two register buffers per wave: one block loading while one is computed.
   // With 2 * kWaves waves per compute unit that is enough bytes in flight to
   // keep HBM streaming; deeper buffering only lengthens the memory queues,
@@ -794,10 +811,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   // Rows this group holds in pieces. The wave holding the group's last piece
   // of a row finishes it: it combines the pieces parked by earlier waves
   // (waves own consecutive ranges, so a row's pieces sit in consecutive
-  // waves), then writes the output (row inside the group's range) or
-  // publishes one group partial and merges the row if it arrives last. Waves
-  // handle their rows independently, so the publication chains overlap.
-  for (int s = 0; s < 2; ++s) {
+  // waves), then writes the output (row inside the group's range), publishes
+  // one group partial (the row continues in a later group) or, in the group
+  // holding the row's last block, merges the partials of the earlier groups
+  // as they arrive. Waves handle their rows independently. A wave's later
+  // piece (slot 1) is handled first: if it is a row continuing into the next
+  // group its publication must not wait behind a merge of the wave's first
+  // piece, or merges would chain from group to group.
+  for (int s = 1; s >= 0; --s) {
     const int row = s_part_row[2 * wave + s];
     if (row < 0) continue;
     long long R;
@@ -805,7 +826,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     row_extent(row, R, nb);
     if (R + nb > whi && whi < ghi) continue;  // a later wave holds more of the row
     const int b = row / Hkv, kvh = row - b * Hkv;
-    const bool inside = R >= glo && R + nb <= ghi;
     float M[G][DPL], Ls[G][DPL], A[G][DPL];
 #pragma unroll
     for (int g = 0; g < G; ++g)
@@ -833,82 +853,128 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       }
       if (!any) break;
     }
-    if (inside) {
+    if (R + nb > ghi) {
+      // The row continues in a later group: publish this group's piece
+      // (slot 0 = the group's first segment, 1 = a later one) and leave.
+      uint32_t* rec = p.ws + ((size_t)w * 2 + (R <= glo ? 0 : 1)) * (size_t)REC;
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int k = 0; k < DPL; ++k) {
           const int d = lane + 64 * k;
-          if (d < D) {
-            const float inv = Ls[g][k] > 0.f ? 1.f / Ls[g][k] : 0.f;
-            ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(A[g][k] * inv);
-          }
+          if (d < D) st_word(rec + (size_t)g * D + d, rec_encode(A[g][k]));
         }
-      continue;
-    }
-    // Group partial: slot 0 = the group's first segment, 1 = a later one.
-    float* rec = p.ws + ((size_t)w * 2 + (R <= glo ? 0 : 1)) * (size_t)REC;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int k = 0; k < DPL; ++k) {
-        const int d = lane + 64 * k;
-        if (d < D) st_dev(rec + (size_t)g * D + d, A[g][k]);
-      }
       if (lane == 0) {
-        st_dev(rec + G * D + g, M[g][0]);
-        st_dev(rec + G * D + G + g, Ls[g][0]);
-      }
-    }
-    // Count the arrival; the last of the row's np groups merges. Group wa
-    // (holding the row's first block) used slot 0 only if its range starts
-    // exactly at the row start.
-    const long long wa = ((R + 1) * we - 1) / total;
-    const long long wb = ((R + nb) * we - 1) / total;
-    const int np = (int)(wb - wa + 1);
-    const bool wa_slot1 = range_lo(wa, total, we) != R;
-    wait_vm_stores();
-    int prev = 0;
-    if (lane == 0)
-      prev = __hip_atomic_fetch_add(p.counters + row, 1, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0, 64);
-    if (prev != np - 1) continue;
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int k = 0; k < DPL; ++k) {
-        M[g][k] = -INFINITY;
-        Ls[g][k] = 0.f;
-        A[g][k] = 0.f;
-      }
-    for (int c = 0; c < np; c += kMergeChunk) {
-      float mv[kMergeChunk][G], lv[kMergeChunk][G], av[kMergeChunk][G][DPL];
-#pragma unroll
-      for (int i = 0; i < kMergeChunk; ++i) {  // issue the chunk's loads together
-        const int j = c + i < np ? c + i : np - 1;
-        const int slot = (j == 0 && wa_slot1) ? 1 : 0;
-        const float* r = p.ws + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          mv[i][g] = ld_dev(r + G * D + g);
-          lv[i][g] = ld_dev(r + G * D + G + g);
+          st_word(rec + G * D + g, rec_encode(M[g][0]));
+          st_word(rec + G * D + G + g, rec_encode(Ls[g][0]));  // l of head G-1 last
+        }
+      }
+      continue;
+    }
+    bool ok = true;
+    if (R < glo) {
+      // The row's last block is in this group: combine the pieces of the
+      // earlier groups wa .. w-1 with this one's, each record once all of its
+      // words have arrived, then clear the records for the next launch. Group
+      // wa used slot 0 only if its range starts exactly at the row start.
+      const long long wa = ((R + 1) * we - 1) / total;
+      const int np = (int)(w - wa);
+      const bool wa_slot1 = range_lo(wa, total, we) != R;
+      auto record = [&](int j) __attribute__((always_inline)) {
+        const int slot = (j == 0 && wa_slot1) ? 1 : 0;
+        return p.ws + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
+      };
+      const unsigned long long t0 = wall_clock64();
+      auto timed_out = [&]() __attribute__((always_inline)) {
+        return wall_clock64() - t0 > kMergeWaitTicks;
+      };
+      for (int c = 0; c < np && ok; c += MC) {
+        uint32_t mv[MC][G], lv[MC][G], av[MC][G][DPL];
+        for (int attempt = 0;; ++attempt) {
+          if (attempt > 0) {
+            // Not all there yet: wait on one word per record, l of the last
+            // head (stored last), with one broadcast load each, before loading
+            // the records again (stores to different words may land out of
+            // order, so every word is checked after each load).
+            for (;;) {
+              if (timed_out()) {
+                ok = false;
+                break;
+              }
+              __builtin_amdgcn_s_sleep(8);
+              bool seen = true;
+#pragma unroll
+              for (int i = 0; i < MC; ++i)
+                if (c + i < np) seen = seen && ld_word(record(c + i) + G * D + 2 * G - 1) != 0u;
+              if (__all(seen)) break;
+            }
+            if (!ok) break;
+          }
+          bool ready = true;
+#pragma unroll
+          for (int i = 0; i < MC; ++i) {  // issue the chunk's loads together
+            if (c + i >= np) {
+#pragma unroll
+              for (int g = 0; g < G; ++g) {
+                mv[i][g] = lv[i][g] = 1u;
+#pragma unroll
+                for (int k = 0; k < DPL; ++k) av[i][g][k] = 1u;
+              }
+              continue;
+            }
+            const uint32_t* r = record(c + i);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              mv[i][g] = ld_word(r + G * D + g);
+              lv[i][g] = ld_word(r + G * D + G + g);
+#pragma unroll
+              for (int k = 0; k < DPL; ++k) {
+                const int d = lane + 64 * k;
+                av[i][g][k] = d < D ? ld_word(r + (size_t)g * D + d) : 1u;
+              }
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < MC; ++i)
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              ready = ready && mv[i][g] != 0u && lv[i][g] != 0u;
+#pragma unroll
+              for (int k = 0; k < DPL; ++k) ready = ready && av[i][g][k] != 0u;
+            }
+          if (__all(ready)) break;
+        }
+        if (!ok) break;
+#pragma unroll
+        for (int i = 0; i < MC; ++i)
+          if (c + i < np)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+              for (int k = 0; k < DPL; ++k)
+                lse_combine(M[g][k], Ls[g][k], A[g][k], rec_decode(mv[i][g]), rec_decode(lv[i][g]),
+                            rec_decode(av[i][g][k]));
+      }
+      for (int j = 0; j < np; ++j) {
+        uint32_t* r = record(j);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
 #pragma unroll
           for (int k = 0; k < DPL; ++k) {
             const int d = lane + 64 * k;
-            av[i][g][k] = d < D ? ld_dev(r + (size_t)g * D + d) : 0.f;
+            if (d < D) st_word(r + (size_t)g * D + d, 0u);
+          }
+          if (lane == 0) {
+            st_word(r + G * D + g, 0u);
+            st_word(r + G * D + G + g, 0u);
           }
         }
       }
-#pragma unroll
-      for (int i = 0; i < kMergeChunk; ++i)
-        if (c + i < np)
-#pragma unroll
-          for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int k = 0; k < DPL; ++k)
-              lse_combine(M[g][k], Ls[g][k], A[g][k], mv[i][g], lv[i][g], av[i][g][k]);
     }
+    // Output of a row inside the group's range or merged above (NaN if a
+    // partial never arrived within kMergeWaitTicks).
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -916,11 +982,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
         const int d = lane + 64 * k;
         if (d < D) {
           const float inv = Ls[g][k] > 0.f ? 1.f / Ls[g][k] : 0.f;
-          ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] = Elem<T>::from_f32(A[g][k] * inv);
+          ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] =
+              Elem<T>::from_f32(ok ? A[g][k] * inv : __builtin_nanf(""));
         }
       }
-    if (lane == 0)
-      __hip_atomic_store(p.counters + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

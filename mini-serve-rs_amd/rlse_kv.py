@@ -476,8 +476,8 @@ def kv_copy_blocks(k_pool, v_pool, layer_stride_elems: int, num_layers: int, src
 
 def decode_workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int) -> int:
     """Bytes of workspace for paged_gqa_decode. A workspace must be zero-filled
-    once before its first use (its row counters return to zero after every
-    launch)."""
+    once before its first use (every launch leaves it zero again: the group
+    that merges a partial record clears it)."""
     n = _sz()
     _check(load().rlse_decode_workspace_size(batch, num_heads, num_kv_heads, head_dim,
                                              ctypes.byref(n)))
