@@ -263,6 +263,24 @@ def test_workspace_records_cleared_between_launches(kv):
             assert int(torch.count_nonzero(ws)) == 0, f"case{i} rep{rep} left records behind"
 
 
+def test_decode_is_deterministic_across_launches(kv):
+    """Rows cut between workgroups are merged in the same launch with their
+    pieces combined in a fixed order, whatever order the groups finish in, so
+    repeated launches on the same inputs give bit-identical outputs."""
+    rng = np.random.default_rng(21)
+    hq, hkv, d, dtype = 16, 8, 128, "bf16"
+    lens = rng.integers(128, 2049, 32)
+    q, kp, vp, tables, lens = make_case(rng, lens, hq, hkv, d, dtype)
+    qd, kd, vd = to_dev(q, dtype), to_dev(kp, dtype), to_dev(vp, dtype)
+    print("determinism: B=32 U[128,2048] Hq=16 Hkv=8 d=128 bf16, 10 launches", flush=True)
+    first = run_decode(kv, qd, kd, vd, tables, lens, hq, hkv, d, dtype, 0.0883)
+    check("determinism vs oracle", as_f32(first, dtype),
+          oracle_decode(q, kp, vp, tables, lens, dtype, 0.0883), dtype)
+    for rep in range(9):
+        again = run_decode(kv, qd, kd, vd, tables, lens, hq, hkv, d, dtype, 0.0883)
+        np.testing.assert_array_equal(again, first, err_msg=f"launch {rep + 1}")
+
+
 # ------------------------------------------------------------- fused step ----
 def _rope_tables_dev(kv, theta, d, max_pos, dtype):
     np_dt = {"f32": np.float32, "bf16": np.uint16, "f16": np.float16}[dtype]
