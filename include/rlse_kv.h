@@ -40,6 +40,7 @@ enum rlse_dtype { RLSE_DTYPE_F32 = 0, RLSE_DTYPE_BF16 = 1, RLSE_DTYPE_F16 = 2 };
 #define RLSE_ERR_CACHE_PRESSURE 10001
 #define RLSE_ERR_UNKNOWN_REQUEST 10002
 #define RLSE_ERR_BUFFER_TOO_SMALL 10003
+#define RLSE_ERR_TOKEN_LIMIT 10004 /* EngineError::TokenLimitExceeded */
 #define RLSE_BLOCK_SIZE 16 /* src/core/constants.rs:1 DEFAULT_BLOCK_SIZE */
 
 /* Message of the last failing call on this thread ("" if none). */
@@ -343,13 +344,81 @@ int rlse_pc_fork(rlse_prefix_cache* pc, const uint32_t* tokens, long long num_to
                  long long restore_tokens, const char* child_id, int32_t* cow_src,
                  int32_t* cow_dst, int cow_capacity, int* num_cow);
 /* Evicts least recently used chunks until the block manager has at least
- * min_free_blocks free (the memory-pressure eviction of reserve_memory,
- * :216-232); RLSE_ERR_CACHE_PRESSURE if the cache empties first. */
+ * min_free_blocks free and, with a memory budget attached, room for that
+ * many pages (the memory-pressure eviction of reserve_memory, :216-244);
+ * RLSE_ERR_CACHE_PRESSURE if the cache empties first. */
 int rlse_pc_reclaim(rlse_prefix_cache* pc, int min_free_blocks, int* evicted);
 int rlse_pc_clear(rlse_prefix_cache* pc);
 /* record_reuse (:368-376). */
 int rlse_pc_record_reuse(rlse_prefix_cache* pc, long long skipped_tokens);
 int rlse_pc_stats(const rlse_prefix_cache* pc, rlse_prefix_stats* out);
+/* PrefixCache::reserve_memory (:229-244): try_reserve on the block
+ * manager's budget, evicting least recently used chunks until the charge
+ * fits; records a rejection and returns RLSE_ERR_CACHE_PRESSURE ("Tensor
+ * memory budget exhausted") when the cache empties first. */
+int rlse_pc_reserve_memory(rlse_prefix_cache* pc, long long active_kv_bytes,
+                           long long execution_bytes, long long prefix_bytes, long long* lease);
+
+/* ------------------------------------------------------------------ */
+/* Tensor memory budget with page-based KV charges: successor of       */
+/* TensorMemoryBudget (src/cache/tensor_memory.rs:41-125) and of       */
+/* CandleBackend::memory_charge (src/backends/candle.rs:241-282).      */
+/* The reference charges each request its whole contiguous capacity,   */
+/* 2*layers*Hkv*d*(prompt+max_tokens)*bytes, at admission. A block     */
+/* manager with an attached budget instead charges each page when it   */
+/* leaves the free stack -- active KV while any request holds it,      */
+/* retained prefix while only prefix-cache chunks hold it -- and       */
+/* uncharges it when its last holder lets go. Host only; updates are   */
+/* serialized by a mutex inside the budget, so workers may share one.  */
+/* Destroy block managers (or detach them) before their budget.        */
+/* ------------------------------------------------------------------ */
+typedef struct rlse_memory_budget rlse_memory_budget;
+typedef struct rlse_memory_stats {   /* TensorMemoryStats (:28-39)       */
+  long long budget_bytes, headroom_bytes;
+  long long active_kv_reserved_bytes;  /* leases + pages held by requests */
+  long long execution_reserved_bytes;
+  long long prefix_retained_bytes;     /* leases + pages held only by chunks */
+  long long reserved_bytes, available_bytes, peak_reserved_bytes;
+  long long rejections;
+} rlse_memory_stats;
+typedef struct rlse_model_shape {    /* the Config fields memory_charge reads */
+  int num_layers, num_heads, num_kv_heads, head_dim;
+  int hidden_size, intermediate_size, vocab_size;
+  int dtype_bytes, context_length, block_size;
+} rlse_model_shape;
+
+/* TensorMemoryBudget::new (:48-67): 0 < headroom < budget, else
+ * RLSE_ERR_INVALID_VALUE; the headroom is reserved from the start. */
+int rlse_mb_create(long long budget_bytes, long long headroom_bytes, rlse_memory_budget** out);
+int rlse_mb_destroy(rlse_memory_budget* mb);
+int rlse_mb_stats(rlse_memory_budget* mb, rlse_memory_stats* out);
+/* try_reserve (:72-90): all or nothing; RLSE_ERR_CACHE_PRESSURE (no
+ * rejection recorded) when the total does not fit or overflows. The lease
+ * id is released with rlse_mb_release (MemoryReservation's Drop, :105-117). */
+int rlse_mb_try_reserve(rlse_memory_budget* mb, long long active_kv_bytes,
+                        long long execution_bytes, long long prefix_bytes, long long* lease);
+int rlse_mb_release(rlse_memory_budget* mb, long long lease);
+/* record_rejection (:92-94). */
+int rlse_mb_record_rejection(rlse_memory_budget* mb);
+/* Charges bm's pages to mb from now on (mb NULL: detach, uncharging them),
+ * page_bytes per page -- 2*layers*Hkv*d*block_size*dtype_bytes, as
+ * rlse_memory_charge reports. The pages held at attach time are charged at
+ * once (all or nothing). With a budget attached, an allocation that does
+ * not fit records a rejection and fails with RLSE_ERR_CACHE_PRESSURE before
+ * any change. */
+int rlse_bm_attach_budget(rlse_block_manager* bm, rlse_memory_budget* mb, long long page_bytes);
+/* memory_charge (candle.rs:241-282) for paged KV, with the same checked
+ * arithmetic and errors (RLSE_ERR_TOKEN_LIMIT for zero tokens or
+ * prompt+max_tokens > context_length, RLSE_ERR_CACHE_PRESSURE on overflow):
+ *   page_bytes = 2*layers*Hkv*d*block_size*B;
+ *   kv_bytes   = ceil(T / block_size) * page_bytes, the most the request's
+ *                pages can be charged (T = prompt + max_tokens);
+ *   execution_bytes = 8*H*P*T*max(B,4) + 16*S*P*B + 8*I*P*B + 8*H*T*D*B
+ *                + 16*V*max(B,4): the reference's estimate without its
+ *                KV-sized staging term (pages are written in place). */
+int rlse_memory_charge(const rlse_model_shape* shape, long long prompt_tokens,
+                       long long max_tokens, long long* kv_bytes, long long* execution_bytes,
+                       long long* page_bytes);
 
 #ifdef __cplusplus
 }

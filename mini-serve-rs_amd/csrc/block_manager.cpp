@@ -27,6 +27,21 @@ using rlse::fail;
 
 static float round3(float x) { return roundf(x * 1000.0f) / 1000.0f; }
 
+// An allocation of n pages that the attached budget cannot hold: counted as a
+// rejection (TensorMemoryBudget::record_rejection) and refused before any change.
+static int budget_pressure(rlse_block_manager* bm, long long n) {
+  long long avail = 0;
+  {
+    std::lock_guard<std::mutex> g(bm->budget->mu);
+    ++bm->budget->rejections;
+    avail = bm->budget->available;
+  }
+  return fail(RLSE_ERR_CACHE_PRESSURE,
+              "Tensor memory budget exhausted: %lld pages of %lld bytes requested, %lld bytes "
+              "available",
+              n, bm->page_bytes, avail);
+}
+
 extern "C" int rlse_bm_create(int total_blocks, int block_size, rlse_block_manager** out) {
   if (!out) return fail(RLSE_ERR_INVALID_VALUE, "bm_create: null output");
   *out = nullptr;
@@ -40,12 +55,14 @@ extern "C" int rlse_bm_create(int total_blocks, int block_size, rlse_block_manag
   bm->free_stack.reserve(total_blocks);
   for (int i = total_blocks - 1; i >= 0; --i) bm->free_stack.push_back(i);
   bm->refcount.assign(total_blocks, 0);
+  bm->cache_refs.assign(total_blocks, 0);
   *out = bm;
   return RLSE_OK;
 }
 
 extern "C" int rlse_bm_destroy(rlse_block_manager* bm) {
   if (!bm) return fail(RLSE_ERR_INVALID_VALUE, "bm_destroy: null");
+  if (bm->budget) rlse_bm_attach_budget(bm, nullptr, 0);  // uncharge every held page
   delete bm;
   return RLSE_OK;
 }
@@ -73,6 +90,7 @@ extern "C" int rlse_bm_allocate(rlse_block_manager* bm, const char* request_id,
   if (out_blocks && capacity < needed)
     return fail(RLSE_ERR_BUFFER_TOO_SMALL, "bm_allocate: capacity %d < %lld blocks", capacity,
                 needed);
+  if (!bm->reserve_pages(needed)) return budget_pressure(bm, needed);
   std::vector<int> blocks;
   blocks.reserve((size_t)needed);
   for (long long i = 0; i < needed; ++i) blocks.push_back(bm->pop());
@@ -89,6 +107,7 @@ extern "C" int rlse_bm_allocate_block(rlse_block_manager* bm, const char* reques
   if (bm->free_stack.empty())
     return fail(RLSE_ERR_CACHE_PRESSURE,
                 "KV cache pressure: no free blocks remaining for incremental allocation");
+  if (!bm->reserve_pages(1)) return budget_pressure(bm, 1);
   const int b = bm->pop();
   bm->allocations[request_id].push_back(b);
   if (out_block) *out_block = b;
@@ -102,7 +121,7 @@ extern "C" int rlse_bm_release(rlse_block_manager* bm, const char* request_id,
   int count = 0;
   if (it != bm->allocations.end()) {
     count = (int)it->second.size();
-    for (int b : it->second) bm->unref(b);
+    for (int b : it->second) bm->unref_request(b);
     bm->allocations.erase(it);
   }
   if (num_released) *num_released = count;
@@ -133,11 +152,12 @@ extern "C" int rlse_bm_fork(rlse_block_manager* bm, const char* parent_id, const
                 "KV cache pressure: no free block for the copy-on-write of a partial block");
   if (partial && (!cow_src || !cow_dst || cow_capacity < 1))
     return fail(RLSE_ERR_BUFFER_TOO_SMALL, "bm_fork: no room for the copy-on-write pair");
+  if (partial && !bm->reserve_pages(1)) return budget_pressure(bm, 1);
   std::vector<int> child;
   child.reserve((size_t)(full + 1));
   for (long long i = 0; i < full; ++i) {
     const int b = parent[(size_t)i];
-    ++bm->refcount[b];
+    bm->ref_request(b);
     child.push_back(b);
   }
   int ncow = 0;

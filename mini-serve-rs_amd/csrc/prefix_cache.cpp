@@ -174,7 +174,7 @@ struct rlse_prefix_cache {
 
   void touch(Chunk& c) { lru.splice(lru.end(), lru, c.lru); }
   void drop(std::unordered_map<std::string, Chunk>::iterator it) {
-    for (int p : it->second.pages) bm->unref(p);
+    for (int p : it->second.pages) bm->unref_cache(p);
     lru.erase(it->second.lru);
     chunks.erase(it);
   }
@@ -298,7 +298,7 @@ extern "C" int rlse_pc_insert_kv(rlse_prefix_cache* pc, const uint32_t* tokens,
     // chunk's references first.
     const std::vector<int>& req = pc->bm->allocations[request_id];
     std::vector<int> pages(req.begin(), req.begin() + (size_t)((i + 1) * pages_per_chunk));
-    for (int p : pages) ++pc->bm->refcount[p];
+    for (int p : pages) pc->bm->ref_cache(p);
     Chunk& c = pc->add(keys[i], std::vector<uint32_t>(tokens + i * pc->chunk_size,
                                                       tokens + (i + 1) * pc->chunk_size));
     c.pages = std::move(pages);
@@ -364,10 +364,15 @@ extern "C" int rlse_pc_fork(rlse_prefix_cache* pc, const uint32_t* tokens, long 
                 "KV cache pressure: no free block for the copy-on-write of a partial block");
   if (partial && (!cow_src || !cow_dst || cow_capacity < 1))
     return fail(RLSE_ERR_BUFFER_TOO_SMALL, "pc_fork: no room for the copy-on-write pair");
+  if (partial && !bm->reserve_pages(1)) {
+    rlse_mb_record_rejection(bm->budget);
+    return fail(RLSE_ERR_CACHE_PRESSURE,
+                "Tensor memory budget exhausted: no room for the copy-on-write page");
+  }
   std::vector<int> child;
   child.reserve((size_t)(full + 1));
   for (long long i = 0; i < full; ++i) {
-    ++bm->refcount[pages[(size_t)i]];
+    bm->ref_request(pages[(size_t)i]);
     child.push_back(pages[(size_t)i]);
   }
   int ncow = 0;
@@ -386,13 +391,35 @@ extern "C" int rlse_pc_fork(rlse_prefix_cache* pc, const uint32_t* tokens, long 
 extern "C" int rlse_pc_reclaim(rlse_prefix_cache* pc, int min_free_blocks, int* evicted) {
   if (!pc || min_free_blocks < 0) return fail(RLSE_ERR_INVALID_VALUE, "pc_reclaim: bad arguments");
   int n = 0;
-  while ((int)pc->bm->free_stack.size() < min_free_blocks && pc->evict_oldest()) ++n;
+  while (!pc->bm->pages_fit(min_free_blocks) && pc->evict_oldest()) ++n;
   if (evicted) *evicted = n;
   if ((int)pc->bm->free_stack.size() < min_free_blocks)
     return fail(RLSE_ERR_CACHE_PRESSURE,
                 "KV cache pressure: %zu free blocks after evicting every cached prefix, %d needed",
                 pc->bm->free_stack.size(), min_free_blocks);
+  if (!pc->bm->pages_fit(min_free_blocks))
+    return fail(RLSE_ERR_CACHE_PRESSURE,
+                "Tensor memory budget exhausted: %d pages do not fit after evicting every cached "
+                "prefix",
+                min_free_blocks);
   return RLSE_OK;
+}
+
+extern "C" int rlse_pc_reserve_memory(rlse_prefix_cache* pc, long long active_kv_bytes,
+                                      long long execution_bytes, long long prefix_bytes,
+                                      long long* lease) {
+  if (!pc || !lease) return fail(RLSE_ERR_INVALID_VALUE, "pc_reserve_memory: bad arguments");
+  rlse_memory_budget* mb = pc->bm->budget;
+  if (!mb)
+    return fail(RLSE_ERR_INVALID_VALUE, "pc_reserve_memory: the block manager has no budget");
+  for (;;) {
+    if (rlse_mb_try_reserve(mb, active_kv_bytes, execution_bytes, prefix_bytes, lease) == RLSE_OK)
+      return RLSE_OK;
+    if (!pc->evict_oldest()) {
+      rlse_mb_record_rejection(mb);
+      return fail(RLSE_ERR_CACHE_PRESSURE, "Tensor memory budget exhausted");
+    }
+  }
 }
 
 extern "C" int rlse_pc_clear(rlse_prefix_cache* pc) {

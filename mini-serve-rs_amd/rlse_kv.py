@@ -41,6 +41,7 @@ ERR_INVALID_VALUE = 1
 ERR_CACHE_PRESSURE = 10001
 ERR_UNKNOWN_REQUEST = 10002
 ERR_BUFFER_TOO_SMALL = 10003
+ERR_TOKEN_LIMIT = 10004
 BLOCK_SIZE = 16
 
 # Every extern "C" symbol of include/rlse_kv.h (checked by the CPU tests).
@@ -60,6 +61,10 @@ EXPORTED = (
     "rlse_pc_create", "rlse_pc_destroy", "rlse_pc_chunk_hashes", "rlse_pc_lookup",
     "rlse_pc_insert", "rlse_pc_insert_kv", "rlse_pc_lookup_kv", "rlse_pc_fork",
     "rlse_pc_reclaim", "rlse_pc_clear", "rlse_pc_record_reuse", "rlse_pc_stats",
+    "rlse_pc_reserve_memory",
+    "rlse_mb_create", "rlse_mb_destroy", "rlse_mb_stats", "rlse_mb_try_reserve",
+    "rlse_mb_release", "rlse_mb_record_rejection", "rlse_bm_attach_budget",
+    "rlse_memory_charge",
 )
 
 
@@ -74,6 +79,38 @@ class RlseError(RuntimeError):
 
 class CachePressure(RlseError):
     """RLSE_ERR_CACHE_PRESSURE, the reference's EngineError::CachePressure."""
+
+
+class TokenLimitExceeded(RlseError):
+    """RLSE_ERR_TOKEN_LIMIT, the reference's EngineError::TokenLimitExceeded."""
+
+
+class _MemoryStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_longlong) for n in (
+        "budget_bytes", "headroom_bytes", "active_kv_reserved_bytes", "execution_reserved_bytes",
+        "prefix_retained_bytes", "reserved_bytes", "available_bytes", "peak_reserved_bytes",
+        "rejections")]
+
+
+@dataclass
+class MemoryStats:
+    """TensorMemoryStats (src/cache/tensor_memory.rs:28-39)."""
+    budget_bytes: int
+    headroom_bytes: int
+    active_kv_reserved_bytes: int
+    execution_reserved_bytes: int
+    prefix_retained_bytes: int
+    reserved_bytes: int
+    available_bytes: int
+    peak_reserved_bytes: int
+    rejections: int
+
+
+class ModelShape(ctypes.Structure):
+    """The Config fields memory_charge reads (src/backends/candle.rs:241-282)."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "num_layers", "num_heads", "num_kv_heads", "head_dim", "hidden_size",
+        "intermediate_size", "vocab_size", "dtype_bytes", "context_length", "block_size")]
 
 
 class _CacheStats(ctypes.Structure):
@@ -169,6 +206,16 @@ _SIGS = {
     "rlse_pc_clear": (_i, [_vp]),
     "rlse_pc_record_reuse": (_i, [_vp, _ll]),
     "rlse_pc_stats": (_i, [_vp, ctypes.POINTER(_PrefixStats)]),
+    "rlse_pc_reserve_memory": (_i, [_vp, _ll, _ll, _ll, ctypes.POINTER(_ll)]),
+    "rlse_mb_create": (_i, [_ll, _ll, ctypes.POINTER(_vp)]),
+    "rlse_mb_destroy": (_i, [_vp]),
+    "rlse_mb_stats": (_i, [_vp, ctypes.POINTER(_MemoryStats)]),
+    "rlse_mb_try_reserve": (_i, [_vp, _ll, _ll, _ll, ctypes.POINTER(_ll)]),
+    "rlse_mb_release": (_i, [_vp, _ll]),
+    "rlse_mb_record_rejection": (_i, [_vp]),
+    "rlse_bm_attach_budget": (_i, [_vp, _vp, _ll]),
+    "rlse_memory_charge": (_i, [ctypes.POINTER(ModelShape), _ll, _ll, ctypes.POINTER(_ll),
+                                ctypes.POINTER(_ll), ctypes.POINTER(_ll)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -201,6 +248,8 @@ def _check(status: int) -> None:
         msg = last_error()
         if status == ERR_CACHE_PRESSURE:
             raise CachePressure(status, msg)
+        if status == ERR_TOKEN_LIMIT:
+            raise TokenLimitExceeded(status, msg)
         raise RlseError(status, msg)
 
 
@@ -310,6 +359,12 @@ class BlockManager:
         return CacheStats(s.total_blocks, s.allocated_blocks, s.free_blocks, s.utilization,
                           s.fragmentation)
 
+    def attach_budget(self, budget: Optional["MemoryBudget"], page_bytes: int = 0) -> None:
+        """Charges this manager's pages to budget from now on (None: detach)."""
+        _check(self._lib.rlse_bm_attach_budget(self._h, budget._h if budget else None,
+                                               page_bytes))
+        self._budget = budget  # the budget must outlive the attachment
+
 
 def _tokens(tokens):
     arr = (ctypes.c_uint32 * max(len(tokens), 1))(*[int(t) & 0xffffffff for t in tokens])
@@ -397,6 +452,72 @@ class PrefixCache:
         _check(self._lib.rlse_pc_stats(self._h, ctypes.byref(st)))
         return PrefixStats(st.hits, st.misses, st.tokens_saved, st.kv_evictions, st.chunks,
                            st.held_pages, st.hit_rate)
+
+    def reserve_memory(self, active_kv: int = 0, execution: int = 0, prefix: int = 0) -> int:
+        """reserve_memory (prefix_cache.rs:229-244) on the block manager's
+        budget: evicts LRU chunks until the charge fits; a lease id, or
+        CachePressure (one rejection recorded)."""
+        lease = _ll()
+        _check(self._lib.rlse_pc_reserve_memory(self._h, active_kv, execution, prefix,
+                                                ctypes.byref(lease)))
+        return lease.value
+
+
+# --------------------------------------------------------------------------
+# Tensor memory budget (TensorMemoryBudget successor, page-based KV charges)
+# --------------------------------------------------------------------------
+class MemoryBudget:
+    """TensorMemoryBudget (src/cache/tensor_memory.rs:41-125). Block
+    managers attached with BlockManager.attach_budget charge their pages to
+    it; leases cover the other reservations."""
+
+    def __init__(self, budget_bytes: int, headroom_bytes: int):
+        lib = load()
+        h = _vp()
+        _check(lib.rlse_mb_create(budget_bytes, headroom_bytes, ctypes.byref(h)))
+        self._h, self._lib = h, lib
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.rlse_mb_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def stats(self) -> MemoryStats:
+        st = _MemoryStats()
+        _check(self._lib.rlse_mb_stats(self._h, ctypes.byref(st)))
+        return MemoryStats(*(getattr(st, f) for f, _ in _MemoryStats._fields_))
+
+    def try_reserve(self, active_kv: int = 0, execution: int = 0,
+                    prefix: int = 0) -> Optional[int]:
+        """try_reserve (:72-90): a lease id, or None when the charge does not fit."""
+        lease = _ll()
+        st = self._lib.rlse_mb_try_reserve(self._h, active_kv, execution, prefix,
+                                           ctypes.byref(lease))
+        if st == ERR_CACHE_PRESSURE:
+            return None
+        _check(st)
+        return lease.value
+
+    def release(self, lease: int) -> None:
+        _check(self._lib.rlse_mb_release(self._h, lease))
+
+    def record_rejection(self) -> None:
+        _check(self._lib.rlse_mb_record_rejection(self._h))
+
+
+def memory_charge(shape: ModelShape, prompt_tokens: int, max_tokens: int) -> Tuple[int, int, int]:
+    """memory_charge (src/backends/candle.rs:241-282) for paged KV:
+    (kv_bytes, execution_bytes, page_bytes)."""
+    kv, ex, page = _ll(), _ll(), _ll()
+    _check(load().rlse_memory_charge(ctypes.byref(shape), prompt_tokens, max_tokens,
+                                     ctypes.byref(kv), ctypes.byref(ex), ctypes.byref(page)))
+    return kv.value, ex.value, page.value
 
 
 # --------------------------------------------------------------------------
