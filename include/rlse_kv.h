@@ -295,6 +295,50 @@ int rlse_bm_block_table(const rlse_block_manager* bm, const char* request_id,
                         int32_t* out_blocks, int capacity, int* num_out);
 int rlse_bm_refcount(const rlse_block_manager* bm, int block);
 int rlse_bm_stats(const rlse_block_manager* bm, rlse_cache_stats* out);
+/* Releases every request's blocks, in request-id order: the KV side of
+ * quarantine (src/backends/candle.rs:689-697 clears every model state). */
+int rlse_bm_release_all(rlse_block_manager* bm, int* num_requests);
+
+/* ------------------------------------------------------------------ */
+/* Per-step block tables: successor of the scheduler's per-step block  */
+/* reservation (src/scheduler/scheduler.rs:422-449) plus the upload of */
+/* the tables the decode kernels read. Row i of the tables is request  */
+/* i of the step's batch. Uploads send only what changed since the     */
+/* previous upload of the same object: the whole row of a request new  */
+/* to its row (or whose block list was replaced), else one (row, col,  */
+/* page) triple per page added. Host object; one upload in flight per  */
+/* staging buffer (two), uploads of one object on one stream.          */
+/* ------------------------------------------------------------------ */
+typedef struct rlse_step_tables rlse_step_tables;
+int rlse_st_create(int max_batch, int max_blocks_per_seq, rlse_step_tables** out);
+int rlse_st_destroy(rlse_step_tables* st);
+/* Forget what the device holds (the next upload sends every row whole),
+ * e.g. after the device tables were reallocated. */
+int rlse_st_reset(rlse_step_tables* st);
+/* The reservation loop for a batch: request i grows to
+ * blocks_needed(next_lens[i]) blocks (rlse_bm_allocate_block); a request
+ * that cannot grow is released and gets status[i] = RLSE_ERR_CACHE_PRESSURE
+ * (the reference's swap_remove + cancel + release), an unknown one
+ * RLSE_ERR_UNKNOWN_REQUEST, one needing more than max_blocks_per_seq
+ * blocks RLSE_ERR_INVALID_VALUE; their length is 0, which the decode
+ * kernels answer with zeros. Then lays out the rows and lengths. */
+int rlse_st_prepare(rlse_step_tables* st, rlse_block_manager* bm,
+                    const char* const* request_ids, const long long* next_lens, int batch,
+                    int* status);
+/* Host image of this step: tables [max_batch][max_blocks_per_seq] (rows <
+ * batch valid up to their block count), lengths, and the triples not yet
+ * uploaded. */
+int rlse_st_host(const rlse_step_tables* st, const int32_t** tables, const int32_t** seq_lens,
+                 int* batch, const int32_t** pending, int* num_pending);
+/* Copies the lengths and pending triples into device tables
+ * [max_batch][max_blocks_per_seq] and seq_lens [max_batch] on stream: one
+ * transfer from pinned memory plus one scatter kernel. Entries past a row's
+ * block count are left as they were (never read). */
+int rlse_st_upload(rlse_step_tables* st, int32_t* tables, int32_t* seq_lens,
+                   rlse_stream_t stream);
+/* For callers that copy the host image themselves: drops the pending
+ * triples as if uploaded. */
+int rlse_st_mark_uploaded(rlse_step_tables* st);
 
 /* ------------------------------------------------------------------ */
 /* Prefix cache over refcounted pages: successor of PrefixCache        */

@@ -16,6 +16,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <new>
 
 #include "block_manager.h"
@@ -97,7 +98,7 @@ extern "C" int rlse_bm_allocate(rlse_block_manager* bm, const char* request_id,
   if (out_blocks)
     for (size_t i = 0; i < blocks.size(); ++i) out_blocks[i] = blocks[i];
   if (num_out) *num_out = (int)needed;
-  bm->allocations[request_id] = std::move(blocks);
+  bm->set_list(request_id, std::move(blocks));
   return RLSE_OK;
 }
 
@@ -109,7 +110,9 @@ extern "C" int rlse_bm_allocate_block(rlse_block_manager* bm, const char* reques
                 "KV cache pressure: no free blocks remaining for incremental allocation");
   if (!bm->reserve_pages(1)) return budget_pressure(bm, 1);
   const int b = bm->pop();
-  bm->allocations[request_id].push_back(b);
+  auto& list = bm->allocations[request_id];
+  if (list.empty()) bm->list_version[request_id] = ++bm->next_version;  // a new request
+  list.push_back(b);
   if (out_block) *out_block = b;
   return RLSE_OK;
 }
@@ -123,8 +126,26 @@ extern "C" int rlse_bm_release(rlse_block_manager* bm, const char* request_id,
     count = (int)it->second.size();
     for (int b : it->second) bm->unref_request(b);
     bm->allocations.erase(it);
+    bm->list_version.erase(request_id);
   }
   if (num_released) *num_released = count;
+  return RLSE_OK;
+}
+
+extern "C" int rlse_bm_release_all(rlse_block_manager* bm, int* num_requests) {
+  if (!bm) return fail(RLSE_ERR_INVALID_VALUE, "bm_release_all: null");
+  // In request-id order, so the free stack (and the ids handed out next) does
+  // not depend on the hash map's iteration order.
+  std::vector<std::string> ids;
+  ids.reserve(bm->allocations.size());
+  for (const auto& kv : bm->allocations) ids.push_back(kv.first);
+  std::sort(ids.begin(), ids.end());
+  for (const std::string& id : ids) {
+    for (int b : bm->allocations[id]) bm->unref_request(b);
+    bm->allocations.erase(id);
+    bm->list_version.erase(id);
+  }
+  if (num_requests) *num_requests = (int)ids.size();
   return RLSE_OK;
 }
 
@@ -169,7 +190,7 @@ extern "C" int rlse_bm_fork(rlse_block_manager* bm, const char* parent_id, const
     ncow = 1;
   }
   if (num_cow) *num_cow = ncow;
-  bm->allocations[child_id] = std::move(child);
+  bm->set_list(child_id, std::move(child));
   return RLSE_OK;
 }
 

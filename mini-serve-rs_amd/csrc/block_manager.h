@@ -58,6 +58,11 @@ struct rlse_block_manager {
   std::vector<int> refcount;    // all holders: requests and prefix-cache chunks
   std::vector<int> cache_refs;  // holders that are prefix-cache chunks
   std::unordered_map<std::string, std::vector<int>> allocations;
+  // Version of each request's list: a new value whenever the list is
+  // replaced (allocate, fork into a child); appends keep it. A table row
+  // built from (request, version) needs only the appended tail afterwards.
+  std::unordered_map<std::string, unsigned long long> list_version;
+  unsigned long long next_version = 0;
   rlse_memory_budget* budget = nullptr;
   long long page_bytes = 0;
 
@@ -98,6 +103,10 @@ struct rlse_block_manager {
     if (__builtin_mul_overflow(n, page_bytes, &bytes)) return false;
     std::lock_guard<std::mutex> g(budget->mu);
     return budget->try_charge(bytes, 0, 0);
+  }
+  void set_list(const std::string& id, std::vector<int>&& blocks) {
+    allocations[id] = std::move(blocks);
+    list_version[id] = ++next_version;
   }
   long long blocks_needed(long long tokens) const {
     if (tokens <= 0) return 1;

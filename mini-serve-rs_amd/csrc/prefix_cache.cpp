@@ -384,7 +384,7 @@ extern "C" int rlse_pc_fork(rlse_prefix_cache* pc, const uint32_t* tokens, long 
     ncow = 1;
   }
   if (num_cow) *num_cow = ncow;
-  bm->allocations[child_id] = std::move(child);
+  bm->set_list(child_id, std::move(child));
   return RLSE_OK;
 }
 

@@ -65,6 +65,8 @@ EXPORTED = (
     "rlse_mb_create", "rlse_mb_destroy", "rlse_mb_stats", "rlse_mb_try_reserve",
     "rlse_mb_release", "rlse_mb_record_rejection", "rlse_bm_attach_budget",
     "rlse_memory_charge",
+    "rlse_bm_release_all", "rlse_st_create", "rlse_st_destroy", "rlse_st_reset",
+    "rlse_st_prepare", "rlse_st_host", "rlse_st_upload", "rlse_st_mark_uploaded",
 )
 
 
@@ -216,6 +218,15 @@ _SIGS = {
     "rlse_bm_attach_budget": (_i, [_vp, _vp, _ll]),
     "rlse_memory_charge": (_i, [ctypes.POINTER(ModelShape), _ll, _ll, ctypes.POINTER(_ll),
                                 ctypes.POINTER(_ll), ctypes.POINTER(_ll)]),
+    "rlse_bm_release_all": (_i, [_vp, ctypes.POINTER(_i)]),
+    "rlse_st_create": (_i, [_i, _i, ctypes.POINTER(_vp)]),
+    "rlse_st_destroy": (_i, [_vp]),
+    "rlse_st_reset": (_i, [_vp]),
+    "rlse_st_prepare": (_i, [_vp, _vp, ctypes.POINTER(_cp), ctypes.POINTER(_ll), _i, _ip]),
+    "rlse_st_host": (_i, [_vp, ctypes.POINTER(_ip), ctypes.POINTER(_ip), ctypes.POINTER(_i),
+                          ctypes.POINTER(_ip), ctypes.POINTER(_i)]),
+    "rlse_st_upload": (_i, [_vp, _vp, _vp, _vp]),
+    "rlse_st_mark_uploaded": (_i, [_vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -358,6 +369,12 @@ class BlockManager:
         _check(self._lib.rlse_bm_stats(self._h, ctypes.byref(s)))
         return CacheStats(s.total_blocks, s.allocated_blocks, s.free_blocks, s.utilization,
                           s.fragmentation)
+
+    def release_all(self) -> int:
+        """Releases every request (the KV side of quarantine); returns how many."""
+        n = _i()
+        _check(self._lib.rlse_bm_release_all(self._h, ctypes.byref(n)))
+        return n.value
 
     def attach_budget(self, budget: Optional["MemoryBudget"], page_bytes: int = 0) -> None:
         """Charges this manager's pages to budget from now on (None: detach)."""
@@ -509,6 +526,63 @@ class MemoryBudget:
 
     def record_rejection(self) -> None:
         _check(self._lib.rlse_mb_record_rejection(self._h))
+
+
+class StepTables:
+    """Per-step block tables (scheduler.rs:422-449 reservation loop + the
+    upload of the tables the decode kernels read, sending only changes)."""
+
+    def __init__(self, max_batch: int, max_blocks_per_seq: int):
+        lib = load()
+        h = _vp()
+        _check(lib.rlse_st_create(max_batch, max_blocks_per_seq, ctypes.byref(h)))
+        self._h, self._lib = h, lib
+        self.max_batch, self.max_blocks_per_seq = max_batch, max_blocks_per_seq
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.rlse_st_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prepare(self, bm: BlockManager, request_ids: Sequence[str],
+                next_lens: Sequence[int]) -> List[int]:
+        """Grows each request to blocks_needed(next_len) and lays out the rows;
+        returns the per-request status (0 OK, else the request left the batch)."""
+        n = len(request_ids)
+        ids = (_cp * max(n, 1))(*[r.encode() for r in request_ids])
+        lens = (_ll * max(n, 1))(*next_lens)
+        status = (ctypes.c_int32 * max(n, 1))()
+        _check(self._lib.rlse_st_prepare(self._h, bm._h, ids, lens, n, status))
+        return list(status[:n])
+
+    def host(self):
+        """(tables [max_batch][max_blocks_per_seq], seq_lens [max_batch], batch,
+        pending (row, col, page) triples) as numpy copies."""
+        import numpy as np
+        t, l, p = _ip(), _ip(), _ip()
+        b, n = _i(), _i()
+        _check(self._lib.rlse_st_host(self._h, ctypes.byref(t), ctypes.byref(l), ctypes.byref(b),
+                                      ctypes.byref(p), ctypes.byref(n)))
+        tables = np.ctypeslib.as_array(t, (self.max_batch, self.max_blocks_per_seq)).copy()
+        lens = np.ctypeslib.as_array(l, (self.max_batch,)).copy()
+        pend = (np.ctypeslib.as_array(p, (n.value, 3)).copy() if n.value
+                else np.zeros((0, 3), np.int32))
+        return tables, lens, b.value, pend
+
+    def upload(self, tables, seq_lens, stream=None) -> None:
+        _check(self._lib.rlse_st_upload(self._h, _ptr(tables), _ptr(seq_lens), _stream(stream)))
+
+    def mark_uploaded(self) -> None:
+        _check(self._lib.rlse_st_mark_uploaded(self._h))
+
+    def reset(self) -> None:
+        _check(self._lib.rlse_st_reset(self._h))
 
 
 def memory_charge(shape: ModelShape, prompt_tokens: int, max_tokens: int) -> Tuple[int, int, int]:

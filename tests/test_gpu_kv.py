@@ -337,3 +337,75 @@ def test_prefix_cache_restore_reads_back_the_cached_prefix(kv):
     np.testing.assert_array_equal(to_host(vo), va[:, :, :64])
     cache.close()
     pool.close()
+
+
+def test_step_table_uploads_match_host_and_feed_decode(kv):
+    """The change-only upload (rlse_st_upload: pinned staging, one copy, one
+    scatter kernel) over 24 steps of joins, growth, forks and finishes: the
+    device rows equal the host image in every valid entry, the lengths match,
+    and decode through the uploaded tables equals decode through a full upload
+    of the same image, bit for bit."""
+    import random
+    rnd = random.Random(11)
+    hq, hkv, d, dtype = 16, 8, 128, "bf16"
+    nb, B, W = 300, 16, 64
+    bm = kv.BlockManager(nb)
+    st = kv.StepTables(B, W)
+    dev_tables = torch.full((B, W), -1, dtype=torch.int32, device=DEV)
+    dev_lens = torch.zeros(B, dtype=torch.int32, device=DEV)
+    rng = np.random.default_rng(4)
+    kp = to_dev(random_values(rng, (nb, hkv, 16, d), dtype), dtype)
+    vp = to_dev(random_values(rng, (nb, hkv, 16, d), dtype), dtype)
+    q = to_dev(random_values(rng, (B, hq, d), dtype), dtype)
+    live, order, nid = {}, [], 0
+    for step in range(24):
+        while len(order) < B and rnd.random() < 0.5:
+            rid = f"r{nid}"
+            nid += 1
+            try:
+                if order and rnd.random() < 0.3:
+                    parent = rnd.choice(order)
+                    n = rnd.randint(1, live[parent])
+                    bm.fork(parent, rid, n)
+                else:
+                    n = rnd.randint(1, 600)
+                    bm.allocate(rid, n)
+            except kv.CachePressure:
+                continue
+            live[rid] = n
+            order.append(rid)
+        if rnd.random() < 0.25 and len(order) > 1:
+            i = rnd.randrange(len(order))
+            bm.release(order[i])
+            del live[order[i]]
+            order[i] = order[-1]
+            order.pop()
+        next_lens = [min(live[r] + 1, W * 16) for r in order]
+        status = st.prepare(bm, order, next_lens)
+        tables, lens, batch, pend = st.host()
+        print(f"step {step}: batch {batch}, {len(pend)} triples", flush=True)
+        st.upload(dev_tables, dev_lens)
+        torch.cuda.synchronize()
+        got_t, got_l = to_host(dev_tables), to_host(dev_lens)
+        np.testing.assert_array_equal(got_l[:batch], lens[:batch])
+        for i in range(batch):
+            n = -(-int(lens[i]) // 16)
+            np.testing.assert_array_equal(got_t[i, :n], tables[i, :n], err_msg=f"row {i}")
+        if step in (8, 23) and batch:
+            out_a = torch.empty_like(q)
+            out_b = torch.empty_like(q)
+            kv.paged_gqa_decode(q, kp, vp, dev_tables, dev_lens, out_a, batch, hq, hkv, d, W, nb,
+                                0.0883, dtype)
+            kv.paged_gqa_decode(q, kp, vp, to_dev(tables), to_dev(lens), out_b, batch, hq, hkv,
+                                d, W, nb, 0.0883, dtype)
+            np.testing.assert_array_equal(to_host(out_a)[:batch], to_host(out_b)[:batch])
+        keep = []
+        for r, s_, nl in zip(order, status, next_lens):
+            if s_ == 0:
+                live[r] = nl
+                keep.append(r)
+            else:
+                del live[r]
+        order = keep
+    bm.release_all()
+    st.close()
