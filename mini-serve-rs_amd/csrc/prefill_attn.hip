@@ -28,8 +28,11 @@
 // accumulator layout and feed
 //   O^T (d x queries) += V^T (d x keys) . P^T (keys x queries)
 // directly as the B operand; the keys of each 16-key MFMA block are taken in
-// the order the accumulator holds them, and V^T is laid out in LDS in that
-// same order so its A operand is one 16-byte read.
+// the order the accumulator holds them (lane half h: keys 4h..4h+3 and
+// 8+4h..11+4h). V is staged in LDS row-major, as K is, and its V^T A operand
+// is read with two ds_read_b64_tr_b16: within each 16-lane group, lane 4j+a
+// points at key row j, columns 4a..4a+3, and lane 4a+e receives column 4a+e
+// of the four key rows -- four consecutive keys of one dimension.
 #include <math.h>
 
 #include "common.cuh"
@@ -42,7 +45,10 @@ constexpr int kPWaves = 4;
 constexpr int kPThreads = 64 * kPWaves;
 constexpr int kBM = 32 * kPWaves;  // rows per workgroup
 constexpr int kBN = 64;            // keys per tile
-constexpr int kPad = 8;            // LDS row padding (elements): conflict-free 16-byte reads
+// LDS row padding (elements): K rows are read as 16-byte packets, V rows by
+// transposing 8-byte reads; these paddings keep both free of bank conflicts.
+constexpr int kPadK = 8;
+constexpr int kPadV = 16;
 constexpr int kMinKeysPerSplit = 512;
 constexpr int kMaxSplits = 16;
 constexpr int kMaxSplitPages = 1024;  // page ids of a split staged in LDS (16384 keys)
@@ -53,6 +59,8 @@ constexpr float kLazyLog2 = 8.f;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 // 16-byte packets are staged as u32x4_t, a native vector, so copies are
 // vector loads and stores (HIP's uint4 struct is copied with memcpy, which
 // keeps an array of them in scratch memory when it is later written to LDS).
@@ -94,12 +102,6 @@ __device__ __forceinline__ float4* part_block(const PrefillParams& p, int sp, in
   return reinterpret_cast<float4*>(p.part) + wgi * (4 * (D / 32) + 1) * kPThreads;
 }
 
-// Position of actual key a (0..15) of a 16-key MFMA block in the order the
-// S^T accumulator holds it: lane half h owns keys 4h..4h+3 and 8+4h..11+4h.
-__device__ __forceinline__ int key_slot(int a) {
-  return ((a >> 2) & 1) * 8 + (a >> 3) * 4 + (a & 3);
-}
-
 template <typename T, int D>
 __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) {
   constexpr int KB = D / 16;                  // 16-wide k-blocks of q.k
@@ -108,8 +110,8 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
   constexpr int KPK = kBN * CPR;              // K packets per tile
   constexpr int KPT = KPK / kPThreads;        // per thread
   static_assert(KPK % kPThreads == 0, "K tile must split evenly");
-  __shared__ __align__(16) uint16_t s_k[2][kBN][D + kPad];   // K rows
-  __shared__ __align__(16) uint16_t s_v[2][D][kBN + kPad];   // V^T, keys in MFMA order
+  __shared__ __align__(16) uint16_t s_k[2][kBN][D + kPadK];  // K rows
+  __shared__ __align__(16) uint16_t s_v[2][kBN][D + kPadV];  // V rows
   __shared__ int s_valid[2];                                 // page-valid bits of the tile
   __shared__ __align__(16) int s_pages[kMaxSplitPages];      // the split's page ids (-1: invalid)
 
@@ -172,68 +174,61 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
       qreg[kb] = *reinterpret_cast<const uint4*>(qb + ((size_t)t * Hq + qh) * D + kb * 16 +
                                                  half * 8);
 
-    const int last_tile = k_begin + ((k_end - 1 - k_begin) / kBN) * kBN;
-    static_assert(kBN == 64 && kPWaves == 4, "a tile spans 4 pages, one per wave");
-    u32x4_t kst[KPT], vst[4];
+   const int last_tile = k_begin + ((k_end - 1 - k_begin) / kBN) * kBN;
+    static_assert(kBN == 64, "a tile spans 4 pages");
+    // Packet u of this thread: key kk of the tile, 16-byte chunk dc of its
+    // row. Its page, kk >> 4, is the same for the whole wave; its offset in
+    // the page tile is a per-lane constant.
+    int voff[KPT], pg_of[KPT];
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int pk = tid + u * kPThreads;
+      const int kk = pk / CPR, dc = pk - kk * CPR;
+      voff[u] = (((kk & 15) * D) + dc * 8) * (int)sizeof(T);
+      pg_of[u] = __builtin_amdgcn_readfirstlane(kk >> 4);
+    }
+    u32x4_t kst[KPT], vst[KPT];
     int4 pid;  // page ids of the tile's 4 pages (-1: invalid), for the valid bits
-    // Page id of page i of the tile at kt, read per lane from the staged
-    // table (no branches), invalid ids replaced by page 0.
-    auto page_of = [&](int kt, int i) __attribute__((always_inline)) {
-      const int r = s_pages[((kt - k_begin) >> 4) + i];
-      return r < 0 ? 0 : r;
-    };
-    // V copy: wave w copies page w of the tile; lane = (dims chunk dc, group
-    // of 4 keys kgl). Lanes past the row (d = 64) repeat the last chunk and
-    // skip the LDS write.
-    const int v_kgl = lane & 3, v_dc = lane >> 2;
-    const int v_dcl = v_dc < CPR ? v_dc : CPR - 1;
-    // Global loads of the tile at kt. Every address is in bounds: page
-    // indices past the context read the last page and invalid page ids read
-    // page 0; those keys are masked in the math.
+    // Global loads of the tile at kt: raw buffer loads through a descriptor
+    // of the packet's (page, head) tile, built in scalar registers. An
+    // invalid page id gets a descriptor of zero records (zeros, no memory
+    // access); page indices past the context read the last page; both are
+    // masked in the math.
+    const size_t tile_elems = (size_t)16 * D;
     auto load_tile = [&](int kt) __attribute__((always_inline)) {
       pid = *reinterpret_cast<const int4*>(&s_pages[(kt - k_begin) >> 4]);
 #pragma unroll
       for (int u = 0; u < KPT; ++u) {
-        // Packet u of this thread: key kk of the tile (its page is
-        // wave-uniform: kk >> 4 = (tid + 256u) / (16 * CPR)), chunk dc.
-        const int pk = tid + u * kPThreads;
-        const int kk = pk / CPR, dc = pk - kk * CPR;
-        const int id = page_of(kt, kk >> 4);
-        kst[u] = *reinterpret_cast<const u32x4_t*>(
-            kp + (((size_t)id * Hkv + h) * 16 + (kk & 15)) * D + dc * 8);
+        const int r = __builtin_amdgcn_readfirstlane(s_pages[((kt - k_begin) >> 4) + pg_of[u]]);
+        const size_t tb = ((size_t)(r < 0 ? 0 : r) * Hkv + h) * tile_elems;
+        const int nrec = r < 0 ? 0 : (int)(tile_elems * sizeof(T));
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kp + tb), 0, nrec,
+                                                          kBufferWord3);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vp + tb), 0, nrec,
+                                                          kBufferWord3);
+        kst[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, voff[u], 0, 0);
+        vst[u] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff[u], 0, 0);
       }
-      const int vid = page_of(kt, wave);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        vst[j] = *reinterpret_cast<const u32x4_t*>(
-            vp + (((size_t)vid * Hkv + h) * 16 + v_kgl * 4 + j) * D + v_dcl * 8);
     };
-    // Staged registers -> LDS buffer bf: K rows as they are, V transposed
-    // with each 16-key block's keys in accumulator order.
+    // Staged registers -> LDS buffer bf: K and V rows as they are.
     auto store_tile = [&](int bf) __attribute__((always_inline)) {
 #pragma unroll
       for (int u = 0; u < KPT; ++u) {
         const int pk = tid + u * kPThreads;
         const int kk = pk / CPR, dc = pk - kk * CPR;
         *reinterpret_cast<u32x4_t*>(&s_k[bf][kk][dc * 8]) = kst[u];
-      }
-      if (v_dc < CPR) {
-        const int slot = wave * 16 + key_slot(v_kgl * 4);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          // Element e of each of the 4 keys: the low or high half of word e/2.
-          const int wi = e >> 1;
-          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t k01 = __builtin_amdgcn_perm(vst[1][wi], vst[0][wi], sel);
-          const uint32_t k23 = __builtin_amdgcn_perm(vst[3][wi], vst[2][wi], sel);
-          *reinterpret_cast<uint2*>(&s_v[bf][v_dc * 8 + e][slot]) = make_uint2(k01, k23);
-        }
+        *reinterpret_cast<u32x4_t*>(&s_v[bf][kk][dc * 8]) = vst[u];
       }
       if (tid == 0) {
         s_valid[bf] = (pid.x >= 0 ? 1 : 0) | (pid.y >= 0 ? 2 : 0) | (pid.z >= 0 ? 4 : 0) |
                       (pid.w >= 0 ? 8 : 0);
       }
     };
+    // V^T operand reads: lane = (group g of 16, j = key row in the group's
+    // 4, a = 4-column block); half h = g / 2 takes keys 4h.. (first read) and
+    // 8+4h.. (second), dimension block g % 2 the columns 16 (g % 2) + 4a.
+    const int tr_g = lane >> 4, tr_j = (lane & 15) >> 2, tr_a = lane & 3;
+    const int tr_row = (tr_g >> 1) * 4 + tr_j, tr_col = (tr_g & 1) * 16 + tr_a * 4;
 
     load_tile(k_begin);
     store_tile(0);
@@ -317,9 +312,12 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(PrefillParams p) 
       for (int kq = 0; kq < 4; ++kq)
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const uint4 a =
-              *reinterpret_cast<const uint4*>(&s_v[bf][db * 32 + col][kq * 16 + half * 8]);
-          o[db] = Mfma<T>::mma(a, pk[kq], o[db]);
+          const uint16_t* v0 = &s_v[bf][kq * 16 + tr_row][db * 32 + tr_col];
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)v0);
+          const i16x4_t hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(v0 + 8 * (D + kPadV)));
+          const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+          o[db] = Mfma<T>::mma(make_uint4(l2.x, l2.y, h2.x, h2.y), pk[kq], o[db]);
         }
 
       if (!more) break;
