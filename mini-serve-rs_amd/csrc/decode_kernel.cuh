@@ -892,8 +892,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       };
       for (int c = 0; c < np && ok; c += MC) {
         uint32_t mv[MC][G], lv[MC][G], av[MC][G][DPL];
+        // With at most two records pending, polling the records themselves
+        // costs little and sees them one round trip sooner.
+        const bool poll_full = np - c <= 2;
         for (int attempt = 0;; ++attempt) {
-          if (attempt > 0) {
+          if (attempt > 0 && poll_full) {
+            if (timed_out()) {
+              ok = false;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(8);
+          } else if (attempt > 0) {
             // Not all there yet: wait on one word per record, l of the last
             // head (stored last), with one broadcast load each, before loading
             // the records again (stores to different words may land out of
