@@ -68,13 +68,28 @@ FORK = {
 }
 
 
+# Whole decode step (every op of step_decode_batch on the device):
+# (model config factory name, batch, len_lo, len_hi, description)
+E2E = {
+    "qwen3_e2e": ("qwen3_0_6b", 32, 128, 2048,
+                  "Qwen3-0.6B whole decode step: embedding, 28 layers (RMSNorm, q/k/v/o "
+                  "projections, q/k norm + RoPE + append + paged GQA decode, SwiGLU MLP), final "
+                  "norm, tied lm_head (151936), greedy argmax; B=32, cached U[128,2048] + 1, "
+                  "bf16, 16-token pages, random weights"),
+    "qwen25_e2e": ("qwen2_5_0_5b", 64, 4096, 4096,
+                   "Qwen2.5-0.5B whole decode step: embedding, 24 layers (q/k/v with bias, "
+                   "14q/2kv heads, d=64), SwiGLU MLP (4864), tied lm_head (151936), greedy "
+                   "argmax; B=64, 4096 cached + 1, bf16, 16-token pages, random weights"),
+}
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="qwen3",
-                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(FORK))
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(FORK) + sorted(E2E))
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -405,6 +420,171 @@ def fork_bench(args):
     pool.close()
 
 
+def e2e_step_bytes(cfg, lens, es):
+    """Algorithmic HBM bytes of one whole decode step: every weight read once
+    (the projections, the norms, lm_head; the tied embedding is read as
+    lm_head and its B gathered rows), each layer's decode-step bytes (K/V of
+    every attended position, the appended rows, q in / out, tables), and the
+    activations each launch reads and writes."""
+    b = len(lens)
+    h, d = cfg.hidden, cfg.head_dim
+    nq, nkv = cfg.heads * d, cfg.kv_heads * d
+    per_layer_w = (h * (nq + 2 * nkv) + nq * h + 2 * cfg.inter * h + cfg.inter * h + 2 * h) * es
+    per_layer_w += ((nq + 2 * nkv) * es if cfg.qkv_bias else 0) + (2 * d * es if cfg.qk_norm
+                                                                   else 0)
+    # activations: q/k/v/o/gate_up/down linears (in + out), two add+norm
+    # launches (x, residual read and written, out written), silu_mul
+    act = b * es * ((h + nq) + 2 * (h + nkv) + (nq + h) + (h + 2 * cfg.inter) +
+                    (cfg.inter + h) + 2 * 4 * h + 3 * cfg.inter)
+    attn = algorithmic_decode_bytes(lens, cfg.heads, cfg.kv_heads, d, es, True) - 2 * b * nq * es
+    head = cfg.vocab * h * es + b * h * es + b * cfg.vocab * es + b * cfg.vocab * es + 4 * b
+    embed = b * (4 + 2 * h * es) + 2 * b * h * es + h * es  # gather, first norm, final norm
+    return cfg.layers * (per_layer_w + act + attn) + head + embed
+
+
+def e2e_bench(args):
+    """One step = DecodeModel.step: every op of step_decode_batch for all B
+    sequences on one stream, the greedy ids of a step fed as the next step's
+    input on the device. Each step appends at the same positions (cached + 1
+    keys), as the attention-only workloads do."""
+    import numpy as np
+    import torch
+
+    import rlse_kv as kv
+    from decode_model import DecodeModel, ModelConfig
+
+    factory, b, lo, hi, desc = E2E[args.workload]
+    cfg = getattr(ModelConfig, factory)()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rng = np.random.default_rng(args.seed)
+    cached = rng.integers(lo, hi + 1, b).astype(np.int32)
+    lens = cached + 1
+    mbps = int(max((int(n) + 15) // 16 for n in lens))
+    need = int(sum((int(n) + 15) // 16 for n in lens))
+    nb = need + 64
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.zeros((b, mbps), np.int32)
+    used = 0
+    for i, n in enumerate(lens):
+        k = (int(n) + 15) // 16
+        tables[i, :k] = perm[used:used + k]
+        used += k
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    bf = torch.bfloat16
+    h, d = cfg.hidden, cfg.head_dim
+    nq, nkv = cfg.heads * d, cfg.kv_heads * d
+
+    def mat(o, i):
+        return (torch.randn((o, i), generator=g, device=dev) / math.sqrt(i)).to(bf)
+
+    def vec(n, base=1.0, sd=0.1):
+        return (base + sd * torch.randn(n, generator=g, device=dev)).to(bf)
+
+    w = {"embed": torch.randn((cfg.vocab, h), generator=g, device=dev).to(bf), "norm": vec(h)}
+    for l in range(cfg.layers):
+        p = f"l{l}."
+        w.update({p + "in_norm": vec(h), p + "post_norm": vec(h), p + "q_w": mat(nq, h),
+                  p + "k_w": mat(nkv, h), p + "v_w": mat(nkv, h), p + "o_w": mat(h, nq),
+                  p + "gate_w": mat(cfg.inter, h), p + "up_w": mat(cfg.inter, h),
+                  p + "down_w": mat(h, cfg.inter)})
+        if cfg.qkv_bias:
+            w.update({p + "q_b": vec(nq, 0), p + "k_b": vec(nkv, 0), p + "v_b": vec(nkv, 0)})
+        if cfg.qk_norm:
+            w.update({p + "q_norm": vec(d), p + "k_norm": vec(d)})
+    model = DecodeModel(cfg, w, "bf16", nb, b, mbps, dev)
+    del w
+    t_dev = torch.from_numpy(tables).to(dev)
+    for i, n in enumerate(cached):   # cached context: N(0,1) K/V in every layer
+        kc = torch.randn((cfg.layers, cfg.kv_heads, int(n), d), generator=g, device=dev).to(bf)
+        vc = torch.randn((cfg.layers, cfg.kv_heads, int(n), d), generator=g, device=dev).to(bf)
+        model.set_kv(t_dev[i], kc, vc)
+        del kc, vc
+    lens_dev = torch.from_numpy(lens).to(dev)
+    ids = torch.from_numpy(rng.integers(0, cfg.vocab, b).astype(np.int32)).to(dev)
+    stream = torch.cuda.current_stream()
+    state = {"ids": ids}
+
+    def step():
+        _, nxt = model.step(state["ids"], t_dev, lens_dev, b, stream)
+        state["ids"] = nxt
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ev_steps = min(args.steps, 20)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(ev_steps)]
+    for a, e in ev:
+        a.record(stream)
+        step()
+        e.record(stream)
+    torch.cuda.synchronize()
+    step_ms = float(np.mean([a.elapsed_time(e) for a, e in ev]))
+    per_step = e2e_step_bytes(cfg, lens, 2)
+    achieved = per_step / (step_ms * 1e-3) / 1e9
+    result = {
+        "metric": f"whole decode step tokens/sec at {factory} shape, 1 GPU",
+        "value": b * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": elapsed * 1e3 / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: random-init weights of the architecture, N(0,1) cached K/V, "
+                "seeded random page permutation",
+        "config": {"workload": desc, "batch": b, "layers": cfg.layers,
+                   "mean_keys": float(np.mean(lens)), "pages_per_layer": need,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "kernel": "whole step (all launches of DecodeModel.step)",
+                     "bytes_per_step": per_step, "avg_step_ms": step_ms,
+                     "timed_steps": ev_steps},
+        "cpu_baseline": None,
+    }
+    model.close()
+    if not args.no_cpu:
+        result["cpu_baseline"] = e2e_cpu_baseline(args, cfg, cached)
+    print(json.dumps(result))
+
+
+def e2e_cpu_baseline(args, cfg, cached):
+    """The oracle's model_step_ref in f32 (the reference CPU path's dtype:
+    numpy products, the C restatement of the attention) for one step of a
+    bounded subset of the batch's sequences, with the same cached lengths."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    spec = O.ModelSpec(cfg.hidden, cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                       cfg.inter, cfg.vocab, cfg.eps, cfg.theta, cfg.qk_norm, cfg.qkv_bias,
+                       cfg.tied)
+    rng = np.random.default_rng(7)
+    w = O.random_weights(spec, rng, "f32")
+    sub = [int(n) for n in cached[:4]]
+    tile = rng.standard_normal((cfg.kv_heads, 1, cfg.head_dim)).astype(np.float32)
+    kc = [[np.ascontiguousarray(np.broadcast_to(tile, (cfg.kv_heads, n, cfg.head_dim)))
+           for n in sub] for _ in range(cfg.layers)]
+    vc = [[x.copy() for x in row] for row in kc]
+    cos_t, sin_t = O.rope_tables_f32(cfg.theta, cfg.head_dim, max(sub) + 2)
+    ids = list(rng.integers(0, cfg.vocab, len(sub)))
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        O.model_step_ref(spec, w, ids, kc, vc, cos_t, sin_t, "f32")
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or steps >= 5:
+            break
+    return {"value": len(sub) * steps / el, "unit": "tokens/s", "cores": O.max_threads(),
+            "kind": "port",
+            "sample": f"{steps} whole step(s) of {len(sub)} of the sequences (cached "
+                      f"{sub}), f32, in {el:.2f} s"}
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -419,6 +599,9 @@ def main():
         return
     if args.workload in FORK:
         fork_bench(args)
+        return
+    if args.workload in E2E:
+        e2e_bench(args)
         return
     import numpy as np
     import torch

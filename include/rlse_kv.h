@@ -251,6 +251,38 @@ int launch_paged_gqa_decode_tiled_bf16(const void* d_q, const void* d_k_pool,
                                        int max_blocks_per_seq, float scale);
 
 /* ------------------------------------------------------------------ */
+/* The rest of a batched decode step on the device: the ops of         */
+/* ModelForCausalLM::step_decode_batch (src/backends/qwen2.rs:628-764) */
+/* around rlse_decode_step, so activations and logits stay in HBM.     */
+/* Element-wise ops round as Candle's per-op bf16/f16 arithmetic does. */
+/* ------------------------------------------------------------------ */
+/* embed_tokens (qwen2.rs:651-652): out[b] = table[ids[b]], rows of hidden
+ * elements (hidden * dtype bytes a multiple of 16); an id outside [0, vocab)
+ * gives a zero row. */
+int rlse_embedding(const int32_t* ids, const void* table, void* out, int batch, int hidden,
+                   int vocab, int dtype, rlse_stream_t stream);
+/* A residual add followed by an RmsNorm (qwen2.rs:748-756, and the next
+ * layer's input_layernorm :665-667): residual <- residual + x (rounded),
+ * out <- RmsNorm(residual) * weight, RmsNorm::forward's cast order. */
+int rlse_add_rmsnorm(const void* x, void* residual, const void* weight, void* out, int rows,
+                     int n, float eps, int dtype, rlse_stream_t stream);
+/* MLP activation (qwen2.rs:170-175): gate_up = [rows][2*inter], gate columns
+ * then up columns; out = silu(gate) * up with silu(v) = v / (1 + exp(-v)). */
+int rlse_silu_mul(const void* gate_up, void* out, int rows, int inter, int dtype,
+                  rlse_stream_t stream);
+/* Greedy branch of sample_token (src/backends/candle.rs:737-751) on the
+ * device: per row the first maximum; NaNs never win, except a NaN at index
+ * 0, which wins outright (the host Tensor::argmax scan). */
+int rlse_argmax(const void* logits, int32_t* out, int rows, int vocab, int dtype,
+                rlse_stream_t stream);
+/* Linear (q/k/v/o_proj, gate/up/down_proj, lm_head; qwen2.rs:233-252,
+ * 153-158): y[rows][out] = x[rows][in] . W[out][in]^T through rocBLAS
+ * gemm_ex with f32 accumulation, rounded once; bias (may be NULL) added
+ * after, rounded again, as Candle's broadcast_add after the matmul. */
+int rlse_linear(const void* x, const void* weight, const void* bias, void* y, int rows,
+                int out_features, int in_features, int dtype, rlse_stream_t stream);
+
+/* ------------------------------------------------------------------ */
 /* Host block manager: the physical successor of KVCache               */
 /* (src/cache/kv_cache.rs:15-145) with per-block refcounts for prefix  */
 /* sharing. Ids pop in ascending order from a free stack (kv_cache.rs: */

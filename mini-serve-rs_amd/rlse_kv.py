@@ -67,6 +67,7 @@ EXPORTED = (
     "rlse_memory_charge",
     "rlse_bm_release_all", "rlse_st_create", "rlse_st_destroy", "rlse_st_reset",
     "rlse_st_prepare", "rlse_st_host", "rlse_st_upload", "rlse_st_mark_uploaded",
+    "rlse_embedding", "rlse_add_rmsnorm", "rlse_silu_mul", "rlse_argmax", "rlse_linear",
 )
 
 
@@ -227,6 +228,11 @@ _SIGS = {
                           ctypes.POINTER(_ip), ctypes.POINTER(_i)]),
     "rlse_st_upload": (_i, [_vp, _vp, _vp, _vp]),
     "rlse_st_mark_uploaded": (_i, [_vp]),
+    "rlse_embedding": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "rlse_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _i, _vp]),
+    "rlse_silu_mul": (_i, [_vp, _vp, _i, _i, _i, _vp]),
+    "rlse_argmax": (_i, [_vp, _vp, _i, _i, _i, _vp]),
+    "rlse_linear": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -759,3 +765,32 @@ def qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, eps: float, cos_t
         num_seqs, _ptr(seq_index), num_tokens, num_heads, num_kv_heads, head_dim,
         max_blocks_per_seq, num_blocks, _ptr(q_out), _ptr(k_pool), _ptr(v_pool), _dt(dtype),
         _stream(stream)))
+
+
+# --------------------------------------------------------------------------
+# The rest of a decode step (step_decode_batch ops around rlse_decode_step)
+# --------------------------------------------------------------------------
+def embedding(ids, table, out, batch: int, hidden: int, vocab: int, dtype, stream=None) -> None:
+    _check(load().rlse_embedding(_ptr(ids), _ptr(table), _ptr(out), batch, hidden, vocab,
+                                 _dt(dtype), _stream(stream)))
+
+
+def add_rmsnorm(x, residual, weight, out, rows: int, n: int, eps: float, dtype,
+                stream=None) -> None:
+    _check(load().rlse_add_rmsnorm(_ptr(x), _ptr(residual), _ptr(weight), _ptr(out), rows, n,
+                                   eps, _dt(dtype), _stream(stream)))
+
+
+def silu_mul(gate_up, out, rows: int, inter: int, dtype, stream=None) -> None:
+    _check(load().rlse_silu_mul(_ptr(gate_up), _ptr(out), rows, inter, _dt(dtype),
+                                _stream(stream)))
+
+
+def argmax(logits, out, rows: int, vocab: int, dtype, stream=None) -> None:
+    _check(load().rlse_argmax(_ptr(logits), _ptr(out), rows, vocab, _dt(dtype), _stream(stream)))
+
+
+def linear(x, weight, bias, y, rows: int, out_features: int, in_features: int, dtype,
+           stream=None) -> None:
+    _check(load().rlse_linear(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), rows, out_features,
+                              in_features, _dt(dtype), _stream(stream)))

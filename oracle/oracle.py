@@ -454,3 +454,206 @@ class PrefixCacheModel:
         else:
             self.hits += 1
             self.tokens_saved += skipped
+
+
+# ---------------------------------------------------------------------------
+# The rest of a batched decode step: ModelForCausalLM::step_decode_batch
+# (src/backends/qwen2.rs:628-764), numpy.
+#
+# Values of every dtype are held as float32 arrays; ``round_to`` rounds a
+# float32 result to the tensor dtype (round to nearest even), which is what
+# Candle's element-wise ops do on bf16/f16 tensors: each op computes in f32
+# (half 2.7.1's bf16/f16 arithmetic converts both operands to f32) and stores
+# its result in the tensor dtype. The reference runs f32 on the CPU
+# (src/backends/candle.rs:185), where ``round_to`` is the identity.
+# The element-wise rules live in candle-core 0.11.0 / candle-nn 0.11.0
+# (Cargo.lock), which are not vendored: they are restated from their
+# published sources and pinned by closed forms in tests/test_oracle_model.py.
+# ---------------------------------------------------------------------------
+DTYPES = ("f32", "bf16", "f16")
+
+
+def round_to(x, dt: str) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float32)
+    if dt == "f32":
+        return x
+    if dt == "bf16":
+        return round_bf16(x)
+    if dt == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    raise ValueError(dt)
+
+
+def embedding_ref(ids, table: np.ndarray) -> np.ndarray:
+    """candle_nn::Embedding::forward (qwen2.rs:651-652): rows of the table
+    by token id. The reference rejects an id outside [0, vocab) with an
+    index error; the device op writes a zero row for it, which is what this
+    returns."""
+    ids = np.asarray(ids, dtype=np.int64)
+    out = np.zeros((len(ids), table.shape[1]), dtype=np.float32)
+    ok = (ids >= 0) & (ids < table.shape[0])
+    out[ok] = table[ids[ok]]
+    return out
+
+
+def rmsnorm_ref(x: np.ndarray, w: np.ndarray, eps: float, dt: str) -> np.ndarray:
+    """RmsNorm::forward (qwen2.rs:68-75): in f32, variance = sum(x^2) * (1/n),
+    norm = sqrt(variance + eps), x / norm cast to the dtype, then the weight
+    product in the dtype."""
+    x = np.asarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    ss = np.zeros(x.shape[:-1], dtype=np.float32)
+    for i in range(n):                      # sequential f32 sum, as the C oracle
+        ss = ss + x[..., i] * x[..., i]
+    norm = np.sqrt(ss * np.float32(1.0 / n) + np.float32(eps)).astype(np.float32)
+    xn = round_to(x / norm[..., None], dt)
+    return round_to(xn * np.asarray(w, np.float32), dt)
+
+
+def add_rmsnorm_ref(x: np.ndarray, residual: np.ndarray, w: np.ndarray, eps: float, dt: str):
+    """`xs_mid = residual + attn_proj` then post_attention_layernorm
+    (qwen2.rs:748-753), and `xs = xs_mid + mlp_out` then the next layer's
+    input_layernorm (:756, :665-667): returns (sum, normed sum)."""
+    h = round_to(np.asarray(residual, np.float32) + np.asarray(x, np.float32), dt)
+    return h, rmsnorm_ref(h, w, eps, dt)
+
+
+def silu_ref(g: np.ndarray, dt: str) -> np.ndarray:
+    """Activation::Silu, candle-core's unary op: v / (1 + exp(-v)), each of
+    exp, the sum and the quotient rounded to the dtype."""
+    g = np.asarray(g, np.float32)
+    with np.errstate(over="ignore"):
+        e = round_to(np.exp(-g), dt)
+    den = round_to(np.float32(1.0) + e, dt)
+    return round_to(g / den, dt)
+
+
+def silu_mul_ref(gate: np.ndarray, up: np.ndarray, dt: str) -> np.ndarray:
+    """MLP::forward (qwen2.rs:170-175) between the projections:
+    act(gate_proj(x)) * up_proj(x), the product rounded."""
+    return round_to(silu_ref(gate, dt) * np.asarray(up, np.float32), dt)
+
+
+def linear_ref(x: np.ndarray, w: np.ndarray, b, dt: str) -> np.ndarray:
+    """candle_nn::Linear::forward: x . W^T, the exact product (float64, one
+    rounding to the dtype), then + bias rounded again (broadcast_add)."""
+    y = round_to(np.asarray(x, np.float64) @ np.asarray(w, np.float64).T, dt)
+    if b is not None:
+        y = round_to(y + np.asarray(b, np.float32), dt)
+    return y
+
+
+def argmax_ref(logits: np.ndarray) -> np.ndarray:
+    """Greedy branch of sample_token (src/backends/candle.rs:737-751):
+    Tensor::argmax(0) of the f32 logits, candle-core's CPU index reduction --
+    start at index 0 and move to i only when value[i] > the current best, so
+    ties keep the first index, a NaN is never taken, and a NaN at index 0 is
+    never left. Per row of a [rows, vocab] array."""
+    logits = np.atleast_2d(np.asarray(logits, np.float32))
+    out = np.zeros(logits.shape[0], dtype=np.int32)
+    for r, row in enumerate(logits):
+        best, idx = row[0], 0
+        for i in range(1, len(row)):
+            if row[i] > best:
+                best, idx = row[i], i
+        out[r] = idx
+    return out
+
+
+def rope_ref(x: np.ndarray, pos, cos_t: np.ndarray, sin_t: np.ndarray, dt: str) -> np.ndarray:
+    """Batched RoPE of step_decode_batch (qwen2.rs:701-719): x * cos +
+    rotate_half(x) * sin with the tables' rows at each position, both
+    products and the sum rounded to the dtype. x [rows, d]; cos_t, sin_t
+    [max_pos, d/2] already in the dtype."""
+    x = np.asarray(x, np.float32)
+    half = x.shape[-1] // 2
+    c = np.asarray(cos_t, np.float32)[np.asarray(pos)]
+    s = np.asarray(sin_t, np.float32)[np.asarray(pos)]
+    c2, s2 = np.concatenate([c, c], -1), np.concatenate([s, s], -1)
+    rot = np.concatenate([-x[..., half:], x[..., :half]], -1)
+    return round_to(round_to(x * c2, dt) + round_to(rot * s2, dt), dt)
+
+
+class ModelSpec:
+    """Shape of a Qwen2/Qwen3 decoder (the fields of qwen2.rs Config that the
+    decode step reads)."""
+
+    def __init__(self, hidden, layers, heads, kv_heads, head_dim, inter, vocab, eps=1e-6,
+                 theta=1e6, qk_norm=True, qkv_bias=False, tied=True):
+        self.hidden, self.layers, self.heads, self.kv_heads = hidden, layers, heads, kv_heads
+        self.head_dim, self.inter, self.vocab, self.eps = head_dim, inter, vocab, eps
+        self.theta, self.qk_norm, self.qkv_bias, self.tied = theta, qk_norm, qkv_bias, tied
+
+
+def random_weights(spec: ModelSpec, rng, dt: str) -> Dict[str, np.ndarray]:
+    """Seeded random weights of the architecture, scaled 1/sqrt(fan_in) so
+    activations stay O(1), norms 1 + 0.1 N(0,1); values rounded to dt."""
+    h, d = spec.hidden, spec.head_dim
+    nq, nkv = spec.heads * d, spec.kv_heads * d
+
+    def mat(o, i):
+        return round_to(rng.standard_normal((o, i)).astype(np.float32) / np.sqrt(i), dt)
+
+    def vec(n, base, sd):
+        return round_to(base + sd * rng.standard_normal(n).astype(np.float32), dt)
+
+    w = {"embed": round_to(rng.standard_normal((spec.vocab, h)).astype(np.float32), dt),
+         "norm": vec(h, 1.0, 0.1)}
+    w["lm_head"] = w["embed"] if spec.tied else mat(spec.vocab, h)
+    for l in range(spec.layers):
+        p = f"l{l}."
+        w[p + "in_norm"] = vec(h, 1.0, 0.1)
+        w[p + "post_norm"] = vec(h, 1.0, 0.1)
+        w[p + "q_w"], w[p + "k_w"], w[p + "v_w"] = mat(nq, h), mat(nkv, h), mat(nkv, h)
+        if spec.qkv_bias:
+            w[p + "q_b"], w[p + "k_b"], w[p + "v_b"] = vec(nq, 0, .1), vec(nkv, 0, .1), \
+                vec(nkv, 0, .1)
+        if spec.qk_norm:
+            w[p + "q_norm"], w[p + "k_norm"] = vec(d, 1.0, 0.1), vec(d, 1.0, 0.1)
+        w[p + "o_w"] = mat(h, nq)
+        w[p + "gate_w"], w[p + "up_w"] = mat(spec.inter, h), mat(spec.inter, h)
+        w[p + "down_w"] = mat(h, spec.inter)
+    return w
+
+
+def model_step_ref(spec: ModelSpec, w: Dict[str, np.ndarray], ids, k_cache, v_cache,
+                   cos_t: np.ndarray, sin_t: np.ndarray, dt: str) -> np.ndarray:
+    """One batched decode step (step_decode_batch, qwen2.rs:628-764): token
+    ids[b] of sequence b at position len(k_cache[l][b]) along axis 1. Appends
+    each layer's new K/V rows to k_cache[l][b] / v_cache[l][b] ([Hkv, len, d]
+    float32 arrays of dt values, replaced in the lists) and returns the
+    logits [B, vocab]. Attention over dt-valued q/K/V is the C restatement in
+    f32 with its output rounded once to the dtype."""
+    b_sz = len(ids)
+    d, hq, hkv = spec.head_dim, spec.heads, spec.kv_heads
+    scale = 1.0 / math.sqrt(d)
+    pos = np.array([k_cache[0][b].shape[1] for b in range(b_sz)], dtype=np.int64)
+    xs = embedding_ref(ids, w["embed"])
+    for l in range(spec.layers):
+        p = f"l{l}."
+        residual = xs
+        hn = rmsnorm_ref(xs, w[p + "in_norm"], spec.eps, dt)
+        q = linear_ref(hn, w[p + "q_w"], w.get(p + "q_b"), dt).reshape(b_sz, hq, d)
+        k = linear_ref(hn, w[p + "k_w"], w.get(p + "k_b"), dt).reshape(b_sz, hkv, d)
+        v = linear_ref(hn, w[p + "v_w"], w.get(p + "v_b"), dt).reshape(b_sz, hkv, d)
+        if spec.qk_norm:
+            q = rmsnorm_ref(q, w[p + "q_norm"], spec.eps, dt)
+            k = rmsnorm_ref(k, w[p + "k_norm"], spec.eps, dt)
+        attn = np.empty((b_sz, hq, d), dtype=np.float32)
+        for b in range(b_sz):
+            qb = rope_ref(q[b], np.full(hq, pos[b]), cos_t, sin_t, dt)
+            kb = rope_ref(k[b], np.full(hkv, pos[b]), cos_t, sin_t, dt)
+            k_cache[l][b] = np.concatenate([k_cache[l][b], kb[:, None]], axis=1)
+            v_cache[l][b] = np.concatenate([v_cache[l][b], v[b][:, None]], axis=1)
+            n = k_cache[l][b].shape[1]
+            attn[b] = decode_batch_f32(qb[None], k_cache[l][b][None], v_cache[l][b][None],
+                                       np.array([n], np.int32), scale)[0]
+        attn = round_to(attn, dt).reshape(b_sz, hq * d)
+        o = linear_ref(attn, w[p + "o_w"], None, dt)
+        xs_mid, hn = add_rmsnorm_ref(o, residual, w[p + "post_norm"], spec.eps, dt)
+        gate = linear_ref(hn, w[p + "gate_w"], None, dt)
+        up = linear_ref(hn, w[p + "up_w"], None, dt)
+        mlp = linear_ref(silu_mul_ref(gate, up, dt), w[p + "down_w"], None, dt)
+        xs = round_to(xs_mid + mlp, dt)
+    xs = rmsnorm_ref(xs, w["norm"], spec.eps, dt)
+    return linear_ref(xs, w["lm_head"], None, dt)

@@ -1,0 +1,257 @@
+"""The rest of the decode step on the GPU against the oracle.
+
+Reference: ModelForCausalLM::step_decode_batch (src/backends/qwen2.rs:628-764)
+and the greedy branch of sample_token (src/backends/candle.rs:737-751). Each
+device op (rlse_embedding, rlse_add_rmsnorm, rlse_silu_mul, rlse_linear,
+rlse_argmax) is checked against its oracle restatement
+(oracle/oracle.py ``*_ref``, pinned in test_oracle_model.py), then whole
+steps of small Qwen3- and Qwen2-style decoders run through DecodeModel
+against model_step_ref.
+
+Bars: embedding, argmax and the residual sums bit-exact; the normalised and
+activated values within a few units in the last place of the dtype, as
+bounded at each test (the sum of squares runs in another order and exp comes
+from another math library); linear and whole-step outputs max-abs 2e-3 (f32)
+and 2e-2 (bf16/f16) relative to the largest reference magnitude, the
+relative error printed beside the max-abs one.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import DEV, TOL, build_tables, err_report
+
+pytestmark = pytest.mark.gpu
+
+_T = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+ULP = {"f32": 2.0 ** -23, "bf16": 2.0 ** -7, "f16": 2.0 ** -10}
+
+
+def dev(a, dt):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV).to(_T[dt])
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def rel_check(name, got, want, dt, bar=None):
+    mx, rel = err_report(got, want)
+    print(f"[{name}] dtype={dt} max_abs={mx:.3e} rel={rel:.3e}")
+    assert np.isfinite(got).all()
+    assert rel <= (TOL[dt] if bar is None else bar), (name, mx, rel)
+
+
+@pytest.mark.parametrize("dt", O.DTYPES)
+def test_embedding_rows_bit_exact(kv, dt):
+    rng = np.random.default_rng(1)
+    table = O.round_to(rng.standard_normal((300, 128)), dt)
+    ids = np.array([5, 0, 299, -1, 300, 17, 17], np.int32)
+    out = torch.full((len(ids), 128), 7.0, dtype=_T[dt], device=DEV)
+    kv.embedding(torch.from_numpy(ids).to(DEV), dev(table, dt), out, len(ids), 128, 300, dt)
+    np.testing.assert_array_equal(host(out), O.embedding_ref(ids, table))
+
+
+@pytest.mark.parametrize("dt", O.DTYPES)
+@pytest.mark.parametrize("rows,n", [(1, 64), (7, 896), (33, 1024), (5, 4096)])
+def test_add_rmsnorm_matches_oracle(kv, dt, rows, n):
+    rng = np.random.default_rng(rows * n)
+    x = O.round_to(rng.standard_normal((rows, n)), dt)
+    r = O.round_to(2 * rng.standard_normal((rows, n)), dt)
+    w = O.round_to(1 + 0.1 * rng.standard_normal(n), dt)
+    xd, rd, out = dev(x, dt), dev(r, dt), torch.empty((rows, n), dtype=_T[dt], device=DEV)
+    kv.add_rmsnorm(xd, rd, dev(w, dt), out, rows, n, 1e-6, dt)
+    h_want, o_want = O.add_rmsnorm_ref(x, r, w, 1e-6, dt)
+    np.testing.assert_array_equal(host(rd), h_want)           # the rounded sum: exact
+    got = host(out)
+    # The sum of squares runs in another order: its f32 relative error is at
+    # most n * 2^-24, the norm's half that; then two roundings to the dtype
+    # (x / norm, then * w) can each move an output by one ulp.
+    bound = (n * 2.0 ** -25 + 2 * ULP[dt]) * np.abs(o_want).max()
+    mx, rel = err_report(got, o_want)
+    print(f"[add_rmsnorm {rows}x{n}] dtype={dt} max_abs={mx:.3e} rel={rel:.3e}")
+    assert mx <= bound, (mx, bound)
+
+
+@pytest.mark.parametrize("dt", O.DTYPES)
+def test_silu_mul_matches_oracle(kv, dt):
+    rng = np.random.default_rng(3)
+    rows, inter = 9, 3072
+    gu = O.round_to(4 * rng.standard_normal((rows, 2 * inter)), dt)
+    gu[0, :8] = [0, -0.0, 30, -30, 88, -88, 11, -11.5]        # exp overflow edges
+    out = torch.empty((rows, inter), dtype=_T[dt], device=DEV)
+    kv.silu_mul(dev(gu, dt), out, rows, inter, dt)
+    want = O.silu_mul_ref(gu[:, :inter], gu[:, inter:], dt)
+    got = host(out)
+    diff = np.abs(got.astype(np.float64) - want)
+    # exp differs between math libraries by up to about two ulps in f32 and
+    # three roundings follow it: four f32 ulps; in bf16/f16 the f32
+    # differences can only flip a rounding, by one ulp at each of the steps.
+    ulps = 4 if dt == "f32" else 2
+    scaled = diff / (ULP[dt] * np.maximum(np.abs(want), 2.0 ** -14))
+    worst = np.unravel_index(np.argmax(scaled), scaled.shape)
+    print(f"[silu_mul] dtype={dt} max_abs={diff.max():.3e} max_ulps={scaled.max():.2f} "
+          f"mismatches={(got != want).sum()}/{got.size} worst: gate={gu[worst]!r} "
+          f"up={gu[worst[0], inter + worst[1]]!r} got={got[worst]!r} want={want[worst]!r}")
+    assert scaled.max() <= ulps
+
+
+@pytest.mark.parametrize("dt", O.DTYPES)
+@pytest.mark.parametrize("rows,n_out,n_in,bias", [(1, 2048, 1024, False), (32, 3072, 1024, True),
+                                                  (33, 896, 4864, False), (64, 1000, 128, True)])
+def test_linear_matches_oracle(kv, dt, rows, n_out, n_in, bias):
+    rng = np.random.default_rng(rows + n_out)
+    x = O.round_to(rng.standard_normal((rows, n_in)), dt)
+    w = O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt)
+    b = O.round_to(rng.standard_normal(n_out), dt) if bias else None
+    y = torch.empty((rows, n_out), dtype=_T[dt], device=DEV)
+    kv.linear(dev(x, dt), dev(w, dt), None if b is None else dev(b, dt), y, rows, n_out, n_in,
+              dt)
+    rel_check(f"linear {rows}x{n_out}x{n_in} bias={bias}", host(y), O.linear_ref(x, w, b, dt),
+              dt)
+
+
+@pytest.mark.parametrize("dt", O.DTYPES)
+def test_argmax_bit_exact_with_ties_and_nans(kv, dt):
+    rng = np.random.default_rng(4)
+    vocab = 151936
+    rows = O.round_to(rng.standard_normal((12, vocab)), dt)
+    rows[1, 1000] = rows[1, 90000] = 50.0                # tie: first index
+    rows[2, 0] = np.nan                                  # NaN at 0 wins outright
+    rows[3, 5] = np.nan
+    rows[3, 77] = 60.0                                   # later NaN never taken
+    rows[4] = -np.inf                                    # all -inf: index 0
+    rows[5, :] = np.nan
+    rows[5, 9] = -np.inf                                 # NaN at 0 again
+    rows[6, vocab - 1] = 70.0                            # maximum at the end
+    rows[7, 3:] = -np.inf
+    rows[7, :3] = [-np.inf, 2.0, 2.0]
+    out = torch.full((12,), -5, dtype=torch.int32, device=DEV)
+    kv.argmax(dev(rows, dt), out, 12, vocab, dt)
+    torch.cuda.synchronize()
+    want = O.argmax_ref(rows)
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
+    assert want[1] == 1000 and want[2] == 0 and want[3] == 77 and want[4] == 0 and \
+        want[6] == vocab - 1 and want[7] == 1
+
+
+# ------------------------------------------------------------ whole steps ---
+SPECS = {
+    "qwen3": dict(hidden=128, layers=2, heads=4, kv_heads=2, head_dim=64, inter=256,
+                  vocab=1000, qk_norm=True, qkv_bias=False, tied=True),
+    "qwen2": dict(hidden=128, layers=2, heads=14, kv_heads=2, head_dim=64, inter=192,
+                  vocab=700, theta=1e4, qk_norm=False, qkv_bias=True, tied=False),
+}
+
+
+def _setup(kv, arch, dt, ctx_lens, steps, seed):
+    from decode_model import DecodeModel, ModelConfig
+    spec = O.ModelSpec(**SPECS[arch])
+    rng = np.random.default_rng(seed)
+    w = O.random_weights(spec, rng, dt)
+    b = len(ctx_lens)
+    mbps = max((n + steps + 15) // 16 for n in ctx_lens) + 1
+    nb = b * mbps + 5
+    tables = build_tables(rng, [mbps * 16] * b, nb, mbps)
+    model = DecodeModel(ModelConfig(**SPECS[arch]), w, dt, nb, b, mbps)
+    # cached context: random K/V (already rotated), the same in pool and oracle
+    kc = [[None] * b for _ in range(spec.layers)]
+    vc = [[None] * b for _ in range(spec.layers)]
+    t_dev = torch.from_numpy(tables).to(DEV)
+    for i, n in enumerate(ctx_lens):
+        k = O.round_to(rng.standard_normal((spec.layers, spec.kv_heads, n, spec.head_dim)), dt)
+        v = O.round_to(rng.standard_normal((spec.layers, spec.kv_heads, n, spec.head_dim)), dt)
+        if n:
+            model.set_kv(t_dev[i], k, v)
+        for l in range(spec.layers):
+            kc[l][i], vc[l][i] = k[l], v[l]
+    cos_t, sin_t = O.rope_tables_f32(spec.theta, spec.head_dim, model.max_pos)
+    return spec, w, model, t_dev, kc, vc, O.round_to(cos_t, dt), O.round_to(sin_t, dt), rng
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("arch", ["qwen3", "qwen2"])
+def test_decode_steps_match_oracle(kv, arch, dt):
+    """Three steps of a 3-sequence batch with ragged cached contexts (0, 17
+    and 40 tokens); each step's ids are the GPU's greedy picks of the last
+    (teacher-forced into the oracle too). Logits, greedy ids and the K/V the
+    steps appended are checked."""
+    ctx = [0, 17, 40]
+    spec, w, model, t_dev, kc, vc, cos_t, sin_t, rng = _setup(kv, arch, dt, ctx, 3, 5)
+    ids = np.array(rng.integers(0, spec.vocab, len(ctx)), np.int32)
+    lens = np.array(ctx, np.int32)
+    for step in range(3):
+        lens = lens + 1
+        logits, nxt = model.step(torch.from_numpy(ids).to(DEV), t_dev,
+                                 torch.from_numpy(lens).to(DEV), len(ctx))
+        want = O.model_step_ref(spec, w, list(ids), kc, vc, cos_t, sin_t, dt)
+        got = host(logits)
+        rel_check(f"{arch} step {step} logits", got, want, dt)
+        g = nxt.cpu().numpy()
+        np.testing.assert_array_equal(g, O.argmax_ref(got))   # argmax of its own logits
+        # the pick is a maximum of the oracle's logits up to the bar
+        top = want.max(1)
+        assert (want[np.arange(len(g)), g] >= top - 2 * TOL[dt] * np.abs(want).max()).all()
+        ids = g.astype(np.int32)
+    for i, n in enumerate(lens):
+        k, v = model.get_kv(t_dev[i], int(n))
+        for l in range(spec.layers):
+            rel_check(f"{arch} K layer {l} seq {i}", host(k[l]), kc[l][i], dt)
+            rel_check(f"{arch} V layer {l} seq {i}", host(v[l]), vc[l][i], dt)
+    model.close()
+
+
+def test_greedy_loop_on_device_with_step_tables(kv):
+    """Tokens of one step feed the next without leaving the device; pages
+    grow through the block manager and StepTables (scheduler.rs:422-449).
+    Eight bf16 steps of four sequences from empty caches, against the oracle
+    teacher-forced on the device's picks."""
+    from decode_model import DecodeModel, ModelConfig
+    dt, arch = "bf16", "qwen3"
+    spec = O.ModelSpec(**SPECS[arch])
+    rng = np.random.default_rng(9)
+    w = O.random_weights(spec, rng, dt)
+    b, mbps, nb = 4, 4, 32
+    bm = kv.BlockManager(nb)
+    st = kv.StepTables(b, mbps)
+    model = DecodeModel(ModelConfig(**SPECS[arch]), w, dt, nb, b, mbps)
+    tables = torch.full((b, mbps), 0, dtype=torch.int32, device=DEV)
+    lens_d = torch.zeros(b, dtype=torch.int32, device=DEV)
+    reqs = [f"r{i}" for i in range(b)]
+    for r in reqs:
+        bm.allocate(r, 1)
+    ids_d = torch.from_numpy(np.array(rng.integers(0, spec.vocab, b), np.int32)).to(DEV)
+    kc = [[np.zeros((spec.kv_heads, 0, spec.head_dim), np.float32) for _ in range(b)]
+          for _ in range(spec.layers)]
+    vc = [[np.zeros((spec.kv_heads, 0, spec.head_dim), np.float32) for _ in range(b)]
+          for _ in range(spec.layers)]
+    cos_t, sin_t = O.rope_tables_f32(spec.theta, spec.head_dim, model.max_pos)
+    cos_t, sin_t = O.round_to(cos_t, dt), O.round_to(sin_t, dt)
+    stream = torch.cuda.current_stream()
+    for step in range(8):
+        # sequence i starts with a 9*i-token cached prefix; lengths grow
+        # across page boundaries as the steps go
+        n = [step + 1 + 9 * i for i in range(b)]
+        if step == 0:
+            for i, r in enumerate(reqs):
+                bm.release(r)
+                bm.allocate(r, n[i])
+        assert st.prepare(bm, reqs, n) == [0] * b
+        st.upload(tables, lens_d, stream)
+        if step == 0:
+            for i in range(1, b):
+                k = O.round_to(rng.standard_normal((spec.layers, spec.kv_heads, 9 * i,
+                                                    spec.head_dim)), dt)
+                v = O.round_to(rng.standard_normal(k.shape), dt)
+                model.set_kv(tables[i], k, v, 0, stream)
+                for l in range(spec.layers):
+                    kc[l][i], vc[l][i] = k[l], v[l]
+        ids = ids_d.cpu().numpy().copy()
+        logits, nxt = model.step(ids_d, tables, lens_d, b, stream)
+        want = O.model_step_ref(spec, w, list(ids), kc, vc, cos_t, sin_t, dt)
+        rel_check(f"greedy step {step}", host(logits), want, dt)
+        ids_d = nxt.clone()
+    assert bm.free_count() == nb - sum(bm.blocks_needed(step + 1 + 9 * i) for i in range(b))
+    model.close()
