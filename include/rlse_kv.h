@@ -263,7 +263,8 @@ int rlse_embedding(const int32_t* ids, const void* table, void* out, int batch, 
                    int vocab, int dtype, rlse_stream_t stream);
 /* A residual add followed by an RmsNorm (qwen2.rs:748-756, and the next
  * layer's input_layernorm :665-667): residual <- residual + x (rounded),
- * out <- RmsNorm(residual) * weight, RmsNorm::forward's cast order. */
+ * out <- RmsNorm(residual) * weight, RmsNorm::forward's cast order. With x
+ * NULL the residual is only normalised (not written): RmsNorm::forward. */
 int rlse_add_rmsnorm(const void* x, void* residual, const void* weight, void* out, int rows,
                      int n, float eps, int dtype, rlse_stream_t stream);
 /* MLP activation (qwen2.rs:170-175): gate_up = [rows][2*inter], gate columns
@@ -272,15 +273,50 @@ int rlse_silu_mul(const void* gate_up, void* out, int rows, int inter, int dtype
                   rlse_stream_t stream);
 /* Greedy branch of sample_token (src/backends/candle.rs:737-751) on the
  * device: per row the first maximum; NaNs never win, except a NaN at index
- * 0, which wins outright (the host Tensor::argmax scan). */
+ * 0, which wins outright (the host Tensor::argmax scan). Two launches; the
+ * workspace (rlse_argmax_workspace_size bytes, 8-byte aligned) holds one
+ * partial per 4096 logits of a row and needs no clearing. */
+int rlse_argmax_workspace_size(int rows, int vocab, size_t* bytes);
 int rlse_argmax(const void* logits, int32_t* out, int rows, int vocab, int dtype,
-                rlse_stream_t stream);
+                void* workspace, size_t workspace_bytes, rlse_stream_t stream);
 /* Linear (q/k/v/o_proj, gate/up/down_proj, lm_head; qwen2.rs:233-252,
- * 153-158): y[rows][out] = x[rows][in] . W[out][in]^T through rocBLAS
- * gemm_ex with f32 accumulation, rounded once; bias (may be NULL) added
- * after, rounded again, as Candle's broadcast_add after the matmul. */
+ * 153-158): y[rows][out] = x[rows][in] . W[out][in]^T with f32
+ * accumulation, rounded once; bias (may be NULL) added after, rounded
+ * again, as Candle's broadcast_add after the matmul. bf16/f16 with at most
+ * 64 rows (a decode step's batch), in a multiple of 32 and out a multiple of
+ * 16 run on the MFMA kernel of the three calls below; other shapes and f32
+ * go through rocBLAS gemm_ex. */
 int rlse_linear(const void* x, const void* weight, const void* bias, void* y, int rows,
                 int out_features, int in_features, int dtype, rlse_stream_t stream);
+/* The three calls below are the decode step's projections fused with their
+ * neighbours on MFMA (bf16/f16; in_features a multiple of 32; any rows,
+ * taken 64 at a time; x and weights 16-byte, outputs 8-byte aligned).
+ * workspace may be NULL; with rlse_dense_workspace_size bytes (for the
+ * call's rows, total output features and in_features; zero-filled before
+ * its first use, every call leaves it zero) an output with few 16-feature
+ * tiles splits K across workgroups so the whole chip streams the weights.
+ * Calls that share a workspace must not overlap. */
+int rlse_dense_workspace_size(int rows, int out_features, int in_features, size_t* bytes);
+/* q/k/v_proj (qwen2.rs:668-679) in one launch over the stacked weights
+ * w_qkv [q_features + 2*kv_features][hidden] (q rows, then k, then v) and
+ * bias b_qkv (may be NULL; Qwen2): q [rows][q_features],
+ * k/v [rows][kv_features], feature counts multiples of 16. */
+int rlse_qkv_proj(const void* x, const void* w_qkv, const void* b_qkv, void* q, void* k,
+                  void* v, int rows, int hidden, int q_features, int kv_features, int dtype,
+                  void* workspace, size_t workspace_bytes, rlse_stream_t stream);
+/* o_proj with `residual + attn_proj` (qwen2.rs:745-748) or down_proj with
+ * `xs_mid + mlp_out` (:755-756): residual <- residual + x . W^T, the product
+ * rounded, then the sum. out_features a multiple of 16. */
+int rlse_linear_residual(const void* x, const void* weight, void* residual, int rows,
+                         int out_features, int in_features, int dtype, void* workspace,
+                         size_t workspace_bytes, rlse_stream_t stream);
+/* MLP front (qwen2.rs:170-175): act = silu(gate_proj(x)) * up_proj(x) with
+ * w_gate_up [2*inter][hidden] (gate rows, then up rows), the projections
+ * rounded, then silu and the product as rlse_silu_mul. inter a multiple
+ * of 8; the workspace is sized for out_features = 2*inter. */
+int rlse_gate_up_silu(const void* x, const void* w_gate_up, void* act, int rows, int hidden,
+                      int inter, int dtype, void* workspace, size_t workspace_bytes,
+                      rlse_stream_t stream);
 
 /* ------------------------------------------------------------------ */
 /* Host block manager: the physical successor of KVCache               */

@@ -207,6 +207,21 @@ __device__ __forceinline__ void st_word(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ uint32_t ld_word(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Partial records handed between workgroups of one launch. Record words hold
+// the complement of a float's bits, so a stored word is never 0 (the bits
+// 0xFFFFFFFF, a NaN, are stored as another NaN) and 0 marks a word not yet
+// written in this launch. Each word is stored once per launch with a single
+// 32-bit agent-scope store, so a reader that sees it non-zero sees the whole
+// value; the merging workgroup clears the words it read.
+__device__ __forceinline__ uint32_t rec_encode(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return ~(u == 0xFFFFFFFFu ? 0x7FFFFFFFu : u);
+}
+__device__ __forceinline__ float rec_decode(uint32_t x) { return __uint_as_float(~x); }
+// A merge waits at most this long (wall clock ticks, 100 MHz: 100 ms) for a
+// partial of an earlier workgroup before it gives up and writes NaN.
+constexpr unsigned long long kMergeWaitTicks = 10000000ull;
+
 // Four dwords as a native vector (element-wise copies, no memcpy).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // Word 3 of a raw buffer descriptor on gfx9-family targets: 32-bit data

@@ -49,9 +49,6 @@ constexpr int kGroupsPerCU = 2;         // workgroups launched per compute unit
 constexpr int kMinBlocksPerGroup = 8;   // smallest share of blocks per workgroup
 constexpr int kMaxDecodeBatch = 8192;   // prefix table lives in LDS
 constexpr int kMaxDecodeRows = 65536;   // batch * num_kv_heads
-// A merge waits at most this long (wall clock ticks, 100 MHz: 100 ms) for a
-// partial of an earlier group before it gives up and writes NaN.
-constexpr unsigned long long kMergeWaitTicks = 10000000ull;
 // The running max of a softmax moves only when a score exceeds it by more
 // than this many powers of two.
 constexpr float kLazyLog2 = 8.f;
@@ -121,16 +118,6 @@ __device__ __forceinline__ int locate_seq(const int* s_pref, int B, int Hkv, lon
 // records stay 16-byte aligned.
 __host__ __device__ constexpr int rec_floats(int G, int D) { return G * D + ((2 * G + 3) & ~3); }
 
-// Record words hold the complement of a float's bits, so a stored word is
-// never 0 (the bits 0xFFFFFFFF, a NaN, are stored as another NaN) and 0 marks
-// a word not yet written in this launch. Each word is stored once per launch
-// with a single 32-bit agent-scope store, so a reader that sees it non-zero
-// sees the whole value; the merging group clears the words it read.
-__device__ __forceinline__ uint32_t rec_encode(float v) {
-  const uint32_t u = __float_as_uint(v);
-  return ~(u == 0xFFFFFFFFu ? 0x7FFFFFFFu : u);
-}
-__device__ __forceinline__ float rec_decode(uint32_t x) { return __uint_as_float(~x); }
 
 struct DecodeParams {
   const void* q;

@@ -10,7 +10,9 @@
 #include <math.h>
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "common.cuh"
 #include "host_common.h"
@@ -32,24 +34,97 @@ __global__ void embedding_kernel(const int32_t* __restrict__ ids, const T* __res
     dst[c] = ok ? src[c] : make_uint4(0, 0, 0, 0);
 }
 
-// residual <- residual + x (rounded); out <- RmsNorm(residual) * w. One wave
-// per row, the sum of squares in the order of rmsnorm_kernel.
+// 16-byte packets of T as floats and back (round to nearest even).
 template <typename T>
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ x,
-                                                          T* __restrict__ residual,
-                                                          const T* __restrict__ w,
-                                                          T* __restrict__ out, int rows, int n,
-                                                          float inv_n, float eps) {
+__device__ __forceinline__ uint4 pack_packet(const float* v) {
+  if constexpr (sizeof(T) == 4) {
+    return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                      __float_as_uint(v[3]));
+  } else {
+    return make_uint4(Packet<T>::pack2(v[0], v[1]), Packet<T>::pack2(v[2], v[3]),
+                      Packet<T>::pack2(v[4], v[5]), Packet<T>::pack2(v[6], v[7]));
+  }
+}
+
+// Sum over a workgroup of kThreads threads, the same order in every thread.
+template <int kThreads>
+__device__ __forceinline__ float block_sum(float v, float* s_part) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) t += s_part[w];
+  return t;
+}
+
+// [residual <- residual + x (rounded)]; out <- RmsNorm(residual) * w, the
+// reference's cast order (RmsNorm::forward). One workgroup per row, each
+// thread holding up to kNormChunks 16-byte chunks of it in registers between
+// the sum of squares and the scaling.
+constexpr int kNormThreads = 256;
+constexpr int kNormChunks = 4;
+template <typename T, bool ADD>
+__global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
+    const T* __restrict__ x, T* __restrict__ residual, const T* __restrict__ w,
+    T* __restrict__ out, int n, float inv_n, float eps) {
+  constexpr int E = 16 / sizeof(T);
+  __shared__ float s_part[kNormThreads / 64];
+  const size_t base = (size_t)blockIdx.x * n;
+  const int chunks = n / E;
+  const uint4* rr = reinterpret_cast<const uint4*>(residual + base);
+  float h[kNormChunks][E];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ci = threadIdx.x + c * kNormThreads;
+    if (ci < chunks) {
+      Packet<T>::unpack(rr[ci], h[c]);
+      if constexpr (ADD) {
+        float xv[E];
+        Packet<T>::unpack(reinterpret_cast<const uint4*>(x + base)[ci], xv);
+#pragma unroll
+        for (int e = 0; e < E; ++e) h[c][e] = round_to<T>(h[c][e] + xv[e]);
+        reinterpret_cast<uint4*>(residual + base)[ci] = pack_packet<T>(h[c]);
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) ss += h[c][e] * h[c][e];
+    }
+  }
+  const float norm = sqrtf(block_sum<kNormThreads>(ss, s_part) * inv_n + eps);
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ci = threadIdx.x + c * kNormThreads;
+    if (ci < chunks) {
+      float wv[E], o[E];
+      Packet<T>::unpack(reinterpret_cast<const uint4*>(w)[ci], wv);
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = round_to<T>(h[c][e] / norm) * wv[e];
+      reinterpret_cast<uint4*>(out + base)[ci] = pack_packet<T>(o);
+    }
+  }
+}
+
+// The same for rows that are not whole 16-byte chunks or longer than the
+// register-held form allows: one wave per row, element loads.
+template <typename T, bool ADD>
+__global__ __launch_bounds__(256) void norm_rows_any_kernel(const T* __restrict__ x,
+                                                            T* __restrict__ residual,
+                                                            const T* __restrict__ w,
+                                                            T* __restrict__ out, int rows, int n,
+                                                            float inv_n, float eps) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const T* xr = x + row * n;
   T* rr = residual + row * n;
   T* orow = out + row * n;
   float ss = 0.f;
   for (int i = lane; i < n; i += 64) {
-    const float h = round_to<T>(Elem<T>::to_f32(rr[i]) + Elem<T>::to_f32(xr[i]));
-    rr[i] = Elem<T>::from_f32(h);
+    float h = Elem<T>::to_f32(rr[i]);
+    if constexpr (ADD) {
+      h = round_to<T>(h + Elem<T>::to_f32(x[row * n + i]));
+      rr[i] = Elem<T>::from_f32(h);
+    }
     ss += h * h;
   }
   ss = wave_sum(ss);
@@ -64,72 +139,421 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ 
 // (gate columns, then up columns): silu(v) = v / (1 + exp(-v)) rounded per
 // op (exp, the sum, the quotient), then the product rounded.
 template <typename T>
-__global__ void silu_mul_kernel(const T* __restrict__ gate_up, T* __restrict__ out, int rows,
-                                int inter) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long long)rows * inter) return;
-  const long long r = i / inter, c = i - r * inter;
-  const float g = Elem<T>::to_f32(gate_up[r * 2 * inter + c]);
-  const float u = Elem<T>::to_f32(gate_up[r * 2 * inter + inter + c]);
+__device__ __forceinline__ float silu_mul_rounded(float g, float u) {
   const float e = round_to<T>(expf(-g));
   const float s = round_to<T>(g / round_to<T>(1.f + e));
-  out[i] = Elem<T>::from_f32(s * u);
+  return s * u;
+}
+
+template <typename T>
+__global__ void silu_mul_kernel(const T* __restrict__ gate_up, T* __restrict__ out, int inter) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= inter) return;
+  const size_t r = blockIdx.y;
+  const float g = Elem<T>::to_f32(gate_up[r * 2 * inter + c]);
+  const float u = Elem<T>::to_f32(gate_up[r * 2 * inter + inter + c]);
+  out[r * inter + c] = Elem<T>::from_f32(silu_mul_rounded<T>(g, u));
 }
 
 // y[r][c] = y[r][c] + bias[c], rounded (Candle's broadcast_add after matmul).
 template <typename T>
-__global__ void bias_add_kernel(T* __restrict__ y, const T* __restrict__ bias, int rows, int n) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long long)rows * n) return;
-  y[i] = Elem<T>::from_f32(Elem<T>::to_f32(y[i]) + Elem<T>::to_f32(bias[i % n]));
+__global__ void bias_add_kernel(T* __restrict__ y, const T* __restrict__ bias, int n) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= n) return;
+  const size_t i = (size_t)blockIdx.y * n + c;
+  y[i] = Elem<T>::from_f32(Elem<T>::to_f32(y[i]) + Elem<T>::to_f32(bias[c]));
 }
 
-// Greedy argmax of one row per workgroup with the sequential scan's answer
-// (Tensor::argmax on the host copy): the first index whose value exceeds
-// every earlier one -- the first maximum; a NaN never wins, except that a NaN
-// at index 0 wins outright (nothing compares greater than it).
+// ---------------------------------------------------------------------------
+// Greedy argmax with the sequential scan's answer (Tensor::argmax on the
+// host copy): the first index whose value exceeds every earlier one. As a
+// reduction: a NaN at index 0 wins outright; otherwise the first index of
+// the largest non-NaN value. Each (value, index) becomes one 64-bit key --
+// the value's bits mapped to an unsigned order (-0 taken as +0, which the
+// scan treats as equal), then the complemented index -- so the largest key
+// is the largest value at its first index, whatever order the partial
+// maxima combine in. Pass 1: one workgroup per kArgChunk logits of a row
+// writes its key; pass 2: one wave per row combines the row's keys.
+// ---------------------------------------------------------------------------
 constexpr int kArgThreads = 256;
-template <typename T>
-__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const T* __restrict__ logits,
-                                                             int32_t* __restrict__ out,
-                                                             int vocab) {
-  const T* row = logits + (size_t)blockIdx.x * vocab;
-  float best = -INFINITY;
-  int idx = 0x7fffffff;
-  for (int i = threadIdx.x; i < vocab; i += kArgThreads) {
-    const float v = Elem<T>::to_f32(row[i]);
-    if (v > best || (v == best && i < idx)) {  // NaN compares false: skipped
-      best = v;
-      idx = i;
-    }
-  }
-  // (value, index) pairs: larger value wins, ties go to the smaller index.
+constexpr int kArgChunk = 4096;
+
+__device__ __forceinline__ unsigned long long arg_key(float v, int i) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) == 0) u = 0;
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)o << 32) | (0xffffffffu - (uint32_t)i);
+}
+
+__device__ __forceinline__ unsigned long long wave_max_key(unsigned long long k) {
+#pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
-    const float ob = __shfl_xor(best, off, 64);
-    const int oi = __shfl_xor(idx, off, 64);
-    if (ob > best || (ob == best && oi < idx)) {
-      best = ob;
-      idx = oi;
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(k >> 32), off, 64);
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)k, off, 64);
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    k = o > k ? o : k;
+  }
+  return k;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kArgThreads) void argmax_partial_kernel(
+    const T* __restrict__ logits, unsigned long long* __restrict__ keys, int vocab, int parts) {
+  const int part = blockIdx.x;
+  const size_t row = blockIdx.y;
+  const T* r = logits + row * vocab;
+  const int begin = part * kArgChunk;
+  const int end = min(vocab, begin + kArgChunk);
+  unsigned long long best = 0;  // below every value's key
+  for (int i = begin + threadIdx.x; i < end; i += kArgThreads) {
+    const float v = Elem<T>::to_f32(r[i]);
+    if (v == v) {
+      const unsigned long long k = arg_key(v, i);
+      best = k > best ? k : best;
     }
   }
-  __shared__ float s_b[kArgThreads / 64];
-  __shared__ int s_i[kArgThreads / 64];
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    s_b[wave] = best;
-    s_i[wave] = idx;
-  }
+  best = wave_max_key(best);
+  __shared__ unsigned long long s_k[kArgThreads / 64];
+  if ((threadIdx.x & 63) == 0) s_k[threadIdx.x >> 6] = best;
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < kArgThreads / 64; ++w)
-      if (s_b[w] > best || (s_b[w] == best && s_i[w] < idx)) {
-        best = s_b[w];
-        idx = s_i[w];
+#pragma unroll
+    for (int w = 1; w < kArgThreads / 64; ++w) best = s_k[w] > best ? s_k[w] : best;
+    keys[row * parts + part] = best;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void argmax_final_kernel(const T* __restrict__ logits,
+                                                          const unsigned long long* __restrict__ keys,
+                                                          int32_t* __restrict__ out, int vocab,
+                                                          int parts) {
+  const size_t row = blockIdx.x;
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < parts; i += 64) {
+    const unsigned long long k = keys[row * parts + i];
+    best = k > best ? k : best;
+  }
+  best = wave_max_key(best);
+  if (threadIdx.x == 0) {
+    const float v0 = Elem<T>::to_f32(logits[row * vocab]);
+    out[row] = (v0 != v0 || best == 0) ? 0 : (int32_t)(0xffffffffu - (uint32_t)best);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode-shaped linear layers on MFMA: y[rows][N] = x[rows][K] . W[N][K]^T for
+// rows <= 64 (one decode step's batch), bf16/f16 in, f32 accumulation.
+//
+// Work split: workgroup (g, ks) owns FT tiles of 16 output features, the
+// whole batch and the ks-th of KS equal slices of K; its four waves split the
+// slice again. Each streams its K range of the 16*FT weight rows from HBM once
+// and the matching x columns from L2. Per 32-wide k step a wave issues
+// v_mfma_f32_16x16x32_{bf16,f16} with A = 16 weight rows x 32 k and B = 32 k x
+// 16 batch rows; lane l loads the 16 bytes at k = 8*(l/16) of weight row l%16
+// (A) and of batch row l%16 (B), and holds D[4*(l/16) + v][l%16], v = 0..3 --
+// four consecutive features of one batch row. U steps' loads are issued
+// before their MFMAs. The waves' partial tiles are summed through LDS in wave
+// order. With KS > 1 (few output tiles: the K split puts every compute unit
+// to work) the slices' sums meet as in the decode kernel's merge: workgroups
+// ks < KS-1 store theirs as self-validating records and leave; workgroup
+// KS-1, dispatched after them, waits for the records, adds them in slice
+// order (so the result does not depend on arrival order), clears them, and
+// runs the epilogue:
+//   kEpiStore     y = round(acc) [+ bias, rounded]               (Linear)
+//   kEpiQkv       the same, columns [0,n1) to q, [n1,n2) to k, [n2,N) to v
+//   kEpiResidual  x_res = round(x_res + round(acc))              (residual add)
+//   kEpiSiluMul   act = round(silu(round(gate)) * round(up)): tile i holds
+//                 gate rows 8i..8i+7 and up rows n1+8i..n1+8i+7
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mma16;
+template <>
+struct Mma16<bf16> {
+  static __device__ __forceinline__ f32x4_t run(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mma16<f16> {
+  static __device__ __forceinline__ f32x4_t run(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+enum : int { kEpiStore = 0, kEpiQkv = 1, kEpiResidual = 2, kEpiSiluMul = 3 };
+
+struct DenseParams {
+  const void* x;     // [rows][K]
+  const void* w;     // [N][K]
+  const void* bias;  // [N] or null (kEpiStore, kEpiQkv)
+  void* out0;        // y [rows][N] | q [rows][n1] | x_res [rows][N] | act [rows][n1]
+  void* out1;        // k [rows][n2 - n1] (kEpiQkv)
+  void* out2;        // v [rows][N - n2] (kEpiQkv)
+  uint32_t* ws;      // KS > 1: (tile groups) x (KS - 1) records of FT*RT*256 words
+  int rows, K, N, n1, n2;
+  int ksplit;        // KS
+  int steps;         // 32-wide k steps per wave
+};
+
+constexpr int kDenseWaves = 4;
+constexpr int kDenseMaxRows = 64;
+constexpr int kDenseMaxSplit = 8;
+
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, float* v) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  const uint4 q = make_uint4(u.x, u.y, 0, 0);
+  float t[8];
+  Packet<T>::unpack(q, t);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = t[e];
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float* v) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(Packet<T>::pack2(v[0], v[1]),
+                                            Packet<T>::pack2(v[2], v[3]));
+}
+
+template <typename T, int RT, int FT, int EPI>
+__global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParams p) {
+  constexpr int U = FT == 1 ? 8 : 4;
+  // An epilogue item is the four consecutive features one lane slot holds
+  // (4*(slot/16).. of batch row slot%16); kEpiSiluMul pairs slot s (gate
+  // features) with slot s+32 (the matching up features) in one item.
+  constexpr int kPair = EPI == kEpiSiluMul ? 2 : 1;
+  constexpr int kItems = FT * RT * 64 / kPair;
+  constexpr int kItemsPerThread = (kItems + 64 * kDenseWaves - 1) / (64 * kDenseWaves);
+  constexpr int kRecWords = FT * RT * 256;
+  __shared__ float red[kDenseWaves][FT][RT][256];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int fi = lane & 15;
+  const int g = lane >> 4;
+  const int K = p.K;
+  const int KS = p.ksplit;
+  const int grp = blockIdx.x / KS;
+  const int ks = blockIdx.x - grp * KS;
+  const T* wr[FT];
+#pragma unroll
+  for (int f = 0; f < FT; ++f) {
+    const int tile = grp * FT + f;
+    int row;
+    if constexpr (EPI == kEpiSiluMul)
+      row = fi < 8 ? tile * 8 + fi : p.n1 + tile * 8 + (fi - 8);
+    else
+      row = tile * 16 + fi;
+    wr[f] = (const T*)p.w + (size_t)row * K + 8 * g;
+  }
+  const T* xr[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+    xr[t] = (const T*)p.x + (size_t)min(16 * t + fi, p.rows - 1) * K + 8 * g;
+  f32x4_t acc[FT][RT];
+#pragma unroll
+  for (int f = 0; f < FT; ++f)
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[f][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int S = K >> 5;
+  const int slice_end = (ks + 1) * S / KS;
+  const int s_begin = ks * S / KS + wave * p.steps;
+  const int s_end = min(slice_end, s_begin + p.steps);
+  for (int s = s_begin; s < s_end; s += U) {
+    u32x4_t a[U][FT], b[U][RT];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      if (s + j < s_end) {
+        const int off = 32 * (s + j);
+#pragma unroll
+        for (int f = 0; f < FT; ++f) a[j][f] = *reinterpret_cast<const u32x4_t*>(wr[f] + off);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) b[j][t] = *reinterpret_cast<const u32x4_t*>(xr[t] + off);
       }
-    const float v0 = Elem<T>::to_f32(row[0]);
-    // Every value was -inf or NaN: the scan keeps index 0; a NaN first
-    // element wins outright.
-    out[blockIdx.x] = (v0 != v0 || idx == 0x7fffffff) ? 0 : idx;
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      if (s + j < s_end) {
+#pragma unroll
+        for (int f = 0; f < FT; ++f)
+#pragma unroll
+          for (int t = 0; t < RT; ++t) acc[f][t] = Mma16<T>::run(a[j][f], b[j][t], acc[f][t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int f = 0; f < FT; ++f)
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][f][t][lane * 4 + v] = acc[f][t][v];
+  __syncthreads();
+
+  // This workgroup's sums of its items (waves in order), kPair slots each.
+  float v[kItemsPerThread][kPair][4];
+#pragma unroll
+  for (int k = 0; k < kItemsPerThread; ++k) {
+    const int it = threadIdx.x + k * 64 * kDenseWaves;
+    if (it < kItems) {
+      const int l2 = it & (64 / kPair - 1);
+      const int ft = it / (64 / kPair);
+      const int t = ft % RT, f = ft / RT;
+#pragma unroll
+      for (int q = 0; q < kPair; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = red[0][f][t][(l2 + 32 * q) * 4 + e];
+#pragma unroll
+          for (int w = 1; w < kDenseWaves; ++w) x += red[w][f][t][(l2 + 32 * q) * 4 + e];
+          v[k][q][e] = x;
+        }
+    }
+  }
+
+  // Epilogue operands read from memory (the residual, the bias) are loaded
+  // before the merge waits, so that round trip overlaps it.
+  float pre[kItemsPerThread][4];
+#pragma unroll
+  for (int k = 0; k < kItemsPerThread; ++k) {
+    const int it = threadIdx.x + k * 64 * kDenseWaves;
+    const int l2 = it & (64 / kPair - 1);
+    const int ft = it / (64 / kPair);
+    const int t = ft % RT, f = ft / RT;
+    const int b = 16 * t + (l2 & 15);
+    const int n = (grp * FT + f) * 16 + 4 * (l2 >> 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pre[k][e] = 0.f;
+    if (it >= kItems || b >= p.rows) continue;
+    if constexpr (EPI == kEpiResidual) load4<T>((const T*)p.out0 + (size_t)b * p.N + n, pre[k]);
+    if constexpr (EPI == kEpiStore || EPI == kEpiQkv)
+      if (p.bias) load4<T>((const T*)p.bias + n, pre[k]);
+  }
+
+  bool ok = true;
+  if (KS > 1) {
+    // Record of slice sl: kItems items of kPair*4 words, as 64-bit halves.
+    constexpr int kHalves = kPair * 2;
+    auto half_ptr = [&](int slice, int it, int h) {
+      return reinterpret_cast<unsigned long long*>(
+                 p.ws + ((size_t)grp * (KS - 1) + slice) * kRecWords) +
+             (size_t)it * kHalves + h;
+    };
+    auto enc2 = [](float a, float b) {
+      return (unsigned long long)rec_encode(a) | ((unsigned long long)rec_encode(b) << 32);
+    };
+    if (ks < KS - 1) {
+#pragma unroll
+      for (int k = 0; k < kItemsPerThread; ++k) {
+        const int it = threadIdx.x + k * 64 * kDenseWaves;
+        if (it < kItems)
+#pragma unroll
+          for (int h = 0; h < kHalves; ++h)
+            __hip_atomic_store(half_ptr(ks, it, h),
+                               enc2(v[k][h >> 1][2 * (h & 1)], v[k][h >> 1][2 * (h & 1) + 1]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return;
+    }
+    // The merging workgroup: every slice's words are requested together,
+    // then only the missing ones again; the sum runs in slice order.
+    const unsigned long long t0 = wall_clock64();
+#pragma unroll
+    for (int k = 0; k < kItemsPerThread; ++k) {
+      const int it = threadIdx.x + k * 64 * kDenseWaves;
+      if (it >= kItems) continue;
+      unsigned long long r[kDenseMaxSplit - 1][kHalves];
+#pragma unroll
+      for (int sl = 0; sl < kDenseMaxSplit - 1; ++sl)
+#pragma unroll
+        for (int h = 0; h < kHalves; ++h) r[sl][h] = 0ull;
+      for (;;) {
+        bool all = true;
+#pragma unroll
+        for (int sl = 0; sl < kDenseMaxSplit - 1; ++sl) {
+          if (sl >= KS - 1) break;
+#pragma unroll
+          for (int h = 0; h < kHalves; ++h) {
+            if ((uint32_t)r[sl][h] == 0u || (uint32_t)(r[sl][h] >> 32) == 0u)
+              r[sl][h] = __hip_atomic_load(half_ptr(sl, it, h), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            all = all && (uint32_t)r[sl][h] != 0u && (uint32_t)(r[sl][h] >> 32) != 0u;
+          }
+        }
+        if (all) break;
+        if (wall_clock64() - t0 > kMergeWaitTicks) {
+          ok = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      float sum[kPair][4];
+#pragma unroll
+      for (int sl = 0; sl < kDenseMaxSplit - 1; ++sl) {
+        if (sl >= KS - 1) break;
+#pragma unroll
+        for (int h = 0; h < kHalves; ++h) {
+          const float lo = rec_decode((uint32_t)r[sl][h]);
+          const float hi = rec_decode((uint32_t)(r[sl][h] >> 32));
+          float& a = sum[h >> 1][2 * (h & 1)];
+          float& c = sum[h >> 1][2 * (h & 1) + 1];
+          a = sl == 0 ? lo : a + lo;
+          c = sl == 0 ? hi : c + hi;
+          __hip_atomic_store(half_ptr(sl, it, h), 0ull, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < kPair; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[k][q][e] = sum[q][e] + v[k][q][e];
+    }
+  }
+
+#pragma unroll
+  for (int k = 0; k < kItemsPerThread; ++k) {
+    const int it = threadIdx.x + k * 64 * kDenseWaves;
+    if (it >= kItems) continue;
+    const int l2 = it & (64 / kPair - 1);
+    const int ft = it / (64 / kPair);
+    const int t = ft % RT, f = ft / RT;
+    const int b = 16 * t + (l2 & 15);
+    const int fq = 4 * (l2 >> 4);
+    if (b >= p.rows) continue;
+    const int tile = grp * FT + f;
+    float o[4];
+    if constexpr (EPI == kEpiSiluMul) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = ok ? silu_mul_rounded<T>(round_to<T>(v[k][0][e]), round_to<T>(v[k][1][e]))
+                  : __builtin_nanf("");
+      store4<T>((T*)p.out0 + (size_t)b * p.n1 + tile * 8 + fq, o);
+    } else if constexpr (EPI == kEpiResidual) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = ok ? pre[k][e] + round_to<T>(v[k][0][e]) : __builtin_nanf("");
+      store4<T>((T*)p.out0 + (size_t)b * p.N + tile * 16 + fq, o);
+    } else {
+      const int n = tile * 16 + fq;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = ok ? round_to<T>(v[k][0][e]) + (p.bias ? pre[k][e] : 0.f) : __builtin_nanf("");
+      T* dst;
+      if (EPI == kEpiQkv && n >= p.n2)
+        dst = (T*)p.out2 + (size_t)b * (p.N - p.n2) + (n - p.n2);
+      else if (EPI == kEpiQkv && n >= p.n1)
+        dst = (T*)p.out1 + (size_t)b * (p.n2 - p.n1) + (n - p.n1);
+      else if (EPI == kEpiQkv)
+        dst = (T*)p.out0 + (size_t)b * p.n1 + n;
+      else
+        dst = (T*)p.out0 + (size_t)b * p.N + n;
+      store4<T>(dst, o);
+    }
   }
 }
 
@@ -146,6 +570,131 @@ int by_dtype(int dtype, F&& f) {
 // One rocBLAS handle per device, created on first use.
 std::mutex g_blas_mu;
 rocblas_handle g_blas[64] = {nullptr};
+
+bool aligned(const void* ptr, size_t a) { return ((uintptr_t)ptr % a) == 0; }
+
+// K slices per output tile group: enough workgroups to cover every compute
+// unit (256 on MI355X) when the output has few 16-feature tiles, each slice
+// at least 4 k steps of 32. Outputs with 256 or more tiles are not split:
+// measured, the merge's extra memory round trip costs them more than the
+// added workgroups gain.
+int dense_split(int groups, int K) {
+  int ks = (256 + groups - 1) / groups;
+  ks = std::min(ks, kDenseMaxSplit);
+  ks = std::min(ks, std::max(1, (K / 32) / 4));
+  return std::max(ks, 1);
+}
+
+// Launches dense_rows_kernel over the batch in chunks of kDenseMaxRows rows
+// (each chunk streams the weights once). Shapes were checked by the caller:
+// K % 32 == 0, 16-feature tiles that never straddle an output, 16-byte
+// aligned x / W and 8-byte aligned outputs; ws holds ws_words words (zero
+// before the first launch; every launch leaves it zero).
+template <typename T, int EPI>
+int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_stride,
+                 size_t o2_stride, size_t ws_words, hipStream_t s) {
+  const int total_rows = p.rows;
+  const int tiles = EPI == kEpiSiluMul ? p.n1 / 8 : p.N / 16;
+  // Wide outputs (lm_head) take four feature tiles per workgroup: the x
+  // columns a wave loads serve four A tiles, a quarter of the L2 reads.
+  const bool wide = EPI == kEpiStore && tiles % 4 == 0 && tiles >= 4096;
+  const int groups = wide ? tiles / 4 : tiles;
+  const int ks = p.ws ? dense_split(groups, p.K) : 1;
+  const int steps_total = p.K / 32;
+  const int slice = (steps_total + ks - 1) / ks;
+  p.ksplit = ks;
+  p.steps = (slice + kDenseWaves - 1) / kDenseWaves;
+  const char* base0 = (const char*)p.out0;
+  const char* base1 = (const char*)p.out1;
+  const char* base2 = (const char*)p.out2;
+  const char* xb = (const char*)p.x;
+  for (int r0 = 0; r0 < total_rows; r0 += kDenseMaxRows) {
+    DenseParams q = p;
+    q.rows = std::min(kDenseMaxRows, total_rows - r0);
+    q.x = xb + (size_t)r0 * x_stride * sizeof(T);
+    q.out0 = (void*)(base0 + (size_t)r0 * o0_stride * sizeof(T));
+    q.out1 = base1 ? (void*)(base1 + (size_t)r0 * o1_stride * sizeof(T)) : nullptr;
+    q.out2 = base2 ? (void*)(base2 + (size_t)r0 * o2_stride * sizeof(T)) : nullptr;
+    const int rt = (q.rows + 15) / 16;
+    if (ks > 1 && (size_t)groups * (ks - 1) * (wide ? 4 : 1) * rt * 256 > ws_words)
+      return fail(RLSE_ERR_INVALID_VALUE, "dense: workspace too small");
+    const dim3 block(64 * kDenseWaves);
+    const dim3 grid(groups * ks);
+    auto run = [&](auto rt_c) {
+      constexpr int RT = decltype(rt_c)::value;
+      if constexpr (EPI == kEpiStore) {
+        if (wide) {
+          hipLaunchKernelGGL((dense_rows_kernel<T, RT, 4, EPI>), grid, block, 0, s, q);
+          return;
+        }
+      }
+      hipLaunchKernelGGL((dense_rows_kernel<T, RT, 1, EPI>), grid, block, 0, s, q);
+    };
+    switch (rt) {
+      case 1: run(std::integral_constant<int, 1>{}); break;
+      case 2: run(std::integral_constant<int, 2>{}); break;
+      case 3: run(std::integral_constant<int, 3>{}); break;
+      default: run(std::integral_constant<int, 4>{}); break;
+    }
+    const int rc = launch_status("dense_rows_kernel");
+    if (rc) return rc;
+  }
+  return RLSE_OK;
+}
+
+// Workspace words a fused projection needs for its K split (0: none).
+size_t dense_ws_words(int rows, int tiles, int K) {
+  if (rows <= 0 || tiles <= 0 || K < 32) return 0;
+  const int ks = dense_split(tiles, K);
+  const int rt = (std::min(rows, kDenseMaxRows) + 15) / 16;
+  return ks > 1 ? (size_t)tiles * (ks - 1) * rt * 256 : 0;
+}
+
+// Shape and alignment checks shared by the MFMA entry points.
+int check_dense(const char* what, int dtype, int rows, int K, const void* x, const void* w,
+                const void* const* outs, int nouts) {
+  if (dtype != RLSE_DTYPE_BF16 && dtype != RLSE_DTYPE_F16)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "%s: bf16 or f16 only (f32 steps use rlse_linear with the element-wise ops)",
+                what);
+  if (rows < 0 || K <= 0 || K % 32)
+    return fail(RLSE_ERR_INVALID_VALUE, "%s: rows %d, in_features %d (a multiple of 32)", what,
+                rows, K);
+  if (rows == 0) return RLSE_OK;
+  if (!x || !w) return fail(RLSE_ERR_INVALID_VALUE, "%s: null pointer", what);
+  if (!aligned(x, 16) || !aligned(w, 16))
+    return fail(RLSE_ERR_INVALID_VALUE, "%s: x and weight must be 16-byte aligned", what);
+  for (int i = 0; i < nouts; ++i) {
+    if (!outs[i]) return fail(RLSE_ERR_INVALID_VALUE, "%s: null output", what);
+    if (!aligned(outs[i], 8))
+      return fail(RLSE_ERR_INVALID_VALUE, "%s: outputs must be 8-byte aligned", what);
+  }
+  return RLSE_OK;
+}
+
+template <int EPI>
+int dense_by_dtype(int dtype, const DenseParams& p, size_t xs, size_t s0, size_t s1, size_t s2,
+                   size_t ws_words, hipStream_t s) {
+  return dtype == RLSE_DTYPE_BF16 ? launch_dense<bf16, EPI>(p, xs, s0, s1, s2, ws_words, s)
+                                  : launch_dense<f16, EPI>(p, xs, s0, s1, s2, ws_words, s);
+}
+
+// The caller's workspace for a fused projection: NULL runs without a K
+// split; otherwise it must hold dense_ws_words words, 4-byte aligned.
+int dense_workspace(const char* what, DenseParams& p, void* workspace, size_t workspace_bytes,
+                    size_t* words) {
+  *words = 0;
+  p.ws = nullptr;
+  if (!workspace) return RLSE_OK;
+  const size_t need = dense_ws_words(p.rows, p.N / 16, p.K);
+  if (need == 0) return RLSE_OK;
+  if (workspace_bytes < need * 4 || !aligned(workspace, 4))
+    return fail(RLSE_ERR_INVALID_VALUE, "%s: workspace of %zu bytes (4-byte aligned) needed, %zu "
+                                        "given", what, need * 4, workspace_bytes);
+  p.ws = (uint32_t*)workspace;
+  *words = need;
+  return RLSE_OK;
+}
 
 }  // namespace
 }  // namespace rlse
@@ -171,50 +720,86 @@ extern "C" int rlse_embedding(const int32_t* ids, const void* table, void* out, 
 
 extern "C" int rlse_add_rmsnorm(const void* x, void* residual, const void* weight, void* out,
                                 int rows, int n, float eps, int dtype, rlse_stream_t stream) {
-  if (!dtype_size(dtype) || rows < 0 || n <= 0 || !(eps >= 0.f))
+  const size_t es = dtype_size(dtype);
+  if (!es || rows < 0 || n <= 0 || !(eps >= 0.f))
     return fail(RLSE_ERR_INVALID_VALUE, "add_rmsnorm: bad arguments");
   if (rows == 0) return RLSE_OK;
-  if (!x || !residual || !weight || !out)
+  if (!residual || !weight || !out)
     return fail(RLSE_ERR_INVALID_VALUE, "add_rmsnorm: null pointer");
   const float inv_n = (float)(1.0 / (double)n);
   hipStream_t s = as_stream(stream);
+  const bool chunked = (n * es) % 16 == 0 && n * es / 16 <= (size_t)kNormThreads * kNormChunks &&
+                       aligned(residual, 16) && aligned(weight, 16) && aligned(out, 16) &&
+                       (!x || aligned(x, 16));
   return by_dtype(dtype, [&](auto t) {
     using T = decltype(t);
-    hipLaunchKernelGGL(add_rmsnorm_kernel<T>, dim3((rows + 3) / 4), dim3(256), 0, s,
-                       (const T*)x, (T*)residual, (const T*)weight, (T*)out, rows, n, inv_n,
-                       eps);
+    const T* xp = (const T*)x;
+    T* rp = (T*)residual;
+    if (chunked) {
+      if (x)
+        hipLaunchKernelGGL((norm_rows_kernel<T, true>), dim3(rows), dim3(kNormThreads), 0, s,
+                           xp, rp, (const T*)weight, (T*)out, n, inv_n, eps);
+      else
+        hipLaunchKernelGGL((norm_rows_kernel<T, false>), dim3(rows), dim3(kNormThreads), 0, s,
+                           xp, rp, (const T*)weight, (T*)out, n, inv_n, eps);
+    } else if (x) {
+      hipLaunchKernelGGL((norm_rows_any_kernel<T, true>), dim3((rows + 3) / 4), dim3(256), 0, s,
+                         xp, rp, (const T*)weight, (T*)out, rows, n, inv_n, eps);
+    } else {
+      hipLaunchKernelGGL((norm_rows_any_kernel<T, false>), dim3((rows + 3) / 4), dim3(256), 0,
+                         s, xp, rp, (const T*)weight, (T*)out, rows, n, inv_n, eps);
+    }
     return launch_status("add_rmsnorm");
   });
 }
 
 extern "C" int rlse_silu_mul(const void* gate_up, void* out, int rows, int inter, int dtype,
                              rlse_stream_t stream) {
-  if (!dtype_size(dtype) || rows < 0 || inter <= 0)
+  if (!dtype_size(dtype) || rows < 0 || inter <= 0 || rows > 65535)
     return fail(RLSE_ERR_INVALID_VALUE, "silu_mul: bad arguments");
   if (rows == 0) return RLSE_OK;
   if (!gate_up || !out) return fail(RLSE_ERR_INVALID_VALUE, "silu_mul: null pointer");
-  const long long n = (long long)rows * inter;
   hipStream_t s = as_stream(stream);
   return by_dtype(dtype, [&](auto t) {
     using T = decltype(t);
-    hipLaunchKernelGGL(silu_mul_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                       (const T*)gate_up, (T*)out, rows, inter);
+    hipLaunchKernelGGL(silu_mul_kernel<T>, dim3((inter + 255) / 256, rows), dim3(256), 0, s,
+                       (const T*)gate_up, (T*)out, inter);
     return launch_status("silu_mul");
   });
 }
 
+extern "C" int rlse_argmax_workspace_size(int rows, int vocab, size_t* bytes) {
+  if (!bytes || rows < 0 || vocab <= 0)
+    return fail(RLSE_ERR_INVALID_VALUE, "argmax_workspace_size: bad arguments");
+  const size_t parts = ((size_t)vocab + kArgChunk - 1) / kArgChunk;
+  *bytes = (size_t)rows * parts * sizeof(unsigned long long);
+  return RLSE_OK;
+}
+
 extern "C" int rlse_argmax(const void* logits, int32_t* out, int rows, int vocab, int dtype,
-                           rlse_stream_t stream) {
-  if (!dtype_size(dtype) || rows < 0 || vocab <= 0)
+                           void* workspace, size_t workspace_bytes, rlse_stream_t stream) {
+  if (!dtype_size(dtype) || rows < 0 || vocab <= 0 || rows > 65535)
     return fail(RLSE_ERR_INVALID_VALUE, "argmax: bad arguments");
   if (rows == 0) return RLSE_OK;
   if (!logits || !out) return fail(RLSE_ERR_INVALID_VALUE, "argmax: null pointer");
+  size_t need = 0;
+  rlse_argmax_workspace_size(rows, vocab, &need);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 8))
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "argmax: workspace of %zu bytes (8-byte aligned) needed, %zu given", need,
+                workspace ? workspace_bytes : 0);
+  const int parts = (vocab + kArgChunk - 1) / kArgChunk;
+  auto* keys = (unsigned long long*)workspace;
   hipStream_t s = as_stream(stream);
   return by_dtype(dtype, [&](auto t) {
     using T = decltype(t);
-    hipLaunchKernelGGL(argmax_kernel<T>, dim3(rows), dim3(kArgThreads), 0, s, (const T*)logits,
-                       out, vocab);
-    return launch_status("argmax");
+    hipLaunchKernelGGL(argmax_partial_kernel<T>, dim3(parts, rows), dim3(kArgThreads), 0, s,
+                       (const T*)logits, keys, vocab, parts);
+    int rc = launch_status("argmax_partial");
+    if (rc) return rc;
+    hipLaunchKernelGGL(argmax_final_kernel<T>, dim3(rows), dim3(64), 0, s, (const T*)logits,
+                       keys, out, vocab, parts);
+    return launch_status("argmax_final");
   });
 }
 
@@ -225,6 +810,21 @@ extern "C" int rlse_linear(const void* x, const void* weight, const void* bias, 
     return fail(RLSE_ERR_INVALID_VALUE, "linear: bad arguments");
   if (rows == 0) return RLSE_OK;
   if (!x || !weight || !y) return fail(RLSE_ERR_INVALID_VALUE, "linear: null pointer");
+  hipStream_t s = as_stream(stream);
+  // Decode-shaped products (a few rows, bf16/f16) run on the MFMA kernel.
+  if ((dtype == RLSE_DTYPE_BF16 || dtype == RLSE_DTYPE_F16) && rows <= kDenseMaxRows &&
+      in_features % 32 == 0 && out_features % 16 == 0 && aligned(x, 16) &&
+      aligned(weight, 16) && aligned(y, 8) && (!bias || aligned(bias, 8))) {
+    DenseParams p{};
+    p.x = x;
+    p.w = weight;
+    p.bias = bias;
+    p.out0 = y;
+    p.rows = rows;
+    p.K = in_features;
+    p.N = out_features;
+    return dense_by_dtype<kEpiStore>(dtype, p, in_features, out_features, 0, 0, 0, s);
+  }
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
     return fail(RLSE_ERR_INVALID_VALUE, "linear: no current device");
@@ -235,7 +835,6 @@ extern "C" int rlse_linear(const void* x, const void* weight, const void* bias, 
       return fail(RLSE_ERR_INVALID_VALUE, "linear: rocblas_create_handle failed");
     h = g_blas[dev];
   }
-  hipStream_t s = as_stream(stream);
   if (rocblas_set_stream(h, s) != rocblas_status_success)
     return fail(RLSE_ERR_INVALID_VALUE, "linear: rocblas_set_stream failed");
   const rocblas_datatype t = dtype == RLSE_DTYPE_F32   ? rocblas_datatype_f32_r
@@ -251,11 +850,99 @@ extern "C" int rlse_linear(const void* x, const void* weight, const void* bias, 
   if (st != rocblas_status_success)
     return fail(RLSE_ERR_INVALID_VALUE, "linear: rocblas_gemm_ex failed (%d)", (int)st);
   if (!bias) return RLSE_OK;
-  const long long n = (long long)rows * out_features;
+  if (rows > 65535) return fail(RLSE_ERR_INVALID_VALUE, "linear: bias add over %d rows", rows);
   return by_dtype(dtype, [&](auto tt) {
     using T = decltype(tt);
-    hipLaunchKernelGGL(bias_add_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                       (T*)y, (const T*)bias, rows, out_features);
+    hipLaunchKernelGGL(bias_add_kernel<T>, dim3((out_features + 255) / 256, rows), dim3(256), 0,
+                       s, (T*)y, (const T*)bias, out_features);
     return launch_status("bias_add");
   });
+}
+
+extern "C" int rlse_dense_workspace_size(int rows, int out_features, int in_features,
+                                         size_t* bytes) {
+  if (!bytes || rows < 0 || out_features <= 0 || in_features <= 0)
+    return fail(RLSE_ERR_INVALID_VALUE, "dense_workspace_size: bad arguments");
+  *bytes = dense_ws_words(rows, out_features / 16, in_features) * 4;
+  return RLSE_OK;
+}
+
+extern "C" int rlse_qkv_proj(const void* x, const void* w_qkv, const void* b_qkv, void* q,
+                             void* k, void* v, int rows, int hidden, int q_features,
+                             int kv_features, int dtype, void* workspace, size_t workspace_bytes,
+                             rlse_stream_t stream) {
+  const void* outs[3] = {q, k, v};
+  int rc = check_dense("qkv_proj", dtype, rows, hidden, x, w_qkv, outs, 3);
+  if (rc || rows == 0) return rc;
+  if (q_features <= 0 || kv_features <= 0 || q_features % 16 || kv_features % 16)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "qkv_proj: q_features %d and kv_features %d must be positive multiples of 16",
+                q_features, kv_features);
+  if (b_qkv && !aligned(b_qkv, 8))
+    return fail(RLSE_ERR_INVALID_VALUE, "qkv_proj: bias must be 8-byte aligned");
+  DenseParams p{};
+  p.x = x;
+  p.w = w_qkv;
+  p.bias = b_qkv;
+  p.out0 = q;
+  p.out1 = k;
+  p.out2 = v;
+  p.rows = rows;
+  p.K = hidden;
+  p.n1 = q_features;
+  p.n2 = q_features + kv_features;
+  p.N = q_features + 2 * kv_features;
+  size_t words = 0;
+  rc = dense_workspace("qkv_proj", p, workspace, workspace_bytes, &words);
+  if (rc) return rc;
+  return dense_by_dtype<kEpiQkv>(dtype, p, hidden, q_features, kv_features, kv_features, words,
+                                 as_stream(stream));
+}
+
+extern "C" int rlse_linear_residual(const void* x, const void* weight, void* residual, int rows,
+                                    int out_features, int in_features, int dtype,
+                                    void* workspace, size_t workspace_bytes,
+                                    rlse_stream_t stream) {
+  const void* outs[1] = {residual};
+  int rc = check_dense("linear_residual", dtype, rows, in_features, x, weight, outs, 1);
+  if (rc || rows == 0) return rc;
+  if (out_features <= 0 || out_features % 16)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "linear_residual: out_features %d must be a positive multiple of 16",
+                out_features);
+  DenseParams p{};
+  p.x = x;
+  p.w = weight;
+  p.out0 = residual;
+  p.rows = rows;
+  p.K = in_features;
+  p.N = out_features;
+  size_t words = 0;
+  rc = dense_workspace("linear_residual", p, workspace, workspace_bytes, &words);
+  if (rc) return rc;
+  return dense_by_dtype<kEpiResidual>(dtype, p, in_features, out_features, 0, 0, words,
+                                      as_stream(stream));
+}
+
+extern "C" int rlse_gate_up_silu(const void* x, const void* w_gate_up, void* act, int rows,
+                                 int hidden, int inter, int dtype, void* workspace,
+                                 size_t workspace_bytes, rlse_stream_t stream) {
+  const void* outs[1] = {act};
+  int rc = check_dense("gate_up_silu", dtype, rows, hidden, x, w_gate_up, outs, 1);
+  if (rc || rows == 0) return rc;
+  if (inter <= 0 || inter % 8)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "gate_up_silu: intermediate size %d must be a positive multiple of 8", inter);
+  DenseParams p{};
+  p.x = x;
+  p.w = w_gate_up;
+  p.out0 = act;
+  p.rows = rows;
+  p.K = hidden;
+  p.N = 2 * inter;
+  p.n1 = inter;
+  size_t words = 0;
+  rc = dense_workspace("gate_up_silu", p, workspace, workspace_bytes, &words);
+  if (rc) return rc;
+  return dense_by_dtype<kEpiSiluMul>(dtype, p, hidden, inter, 0, 0, words, as_stream(stream));
 }

@@ -8,22 +8,25 @@ feed the next without a host round trip (the reference copies the logits to
 the host for sample_token, src/backends/candle.rs:737-751).
 
 Per step, for a batch of B sequences with their new token at position
-seq_lens[b] - 1:
+seq_lens[b] - 1 (bf16 / f16: the projections on the MFMA kernels, fused with
+their neighbours):
 
     x = embed_tokens[ids]                                  rlse_embedding
-    h = input_layernorm(x)                                 rlse_rmsnorm (layer 0)
+    h = input_layernorm(x)                                 rlse_add_rmsnorm (no add)
     per layer:
-      q, k, v = q/k/v_proj(h)                              rlse_linear x 3
+      q, k, v = q/k/v_proj(h)                              rlse_qkv_proj (one launch)
       attn = q/k norm + RoPE + append + paged GQA decode    rlse_decode_step
-      x, h = x + o_proj(attn), post_attention_layernorm     rlse_linear, rlse_add_rmsnorm
-      a = silu(gate_proj(h)) * up_proj(h)                  rlse_linear (gate|up), rlse_silu_mul
-      x, h = x + down_proj(a), next input_layernorm        rlse_linear, rlse_add_rmsnorm
-             (the final norm after the last layer)
+      x += o_proj(attn)                                    rlse_linear_residual
+      h = post_attention_layernorm(x)                      rlse_add_rmsnorm (no add)
+      a = silu(gate_proj(h)) * up_proj(h)                  rlse_gate_up_silu
+      x += down_proj(a)                                    rlse_linear_residual
+      h = next input_layernorm(x) (the final norm last)    rlse_add_rmsnorm (no add)
     logits = lm_head(h); next = argmax(logits)             rlse_linear, rlse_argmax
 
-gate_proj and up_proj run as one product over their stacked weights (each
-output element is the same dot product, rounded once). torch is used only to
-hold device memory; nothing here computes on the CPU or through torch ops.
+f32 (a parity dtype, not a performance one) runs the same math as separate
+ops: rlse_linear per projection, rlse_add_rmsnorm for the residual adds and
+rlse_silu_mul. Each output element is rounded at the same points either way
+(the projection, the bias, the residual sum, each step of silu).
 """
 from __future__ import annotations
 
@@ -89,14 +92,20 @@ class DecodeModel:
         self.embed = up("embed")
         self.norm = up("norm")
         self.lm_head = self.embed if cfg.tied else up("lm_head")
+        self.fused = dtype != "f32"
         self.layers = []
         for l in range(cfg.layers):
             p = f"l{l}."
-            L = {n: up(p + n) for n in ("in_norm", "post_norm", "q_w", "k_w", "v_w", "o_w",
-                                        "down_w")}
+            L = {n: up(p + n) for n in ("in_norm", "post_norm", "o_w", "down_w")}
             L["gate_up_w"] = torch.cat([up(p + "gate_w"), up(p + "up_w")], 0).contiguous()
-            for n in ("q_b", "k_b", "v_b") if cfg.qkv_bias else ():
-                L[n] = up(p + n)
+            qkv = [up(p + n) for n in ("q_w", "k_w", "v_w")]
+            bias = [up(p + n) for n in ("q_b", "k_b", "v_b")] if cfg.qkv_bias else None
+            if self.fused:
+                L["qkv_w"] = torch.cat(qkv, 0).contiguous()
+                L["qkv_b"] = torch.cat(bias, 0).contiguous() if bias else None
+            else:
+                L["q_w"], L["k_w"], L["v_w"] = qkv
+                L["q_b"], L["k_b"], L["v_b"] = bias if bias else (None, None, None)
             for n in ("q_norm", "k_norm") if cfg.qk_norm else ():
                 L[n] = up(p + n)
             self.layers.append(L)
@@ -114,9 +123,19 @@ class DecodeModel:
         z = lambda *s: torch.zeros(s, dtype=t, device=dev)  # noqa: E731
         self.x, self.h, self.o = z(B, cfg.hidden), z(B, cfg.hidden), z(B, cfg.hidden)
         self.q, self.k, self.v, self.attn = z(B, nq), z(B, nkv), z(B, nkv), z(B, nq)
-        self.gu, self.act = z(B, 2 * cfg.inter), z(B, cfg.inter)
+        self.gu = None if self.fused else z(B, 2 * cfg.inter)
+        self.act = z(B, cfg.inter)
         self.logits = z(B, cfg.vocab)
         self.next_ids = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.arg_ws = torch.zeros(max(kv.argmax_workspace_size(B, cfg.vocab), 8),
+                                  dtype=torch.uint8, device=dev)
+        # One workspace for the K split of every fused projection (they run
+        # one after another on the step's stream); zero-filled once, as each
+        # call leaves it.
+        dense_ws = max([kv.dense_workspace_size(B, n, k) for n, k in (
+            (nq + 2 * nkv, cfg.hidden), (cfg.hidden, nq), (2 * cfg.inter, cfg.hidden),
+            (cfg.hidden, cfg.inter))] + [4])
+        self.dense_ws = torch.zeros(dense_ws, dtype=torch.uint8, device=dev)
         ws = kv.decode_workspace_size(B, cfg.heads, cfg.kv_heads, cfg.head_dim)
         # Zero once: every launch of the decode kernel leaves it zero again.
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=dev)
@@ -162,26 +181,45 @@ class DecodeModel:
         if stream is None:
             stream = torch.cuda.current_stream(self.device)
         H, nq, nkv = cfg.hidden, cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+        inter = cfg.inter
         kv.embedding(ids, self.embed, self.x, batch, H, cfg.vocab, dt, stream)
-        kv.rmsnorm(self.x, self.layers[0]["in_norm"], self.h, batch, H, cfg.eps, dt, stream)
+        kv.add_rmsnorm(None, self.x, self.layers[0]["in_norm"], self.h, batch, H, cfg.eps, dt,
+                       stream)
         for l, L in enumerate(self.layers):
-            kv.linear(self.h, L["q_w"], L.get("q_b"), self.q, batch, nq, H, dt, stream)
-            kv.linear(self.h, L["k_w"], L.get("k_b"), self.k, batch, nkv, H, dt, stream)
-            kv.linear(self.h, L["v_w"], L.get("v_b"), self.v, batch, nkv, H, dt, stream)
+            if self.fused:
+                kv.qkv_proj(self.h, L["qkv_w"], L["qkv_b"], self.q, self.k, self.v, batch, H, nq,
+                            nkv, dt, self.dense_ws, stream)
+            else:
+                kv.linear(self.h, L["q_w"], L["q_b"], self.q, batch, nq, H, dt, stream)
+                kv.linear(self.h, L["k_w"], L["k_b"], self.k, batch, nkv, H, dt, stream)
+                kv.linear(self.h, L["v_w"], L["v_b"], self.v, batch, nkv, H, dt, stream)
             kp, vp = self.pool.layer(l)
             kv.decode_step(self.q, self.k, self.v, L.get("q_norm"), L.get("k_norm"), cfg.eps,
                            self.cos, self.sin, self.max_pos, kp, vp, block_tables, seq_lens,
                            self.attn, batch, cfg.heads, cfg.kv_heads, cfg.head_dim, self.mbps,
                            self.num_blocks, self.scale, dt, self.workspace,
                            self.workspace.numel(), stream)
-            kv.linear(self.attn, L["o_w"], None, self.o, batch, H, nq, dt, stream)
-            kv.add_rmsnorm(self.o, self.x, L["post_norm"], self.h, batch, H, cfg.eps, dt, stream)
-            kv.linear(self.h, L["gate_up_w"], None, self.gu, batch, 2 * cfg.inter, H, dt,
-                      stream)
-            kv.silu_mul(self.gu, self.act, batch, cfg.inter, dt, stream)
-            kv.linear(self.act, L["down_w"], None, self.o, batch, H, cfg.inter, dt, stream)
             nxt = self.layers[l + 1]["in_norm"] if l + 1 < cfg.layers else self.norm
-            kv.add_rmsnorm(self.o, self.x, nxt, self.h, batch, H, cfg.eps, dt, stream)
+            if self.fused:
+                kv.linear_residual(self.attn, L["o_w"], self.x, batch, H, nq, dt, self.dense_ws,
+                                   stream)
+                kv.add_rmsnorm(None, self.x, L["post_norm"], self.h, batch, H, cfg.eps, dt,
+                               stream)
+                kv.gate_up_silu(self.h, L["gate_up_w"], self.act, batch, H, inter, dt,
+                                self.dense_ws, stream)
+                kv.linear_residual(self.act, L["down_w"], self.x, batch, H, inter, dt,
+                                   self.dense_ws, stream)
+                kv.add_rmsnorm(None, self.x, nxt, self.h, batch, H, cfg.eps, dt, stream)
+            else:
+                kv.linear(self.attn, L["o_w"], None, self.o, batch, H, nq, dt, stream)
+                kv.add_rmsnorm(self.o, self.x, L["post_norm"], self.h, batch, H, cfg.eps, dt,
+                               stream)
+                kv.linear(self.h, L["gate_up_w"], None, self.gu, batch, 2 * inter, H, dt,
+                          stream)
+                kv.silu_mul(self.gu, self.act, batch, inter, dt, stream)
+                kv.linear(self.act, L["down_w"], None, self.o, batch, H, inter, dt, stream)
+                kv.add_rmsnorm(self.o, self.x, nxt, self.h, batch, H, cfg.eps, dt, stream)
         kv.linear(self.h, self.lm_head, None, self.logits, batch, cfg.vocab, H, dt, stream)
-        kv.argmax(self.logits, self.next_ids, batch, cfg.vocab, dt, stream)
+        kv.argmax(self.logits, self.next_ids, batch, cfg.vocab, dt, self.arg_ws,
+                  self.arg_ws.numel(), stream)
         return self.logits[:batch], self.next_ids[:batch]

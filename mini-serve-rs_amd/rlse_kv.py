@@ -68,6 +68,8 @@ EXPORTED = (
     "rlse_bm_release_all", "rlse_st_create", "rlse_st_destroy", "rlse_st_reset",
     "rlse_st_prepare", "rlse_st_host", "rlse_st_upload", "rlse_st_mark_uploaded",
     "rlse_embedding", "rlse_add_rmsnorm", "rlse_silu_mul", "rlse_argmax", "rlse_linear",
+    "rlse_argmax_workspace_size", "rlse_qkv_proj", "rlse_linear_residual", "rlse_gate_up_silu",
+    "rlse_dense_workspace_size",
 )
 
 
@@ -231,8 +233,13 @@ _SIGS = {
     "rlse_embedding": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rlse_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _i, _vp]),
     "rlse_silu_mul": (_i, [_vp, _vp, _i, _i, _i, _vp]),
-    "rlse_argmax": (_i, [_vp, _vp, _i, _i, _i, _vp]),
+    "rlse_argmax_workspace_size": (_i, [_i, _i, ctypes.POINTER(_sz)]),
+    "rlse_argmax": (_i, [_vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_linear": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "rlse_dense_workspace_size": (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
+    "rlse_qkv_proj": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "rlse_linear_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "rlse_gate_up_silu": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -786,11 +793,57 @@ def silu_mul(gate_up, out, rows: int, inter: int, dtype, stream=None) -> None:
                                 _stream(stream)))
 
 
-def argmax(logits, out, rows: int, vocab: int, dtype, stream=None) -> None:
-    _check(load().rlse_argmax(_ptr(logits), _ptr(out), rows, vocab, _dt(dtype), _stream(stream)))
+def argmax_workspace_size(rows: int, vocab: int) -> int:
+    n = _sz(0)
+    _check(load().rlse_argmax_workspace_size(rows, vocab, ctypes.byref(n)))
+    return n.value
+
+
+def argmax(logits, out, rows: int, vocab: int, dtype, workspace, workspace_bytes: int,
+           stream=None) -> None:
+    _check(load().rlse_argmax(_ptr(logits), _ptr(out), rows, vocab, _dt(dtype), _ptr(workspace),
+                              workspace_bytes, _stream(stream)))
 
 
 def linear(x, weight, bias, y, rows: int, out_features: int, in_features: int, dtype,
            stream=None) -> None:
     _check(load().rlse_linear(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), rows, out_features,
                               in_features, _dt(dtype), _stream(stream)))
+
+
+def dense_workspace_size(rows: int, out_features: int, in_features: int) -> int:
+    """Bytes of workspace for the K split of qkv_proj / linear_residual /
+    gate_up_silu (out_features: all outputs of the call, 2*inter for
+    gate_up_silu). Zero-fill it once before first use."""
+    n = _sz(0)
+    _check(load().rlse_dense_workspace_size(rows, out_features, in_features, ctypes.byref(n)))
+    return n.value
+
+
+def _ws(workspace):
+    if workspace is None:
+        return None, 0
+    return _ptr(workspace), int(workspace.numel() * workspace.element_size())
+
+
+def qkv_proj(x, w_qkv, b_qkv, q, k, v, rows: int, hidden: int, q_features: int,
+             kv_features: int, dtype, workspace=None, stream=None) -> None:
+    wp, wb = _ws(workspace)
+    _check(load().rlse_qkv_proj(_ptr(x), _ptr(w_qkv), _ptr(b_qkv), _ptr(q), _ptr(k), _ptr(v),
+                                rows, hidden, q_features, kv_features, _dt(dtype), wp, wb,
+                                _stream(stream)))
+
+
+def linear_residual(x, weight, residual, rows: int, out_features: int, in_features: int, dtype,
+                    workspace=None, stream=None) -> None:
+    wp, wb = _ws(workspace)
+    _check(load().rlse_linear_residual(_ptr(x), _ptr(weight), _ptr(residual), rows,
+                                       out_features, in_features, _dt(dtype), wp, wb,
+                                       _stream(stream)))
+
+
+def gate_up_silu(x, w_gate_up, act, rows: int, hidden: int, inter: int, dtype, workspace=None,
+                 stream=None) -> None:
+    wp, wb = _ws(workspace)
+    _check(load().rlse_gate_up_silu(_ptr(x), _ptr(w_gate_up), _ptr(act), rows, hidden, inter,
+                                    _dt(dtype), wp, wb, _stream(stream)))

@@ -128,13 +128,157 @@ def test_argmax_bit_exact_with_ties_and_nans(kv, dt):
     rows[6, vocab - 1] = 70.0                            # maximum at the end
     rows[7, 3:] = -np.inf
     rows[7, :3] = [-np.inf, 2.0, 2.0]
+    rows[8, 100] = -0.0
+    rows[8, 200] = 0.0
+    rows[8, :100] = -1.0
+    rows[8, 101:] = -1.0
+    rows[8, 200] = 0.0                                   # -0 then +0: the first (scan: equal)
     out = torch.full((12,), -5, dtype=torch.int32, device=DEV)
-    kv.argmax(dev(rows, dt), out, 12, vocab, dt)
+    nbytes = kv.argmax_workspace_size(12, vocab)
+    ws = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device=DEV)   # needs no clearing
+    kv.argmax(dev(rows, dt), out, 12, vocab, dt, ws, nbytes)
     torch.cuda.synchronize()
     want = O.argmax_ref(rows)
     np.testing.assert_array_equal(out.cpu().numpy(), want)
     assert want[1] == 1000 and want[2] == 0 and want[3] == 77 and want[4] == 0 and \
-        want[6] == vocab - 1 and want[7] == 1
+        want[6] == vocab - 1 and want[7] == 1 and want[8] == 100
+    with pytest.raises(kv.RlseError):
+        kv.argmax(dev(rows, dt), out, 12, vocab, dt, ws, nbytes - 8)
+
+
+@pytest.mark.parametrize("vocab", [1, 4095, 4096, 4097, 9000])
+def test_argmax_chunk_edges(kv, vocab):
+    rng = np.random.default_rng(vocab)
+    rows = O.round_to(rng.standard_normal((5, vocab)), "bf16")
+    rows[1, vocab - 1] = 9.0
+    rows[2, min(4095, vocab - 1)] = 9.0
+    rows[3, :] = 1.0
+    out = torch.empty(5, dtype=torch.int32, device=DEV)
+    nbytes = kv.argmax_workspace_size(5, vocab)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    kv.argmax(dev(rows, "bf16"), out, 5, vocab, "bf16", ws, nbytes)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), O.argmax_ref(rows))
+
+
+# ------------------------------------------------ fused MFMA projections ---
+ROWS = [1, 5, 16, 33, 64, 100]
+
+
+def _dense_ws(kv, rows, n_out, n_in, use):
+    """The K-split workspace (zero-filled, as the contract asks), or None."""
+    if not use:
+        return None
+    n = kv.dense_workspace_size(rows, n_out, n_in)
+    return torch.zeros(max(n, 4), dtype=torch.uint8, device=DEV)
+
+
+def _assert_clean(ws):
+    if ws is not None:
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(ws)) == 0     # every call leaves it zero
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows", ROWS)
+@pytest.mark.parametrize("hidden,nq,nkv,bias", [(1024, 2048, 1024, False), (896, 896, 128, True)])
+def test_qkv_proj_matches_three_linears(kv, dt, rows, hidden, nq, nkv, bias):
+    rng = np.random.default_rng(rows * 7 + hidden)
+    x = O.round_to(rng.standard_normal((rows, hidden)), dt)
+    ws = [O.round_to(rng.standard_normal((n, hidden)) / np.sqrt(hidden), dt)
+          for n in (nq, nkv, nkv)]
+    bs = [O.round_to(0.1 * rng.standard_normal(n), dt) if bias else None for n in (nq, nkv, nkv)]
+    outs = [torch.full((rows, n), 5.0, dtype=_T[dt], device=DEV) for n in (nq, nkv, nkv)]
+    wk = _dense_ws(kv, rows, nq + 2 * nkv, hidden, rows % 2 == 1)
+    kv.qkv_proj(dev(x, dt), dev(np.concatenate(ws), dt),
+                dev(np.concatenate(bs), dt) if bias else None, *outs, rows, hidden, nq, nkv, dt,
+                wk)
+    _assert_clean(wk)
+    for name, o, w_, b_ in zip("qkv", outs, ws, bs):
+        rel_check(f"qkv_proj {name} rows={rows}", host(o), O.linear_ref(x, w_, b_, dt), dt)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows", ROWS)
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("n_out,n_in", [(1024, 2048), (1024, 3072), (896, 4864), (64, 160)])
+def test_linear_residual_matches_oracle(kv, dt, rows, split, n_out, n_in):
+    rng = np.random.default_rng(rows + n_in)
+    x = O.round_to(rng.standard_normal((rows, n_in)), dt)
+    w = O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt)
+    r = O.round_to(2 * rng.standard_normal((rows, n_out)), dt)
+    rd = dev(r, dt)
+    wk = _dense_ws(kv, rows, n_out, n_in, split)
+    kv.linear_residual(dev(x, dt), dev(w, dt), rd, rows, n_out, n_in, dt, wk)
+    _assert_clean(wk)
+    want = O.round_to(r + O.linear_ref(x, w, None, dt), dt)
+    rel_check(f"linear_residual rows={rows} {n_out}x{n_in} split={split}", host(rd), want, dt)
+
+
+def test_k_split_is_deterministic_and_equals_unsplit_closely(kv):
+    """The merged K slices add in slice order: repeated calls give the same
+    bits; the split and unsplit sums differ only by rounding order."""
+    rng = np.random.default_rng(31)
+    rows, n_out, n_in, dt = 32, 1024, 3072, "bf16"
+    x = dev(O.round_to(rng.standard_normal((rows, n_in)), dt), dt)
+    w = dev(O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt), dt)
+    wk = _dense_ws(kv, rows, n_out, n_in, True)
+    assert wk.numel() > 4                    # this shape splits K
+    outs = []
+    for use in (True, True, True, False):
+        r = torch.zeros((rows, n_out), dtype=torch.bfloat16, device=DEV)
+        kv.linear_residual(x, w, r, rows, n_out, n_in, dt, wk if use else None)
+        outs.append(host(r))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    np.testing.assert_array_equal(outs[0], outs[2])
+    assert np.abs(outs[0] - outs[3]).max() <= 2 * ULP[dt] * np.abs(outs[3]).max()
+    _assert_clean(wk)
+    with pytest.raises(kv.RlseError):        # a workspace too small is refused
+        kv.linear_residual(x, w, r, rows, n_out, n_in, dt, wk[:64])
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows", ROWS)
+@pytest.mark.parametrize("hidden,inter", [(1024, 3072), (896, 4864), (128, 8)])
+def test_gate_up_silu_matches_oracle(kv, dt, rows, hidden, inter):
+    rng = np.random.default_rng(rows + inter)
+    x = O.round_to(rng.standard_normal((rows, hidden)), dt)
+    wg = O.round_to(rng.standard_normal((inter, hidden)) / np.sqrt(hidden) * 3, dt)
+    wu = O.round_to(rng.standard_normal((inter, hidden)) / np.sqrt(hidden), dt)
+    act = torch.full((rows, inter), 7.0, dtype=_T[dt], device=DEV)
+    wk = _dense_ws(kv, rows, 2 * inter, hidden, rows != 16)
+    kv.gate_up_silu(dev(x, dt), dev(np.concatenate([wg, wu]), dt), act, rows, hidden, inter, dt,
+                    wk)
+    _assert_clean(wk)
+    want = O.silu_mul_ref(O.linear_ref(x, wg, None, dt), O.linear_ref(x, wu, None, dt), dt)
+    rel_check(f"gate_up_silu rows={rows} {hidden}->{inter}", host(act), want, dt)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_linear_wide_output_tiles(kv, dt):
+    """An lm_head-sized output (4+ thousand 16-feature tiles) takes the
+    four-tiles-per-workgroup form; the rows straddle a 16-row tile."""
+    rng = np.random.default_rng(21)
+    rows, n_out, n_in = 20, 65536 + 64, 256
+    x = O.round_to(rng.standard_normal((rows, n_in)), dt)
+    w = O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt)
+    y = torch.empty((rows, n_out), dtype=_T[dt], device=DEV)
+    kv.linear(dev(x, dt), dev(w, dt), None, y, rows, n_out, n_in, dt)
+    rel_check("linear wide", host(y), O.linear_ref(x, w, None, dt), dt)
+
+
+def test_fused_projections_reject_bad_shapes(kv):
+    x = torch.zeros((4, 96), dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros((48, 96), dtype=torch.bfloat16, device=DEV)
+    o = torch.zeros((4, 48), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(kv.RlseError):   # in_features not a multiple of 32
+        kv.linear_residual(x[:, :80].contiguous(), w[:, :80].contiguous(), o, 4, 48, 80, "bf16")
+    with pytest.raises(kv.RlseError):   # f32 has no MFMA form here
+        kv.linear_residual(x.float(), w.float(), o.float(), 4, 48, 96, "f32")
+    with pytest.raises(kv.RlseError):   # feature counts must be multiples of 16
+        kv.qkv_proj(x, w, None, o, o, o, 4, 96, 24, 12, "bf16")
+    with pytest.raises(kv.RlseError):   # misaligned input
+        kv.gate_up_silu(x.view(-1)[1:].data_ptr(), w, o, 4, 96, 24, "bf16")
 
 
 # ------------------------------------------------------------ whole steps ---
@@ -171,7 +315,7 @@ def _setup(kv, arch, dt, ctx_lens, steps, seed):
     return spec, w, model, t_dev, kc, vc, O.round_to(cos_t, dt), O.round_to(sin_t, dt), rng
 
 
-@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("arch", ["qwen3", "qwen2"])
 def test_decode_steps_match_oracle(kv, arch, dt):
     """Three steps of a 3-sequence batch with ragged cached contexts (0, 17
