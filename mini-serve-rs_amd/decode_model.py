@@ -140,12 +140,53 @@ class DecodeModel:
         # Zero once: every launch of the decode kernel leaves it zero again.
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=dev)
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
+        self.layer_pools = [self.pool.layer(l) for l in range(cfg.layers)]
+        # Inputs of captured steps: the graph reads them at these addresses.
+        self.ids_in = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.tables_in = torch.zeros((B, max_blocks_per_seq), dtype=torch.int32, device=dev)
+        self.lens_in = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.graphs = {}
 
     def close(self) -> None:
         if getattr(self, "pool", None) is not None:
             torch.cuda.synchronize(self.device)
+            self.graphs.clear()
             self.pool.close()
             self.pool = None
+
+    # -- captured steps ------------------------------------------------------
+    def capture(self, batch: int, feed_back: bool = True) -> None:
+        """Records step(ids_in, tables_in, lens_in, batch) into a HIP graph
+        (through torch.cuda.CUDAGraph): a replay issues the step's ~200
+        launches at once instead of one host call each. With feed_back the
+        graph ends by copying the greedy ids into ids_in, so successive
+        replays decode greedily on the device alone. No launch of the step
+        records a memset: every workspace it uses is left zero by the kernels
+        themselves."""
+        torch.cuda.synchronize(self.device)
+        # One eager run first, outside the capture, with every length zero
+        # (nothing is appended or attended), then the inputs are restored.
+        saved = self.lens_in.clone()
+        self.lens_in.zero_()
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.step(self.ids_in, self.tables_in, self.lens_in, batch)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        self.lens_in.copy_(saved)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            _, nxt = self.step(self.ids_in, self.tables_in, self.lens_in, batch)
+            if feed_back:
+                self.ids_in[:batch].copy_(nxt)
+        self.graphs[batch] = g
+
+    def replay(self, batch: int):
+        """Runs the step captured for `batch` on the current stream; returns
+        views of its logits and greedy ids (as step does)."""
+        self.graphs[batch].replay()
+        return self.logits[:batch], self.next_ids[:batch]
 
     # -- KV snapshots (Attention::set_kv_snapshot / get_kv_snapshot) --------
     def set_kv(self, block_table, k, v, start: int = 0, stream=None) -> None:
@@ -193,7 +234,7 @@ class DecodeModel:
                 kv.linear(self.h, L["q_w"], L["q_b"], self.q, batch, nq, H, dt, stream)
                 kv.linear(self.h, L["k_w"], L["k_b"], self.k, batch, nkv, H, dt, stream)
                 kv.linear(self.h, L["v_w"], L["v_b"], self.v, batch, nkv, H, dt, stream)
-            kp, vp = self.pool.layer(l)
+            kp, vp = self.layer_pools[l]
             kv.decode_step(self.q, self.k, self.v, L.get("q_norm"), L.get("k_norm"), cfg.eps,
                            self.cos, self.sin, self.max_pos, kp, vp, block_tables, seq_lens,
                            self.attn, batch, cfg.heads, cfg.kv_heads, cfg.head_dim, self.mbps,

@@ -399,3 +399,52 @@ def test_greedy_loop_on_device_with_step_tables(kv):
         ids_d = nxt.clone()
     assert bm.free_count() == nb - sum(bm.blocks_needed(step + 1 + 9 * i) for i in range(b))
     model.close()
+
+
+def test_captured_step_replays_equal_eager_steps(kv):
+    """DecodeModel.capture records one step into a HIP graph; five replays
+    (each after eager work on the same stream and a synchronisation) give the
+    logits, greedy ids and K/V that five eager steps of an identical model
+    give, bit for bit, and the fed-back ids drive the next replay."""
+    from decode_model import DecodeModel, ModelConfig
+    dt, arch = "bf16", "qwen3"
+    spec = O.ModelSpec(**SPECS[arch])
+    rng = np.random.default_rng(17)
+    w = O.random_weights(spec, rng, dt)
+    b, mbps, nb = 3, 4, 16
+    ctx = [5, 20, 33]
+    tables = build_tables(rng, [mbps * 16] * b, nb, mbps)
+    eager = DecodeModel(ModelConfig(**SPECS[arch]), w, dt, nb, b, mbps)
+    graph = DecodeModel(ModelConfig(**SPECS[arch]), w, dt, nb, b, mbps)
+    t_dev = torch.from_numpy(tables).to(DEV)
+    for i, n in enumerate(ctx):
+        k = O.round_to(rng.standard_normal((spec.layers, spec.kv_heads, n, spec.head_dim)), dt)
+        v = O.round_to(rng.standard_normal(k.shape), dt)
+        eager.set_kv(t_dev[i], k, v)
+        graph.set_kv(t_dev[i], k, v)
+    ids = torch.from_numpy(np.array(rng.integers(0, spec.vocab, b), np.int32)).to(DEV)
+    graph.tables_in.copy_(t_dev)
+    graph.ids_in.copy_(ids)
+    graph.capture(b)
+    lens = np.array(ctx, np.int32)
+    for step in range(5):
+        lens = lens + 1
+        lens_d = torch.from_numpy(lens).to(DEV)
+        le, ne = eager.step(ids, t_dev, lens_d, b)
+        le, ne = le.clone(), ne.clone()
+        scratch = torch.randn(1 << 20, device=DEV).sum()      # eager work between replays
+        torch.cuda.synchronize()
+        graph.lens_in.copy_(lens_d)
+        lg, ng = graph.replay(b)
+        torch.cuda.synchronize()
+        assert torch.equal(le, lg), step
+        assert torch.equal(ne, ng), step
+        assert torch.equal(graph.ids_in, ne)                   # fed back for the next replay
+        ids = ne.clone()
+        del scratch
+    for i, n in enumerate(lens):
+        ke, ve = eager.get_kv(t_dev[i], int(n))
+        kg, vg = graph.get_kv(t_dev[i], int(n))
+        assert torch.equal(ke, kg) and torch.equal(ve, vg)
+    eager.close()
+    graph.close()
