@@ -584,14 +584,15 @@ def e2e_cpu_baseline(args, cfg, cached):
     kc = [[np.ascontiguousarray(np.broadcast_to(tile, (cfg.kv_heads, n, cfg.head_dim)))
            for n in sub] for _ in range(cfg.layers)]
     vc = [[x.copy() for x in row] for row in kc]
-    cos_t, sin_t = O.rope_tables_f32(cfg.theta, cfg.head_dim, max(sub) + 2)
+    max_steps = 5
+    cos_t, sin_t = O.rope_tables_f32(cfg.theta, cfg.head_dim, max(sub) + max_steps + 1)
     ids = list(rng.integers(0, cfg.vocab, len(sub)))
     steps, t0 = 0, time.perf_counter()
     while True:
         O.model_step_ref(spec, w, ids, kc, vc, cos_t, sin_t, "f32")
         steps += 1
         el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or steps >= 5:
+        if el >= args.cpu_seconds or steps >= max_steps:
             break
     return {"value": len(sub) * steps / el, "unit": "tokens/s", "cores": O.max_threads(),
             "kind": "port",
