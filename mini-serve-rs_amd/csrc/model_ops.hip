@@ -73,6 +73,14 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
   const size_t base = (size_t)blockIdx.x * n;
   const int chunks = n / E;
   const uint4* rr = reinterpret_cast<const uint4*>(residual + base);
+  // The weight is requested with the row, so its loads are not a second
+  // round trip after the sum of squares.
+  uint4 wp[kNormChunks];
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ci = threadIdx.x + c * kNormThreads;
+    wp[c] = ci < chunks ? reinterpret_cast<const uint4*>(w)[ci] : make_uint4(0, 0, 0, 0);
+  }
   float h[kNormChunks][E];
   float ss = 0.f;
 #pragma unroll
@@ -97,7 +105,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
     const int ci = threadIdx.x + c * kNormThreads;
     if (ci < chunks) {
       float wv[E], o[E];
-      Packet<T>::unpack(reinterpret_cast<const uint4*>(w)[ci], wv);
+      Packet<T>::unpack(wp[c], wv);
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] = round_to<T>(h[c][e] / norm) * wv[e];
       reinterpret_cast<uint4*>(out + base)[ci] = pack_packet<T>(o);
@@ -361,6 +369,27 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
   for (int f = 0; f < FT; ++f)
 #pragma unroll
     for (int t = 0; t < RT; ++t) acc[f][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // Epilogue operands read from memory (the residual, the bias) are
+  // requested before the main loop: they arrive with its loads instead of
+  // costing a round trip after it. Only the merging slice (or an unsplit
+  // workgroup) needs them.
+  float pre[kItemsPerThread][4];
+#pragma unroll
+  for (int k = 0; k < kItemsPerThread; ++k) {
+    const int it = threadIdx.x + k * 64 * kDenseWaves;
+    const int l2 = it & (64 / kPair - 1);
+    const int ft = it / (64 / kPair);
+    const int t = ft % RT, f = ft / RT;
+    const int b = 16 * t + (l2 & 15);
+    const int n = (grp * FT + f) * 16 + 4 * (l2 >> 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pre[k][e] = 0.f;
+    if (it >= kItems || b >= p.rows || ks != KS - 1) continue;
+    if constexpr (EPI == kEpiResidual) load4<T>((const T*)p.out0 + (size_t)b * p.N + n, pre[k]);
+    if constexpr (EPI == kEpiStore || EPI == kEpiQkv)
+      if (p.bias) load4<T>((const T*)p.bias + n, pre[k]);
+  }
+
   const int S = K >> 5;
   const int slice_end = (ks + 1) * S / KS;
   const int s_begin = ks * S / KS + wave * p.steps;
@@ -414,25 +443,6 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
           v[k][q][e] = x;
         }
     }
-  }
-
-  // Epilogue operands read from memory (the residual, the bias) are loaded
-  // before the merge waits, so that round trip overlaps it.
-  float pre[kItemsPerThread][4];
-#pragma unroll
-  for (int k = 0; k < kItemsPerThread; ++k) {
-    const int it = threadIdx.x + k * 64 * kDenseWaves;
-    const int l2 = it & (64 / kPair - 1);
-    const int ft = it / (64 / kPair);
-    const int t = ft % RT, f = ft / RT;
-    const int b = 16 * t + (l2 & 15);
-    const int n = (grp * FT + f) * 16 + 4 * (l2 >> 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) pre[k][e] = 0.f;
-    if (it >= kItems || b >= p.rows) continue;
-    if constexpr (EPI == kEpiResidual) load4<T>((const T*)p.out0 + (size_t)b * p.N + n, pre[k]);
-    if constexpr (EPI == kEpiStore || EPI == kEpiQkv)
-      if (p.bias) load4<T>((const T*)p.bias + n, pre[k]);
   }
 
   bool ok = true;
