@@ -350,7 +350,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(PrefillParams p) 
   }
   // Key splits: store this split's (acc, m, l) for the workgroup's rows in
   // its register layout -- float4 slot k of thread tid at
-  // blk + (k*256 + tid)*4 floats, slots 0..4*DB-1 holding acc and slot 4*DB
+  // blk + (k*kPThreads + tid)*4 floats, slots 0..4*DB-1 holding acc and slot 4*DB
   // (m, l) -- so every store covers 1 KB of consecutive bytes. The merge
   // launch reads them back with the same thread-to-row map.
   float4* blk = part_block<D>(p, split, h, rt) + tid;
@@ -363,50 +363,71 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(PrefillParams p) 
   blk[4 * DB * kPThreads] = make_float4(m, lsum, 0.f, 0.f);
 }
 
-// Log-sum-exp merge of the key splits: one workgroup per (row tile, KV
-// head), thread tid combining the slots thread tid of every split stored.
+// Log-sum-exp merge of the key splits. Workgroup (row tile, KV head, q)
+// combines slots 4q..4q+3 of every row: thread tid reads what thread tid of
+// each split stored, so all the loads of kMergeBatch splits are in flight
+// together and D/32 workgroups share a tile. The splits combine online in
+// split order (a deterministic result): with (M, L, A) so far and a split's
+// (m, l, a), M' = max(M, m) and L, A scale by 2^(M - M') and 2^(m - M').
+constexpr int kMergeBatch = 4;
 template <typename T, int D>
 __global__ __launch_bounds__(kPThreads) void prefill_merge_kernel(PrefillParams p) {
   constexpr int DB = D / 32;
+  constexpr int KQ = 4;  // float4 slots per thread: 4*DB slots over DB workgroups
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, half = lane >> 5, col = lane & 31;
-  const int rt = blockIdx.x % p.row_tiles, h = blockIdx.x / p.row_tiles;
+  const int q = blockIdx.x % DB;
+  const int tile = blockIdx.x / DB;
+  const int rt = tile % p.row_tiles, h = tile / p.row_tiles;
   const int G = p.G, Hq = p.Hq;
   const int rows = p.Tq * G;
   const int myrow = rt * kBM + wave * 32 + col;
   if (myrow >= rows) return;
   const int t = myrow / G, qh = h * G + (myrow - (myrow / G) * G);
-  float M = -INFINITY;
-  for (int sp = 0; sp < p.splits; ++sp)
-    M = fmaxf(M, (part_block<D>(p, sp, h, rt) + tid)[4 * DB * kPThreads].x);
-  const float Ms = M == -INFINITY ? 0.f : M;
-  float Lw = 0.f;
-  float acc[DB * 16];
+  float M = -INFINITY, L = 0.f;
+  float acc[KQ * 4];
 #pragma unroll
-  for (int i = 0; i < DB * 16; ++i) acc[i] = 0.f;
-  for (int sp = 0; sp < p.splits; ++sp) {
-    const float4* blk = part_block<D>(p, sp, h, rt) + tid;
-    const float4 ml = blk[4 * DB * kPThreads];
-    const float w = __builtin_amdgcn_exp2f(ml.x - Ms);
-    Lw += w * ml.y;
+  for (int i = 0; i < KQ * 4; ++i) acc[i] = 0.f;
+  for (int s0 = 0; s0 < p.splits; s0 += kMergeBatch) {
+    float4 ml[kMergeBatch], a[kMergeBatch][KQ];
 #pragma unroll
-    for (int k = 0; k < 4 * DB; ++k) {
-      const float4 a = blk[k * kPThreads];
-      acc[k * 4] += w * a.x;
-      acc[k * 4 + 1] += w * a.y;
-      acc[k * 4 + 2] += w * a.z;
-      acc[k * 4 + 3] += w * a.w;
+    for (int j = 0; j < kMergeBatch; ++j) {
+      // Past the last split: re-read the last one (never combined).
+      const int sp = s0 + j < p.splits ? s0 + j : p.splits - 1;
+      const float4* blk = part_block<D>(p, sp, h, rt) + tid;
+      ml[j] = blk[4 * DB * kPThreads];
+#pragma unroll
+      for (int kk = 0; kk < KQ; ++kk) a[j][kk] = blk[(q * KQ + kk) * kPThreads];
+    }
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {
+      if (s0 + j >= p.splits) break;
+      const float m = ml[j].x;
+      const float Mn = fmaxf(M, m);
+      if (Mn == -INFINITY) continue;  // no visible key so far
+      const float sa = __builtin_amdgcn_exp2f(M - Mn);
+      const float sb = __builtin_amdgcn_exp2f(m - Mn);
+      L = L * sa + ml[j].y * sb;
+#pragma unroll
+      for (int kk = 0; kk < KQ; ++kk) {
+        acc[kk * 4] = acc[kk * 4] * sa + a[j][kk].x * sb;
+        acc[kk * 4 + 1] = acc[kk * 4 + 1] * sa + a[j][kk].y * sb;
+        acc[kk * 4 + 2] = acc[kk * 4 + 2] * sa + a[j][kk].z * sb;
+        acc[kk * 4 + 3] = acc[kk * 4 + 3] * sa + a[j][kk].w * sb;
+      }
+      M = Mn;
     }
   }
-  const float inv = Lw > 0.f ? 1.f / Lw : 0.f;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
   T* dst = reinterpret_cast<T*>(p.out) + ((size_t)t * Hq + qh) * D;
 #pragma unroll
-  for (int k = 0; k < 4 * DB; ++k) {
+  for (int kk = 0; kk < KQ; ++kk) {
     // slot k = (db, i4): dims 32*db + 8*i4 + 4*half .. +3
+    const int k = q * KQ + kk;
     const int d0 = (k >> 2) * 32 + (k & 3) * 8 + half * 4;
     *reinterpret_cast<uint2*>(dst + d0) =
-        make_uint2(Packet<T>::pack2(acc[k * 4] * inv, acc[k * 4 + 1] * inv),
-                   Packet<T>::pack2(acc[k * 4 + 2] * inv, acc[k * 4 + 3] * inv));
+        make_uint2(Packet<T>::pack2(acc[kk * 4] * inv, acc[kk * 4 + 1] * inv),
+                   Packet<T>::pack2(acc[kk * 4 + 2] * inv, acc[kk * 4 + 3] * inv));
   }
 }
 
@@ -447,8 +468,8 @@ int launch_prefill(PrefillParams& pp, hipStream_t stream) {
   hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(nwg), dim3(kPThreads), 0, stream, pp);
   const int st = launch_status("prefill_kernel");
   if (st || pp.splits == 1) return st;
-  hipLaunchKernelGGL((prefill_merge_kernel<T, D>), dim3(pp.row_tiles * pp.Hkv), dim3(kPThreads),
-                     0, stream, pp);
+  hipLaunchKernelGGL((prefill_merge_kernel<T, D>), dim3(pp.row_tiles * pp.Hkv * (D / 32)),
+                     dim3(kPThreads), 0, stream, pp);
   return launch_status("prefill_merge_kernel");
 }
 
