@@ -366,17 +366,21 @@ def fork_bench(args):
     out = torch.empty((b, hq, d), device=dev, dtype=bf)
     ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    plan_bytes = kv.decode_plan_size()
+    plan = torch.zeros(plan_bytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     scale = 1.0 / math.sqrt(d)
     ptrs = [pool.layer(layer) for layer in range(layers)]
 
     def step(evs=None):
+        kv.decode_plan(t_dev, lens_dev, b, hkv, mbps, nb, plan, plan_bytes, stream)
         for layer in range(layers):
             if evs is not None:
                 evs[layer][0].record(stream)
-            kv.decode_step(q_in[layer], k_in[layer], v_in[layer], qw, kw, 1e-6, cos_t, sin_t,
-                           max_pos, ptrs[layer][0], ptrs[layer][1], t_dev, lens_dev, out, b, hq,
-                           hkv, d, mbps, nb, scale, "bf16", ws, ws_bytes, stream)
+            kv.decode_step_planned(q_in[layer], k_in[layer], v_in[layer], qw, kw, 1e-6, cos_t,
+                                   sin_t, max_pos, ptrs[layer][0], ptrs[layer][1], t_dev,
+                                   lens_dev, out, b, hq, hkv, d, mbps, nb, scale, "bf16", plan,
+                                   ws, ws_bytes, stream)
             if evs is not None:
                 evs[layer][1].record(stream)
 
@@ -663,6 +667,8 @@ def main():
     out = torch.empty((b, hq, d), device=dev, dtype=bf)
     ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # zero-filled before first use
+    plan_bytes = kv.decode_plan_size()
+    plan = torch.zeros(plan_bytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     scale = 1.0 / math.sqrt(d)
     ev_steps = min(args.steps, 50)
@@ -671,6 +677,9 @@ def main():
     ev_b = [torch.cuda.Event(enable_timing=True) for _ in range(n_events)]
 
     def step(timed_index=None):
+        if not args.unfused:
+            # One plan per step (the tables and lengths of every layer).
+            kv.decode_plan(t_dev, lens_dev, b, hkv, mbps, nb, plan, plan_bytes, stream)
         for layer in range(layers):
             if args.unfused:
                 kv.qk_norm_rope_append(q_in[layer], k_in[layer], v_in[layer], qw[layer],
@@ -683,10 +692,10 @@ def main():
                 kv.paged_gqa_decode(q_rot, k_pools[layer], v_pools[layer], t_dev, lens_dev, out,
                                     b, hq, hkv, d, mbps, nb, scale, "bf16", ws, ws_bytes, stream)
             else:
-                kv.decode_step(q_in[layer], k_in[layer], v_in[layer], qw[layer], kw[layer], 1e-6,
-                               cos_t, sin_t, max_pos, k_pools[layer], v_pools[layer], t_dev,
-                               lens_dev, out, b, hq, hkv, d, mbps, nb, scale, "bf16", ws,
-                               ws_bytes, stream)
+                kv.decode_step_planned(q_in[layer], k_in[layer], v_in[layer], qw[layer],
+                                       kw[layer], 1e-6, cos_t, sin_t, max_pos, k_pools[layer],
+                                       v_pools[layer], t_dev, lens_dev, out, b, hq, hkv, d, mbps,
+                                       nb, scale, "bf16", plan, ws, ws_bytes, stream)
             if timed_index is not None:
                 ev_b[timed_index * layers + layer].record(stream)
 

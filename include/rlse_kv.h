@@ -162,6 +162,30 @@ int rlse_decode_step(const void* q, const void* k_new, const void* v_new,
                      int max_blocks_per_seq, int num_blocks, float scale, int dtype,
                      void* workspace, size_t workspace_bytes, rlse_stream_t stream);
 
+/* Per-step plan for rlse_decode_step_planned: the first block descriptors
+ * of every wave of a decode launch (page id, valid rows, row, new-token
+ * position), computed once from the step's block tables and lengths instead
+ * of by every layer's launch. No counterpart in the reference: its decode
+ * runs per sequence on contiguous buffers, with no page tables to walk.
+ * plan: rlse_decode_plan_size bytes, 16-byte aligned. */
+int rlse_decode_plan_size(size_t* bytes);
+int rlse_decode_plan(const int32_t* block_tables, const int32_t* seq_lens, int batch,
+                     int num_kv_heads, int max_blocks_per_seq, int num_blocks, void* plan,
+                     size_t plan_bytes, rlse_stream_t stream);
+/* rlse_decode_step with a plan that rlse_decode_plan built from the same
+ * block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq and
+ * num_blocks (every layer of a decode step shares them): each wave's page
+ * ids then arrive with its first load instead of after a table walk.
+ * Results are identical to rlse_decode_step's. */
+int rlse_decode_step_planned(const void* q, const void* k_new, const void* v_new,
+                             const void* q_norm_weight, const void* k_norm_weight, float eps,
+                             const void* cos_table, const void* sin_table, int max_pos,
+                             void* k_pool, void* v_pool, const int32_t* block_tables,
+                             const int32_t* seq_lens, void* out, int batch, int num_heads,
+                             int num_kv_heads, int head_dim, int max_blocks_per_seq,
+                             int num_blocks, float scale, int dtype, void* workspace,
+                             size_t workspace_bytes, const void* plan, rlse_stream_t stream);
+
 /* Chunked-prefill attention of one sequence: the prefill branch of
  * Attention::forward (src/backends/qwen2.rs:329-345) with the causal mask
  * of prepare_causal_attention_mask (src/backends/qwen2.rs:476-503), read

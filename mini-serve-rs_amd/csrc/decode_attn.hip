@@ -14,6 +14,37 @@ RLSE_DECODE_INSTANCES(extern template, bf16, true)
 RLSE_DECODE_INSTANCES(extern template, f16, false)
 RLSE_DECODE_INSTANCES(extern template, f16, true)
 
+// Per-step plan: for every wave of every workgroup of a decode launch, the
+// descriptors of its first 64 blocks -- exactly what the wave would compute
+// with the same lengths and tables (same prefix, ranges and block_desc).
+// One launch serves every layer of a step: the tables and lengths are the
+// same in each.
+__global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __restrict__ tables,
+                                                               const int* __restrict__ seq_lens,
+                                                               int B, int Hkv, int mbps,
+                                                               int num_blocks, int W,
+                                                               int4* __restrict__ plan) {
+  extern __shared__ int s_pref[];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  if (wave == 0) block_prefix(seq_lens, B, mbps, s_pref);
+  __syncthreads();
+  const long long w = blockIdx.x;
+  const long long total = (long long)Hkv * s_pref[B];
+  int4 d = make_int4(0, 0, -1, 0);
+  if (total > 0) {
+    const long long we = effective_groups(total, W);
+    if (w < we) {
+      const long long glo = range_lo(w, total, we);
+      const long long ghi = range_lo(w + 1, total, we);
+      const long long wlo = glo + (ghi - glo) * wave / kWaves;
+      const long long whi = glo + (ghi - glo) * (wave + 1) / kWaves;
+      d = block_desc(wlo + lane, whi, s_pref, tables, seq_lens, B, Hkv, mbps, num_blocks);
+    }
+  }
+  plan[((size_t)w * kWaves + wave) * 64 + lane] = d;
+}
+
 static int decode_groups(int* W) {
   int cus = 0;
   int st = device_cu_count(&cus);
@@ -177,14 +208,48 @@ extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const vo
                                     as_stream(stream));
 }
 
-extern "C" int rlse_decode_step(const void* q, const void* k_new, const void* v_new,
+extern "C" int rlse_decode_plan_size(size_t* bytes) {
+  if (!bytes) return fail(RLSE_ERR_INVALID_VALUE, "decode_plan_size: null output");
+  int W = 0;
+  const int st = decode_groups(&W);
+  if (st) return st;
+  *bytes = (size_t)W * kWaves * 64 * sizeof(int4);
+  return RLSE_OK;
+}
+
+extern "C" int rlse_decode_plan(const int32_t* block_tables, const int32_t* seq_lens, int batch,
+                                int num_kv_heads, int max_blocks_per_seq, int num_blocks,
+                                void* plan, size_t plan_bytes, rlse_stream_t stream) {
+  if (batch <= 0 || batch > kMaxDecodeBatch || num_kv_heads <= 0 ||
+      (long long)batch * num_kv_heads > kMaxDecodeRows || max_blocks_per_seq <= 0 ||
+      num_blocks <= 0 || (long long)max_blocks_per_seq * 16 > 0x7fffffffLL)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_plan: bad shape");
+  if (!block_tables || !seq_lens || !plan)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_plan: null pointer argument");
+  size_t need = 0;
+  int st = rlse_decode_plan_size(&need);
+  if (st) return st;
+  if (plan_bytes < need || (uintptr_t)plan % 16)
+    return fail(RLSE_ERR_BUFFER_TOO_SMALL, "decode_plan: %zu bytes (16-byte aligned) needed, %zu "
+                                           "given", need, plan_bytes);
+  int W = 0;
+  st = decode_groups(&W);
+  if (st) return st;
+  const size_t lds = (size_t)(batch + 1) * sizeof(int);
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(W), dim3(kThreads), lds, as_stream(stream),
+                     block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq, num_blocks,
+                     W, reinterpret_cast<int4*>(plan));
+  return launch_status("decode_plan_kernel");
+}
+
+static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
                                 const void* q_norm_weight, const void* k_norm_weight, float eps,
                                 const void* cos_table, const void* sin_table, int max_pos,
                                 void* k_pool, void* v_pool, const int32_t* block_tables,
                                 const int32_t* seq_lens, void* out, int batch, int num_heads,
                                 int num_kv_heads, int head_dim, int max_blocks_per_seq,
                                 int num_blocks, float scale, int dtype, void* workspace,
-                                size_t workspace_bytes, rlse_stream_t stream) {
+                                size_t workspace_bytes, const void* plan, rlse_stream_t stream) {
   DecodeParams p;
   const int st = prepare_decode(p, q, k_pool, v_pool, block_tables, seq_lens, out, batch,
                                 num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
@@ -206,8 +271,39 @@ extern "C" int rlse_decode_step(const void* q, const void* k_new, const void* v_
   p.sin_t = sin_table;
   p.eps = eps;
   p.inv_d = (float)(1.0 / (double)head_dim);
+  if (plan && (uintptr_t)plan % 16)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_step: plan must be 16-byte aligned");
+  p.plan = reinterpret_cast<const int4*>(plan);
   return launch_decode_dtype<true>(dtype, head_dim, num_heads / num_kv_heads, p,
                                    as_stream(stream));
+}
+
+extern "C" int rlse_decode_step(const void* q, const void* k_new, const void* v_new,
+                                const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                const void* cos_table, const void* sin_table, int max_pos,
+                                void* k_pool, void* v_pool, const int32_t* block_tables,
+                                const int32_t* seq_lens, void* out, int batch, int num_heads,
+                                int num_kv_heads, int head_dim, int max_blocks_per_seq,
+                                int num_blocks, float scale, int dtype, void* workspace,
+                                size_t workspace_bytes, rlse_stream_t stream) {
+  return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
+                          sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
+                          num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
+                          scale, dtype, workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" int rlse_decode_step_planned(
+    const void* q, const void* k_new, const void* v_new, const void* q_norm_weight,
+    const void* k_norm_weight, float eps, const void* cos_table, const void* sin_table,
+    int max_pos, void* k_pool, void* v_pool, const int32_t* block_tables,
+    const int32_t* seq_lens, void* out, int batch, int num_heads, int num_kv_heads, int head_dim,
+    int max_blocks_per_seq, int num_blocks, float scale, int dtype, void* workspace,
+    size_t workspace_bytes, const void* plan, rlse_stream_t stream) {
+  if (!plan) return fail(RLSE_ERR_INVALID_VALUE, "decode_step_planned: null plan");
+  return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
+                          sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
+                          num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
+                          scale, dtype, workspace, workspace_bytes, plan, stream);
 }
 
 static int compat_decode(const void* q, const void* k, const void* v, const int* tables,

@@ -114,6 +114,34 @@ __device__ __forceinline__ int locate_seq(const int* s_pref, int B, int Hkv, lon
   return lo;
 }
 
+// Descriptor of block f of the page stream (f < the wave's end): the page id,
+// the valid rows in bits 0-7 (0 for a page id outside the pool) with bit 8
+// set on the last block of its row, the (sequence, KV head) row and the
+// row's new-token position. Blocks past the wave's end get {0, 0, -1, 0}.
+__device__ __forceinline__ int4 block_desc(long long f, long long whi, const int* s_pref,
+                                           const int* __restrict__ tables,
+                                           const int* __restrict__ seq_lens, int B, int Hkv,
+                                           int mbps, int num_blocks) {
+  int4 d = make_int4(0, 0, -1, 0);
+  if (f < whi) {
+    const int b = locate_seq(s_pref, B, Hkv, f);
+    const int nb = s_pref[b + 1] - s_pref[b];
+    const long long o = f - (long long)Hkv * s_pref[b];
+    const int kvh = (int)(o / nb), blk = (int)(o % nb);
+    d.z = b * Hkv + kvh;
+    d.x = tables[(size_t)b * mbps + blk];
+    const int L = clamp_len(seq_lens[b], mbps);
+    const int nv = L - blk * 16;
+    d.y = nv > 16 ? 16 : nv;
+    d.w = L - 1;
+    if ((unsigned)d.x >= (unsigned)num_blocks)
+      d.y = 0;
+    else if (blk == nb - 1)
+      d.y |= 256;
+  }
+  return d;
+}
+
 // Words of one partial record: acc[G][D], then m[G] and l[G], padded so
 // records stay 16-byte aligned.
 __host__ __device__ constexpr int rec_floats(int G, int D) { return G * D + ((2 * G + 3) & ~3); }
@@ -144,6 +172,10 @@ struct DecodeParams {
   const void* sin_t;
   float eps;
   float inv_d;
+  // Optional per-step plan (rlse_decode_plan): the first 64 block
+  // descriptors of every wave, as block_desc computes them. Null: each wave
+  // derives them from the lengths and the block tables.
+  const int4* plan;
 };
 
 // Combines (m, l, a) with (mo, lo, ao), all in log2 units; -inf maxima mean
@@ -291,6 +323,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   T* __restrict__ ob = reinterpret_cast<T*>(p.out);
 
   int* s_len = s_pref + B + 1;  // fused step: clamped sequence lengths
+  // With a plan the wave's first descriptors are requested first of all:
+  // they then arrive while wave 0 computes the block prefix, instead of a
+  // page-table walk starting after it.
+  int4 plan_d = make_int4(0, 0, -1, 0);
+  if (p.plan) plan_d = p.plan[((size_t)blockIdx.x * kWaves + wave) * 64 + lane];
   if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref);
   if constexpr (FUSED) {
     for (int b = tid; b < B; b += kThreads) s_len[b] = clamp_len(p.seq_lens[b], mbps);
@@ -337,27 +374,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     int d_id = 0, d_nv = 0, d_row = -1, d_pos = 0, cbase = 0;
     auto load_chunk = [&](int base) __attribute__((always_inline)) {
       cbase = base;
-      const long long f = wlo + base + lane;
-      d_id = 0;
-      d_nv = 0;
-      d_row = -1;
-      d_pos = 0;
-      if (f < whi) {
-        const int b = locate_seq(s_pref, B, Hkv, f);
-        const int nb = s_pref[b + 1] - s_pref[b];
-        const long long o = f - (long long)Hkv * s_pref[b];
-        const int kvh = (int)(o / nb), blk = (int)(o % nb);
-        d_row = b * Hkv + kvh;
-        d_id = p.tables[(size_t)b * mbps + blk];
-        const int L = clamp_len(p.seq_lens[b], mbps);
-        const int nv = L - blk * 16;
-        d_nv = nv > 16 ? 16 : nv;
-        d_pos = L - 1;
-        if ((unsigned)d_id >= (unsigned)p.num_blocks)
-          d_nv = 0;
-        else if (blk == nb - 1)
-          d_nv |= 256;
-      }
+      int4 d;
+      if (base == 0 && p.plan)  // the plan's copy, loaded before the barrier
+        d = plan_d;
+      else
+        d = block_desc(wlo + base + lane, whi, s_pref, p.tables, p.seq_lens, B, Hkv, mbps,
+                       p.num_blocks);
+      d_id = d.x;
+      d_nv = d.y;
+      d_row = d.z;
+      d_pos = d.w;
     };
     load_chunk(0);
 

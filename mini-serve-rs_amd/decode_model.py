@@ -13,9 +13,10 @@ their neighbours):
 
     x = embed_tokens[ids]                                  rlse_embedding
     h = input_layernorm(x)                                 rlse_add_rmsnorm (no add)
+    the step's decode plan (page ids per wave)             rlse_decode_plan
     per layer:
       q, k, v = q/k/v_proj(h)                              rlse_qkv_proj (one launch)
-      attn = q/k norm + RoPE + append + paged GQA decode    rlse_decode_step
+      attn = q/k norm + RoPE + append + paged GQA decode    rlse_decode_step_planned
       x += o_proj(attn)                                    rlse_linear_residual
       h = post_attention_layernorm(x)                      rlse_add_rmsnorm (no add)
       a = silu(gate_proj(h)) * up_proj(h)                  rlse_gate_up_silu
@@ -139,6 +140,8 @@ class DecodeModel:
         ws = kv.decode_workspace_size(B, cfg.heads, cfg.kv_heads, cfg.head_dim)
         # Zero once: every launch of the decode kernel leaves it zero again.
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=dev)
+        # The step's decode plan: built once per step, read by every layer.
+        self.plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=dev)
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
         self.layer_pools = [self.pool.layer(l) for l in range(cfg.layers)]
         # Inputs of captured steps: the graph reads them at these addresses.
@@ -226,6 +229,8 @@ class DecodeModel:
         kv.embedding(ids, self.embed, self.x, batch, H, cfg.vocab, dt, stream)
         kv.add_rmsnorm(None, self.x, self.layers[0]["in_norm"], self.h, batch, H, cfg.eps, dt,
                        stream)
+        kv.decode_plan(block_tables, seq_lens, batch, cfg.kv_heads, self.mbps, self.num_blocks,
+                       self.plan, self.plan.numel(), stream)
         for l, L in enumerate(self.layers):
             if self.fused:
                 kv.qkv_proj(self.h, L["qkv_w"], L["qkv_b"], self.q, self.k, self.v, batch, H, nq,
@@ -235,11 +240,12 @@ class DecodeModel:
                 kv.linear(self.h, L["k_w"], L["k_b"], self.k, batch, nkv, H, dt, stream)
                 kv.linear(self.h, L["v_w"], L["v_b"], self.v, batch, nkv, H, dt, stream)
             kp, vp = self.layer_pools[l]
-            kv.decode_step(self.q, self.k, self.v, L.get("q_norm"), L.get("k_norm"), cfg.eps,
-                           self.cos, self.sin, self.max_pos, kp, vp, block_tables, seq_lens,
-                           self.attn, batch, cfg.heads, cfg.kv_heads, cfg.head_dim, self.mbps,
-                           self.num_blocks, self.scale, dt, self.workspace,
-                           self.workspace.numel(), stream)
+            kv.decode_step_planned(self.q, self.k, self.v, L.get("q_norm"), L.get("k_norm"),
+                                   cfg.eps, self.cos, self.sin, self.max_pos, kp, vp,
+                                   block_tables, seq_lens, self.attn, batch, cfg.heads,
+                                   cfg.kv_heads, cfg.head_dim, self.mbps, self.num_blocks,
+                                   self.scale, dt, self.plan, self.workspace,
+                                   self.workspace.numel(), stream)
             nxt = self.layers[l + 1]["in_norm"] if l + 1 < cfg.layers else self.norm
             if self.fused:
                 kv.linear_residual(self.attn, L["o_w"], self.x, batch, H, nq, dt, self.dense_ws,

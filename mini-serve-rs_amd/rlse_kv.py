@@ -69,7 +69,8 @@ EXPORTED = (
     "rlse_st_prepare", "rlse_st_host", "rlse_st_upload", "rlse_st_mark_uploaded",
     "rlse_embedding", "rlse_add_rmsnorm", "rlse_silu_mul", "rlse_argmax", "rlse_linear",
     "rlse_argmax_workspace_size", "rlse_qkv_proj", "rlse_linear_residual", "rlse_gate_up_silu",
-    "rlse_dense_workspace_size",
+    "rlse_dense_workspace_size", "rlse_decode_plan_size", "rlse_decode_plan",
+    "rlse_decode_step_planned",
 )
 
 
@@ -173,6 +174,8 @@ _SIGS = {
                                    _i, _vp, _sz, _vp]),
     "rlse_decode_step": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                               _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp]),
+    "rlse_decode_step_planned": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp,
+                              _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _vp]),
     "rlse_prefill_workspace_size": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz)]),
     "rlse_prefill_attn": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp,
                                _sz, _vp]),
@@ -237,6 +240,8 @@ _SIGS = {
     "rlse_argmax": (_i, [_vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_linear": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rlse_dense_workspace_size": (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
+    "rlse_decode_plan_size": (_i, [ctypes.POINTER(_sz)]),
+    "rlse_decode_plan": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_qkv_proj": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_linear_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_gate_up_silu": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
@@ -716,6 +721,36 @@ def decode_step(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: float, cos_t
         _ptr(block_tables), _ptr(seq_lens), _ptr(out), batch, num_heads, num_kv_heads, head_dim,
         max_blocks_per_seq, num_blocks, scale, _dt(dtype), _ptr(workspace), workspace_bytes,
         _stream(stream)))
+
+
+def decode_plan_size() -> int:
+    """Bytes of a per-step decode plan (rlse_decode_plan)."""
+    n = _sz(0)
+    _check(load().rlse_decode_plan_size(ctypes.byref(n)))
+    return n.value
+
+
+def decode_plan(block_tables, seq_lens, batch: int, num_kv_heads: int, max_blocks_per_seq: int,
+                num_blocks: int, plan, plan_bytes: int, stream=None) -> None:
+    """Builds the per-step plan every layer's decode_step_planned then reads."""
+    _check(load().rlse_decode_plan(_ptr(block_tables), _ptr(seq_lens), batch, num_kv_heads,
+                                   max_blocks_per_seq, num_blocks, _ptr(plan), plan_bytes,
+                                   _stream(stream)))
+
+
+def decode_step_planned(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: float, cos_table,
+                        sin_table, max_pos: int, k_pool, v_pool, block_tables, seq_lens, out,
+                        batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                        max_blocks_per_seq: int, num_blocks: int, scale: float, dtype, plan,
+                        workspace=None, workspace_bytes: int = 0, stream=None) -> None:
+    """decode_step with a plan built by decode_plan from the same tables and
+    lengths; the results are the same bit for bit."""
+    _check(load().rlse_decode_step_planned(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(q_norm_weight), _ptr(k_norm_weight), eps,
+        _ptr(cos_table), _ptr(sin_table), max_pos, _ptr(k_pool), _ptr(v_pool),
+        _ptr(block_tables), _ptr(seq_lens), _ptr(out), batch, num_heads, num_kv_heads, head_dim,
+        max_blocks_per_seq, num_blocks, scale, _dt(dtype), _ptr(workspace), workspace_bytes,
+        _ptr(plan), _stream(stream)))
 
 
 def prefill_workspace_size(num_tokens: int, ctx_len: int, num_heads: int, num_kv_heads: int,

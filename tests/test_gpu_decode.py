@@ -358,3 +358,59 @@ def test_fused_decode_step_matches_two_kernel_path_and_oracle(kv, dtype, hq, hkv
     want = O.decode_paged_f32(q_ref.reshape(b, hq, d), as_f32(pk1, dtype), as_f32(pv1, dtype),
                               tables, lens, scale)
     check(f"fused vs oracle {dtype} G={hq // hkv}", got, want, dtype)
+
+
+@pytest.mark.parametrize("hq,hkv,d,lens", [
+    (16, 8, 128, [1, 2, 15, 16, 17, 33, 300, 2049, 0, 64]),     # Qwen3 shape, ragged, an empty row
+    (14, 2, 64, [4097] * 6 + [5, 0]),                           # Qwen2.5 shape, G = 7
+    (8, 8, 64, [20]),                                           # most workgroups idle
+    (2, 2, 64, [16384] * 72),                                   # > 64 blocks per wave
+])
+def test_planned_step_equals_unplanned(kv, hq, hkv, d, lens):
+    """rlse_decode_step_planned with a plan from rlse_decode_plan gives the
+    outputs and pool contents of rlse_decode_step bit for bit, including rows
+    of length 0, idle workgroups and waves whose range spans several 64-block
+    chunks."""
+    dtype = "bf16"
+    rng = np.random.default_rng(len(lens) * 7 + d)
+    lens = np.asarray(lens, np.int32)
+    b = len(lens)
+    mbps = max(1, int(max((int(n) + 15) // 16 for n in lens)))
+    nb = int(sum((int(n) + 15) // 16 for n in lens)) + 3
+    tables = build_tables(rng, lens, nb, mbps)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(5)
+    bf = torch.bfloat16
+    kp = torch.randn((nb, hkv, 16, d), generator=g, device=DEV).to(bf)
+    vp = torch.randn((nb, hkv, 16, d), generator=g, device=DEV).to(bf)
+    q = torch.randn((b, hq, d), generator=g, device=DEV).to(bf)
+    kn = torch.randn((b, hkv, d), generator=g, device=DEV).to(bf)
+    vn = torch.randn((b, hkv, d), generator=g, device=DEV).to(bf)
+    qw = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(bf)
+    kw = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(bf)
+    max_pos = mbps * 16
+    cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, "bf16")
+    c = torch.frombuffer(bytearray(cos_b), dtype=torch.int16).to(DEV).view(bf)
+    s = torch.frombuffer(bytearray(sin_b), dtype=torch.int16).to(DEV).view(bf)
+    t_dev, l_dev = to_dev(tables), to_dev(lens)
+    scale = 1.0 / math.sqrt(d)
+    outs, pools = [], []
+    plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=DEV)
+    for planned in (False, True, True):
+        kp_i, vp_i = kp.clone(), vp.clone()
+        out = torch.full((b, hq, d), 3.0, dtype=bf, device=DEV)
+        args = (q, kn, vn, qw, kw, 1e-6, c, s, max_pos, kp_i, vp_i, t_dev, l_dev, out, b, hq, hkv,
+                d, mbps, nb, scale, "bf16")
+        if planned:
+            kv.decode_plan(t_dev, l_dev, b, hkv, mbps, nb, plan, plan.numel())
+            kv.decode_step_planned(*args, plan)
+        else:
+            kv.decode_step(*args)
+        torch.cuda.synchronize()
+        outs.append(out)
+        pools.append((kp_i, vp_i))
+    for i in (1, 2):
+        assert torch.equal(outs[0].view(torch.int16), outs[i].view(torch.int16)), i
+        assert torch.equal(pools[0][0].view(torch.int16), pools[i][0].view(torch.int16)), i
+        assert torch.equal(pools[0][1].view(torch.int16), pools[i][1].view(torch.int16)), i
+    print(f"[planned] hq={hq} hkv={hkv} d={d} B={b}: outputs and pools identical")
