@@ -583,6 +583,22 @@ rocblas_handle g_blas[64] = {nullptr};
 
 bool aligned(const void* ptr, size_t a) { return ((uintptr_t)ptr % a) == 0; }
 
+// 16-feature tiles per workgroup. Every workgroup reads the whole batch's x
+// columns of its K range, so x costs (rows / (16 * tiles per group)) times
+// the weight bytes in L2 reads: lm_head-sized outputs take four tiles
+// (plain stores only); batches of more than 32 rows take two when the
+// output still has 256 groups of two, so no K split is needed (the rows of
+// the first 64-row chunk decide; every chunk uses the same grouping).
+// Measured at 64 rows: gate/up of 9728 x 896, 18.4 -> 16.0 us; for outputs
+// that then needed a K split (q/k/v 1152 x 896: 7.9 -> 11.6 us) two tiles
+// cost more than they saved.
+int dense_tiles_per_group(bool plain_store, int rows, int tiles) {
+  if (plain_store && tiles % 4 == 0 && tiles >= 4096) return 4;
+  const int rt = (std::min(rows, kDenseMaxRows) + 15) / 16;
+  if (rt >= 3 && tiles % 2 == 0 && tiles / 2 >= 256) return 2;
+  return 1;
+}
+
 // K slices per output tile group: enough workgroups to cover every compute
 // unit (256 on MI355X) when the output has few 16-feature tiles, each slice
 // at least 4 k steps of 32. Outputs with 256 or more tiles are not split:
@@ -605,10 +621,9 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
                  size_t o2_stride, size_t ws_words, hipStream_t s) {
   const int total_rows = p.rows;
   const int tiles = EPI == kEpiSiluMul ? p.n1 / 8 : p.N / 16;
-  // Wide outputs (lm_head) take four feature tiles per workgroup: the x
-  // columns a wave loads serve four A tiles, a quarter of the L2 reads.
-  const bool wide = EPI == kEpiStore && tiles % 4 == 0 && tiles >= 4096;
-  const int groups = wide ? tiles / 4 : tiles;
+  const int ft = dense_tiles_per_group(EPI == kEpiStore, total_rows, tiles);
+  const bool wide = ft == 4;
+  const int groups = tiles / ft;
   const int ks = p.ws ? dense_split(groups, p.K) : 1;
   const int steps_total = p.K / 32;
   const int slice = (steps_total + ks - 1) / ks;
@@ -626,7 +641,7 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
     q.out1 = base1 ? (void*)(base1 + (size_t)r0 * o1_stride * sizeof(T)) : nullptr;
     q.out2 = base2 ? (void*)(base2 + (size_t)r0 * o2_stride * sizeof(T)) : nullptr;
     const int rt = (q.rows + 15) / 16;
-    if (ks > 1 && (size_t)groups * (ks - 1) * (wide ? 4 : 1) * rt * 256 > ws_words)
+    if (ks > 1 && (size_t)groups * (ks - 1) * ft * rt * 256 > ws_words)
       return fail(RLSE_ERR_INVALID_VALUE, "dense: workspace too small");
     const dim3 block(64 * kDenseWaves);
     const dim3 grid(groups * ks);
@@ -637,6 +652,10 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
           hipLaunchKernelGGL((dense_rows_kernel<T, RT, 4, EPI>), grid, block, 0, s, q);
           return;
         }
+      }
+      if (ft == 2) {  // every chunk keeps the grouping (a short last chunk too)
+        hipLaunchKernelGGL((dense_rows_kernel<T, RT, 2, EPI>), grid, block, 0, s, q);
+        return;
       }
       hipLaunchKernelGGL((dense_rows_kernel<T, RT, 1, EPI>), grid, block, 0, s, q);
     };
@@ -655,9 +674,10 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
 // Workspace words a fused projection needs for its K split (0: none).
 size_t dense_ws_words(int rows, int tiles, int K) {
   if (rows <= 0 || tiles <= 0 || K < 32) return 0;
-  const int ks = dense_split(tiles, K);
+  const int ft = dense_tiles_per_group(false, rows, tiles);
+  const int ks = dense_split(tiles / ft, K);
   const int rt = (std::min(rows, kDenseMaxRows) + 15) / 16;
-  return ks > 1 ? (size_t)tiles * (ks - 1) * rt * 256 : 0;
+  return ks > 1 ? (size_t)(tiles / ft) * (ks - 1) * ft * rt * 256 : 0;
 }
 
 // Shape and alignment checks shared by the MFMA entry points.

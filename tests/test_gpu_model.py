@@ -100,7 +100,8 @@ def test_silu_mul_matches_oracle(kv, dt):
 
 @pytest.mark.parametrize("dt", O.DTYPES)
 @pytest.mark.parametrize("rows,n_out,n_in,bias", [(1, 2048, 1024, False), (32, 3072, 1024, True),
-                                                  (33, 896, 4864, False), (64, 1000, 128, True)])
+                                                  (33, 896, 4864, False), (64, 1000, 128, True),
+                                                  (40, 8192, 256, True)])   # two tiles per group
 def test_linear_matches_oracle(kv, dt, rows, n_out, n_in, bias):
     rng = np.random.default_rng(rows + n_out)
     x = O.round_to(rng.standard_normal((rows, n_in)), dt)
@@ -201,7 +202,8 @@ def test_qkv_proj_matches_three_linears(kv, dt, rows, hidden, nq, nkv, bias):
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("rows", ROWS)
 @pytest.mark.parametrize("split", [True, False])
-@pytest.mark.parametrize("n_out,n_in", [(1024, 2048), (1024, 3072), (896, 4864), (64, 160)])
+@pytest.mark.parametrize("n_out,n_in", [(1024, 2048), (1024, 3072), (896, 4864), (64, 160),
+                                        (8192, 128)])
 def test_linear_residual_matches_oracle(kv, dt, rows, split, n_out, n_in):
     rng = np.random.default_rng(rows + n_in)
     x = O.round_to(rng.standard_normal((rows, n_in)), dt)
