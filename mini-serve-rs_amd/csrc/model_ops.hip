@@ -204,7 +204,7 @@ __device__ __forceinline__ unsigned long long wave_max_key(unsigned long long k)
   return k;
 }
 
-template <typename T>
+template <typename T, bool VEC>
 __global__ __launch_bounds__(kArgThreads) void argmax_partial_kernel(
     const T* __restrict__ logits, unsigned long long* __restrict__ keys, int vocab, int parts) {
   const int part = blockIdx.x;
@@ -213,12 +213,28 @@ __global__ __launch_bounds__(kArgThreads) void argmax_partial_kernel(
   const int begin = part * kArgChunk;
   const int end = min(vocab, begin + kArgChunk);
   unsigned long long best = 0;  // below every value's key
-  for (int i = begin + threadIdx.x; i < end; i += kArgThreads) {
-    const float v = Elem<T>::to_f32(r[i]);
+  auto take = [&](float v, int i) __attribute__((always_inline)) {
     if (v == v) {
       const unsigned long long k = arg_key(v, i);
       best = k > best ? k : best;
     }
+  };
+  if constexpr (VEC) {
+    // Rows of whole 16-byte packets: each thread reads packets tid and
+    // tid + kArgThreads of the chunk (kArgChunk = 2 * kArgThreads * E).
+    constexpr int E = 16 / sizeof(T);
+#pragma unroll
+    for (int h = 0; h < kArgChunk / (kArgThreads * E); ++h) {
+      const int i0 = begin + (threadIdx.x + h * kArgThreads) * E;
+      if (i0 < end) {
+        float v[E];
+        Packet<T>::unpack(*reinterpret_cast<const uint4*>(r + i0), v);
+#pragma unroll
+        for (int e = 0; e < E; ++e) take(v[e], i0 + e);
+      }
+    }
+  } else {
+    for (int i = begin + threadIdx.x; i < end; i += kArgThreads) take(Elem<T>::to_f32(r[i]), i);
   }
   best = wave_max_key(best);
   __shared__ unsigned long long s_k[kArgThreads / 64];
@@ -823,8 +839,14 @@ extern "C" int rlse_argmax(const void* logits, int32_t* out, int rows, int vocab
   hipStream_t s = as_stream(stream);
   return by_dtype(dtype, [&](auto t) {
     using T = decltype(t);
-    hipLaunchKernelGGL(argmax_partial_kernel<T>, dim3(parts, rows), dim3(kArgThreads), 0, s,
-                       (const T*)logits, keys, vocab, parts);
+    // Whole 16-byte packets per row (and the chunk boundaries on packets):
+    // vector loads.
+    if (sizeof(T) == 2 && (vocab * sizeof(T)) % 16 == 0 && aligned(logits, 16))
+      hipLaunchKernelGGL((argmax_partial_kernel<T, true>), dim3(parts, rows), dim3(kArgThreads),
+                         0, s, (const T*)logits, keys, vocab, parts);
+    else
+      hipLaunchKernelGGL((argmax_partial_kernel<T, false>), dim3(parts, rows),
+                         dim3(kArgThreads), 0, s, (const T*)logits, keys, vocab, parts);
     int rc = launch_status("argmax_partial");
     if (rc) return rc;
     hipLaunchKernelGGL(argmax_final_kernel<T>, dim3(rows), dim3(64), 0, s, (const T*)logits,
