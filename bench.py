@@ -231,14 +231,16 @@ def prefill_bench(args):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(min(args.steps, 50))]
-    for a, e in ev:
-        a.record(stream)
+    # Launch duration by HIP events on the launch stream: one pair around
+    # n back-to-back calls (no event-record stall between them), / n.
+    n_ev = min(args.steps, 50)
+    ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev_a.record(stream)
+    for _ in range(n_ev):
         step()
-        e.record(stream)
+    ev_b.record(stream)
     torch.cuda.synchronize()
-    avg_ms = float(np.mean([a.elapsed_time(e) for a, e in ev]))
+    avg_ms = ev_a.elapsed_time(ev_b) / n_ev
     flops = prefill_flops(hq, d, tq, offset)
     achieved = flops / (avg_ms * 1e-3) / 1e12
     result = {
@@ -255,7 +257,7 @@ def prefill_bench(args):
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
                      "kernel": "prefill_kernel + prefill_merge_kernel (rlse_prefill_attn)",
                      "flops_per_launch": flops, "avg_launch_ms": avg_ms,
-                     "timed_launches": len(ev)},
+                     "timed_launches": n_ev},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
@@ -373,16 +375,17 @@ def fork_bench(args):
     ptrs = [pool.layer(layer) for layer in range(layers)]
 
     def step(evs=None):
+        # evs: one event pair around the step's back-to-back decode launches.
         kv.decode_plan(t_dev, lens_dev, b, hkv, mbps, nb, plan, plan_bytes, stream)
+        if evs is not None:
+            evs[0].record(stream)
         for layer in range(layers):
-            if evs is not None:
-                evs[layer][0].record(stream)
             kv.decode_step_planned(q_in[layer], k_in[layer], v_in[layer], qw, kw, 1e-6, cos_t,
                                    sin_t, max_pos, ptrs[layer][0], ptrs[layer][1], t_dev,
                                    lens_dev, out, b, hq, hkv, d, mbps, nb, scale, "bf16", plan,
                                    ws, ws_bytes, stream)
-            if evs is not None:
-                evs[layer][1].record(stream)
+        if evs is not None:
+            evs[1].record(stream)
 
     for _ in range(args.warmup):
         step()
@@ -393,12 +396,12 @@ def fork_bench(args):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ev_steps = min(args.steps, 50)
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(layers)] for _ in range(ev_steps)]
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(ev_steps)]
     for e in evs:
         step(e)
     torch.cuda.synchronize()
-    avg_ms = float(np.mean([a.elapsed_time(z) for e in evs for a, z in e]))
+    avg_ms = float(np.mean([a.elapsed_time(z) for a, z in evs])) / layers
     row = 2 * hkv * d * 2  # K+V bytes of one token
     extra = 2 * b * hq * d * 2 + sum(((int(n) + 15) // 16) * 4 for n in lens) + 4 * b + \
         2 * b * row + b * d * 2 + 2 * d * 2
@@ -672,7 +675,12 @@ def main():
     stream = torch.cuda.current_stream()
     scale = 1.0 / math.sqrt(d)
     ev_steps = min(args.steps, 50)
-    n_events = layers * ev_steps
+    # Decode-kernel duration by HIP events on the launch stream. Fused step:
+    # one event pair around each step's `layers` back-to-back decode launches
+    # (after the plan), so the average per launch includes the gaps between
+    # launches but no event-record stall inside the span. Two-launch mode: a
+    # pair around every decode launch (the append kernel sits between them).
+    n_events = ev_steps if not args.unfused else layers * ev_steps
     ev_a = [torch.cuda.Event(enable_timing=True) for _ in range(n_events)]
     ev_b = [torch.cuda.Event(enable_timing=True) for _ in range(n_events)]
 
@@ -680,14 +688,16 @@ def main():
         if not args.unfused:
             # One plan per step (the tables and lengths of every layer).
             kv.decode_plan(t_dev, lens_dev, b, hkv, mbps, nb, plan, plan_bytes, stream)
+            if timed_index is not None:
+                ev_a[timed_index].record(stream)
         for layer in range(layers):
             if args.unfused:
                 kv.qk_norm_rope_append(q_in[layer], k_in[layer], v_in[layer], qw[layer],
                                        kw[layer], 1e-6, cos_t, sin_t, max_pos, pos_dev, t_dev, b,
                                        None, b, hq, hkv, d, mbps, nb, q_rot, k_pools[layer],
                                        v_pools[layer], "bf16", stream)
-            if timed_index is not None:
-                ev_a[timed_index * layers + layer].record(stream)
+                if timed_index is not None:
+                    ev_a[timed_index * layers + layer].record(stream)
             if args.unfused:
                 kv.paged_gqa_decode(q_rot, k_pools[layer], v_pools[layer], t_dev, lens_dev, out,
                                     b, hq, hkv, d, mbps, nb, scale, "bf16", ws, ws_bytes, stream)
@@ -696,8 +706,10 @@ def main():
                                        kw[layer], 1e-6, cos_t, sin_t, max_pos, k_pools[layer],
                                        v_pools[layer], t_dev, lens_dev, out, b, hq, hkv, d, mbps,
                                        nb, scale, "bf16", plan, ws, ws_bytes, stream)
-            if timed_index is not None:
+            if args.unfused and timed_index is not None:
                 ev_b[timed_index * layers + layer].record(stream)
+        if not args.unfused and timed_index is not None:
+            ev_b[timed_index].record(stream)
 
     for _ in range(args.warmup):
         step()
@@ -715,8 +727,8 @@ def main():
     for s in range(ev_steps):
         step(s)
     torch.cuda.synchronize()
-    kernel_ms = [a.elapsed_time(e) for a, e in zip(ev_a, ev_b)]
-    avg_ms = float(np.mean(kernel_ms))
+    spans = [a.elapsed_time(e) for a, e in zip(ev_a, ev_b)]
+    avg_ms = float(np.mean(spans)) / (layers if not args.unfused else 1)
     per_launch = algorithmic_decode_bytes(lens, hq, hkv, d, 2, not args.unfused)
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
     ms_per_step = elapsed * 1e3 / args.steps
@@ -743,7 +755,9 @@ def main():
                      "kernel": ("decode_kernel (rlse_paged_gqa_decode)" if args.unfused else
                                 "decode_kernel fused step (rlse_decode_step)"),
                      "bytes_per_launch": per_launch, "avg_launch_ms": avg_ms,
-                     "timed_launches": len(kernel_ms)},
+                     "timed_launches": ev_steps * layers,
+                     "event_spans": ("one per step around its back-to-back decode launches"
+                                     if not args.unfused else "one per decode launch")},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
