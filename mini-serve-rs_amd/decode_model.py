@@ -54,6 +54,35 @@ class ModelConfig:
         self.theta, self.qk_norm, self.qkv_bias, self.tied = theta, qk_norm, qkv_bias, tied
 
     @classmethod
+    def from_config(cls, config: dict, tensors=()):
+        """The decode step's fields from a config.json dict as the reference
+        deserialises it (Config, qwen2.rs:9-54): serde defaults
+        tie_word_embeddings true, rope_theta 1e6, rms_norm_eps 1e-6;
+        head_dim = the explicit field, else hidden_size / num_attention_heads
+        (Config::head_dim, :50-53). `tensors` holds the checkpoint's tensor
+        names: q/k/v carry a bias when q_proj has one or attention_bias is
+        true (:231-232), and q_norm/k_norm exist when the checkpoint has them
+        (:251-260)."""
+        heads, hidden = config["num_attention_heads"], config["hidden_size"]
+        head_dim = config.get("head_dim")
+        if head_dim is None:
+            head_dim = hidden // heads
+        names = set(tensors)
+        has = lambda suffix: any(n.endswith(suffix) for n in names)  # noqa: E731
+        return cls(hidden=hidden, layers=config["num_hidden_layers"], heads=heads,
+                   kv_heads=config["num_key_value_heads"], head_dim=head_dim,
+                   inter=config["intermediate_size"], vocab=config["vocab_size"],
+                   eps=config.get("rms_norm_eps", 1e-6), theta=config.get("rope_theta", 1e6),
+                   qk_norm=has("self_attn.q_norm.weight"),
+                   qkv_bias=has("self_attn.q_proj.bias") or bool(config.get("attention_bias")),
+                   tied=config.get("tie_word_embeddings", True))
+
+    @property
+    def groups(self) -> int:
+        """Query heads per KV head (num_kv_groups, qwen2.rs:227)."""
+        return self.heads // self.kv_heads
+
+    @classmethod
     def qwen3_0_6b(cls):
         return cls(hidden=1024, layers=28, heads=16, kv_heads=8, head_dim=128, inter=3072,
                    vocab=151936, eps=1e-6, theta=1e6, qk_norm=True, qkv_bias=False, tied=True)
