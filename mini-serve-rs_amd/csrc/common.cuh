@@ -179,6 +179,37 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// group_sum of N independent values, one butterfly step at a time across
+// all of them: consecutive DPP adds are then independent, so none waits out
+// the DPP read-after-write hazard of its predecessor.
+template <int LANES, int N>
+__device__ __forceinline__ void group_sum_n(float (&x)[N]) {
+  if constexpr (LANES >= 2) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += dpp_f32<0xB1>(x[i]);
+  }
+  if constexpr (LANES >= 4) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += dpp_f32<0x4E>(x[i]);
+  }
+  if constexpr (LANES >= 8) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += dpp_f32<0x141>(x[i]);
+  }
+  if constexpr (LANES >= 16) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += dpp_f32<0x140>(x[i]);
+  }
+  if constexpr (LANES >= 32) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += __shfl_xor(x[i], 16, 64);
+  }
+  if constexpr (LANES >= 64) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += __shfl_xor(x[i], 32, 64);
+  }
+}
+
 __device__ __forceinline__ float wave_sum(float x) { return group_sum<64>(x); }
 
 __device__ __forceinline__ float wave_max(float x) {

@@ -722,13 +722,21 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
           }
         }
       }
-      // Raw scores q.k, summed over the LPR lanes of each row.
+      // Raw scores q.k, summed over the LPR lanes of each row (all G*NR
+      // partial dots first, then the reduction steps across all of them).
       float s[G][NR];
+      {
+        float part[G * NR];
 #pragma unroll
-      for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int r = 0; r < NR; ++r)
-          s[g][r] = group_sum<LPR>(Packet<T>::dot(qv[g], kr[r], 0.f));
+          for (int r = 0; r < NR; ++r) part[g * NR + r] = Packet<T>::dot(qv[g], kr[r], 0.f);
+        group_sum_n<LPR>(part);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) s[g][r] = part[g * NR + r];
+      }
       if (nv < 16) {  // tail block: rows past the sequence end get p = 0 and V = 0
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
