@@ -625,13 +625,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       }
     };
 
-    float m[G], l[G], acc[G][EPL];
+    // nms[g] is the exponent offset -m[g] (0 while m[g] is -inf), kept
+    // beside m[g] as it changes only when the running max moves.
+    float m[G], l[G], acc[G][EPL], nms[G];
     uint4 qv[G];
     int cur_row = -1;
     auto reset = [&]() __attribute__((always_inline)) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
+        nms[g] = 0.f;
         l[g] = 0.f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
@@ -769,10 +772,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float mx = s[g][0];
+        // The largest scaled score (c > 0, so this is the largest score
+        // times c; products need no NaN canonicalisation before the max).
+        float cand = s[g][0] * p.c;
 #pragma unroll
-        for (int r = 1; r < NR; ++r) mx = fmaxf(mx, s[g][r]);
-        const float cand = mx * p.c;
+        for (int r = 1; r < NR; ++r) cand = fmaxf(cand, s[g][r] * p.c);
         // Lazy rescaling: the running max moves only when a score exceeds it
         // by more than kLazyLog2 (probabilities then stay below 2^kLazyLog2).
         if (__any(cand > m[g] + kLazyLog2)) {
@@ -782,12 +786,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
 #pragma unroll
           for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
           m[g] = mn;
+          nms[g] = (mn == -INFINITY) ? 0.f : -mn;
         }
-        const float nms = (m[g] == -INFINITY) ? 0.f : -m[g];
         float pr[NR];
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-          pr[r] = __builtin_amdgcn_exp2f(fmaf(s[g][r], p.c, nms));
+          pr[r] = __builtin_amdgcn_exp2f(fmaf(s[g][r], p.c, nms[g]));
           l[g] += pr[r];
         }
         if constexpr (kPacked) {
