@@ -162,6 +162,34 @@ def test_argmax_chunk_edges(kv, vocab):
     np.testing.assert_array_equal(out.cpu().numpy(), O.argmax_ref(rows))
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_argmax_packet_paths_agree(kv, dt):
+    """16-bit rows of whole 16-byte packets take the packet-load path; the
+    same rows one element into the buffer (not 16-byte aligned) take the
+    element path. Both give the scan's answer: ties inside one packet and
+    across the lanes of one chunk go to the first index."""
+    rng = np.random.default_rng(6)
+    vocab, n = 8192, 4
+    rows = O.round_to(rng.standard_normal((n, vocab)), dt)
+    rows[0, 8 * 37 + 5] = rows[0, 8 * 37 + 2] = 30.0      # tie inside one packet
+    rows[1, 8 * 300 + 1] = rows[1, 8 * 12 + 7] = 30.0     # tie across lanes, first is later
+    rows[2, 4096 + 3] = rows[2, 4095] = 30.0              # tie across the chunk edge
+    rows[3, 7] = np.nan
+    rows[3, 8 * 500] = 30.0                               # NaN after index 0: skipped
+    want = O.argmax_ref(rows)
+    assert list(want) == [8 * 37 + 2, 8 * 12 + 7, 4095, 8 * 500]
+    nbytes = kv.argmax_workspace_size(n, vocab)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    flat = torch.empty(n * vocab + 8, dtype=_T[dt], device=DEV)
+    for off in (0, 1):                                    # aligned, then misaligned
+        view = flat[off:off + n * vocab].view(n, vocab)
+        view.copy_(dev(rows, dt))
+        out = torch.full((n,), -1, dtype=torch.int32, device=DEV)
+        kv.argmax(view, out, n, vocab, dt, ws, nbytes)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
 # ------------------------------------------------ fused MFMA projections ---
 ROWS = [1, 5, 16, 33, 64, 100]
 
