@@ -225,21 +225,18 @@ def prefill_bench(args):
 
     for _ in range(args.warmup):
         step()
+    # Launch duration by HIP events on the launch stream: one pair around
+    # the timed calls (no event-record stall between them), / calls.
+    n_ev = args.steps
+    ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    # Launch duration by HIP events on the launch stream: one pair around
-    # n back-to-back calls (no event-record stall between them), / n.
-    n_ev = min(args.steps, 50)
-    ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev_a.record(stream)
-    for _ in range(n_ev):
+    for _ in range(args.steps):
         step()
     ev_b.record(stream)
     torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
     avg_ms = ev_a.elapsed_time(ev_b) / n_ev
     flops = prefill_flops(hq, d, tq, offset)
     achieved = flops / (avg_ms * 1e-3) / 1e12
@@ -389,18 +386,15 @@ def fork_bench(args):
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ev_steps = min(args.steps, 50)
+    ev_steps = args.steps   # an event pair in every timed step
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(ev_steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
     for e in evs:
         step(e)
     torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
     avg_ms = float(np.mean([a.elapsed_time(z) for a, z in evs])) / layers
     row = 2 * hkv * d * 2  # K+V bytes of one token
     extra = 2 * b * hq * d * 2 + sum(((int(n) + 15) // 16) * 4 for n in lens) + 4 * b + \
@@ -532,21 +526,18 @@ def e2e_bench(args):
 
     for _ in range(args.warmup):
         step()
+    # Step duration by HIP events on the step's stream: one pair around the
+    # timed steps, / steps.
+    ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev_a.record(stream)
     for _ in range(args.steps):
         step()
+    ev_b.record(stream)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    ev_steps = min(args.steps, 20)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(ev_steps)]
-    for a, e in ev:
-        a.record(stream)
-        step()
-        e.record(stream)
-    torch.cuda.synchronize()
-    step_ms = float(np.mean([a.elapsed_time(e) for a, e in ev]))
+    step_ms = ev_a.elapsed_time(ev_b) / args.steps
     per_step = e2e_step_bytes(cfg, lens, 2)
     achieved = per_step / (step_ms * 1e-3) / 1e9
     result = {
@@ -565,7 +556,7 @@ def e2e_bench(args):
                      "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
                      "kernel": "whole step (all launches of DecodeModel.step)",
                      "bytes_per_step": per_step, "avg_step_ms": step_ms,
-                     "timed_steps": ev_steps},
+                     "timed_steps": args.steps},
         "cpu_baseline": None,
     }
     model.close()
@@ -674,12 +665,14 @@ def main():
     plan = torch.zeros(plan_bytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     scale = 1.0 / math.sqrt(d)
-    ev_steps = min(args.steps, 50)
     # Decode-kernel duration by HIP events on the launch stream. Fused step:
-    # one event pair around each step's `layers` back-to-back decode launches
-    # (after the plan), so the average per launch includes the gaps between
-    # launches but no event-record stall inside the span. Two-launch mode: a
-    # pair around every decode launch (the append kernel sits between them).
+    # one event pair around each timed step's `layers` back-to-back decode
+    # launches (after the plan), recorded in the timed steps themselves; the
+    # average per launch includes the gaps between launches but no
+    # event-record stall inside a span. Two-launch mode: a pair around every
+    # decode launch (the append kernel sits between them), in a second pass
+    # so the timed steps carry no event between their launches.
+    ev_steps = args.steps if not args.unfused else min(args.steps, 50)
     n_events = ev_steps if not args.unfused else layers * ev_steps
     ev_a = [torch.cuda.Event(enable_timing=True) for _ in range(n_events)]
     ev_b = [torch.cuda.Event(enable_timing=True) for _ in range(n_events)]
@@ -713,20 +706,16 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    # Throughput: K steps with nothing but the step's own launches on the
-    # stream (an event record between launches costs the GPU several
-    # microseconds of idle time, so the per-launch timing is a second pass).
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        step(None if args.unfused else i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    # Per-launch duration of the decode kernel: HIP events recorded on the
-    # launch stream around every decode launch of the event steps.
-    for s in range(ev_steps):
-        step(s)
-    torch.cuda.synchronize()
+    if args.unfused:
+        for i in range(ev_steps):
+            step(i)
+        torch.cuda.synchronize()
     spans = [a.elapsed_time(e) for a, e in zip(ev_a, ev_b)]
     avg_ms = float(np.mean(spans)) / (layers if not args.unfused else 1)
     per_launch = algorithmic_decode_bytes(lens, hq, hkv, d, 2, not args.unfused)
@@ -756,8 +745,9 @@ def main():
                                 "decode_kernel fused step (rlse_decode_step)"),
                      "bytes_per_launch": per_launch, "avg_launch_ms": avg_ms,
                      "timed_launches": ev_steps * layers,
-                     "event_spans": ("one per step around its back-to-back decode launches"
-                                     if not args.unfused else "one per decode launch")},
+                     "event_spans": ("one per timed step around its back-to-back decode "
+                                     "launches" if not args.unfused else
+                                     "one per decode launch, second pass")},
         "cpu_baseline": None,
     }
     if not args.no_cpu:
