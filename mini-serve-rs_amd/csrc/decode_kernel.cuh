@@ -926,7 +926,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
               ok = false;
               break;
             }
-            __builtin_amdgcn_s_sleep(8);
+            __builtin_amdgcn_s_sleep(2);
           } else if (attempt > 0) {
             // Not all there yet: wait on one word per record, l of the last
             // head (stored last), with one broadcast load each, before loading
@@ -937,7 +937,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
                 ok = false;
                 break;
               }
-              __builtin_amdgcn_s_sleep(8);
+              __builtin_amdgcn_s_sleep(2);
               bool seen = true;
 #pragma unroll
               for (int i = 0; i < MC; ++i)
