@@ -136,7 +136,8 @@ int rlse_decode_workspace_size(int batch, int num_heads, int num_kv_heads, int h
  * first need). A caller workspace must be zero-filled once before its first
  * use; every launch leaves it zero-filled again (the group that merges a
  * partial record clears it).
- * Launches that share a workspace must be ordered (same stream). */
+ * Launches that share a workspace, the library-owned one included, must be
+ * ordered (same stream). */
 int rlse_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                           const int32_t* block_tables, const int32_t* seq_lens, void* out,
                           int batch, int num_heads, int num_kv_heads, int head_dim,
@@ -198,7 +199,8 @@ int rlse_decode_step_planned(const void* q, const void* k_new, const void* v_new
  * pages with ids outside [0, num_blocks) are skipped. out [num_tokens]
  * [num_heads][head_dim]. bf16 and f16 only (MFMA tiles), head_dim 64 or
  * 128. workspace: rlse_prefill_workspace_size bytes (may be 0), or NULL
- * for a library-owned one per device. */
+ * for a library-owned one per device. Calls that share a workspace, the
+ * library-owned one included, must be ordered (same stream). */
 int rlse_prefill_workspace_size(int num_tokens, int ctx_len, int num_heads, int num_kv_heads,
                                 int head_dim, size_t* bytes);
 int rlse_prefill_attn(const void* q, const void* k_pool, const void* v_pool,

@@ -3,6 +3,8 @@
 // kernel itself is in decode_kernel.cuh.
 #include <math.h>
 
+#include <mutex>
+
 #include "decode_kernel.cuh"
 
 namespace rlse {
@@ -94,9 +96,11 @@ static int launch_decode_dtype(int dtype, int D, int G, const DecodeParams& p, h
   return fail(RLSE_ERR_INVALID_VALUE, "decode: bad dtype %d", dtype);
 }
 
-// Library-owned workspace per device, for callers that pass none.
+// Library-owned workspace per device, for callers that pass none; the
+// mutex serialises its growth across host threads.
 static void* g_ws_ptr[64] = {nullptr};
 static size_t g_ws_size[64] = {0};
+static std::mutex g_ws_mu;
 
 static int validate_decode(int batch, int num_heads, int num_kv_heads, int head_dim,
                            int max_blocks_per_seq, int num_blocks, int dtype) {
@@ -161,6 +165,7 @@ static int prepare_decode(DecodeParams& p, const void* q, const void* k_pool,
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess || dev < 0 || dev >= 64)
       return fail(RLSE_ERR_INVALID_VALUE, "decode: no current device");
+    std::lock_guard<std::mutex> lock(g_ws_mu);
     if (g_ws_size[dev] < need) {
       if (g_ws_ptr[dev]) (void)hipFree(g_ws_ptr[dev]);
       g_ws_ptr[dev] = nullptr;

@@ -35,6 +35,8 @@
 // of the four key rows -- four consecutive keys of one dimension.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.cuh"
 #include "host_common.h"
 
@@ -473,8 +475,11 @@ int launch_prefill(PrefillParams& pp, hipStream_t stream) {
   return launch_status("prefill_merge_kernel");
 }
 
+// Library-owned workspace per device, for callers that pass none; the
+// mutex serialises its growth across host threads.
 void* g_pws_ptr[64] = {nullptr};
 size_t g_pws_size[64] = {0};
+std::mutex g_pws_mu;
 
 int validate_prefill(int num_tokens, int ctx_len, int Hq, int Hkv, int D, int mbps,
                      int num_blocks, int dtype) {
@@ -537,6 +542,7 @@ extern "C" int rlse_prefill_attn(const void* q, const void* k_pool, const void* 
       hipError_t e = hipGetDevice(&dev);
       if (e != hipSuccess || dev < 0 || dev >= 64)
         return fail(RLSE_ERR_INVALID_VALUE, "prefill: no current device");
+      std::lock_guard<std::mutex> lock(g_pws_mu);
       if (g_pws_size[dev] < plan.ws_bytes) {
         if (g_pws_ptr[dev]) (void)hipFree(g_pws_ptr[dev]);
         g_pws_ptr[dev] = nullptr;
