@@ -41,12 +41,41 @@ enum rlse_dtype { RLSE_DTYPE_F32 = 0, RLSE_DTYPE_BF16 = 1, RLSE_DTYPE_F16 = 2 };
 #define RLSE_ERR_UNKNOWN_REQUEST 10002
 #define RLSE_ERR_BUFFER_TOO_SMALL 10003
 #define RLSE_ERR_TOKEN_LIMIT 10004 /* EngineError::TokenLimitExceeded */
+#define RLSE_ERR_DEVICE_TIMEOUT 10005 /* a merge on the device gave up waiting */
 #define RLSE_BLOCK_SIZE 16 /* src/core/constants.rs:1 DEFAULT_BLOCK_SIZE */
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* rlse_last_error(void);
 /* Library ABI version (major*10000 + minor*100 + patch). */
 int rlse_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Device-side failures. Kernels that hand partial results between     */
+/* workgroups (decode, the K-split projections) raise sticky flags in  */
+/* word 0 of their workspace instead of failing silently:              */
+/*   RLSE_WS_ERR_MERGE_TIMEOUT: a merge gave up waiting for a partial  */
+/*     (the affected output rows are NaN);                              */
+/*   RLSE_WS_ERR_LENGTH: a sequence length exceeded its block table    */
+/*     (max_blocks_per_seq*16); its output row is zeros and nothing was */
+/*     appended for it.                                                 */
+/* The reference turns a failed step into BackendError and quarantines */
+/* the backend (src/backends/candle.rs:689-696); a caller maps a       */
+/* nonzero rlse_workspace_check to the same.                           */
+/* ------------------------------------------------------------------ */
+#define RLSE_WS_ERR_MERGE_TIMEOUT 1u
+#define RLSE_WS_ERR_LENGTH 2u
+/* Synchronises stream, then reads and clears the flags of a decode or
+ * projection workspace (NULL: the library-owned decode workspace of the
+ * current device). *flags (may be NULL) receives them. Returns
+ * RLSE_ERR_DEVICE_TIMEOUT if a merge timed out, else RLSE_ERR_TOKEN_LIMIT
+ * if a length exceeded its table, else 0 (or a hip error). No counterpart
+ * in the reference: its CPU/Candle ops return errors synchronously. */
+int rlse_workspace_check(void* workspace, rlse_stream_t stream, unsigned* flags);
+/* Bound on a merge's wait for an earlier workgroup's partial, in
+ * nanoseconds, for launches queued after the call (default 100 ms; 0 =
+ * give up at the first miss). Process-wide. Meant for tests of the failure
+ * path: every kernel still ends normally. */
+int rlse_set_merge_wait_ns(unsigned long long ns);
 
 /* ------------------------------------------------------------------ */
 /* Physical paged KV pool (device memory owned by the handle).         */
@@ -121,9 +150,11 @@ int rlse_kv_copy_blocks(void* k_pool, void* v_pool, long long layer_stride_elems
 /* seq_lens[b] = keys attended (cached + appended). Result is          */
 /* softmax(q K^T * scale) V per head, as decode_attention_gqa_zero_copy */
 /* (src/backends/qwen2.rs:177-203) computes on contiguous buffers.     */
-/* Rows with seq_len <= 0 produce zeros; seq_len is clamped to          */
-/* max_blocks_per_seq*16; blocks with ids outside [0, num_blocks) are  */
-/* not read and contribute nothing.                                    */
+/* Rows with seq_len <= 0 produce zeros. A row with seq_len above      */
+/* max_blocks_per_seq*16 is invalid: it produces zeros, nothing is     */
+/* appended for it and RLSE_WS_ERR_LENGTH is raised in the workspace.  */
+/* Blocks with ids outside [0, num_blocks) are not read and contribute */
+/* nothing.                                                            */
 /* ------------------------------------------------------------------ */
 
 /* Bytes of split-K workspace needed by rlse_paged_gqa_decode on the
@@ -134,10 +165,11 @@ int rlse_decode_workspace_size(int batch, int num_heads, int num_kv_heads, int h
 /* Split-K decode in one launch. workspace may be NULL, in which case a
  * library-owned per-device workspace is used (allocated and zero-filled on
  * first need). A caller workspace must be zero-filled once before its first
- * use; every launch leaves it zero-filled again (the group that merges a
- * partial record clears it).
- * Launches that share a workspace, the library-owned one included, must be
- * ordered (same stream). */
+ * use and then left to the library: it holds sticky error flags
+ * (rlse_workspace_check), per-wave launch counters and epoch-tagged
+ * partial records, which never need clearing. One workspace serves calls
+ * of any shape on its device. Launches that share a workspace, the
+ * library-owned one included, must be ordered (same stream). */
 int rlse_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                           const int32_t* block_tables, const int32_t* seq_lens, void* out,
                           int batch, int num_heads, int num_kv_heads, int head_dim,
@@ -318,10 +350,11 @@ int rlse_linear(const void* x, const void* weight, const void* bias, void* y, in
  * neighbours on MFMA (bf16/f16; in_features a multiple of 32; any rows,
  * taken 64 at a time; x and weights 16-byte, outputs 8-byte aligned).
  * workspace may be NULL; with rlse_dense_workspace_size bytes (for the
- * call's rows, total output features and in_features; zero-filled before
- * its first use, every call leaves it zero) an output with few 16-feature
- * tiles splits K across workgroups so the whole chip streams the weights.
- * Calls that share a workspace must not overlap. */
+ * call's rows, total output features and in_features; zero-filled once
+ * before its first use, then left to the library: error flags, launch
+ * counters, epoch-tagged records) an output with few 16-feature tiles
+ * splits K across workgroups so the whole chip streams the weights. Calls
+ * that share a workspace must not overlap. */
 int rlse_dense_workspace_size(int rows, int out_features, int in_features, size_t* bytes);
 /* q/k/v_proj (qwen2.rs:668-679) in one launch over the stacked weights
  * w_qkv [q_features + 2*kv_features][hidden] (q rows, then k, then v) and

@@ -63,6 +63,19 @@ struct Elem<f16> {
   static __device__ __forceinline__ f16 from_f32(float v) { return (f16)v; }
 };
 
+// A product or a sum rounded on its own: the operators sit under
+// contract(off), so the compiler never fuses a product into the add that
+// consumes it. (HIP's __fmul_rn / __fadd_rn are plain operators defined
+// where contraction is allowed, so they do not prevent that fusion.)
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
 // Round a float to the precision of T (identity for float).
 template <typename T>
 __device__ __forceinline__ float round_to(float v) {
@@ -212,6 +225,49 @@ __device__ __forceinline__ void group_sum_n(float (&x)[N]) {
 
 __device__ __forceinline__ float wave_sum(float x) { return group_sum<64>(x); }
 
+// Sum of squares of a row of n elements in the one order every RMSNorm that
+// writes cached K follows (the fused decode step's q/k norm computes the same
+// tree with one packet per lane): 16-byte packets of EPL = 16 / sizeof(T)
+// elements, each packet's squares summed in element order from 0, then a
+// balanced pairwise tree over the packets zero-padded to a power of two.
+// One wave: lane c holds packets [c*M, c*M + M), added by the tree's bottom
+// levels; the lane butterfly adds the upper ones. M = max(1, P2 / 64) for P2
+// the packet count rounded up to a power of two. Every lane returns the sum.
+template <typename T, int M>
+__device__ __forceinline__ float sumsq_tree(const T* __restrict__ x, int n) {
+  constexpr int EPL = 16 / (int)sizeof(T);
+  const int lane = threadIdx.x & 63;
+  float ps[M];
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int base = (lane * M + j) * EPL;
+    float a = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int i = base + e;
+      const float v = i < n ? Elem<T>::to_f32(x[i]) : 0.f;
+      a = add_rn(a, mul_rn(v, v));
+    }
+    ps[j] = a;
+  }
+#pragma unroll
+  for (int span = 1; span < M; span <<= 1)
+#pragma unroll
+    for (int j = 0; j < M; j += 2 * span) ps[j] = add_rn(ps[j], ps[j + span]);
+  return wave_sum(ps[0]);
+}
+
+// Packets per lane (the M of sumsq_tree) for a row of n elements of es
+// bytes, or 0 when the row has more than 64 * 64 packets.
+__host__ __device__ inline int sumsq_lane_packets(int n, int es) {
+  const int epl = 16 / es;
+  const int np = (n + epl - 1) / epl;
+  int p2 = 1;
+  while (p2 < np) p2 <<= 1;
+  const int m = p2 > 64 ? p2 / 64 : 1;
+  return m > 64 ? 0 : m;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, dpp_f32<0xB1>(x));
   x = fmaxf(x, dpp_f32<0x4E>(x));
@@ -238,19 +294,45 @@ __device__ __forceinline__ void st_word(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ uint32_t ld_word(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Partial records handed between workgroups of one launch. Record words hold
-// the complement of a float's bits, so a stored word is never 0 (the bits
-// 0xFFFFFFFF, a NaN, are stored as another NaN) and 0 marks a word not yet
-// written in this launch. Each word is stored once per launch with a single
-// 32-bit agent-scope store, so a reader that sees it non-zero sees the whole
-// value; the merging workgroup clears the words it read.
-__device__ __forceinline__ uint32_t rec_encode(float v) {
-  const uint32_t u = __float_as_uint(v);
-  return ~(u == 0xFFFFFFFFu ? 0x7FFFFFFFu : u);
+// Partial records handed between workgroups of one launch are tagged 64-bit
+// words: the launch's epoch in the high half, a float's bits in the low half,
+// written and read with single 64-bit agent-scope atomics, so a reader sees
+// a word whole or not at all. A word counts as written in this launch only
+// if it carries this launch's epoch; words of earlier launches -- including
+// a publication that landed after its merge had given up waiting -- are
+// never taken, so records need no clearing between launches.
+__device__ __forceinline__ void st_tagged(uint64_t* p, uint32_t tag, float v) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float rec_decode(uint32_t x) { return __uint_as_float(~x); }
-// A merge waits at most this long (wall clock ticks, 100 MHz: 100 ms) for a
-// partial of an earlier workgroup before it gives up and writes NaN.
+__device__ __forceinline__ uint64_t ld_tagged(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_is(uint64_t w, uint32_t tag) {
+  return (uint32_t)(w >> 32) == tag;
+}
+__device__ __forceinline__ float tag_value(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
+// Launch epochs. Every wave of a launch that hands records between
+// workgroups owns one counter word of the workspace: it reads the word at
+// its start, tags what it publishes with next_epoch(word) and stores that
+// value back before it ends. Each launch thus advances every counter word
+// exactly once (waves of a launch with fewer waves than counters also
+// advance the surplus words, which no wave of that launch reads), so all
+// counters stay equal and a merging wave expects the tag its own counter
+// gives. 0 is never an epoch: a zero-filled workspace holds no valid word.
+__device__ __forceinline__ uint32_t next_epoch(uint32_t c) { return c + 1u == 0u ? 1u : c + 1u; }
+
+// Workspace header shared by the kernels that hand records between
+// workgroups: word 0 holds sticky error flags (RLSE_WS_ERR_*), raised by
+// the device and read and cleared by rlse_workspace_check; the rest of the
+// 256-byte header is reserved. Counter words follow, then the records.
+__device__ __forceinline__ void ws_raise(uint32_t* err, uint32_t flag) {
+  __hip_atomic_fetch_or(err, flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Default bound on a merge's wait for a partial of an earlier workgroup
+// (wall clock ticks, 100 MHz: 100 ms); past it the merge gives up, writes
+// NaN and raises RLSE_WS_ERR_MERGE_TIMEOUT.
 constexpr unsigned long long kMergeWaitTicks = 10000000ull;
 
 // Four dwords as a native vector (element-wise copies, no memcpy).

@@ -55,11 +55,22 @@ static int decode_groups(int* W) {
   return RLSE_OK;
 }
 
-// Workspace: two partial records per workgroup. Every launch leaves the
-// records zero (each is cleared by the group that reads it), so one
-// zero-filled workspace stays valid across calls of any shape.
+// Workspace: the header (sticky error flags), one launch counter per wave of
+// the grid, then two tagged partial records per workgroup. Records carry
+// their launch's epoch and need no clearing, so one zero-filled workspace
+// stays valid across calls of any shape.
 static size_t decode_ws_bytes(int W, int G, int D) {
-  return (size_t)W * 2 * (size_t)rec_floats(G, D) * sizeof(uint32_t);
+  return (kWsHeaderWords + decode_ctr_words(W)) * sizeof(uint32_t) +
+         (size_t)W * 2 * (size_t)rec_words(G, D) * sizeof(uint64_t);
+}
+
+// Points the kernel parameters at the parts of a workspace.
+static void set_workspace(DecodeParams& p, void* workspace, int W) {
+  uint32_t* base = reinterpret_cast<uint32_t*>(workspace);
+  p.ws_err = base;
+  p.ws_ctr = base + kWsHeaderWords;
+  p.ws_rec = reinterpret_cast<uint64_t*>(base + kWsHeaderWords + decode_ctr_words(W));
+  p.wait_ticks = merge_wait_ticks();
 }
 
 template <typename T, int D, bool FUSED>
@@ -96,8 +107,10 @@ static int launch_decode_dtype(int dtype, int D, int G, const DecodeParams& p, h
   return fail(RLSE_ERR_INVALID_VALUE, "decode: bad dtype %d", dtype);
 }
 
-// Library-owned workspace per device, for callers that pass none; the
-// mutex serialises its growth across host threads.
+// Library-owned workspace per device, for callers that pass none. The mutex
+// is held from the workspace lookup until the launch is queued, so a thread
+// that grows (frees and reallocates) the buffer never frees one another
+// thread is about to launch on; hipFree waits for launches already queued.
 static void* g_ws_ptr[64] = {nullptr};
 static size_t g_ws_size[64] = {0};
 static std::mutex g_ws_mu;
@@ -143,8 +156,10 @@ extern "C" int rlse_decode_workspace_size(int batch, int num_heads, int num_kv_h
 }
 
 // Validates the shared decode arguments and fills p (workspace included).
-static int prepare_decode(DecodeParams& p, const void* q, const void* k_pool,
-                          const void* v_pool, const int32_t* block_tables,
+// With a library-owned workspace, `lock` holds its mutex on return; the
+// caller keeps it until the launch is queued.
+static int prepare_decode(DecodeParams& p, std::unique_lock<std::mutex>& lock, const void* q,
+                          const void* k_pool, const void* v_pool, const int32_t* block_tables,
                           const int32_t* seq_lens, void* out, int batch, int num_heads,
                           int num_kv_heads, int head_dim, int max_blocks_per_seq, int num_blocks,
                           float scale, int dtype, void* workspace, size_t workspace_bytes) {
@@ -165,7 +180,7 @@ static int prepare_decode(DecodeParams& p, const void* q, const void* k_pool,
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess || dev < 0 || dev >= 64)
       return fail(RLSE_ERR_INVALID_VALUE, "decode: no current device");
-    std::lock_guard<std::mutex> lock(g_ws_mu);
+    lock = std::unique_lock<std::mutex>(g_ws_mu);
     if (g_ws_size[dev] < need) {
       if (g_ws_ptr[dev]) (void)hipFree(g_ws_ptr[dev]);
       g_ws_ptr[dev] = nullptr;
@@ -180,6 +195,8 @@ static int prepare_decode(DecodeParams& p, const void* q, const void* k_pool,
   } else if (workspace_bytes < need) {
     return fail(RLSE_ERR_BUFFER_TOO_SMALL, "decode: workspace %zu bytes < %zu needed",
                 workspace_bytes, need);
+  } else if ((uintptr_t)workspace % 8) {
+    return fail(RLSE_ERR_INVALID_VALUE, "decode: workspace must be 8-byte aligned");
   }
   p = DecodeParams{};
   p.q = q;
@@ -188,7 +205,7 @@ static int prepare_decode(DecodeParams& p, const void* q, const void* k_pool,
   p.tables = block_tables;
   p.seq_lens = seq_lens;
   p.out = out;
-  p.ws = reinterpret_cast<uint32_t*>(workspace);
+  set_workspace(p, workspace, W);
   p.B = batch;
   p.Hkv = num_kv_heads;
   p.mbps = max_blocks_per_seq;
@@ -205,7 +222,8 @@ extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const vo
                                      float scale, int dtype, void* workspace,
                                      size_t workspace_bytes, rlse_stream_t stream) {
   DecodeParams p;
-  const int st = prepare_decode(p, q, k_pool, v_pool, block_tables, seq_lens, out, batch,
+  std::unique_lock<std::mutex> lock;
+  const int st = prepare_decode(p, lock, q, k_pool, v_pool, block_tables, seq_lens, out, batch,
                                 num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
                                 num_blocks, scale, dtype, workspace, workspace_bytes);
   if (st) return st;
@@ -256,7 +274,8 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
                                 int num_blocks, float scale, int dtype, void* workspace,
                                 size_t workspace_bytes, const void* plan, rlse_stream_t stream) {
   DecodeParams p;
-  const int st = prepare_decode(p, q, k_pool, v_pool, block_tables, seq_lens, out, batch,
+  std::unique_lock<std::mutex> lock;
+  const int st = prepare_decode(p, lock, q, k_pool, v_pool, block_tables, seq_lens, out, batch,
                                 num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
                                 num_blocks, scale, dtype, workspace, workspace_bytes);
   if (st) return st;
@@ -349,4 +368,18 @@ extern "C" int launch_paged_gqa_decode_tiled_bf16(const void* d_q, const void* d
                                                   float scale) {
   return compat_decode(d_q, d_k_pool, d_v_pool, d_block_tables, d_seq_lens, d_out, batch_size,
                        num_heads, num_kv_heads, max_blocks_per_seq, scale, RLSE_DTYPE_BF16);
+}
+
+extern "C" int rlse_workspace_check(void* workspace, rlse_stream_t stream, unsigned* flags) {
+  if (flags) *flags = 0;
+  hipStream_t s = as_stream(stream);
+  if (!workspace) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+      return fail(RLSE_ERR_INVALID_VALUE, "workspace_check: no current device");
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (!g_ws_ptr[dev]) return RLSE_OK;  // no library-owned decode has run on this device
+    workspace = g_ws_ptr[dev];
+  }
+  return read_and_clear_ws_flags(workspace, s, flags);
 }

@@ -18,11 +18,12 @@
 // (m, l, acc) partial per earlier group in the workspace, and the group
 // holding the row's last block merges them with a log-sum-exp combine in the
 // same launch, taking each partial as soon as all of its words have arrived
-// (record words are self-validating: 0 = not written). Groups are dispatched
-// in index order and the grid never exceeds two groups per compute unit, so a
-// merging group only ever waits for groups that are running or done. The
-// merging group clears the records it read, so a workspace only needs
-// zero-filling once, before first use.
+// (record words carry the launch's epoch, so a word of an earlier launch is
+// never taken for one of this launch). Groups are dispatched in index order
+// and the grid never exceeds two groups per compute unit, so a merging group
+// only ever waits for groups that are running or done; the wait is bounded,
+// and a merge that gives up writes NaN and raises a sticky error flag in the
+// workspace. A workspace only needs zero-filling once, before first use.
 //
 // Inside a wave a K/V block is read as 16-byte packets: LPR lanes cover one
 // 16-token row's head_dim, RPL = 64/LPR rows are read per instruction and each
@@ -65,10 +66,10 @@ struct DecodeShape {
   static_assert(RPL >= 1 && RPL <= 16, "bad rows per load");
 };
 
-__device__ __forceinline__ int clamp_len(int L, int mbps) {
-  L = L < 0 ? 0 : L;
-  const int cap = mbps * 16;
-  return L > cap ? cap : L;
+// Keys of a row: its length, or 0 for a row with no keys (L <= 0) and for
+// an invalid row whose length exceeds its block table (L > mbps*16).
+__device__ __forceinline__ int valid_len(int L, int mbps) {
+  return (L <= 0 || L > mbps * 16) ? 0 : L;
 }
 
 // Exclusive prefix of per-sequence block counts into s_pref[0..B] (one wave).
@@ -78,7 +79,7 @@ __device__ void block_prefix(const int* __restrict__ seq_lens, int B, int mbps, 
   for (int base = 0; base < B; base += 64) {
     const int b = base + lane;
     int nb = 0;
-    if (b < B) nb = (clamp_len(seq_lens[b], mbps) + 15) >> 4;
+    if (b < B) nb = (valid_len(seq_lens[b], mbps) + 15) >> 4;
     int x = nb;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -130,7 +131,7 @@ __device__ __forceinline__ int4 block_desc(long long f, long long whi, const int
     const int kvh = (int)(o / nb), blk = (int)(o % nb);
     d.z = b * Hkv + kvh;
     d.x = tables[(size_t)b * mbps + blk];
-    const int L = clamp_len(seq_lens[b], mbps);
+    const int L = valid_len(seq_lens[b], mbps);
     const int nv = L - blk * 16;
     d.y = nv > 16 ? 16 : nv;
     d.w = L - 1;
@@ -142,9 +143,16 @@ __device__ __forceinline__ int4 block_desc(long long f, long long whi, const int
   return d;
 }
 
-// Words of one partial record: acc[G][D], then m[G] and l[G], padded so
-// records stay 16-byte aligned.
-__host__ __device__ constexpr int rec_floats(int G, int D) { return G * D + ((2 * G + 3) & ~3); }
+// Tagged 64-bit words of one partial record: acc[G][D], then m[G] and l[G].
+__host__ __device__ constexpr int rec_words(int G, int D) { return G * D + 2 * G; }
+
+// Workspace layout (32-bit words): the 256-byte header (word 0: sticky
+// error flags), one launch counter per wave of the grid (rounded up to 256
+// bytes), then two records per workgroup.
+constexpr int kWsHeaderWords = 64;
+__host__ __device__ constexpr size_t decode_ctr_words(int W) {
+  return ((size_t)W * kWaves + 63) & ~(size_t)63;
+}
 
 
 struct DecodeParams {
@@ -154,7 +162,10 @@ struct DecodeParams {
   const int* tables;
   const int* seq_lens;
   void* out;
-  uint32_t* ws;  // partial records (encoded words), two slots per workgroup; zero between launches
+  uint32_t* ws_err;  // workspace word 0: sticky RLSE_WS_ERR_* flags
+  uint32_t* ws_ctr;  // one launch counter per wave of the grid
+  uint64_t* ws_rec;  // tagged partial records, two slots per workgroup
+  unsigned long long wait_ticks;  // bound on a merge's wait (100 MHz ticks)
   int B;
   int Hkv;
   int mbps;
@@ -254,7 +265,9 @@ __device__ __forceinline__ uint4 pack_packet(const float* y) {
 // pairs element i with i + D/2, held by lane col ^ LPR/2. Rounding follows
 // Candle's op sequence (RmsNorm::forward, apply_rope; src/backends/qwen2.rs:
 // 68-75, 133-142): x/norm and *w rounded to T, x*cos and rot*sin rounded,
-// then the sum rounded; no fused multiply-adds.
+// then the sum rounded; no fused multiply-adds (mul_rn / add_rn). The sum
+// of squares is sumsq_tree's order with one packet per lane, so every entry
+// point that writes K stores the same bytes.
 template <typename T, int D>
 __device__ __forceinline__ uint4 norm_rope_packet(uint4 x, bool norm, uint4 w, float inv_d,
                                                   float eps, uint4 cs, uint4 sn, int col) {
@@ -266,11 +279,11 @@ __device__ __forceinline__ uint4 norm_rope_packet(uint4 x, bool norm, uint4 w, f
     Packet<T>::unpack(w, wf);
     float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) ss = __fadd_rn(ss, __fmul_rn(xf[e], xf[e]));
+    for (int e = 0; e < EPL; ++e) ss = add_rn(ss, mul_rn(xf[e], xf[e]));
     ss = group_sum<LPR>(ss);
-    const float nrm = sqrtf(__fadd_rn(__fmul_rn(ss, inv_d), eps));
+    const float nrm = sqrtf(add_rn(mul_rn(ss, inv_d), eps));
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) xf[e] = round_sel<T>(__fmul_rn(round_sel<T>(xf[e] / nrm), wf[e]));
+    for (int e = 0; e < EPL; ++e) xf[e] = round_sel<T>(mul_rn(round_sel<T>(xf[e] / nrm), wf[e]));
   }
   Packet<T>::unpack(cs, cf);
   Packet<T>::unpack(sn, sf);
@@ -279,9 +292,9 @@ __device__ __forceinline__ uint4 norm_rope_packet(uint4 x, bool norm, uint4 w, f
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     const float pf = __shfl_xor(xf[e], LPR / 2, 64);
-    const float a = round_sel<T>(__fmul_rn(xf[e], cf[e]));
-    const float bb = round_sel<T>(__fmul_rn(upper ? pf : -pf, sf[e]));
-    y[e] = __fadd_rn(a, bb);
+    const float a = round_sel<T>(mul_rn(xf[e], cf[e]));
+    const float bb = round_sel<T>(mul_rn(upper ? pf : -pf, sf[e]));
+    y[e] = add_rn(a, bb);
   }
   return pack_packet<T>(y);
 }
@@ -290,7 +303,7 @@ template <typename T, int D, int G, bool FUSED>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   using S = DecodeShape<T, D>;
   constexpr int EPL = S::EPL, LPR = S::LPR, RPL = S::RPL, NR = S::NR;
-  constexpr int REC = rec_floats(G, D);
+  constexpr int REC = rec_words(G, D);
   constexpr int NPART = 2 * kWaves;
   constexpr int DPL = (D + 63) / 64;  // output dims per lane in the row epilogue
   constexpr int QR = q_stage_rows<T, D, G>();
@@ -322,30 +335,45 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   const int Hq = Hkv * G;
   T* __restrict__ ob = reinterpret_cast<T*>(p.out);
 
-  int* s_len = s_pref + B + 1;  // fused step: clamped sequence lengths
+  int* s_len = s_pref + B + 1;  // fused step: valid sequence lengths
   // With a plan the wave's first descriptors are requested first of all:
   // they then arrive while wave 0 computes the block prefix, instead of a
   // page-table walk starting after it.
   int4 plan_d = make_int4(0, 0, -1, 0);
   if (p.plan) plan_d = p.plan[((size_t)blockIdx.x * kWaves + wave) * 64 + lane];
+  // This wave's launch counter: the epoch tags its records and is expected
+  // on the records it merges; stored back on every exit path.
+  uint32_t* const ctr = p.ws_ctr + (size_t)blockIdx.x * kWaves + wave;
+  const uint32_t ctr0 = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  auto end_epoch = [&](uint32_t ep) __attribute__((always_inline)) {
+    if (lane == 0) __hip_atomic_store(ctr, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref);
   if constexpr (FUSED) {
-    for (int b = tid; b < B; b += kThreads) s_len[b] = clamp_len(p.seq_lens[b], mbps);
+    for (int b = tid; b < B; b += kThreads) s_len[b] = valid_len(p.seq_lens[b], mbps);
   }
   if (tid < NPART) s_part_row[tid] = -1;
   __syncthreads();
   const long long w = blockIdx.x;
-  if (w == 0) {  // rows of sequences without keys produce zeros
+  if (w == 0) {  // rows without keys and invalid rows produce zeros
     for (int b = 0; b < B; ++b) {
       if (s_pref[b + 1] != s_pref[b]) continue;
+      if (tid == 0 && p.seq_lens[b] > mbps * 16) ws_raise(p.ws_err, RLSE_WS_ERR_LENGTH);
       for (int i = tid; i < Hq * D; i += kThreads)
         ob[(size_t)b * Hq * D + i] = Elem<T>::from_f32(0.f);
     }
   }
+  const uint32_t ep = next_epoch(ctr0);
   const long long total = (long long)Hkv * __builtin_amdgcn_readfirstlane(s_pref[B]);
-  if (total == 0) return;
+  if (total == 0) {
+    end_epoch(ep);
+    return;
+  }
   const long long we = effective_groups(total, p.W);
-  if (w >= we) return;
+  if (w >= we) {
+    end_epoch(ep);
+    return;
+  }
   const long long glo = range_lo(w, total, we);
   const long long ghi = range_lo(w + 1, total, we);
   // This wave's contiguous share of the group's range.
@@ -881,19 +909,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     if (R + nb > ghi) {
       // The row continues in a later group: publish this group's piece
       // (slot 0 = the group's first segment, 1 = a later one) and leave.
-      uint32_t* rec = p.ws + ((size_t)w * 2 + (R <= glo ? 0 : 1)) * (size_t)REC;
+      uint64_t* rec = p.ws_rec + ((size_t)w * 2 + (R <= glo ? 0 : 1)) * (size_t)REC;
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int k = 0; k < DPL; ++k) {
           const int d = lane + 64 * k;
-          if (d < D) st_word(rec + (size_t)g * D + d, rec_encode(A[g][k]));
+          if (d < D) st_tagged(rec + (size_t)g * D + d, ep, A[g][k]);
         }
       if (lane == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          st_word(rec + G * D + g, rec_encode(M[g][0]));
-          st_word(rec + G * D + G + g, rec_encode(Ls[g][0]));  // l of head G-1 last
+          st_tagged(rec + G * D + g, ep, M[g][0]);
+          st_tagged(rec + G * D + G + g, ep, Ls[g][0]);  // l of head G-1 last
         }
       }
       continue;
@@ -902,21 +930,21 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     if (R < glo) {
       // The row's last block is in this group: combine the pieces of the
       // earlier groups wa .. w-1 with this one's, each record once all of its
-      // words have arrived, then clear the records for the next launch. Group
-      // wa used slot 0 only if its range starts exactly at the row start.
+      // words carry this launch's epoch. Group wa used slot 0 only if its
+      // range starts exactly at the row start.
       const long long wa = ((R + 1) * we - 1) / total;
       const int np = (int)(w - wa);
       const bool wa_slot1 = range_lo(wa, total, we) != R;
       auto record = [&](int j) __attribute__((always_inline)) {
         const int slot = (j == 0 && wa_slot1) ? 1 : 0;
-        return p.ws + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
+        return p.ws_rec + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
       };
       const unsigned long long t0 = wall_clock64();
       auto timed_out = [&]() __attribute__((always_inline)) {
-        return wall_clock64() - t0 > kMergeWaitTicks;
+        return wall_clock64() - t0 > p.wait_ticks;
       };
       for (int c = 0; c < np && ok; c += MC) {
-        uint32_t mv[MC][G], lv[MC][G], av[MC][G][DPL];
+        uint64_t mv[MC][G], lv[MC][G], av[MC][G][DPL];
         // With at most two records pending, polling the records themselves
         // costs little and sees them one round trip sooner.
         const bool poll_full = np - c <= 2;
@@ -941,7 +969,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
               bool seen = true;
 #pragma unroll
               for (int i = 0; i < MC; ++i)
-                if (c + i < np) seen = seen && ld_word(record(c + i) + G * D + 2 * G - 1) != 0u;
+                if (c + i < np) seen = seen && tag_is(ld_tagged(record(c + i) + G * D + 2 * G - 1), ep);
               if (__all(seen)) break;
             }
             if (!ok) break;
@@ -949,24 +977,25 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
           bool ready = true;
 #pragma unroll
           for (int i = 0; i < MC; ++i) {  // issue the chunk's loads together
+            const uint64_t fill = (uint64_t)ep << 32;  // slots past the end count as arrived
             if (c + i >= np) {
 #pragma unroll
               for (int g = 0; g < G; ++g) {
-                mv[i][g] = lv[i][g] = 1u;
+                mv[i][g] = lv[i][g] = fill;
 #pragma unroll
-                for (int k = 0; k < DPL; ++k) av[i][g][k] = 1u;
+                for (int k = 0; k < DPL; ++k) av[i][g][k] = fill;
               }
               continue;
             }
-            const uint32_t* r = record(c + i);
+            const uint64_t* r = record(c + i);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-              mv[i][g] = ld_word(r + G * D + g);
-              lv[i][g] = ld_word(r + G * D + G + g);
+              mv[i][g] = ld_tagged(r + G * D + g);
+              lv[i][g] = ld_tagged(r + G * D + G + g);
 #pragma unroll
               for (int k = 0; k < DPL; ++k) {
                 const int d = lane + 64 * k;
-                av[i][g][k] = d < D ? ld_word(r + (size_t)g * D + d) : 1u;
+                av[i][g][k] = d < D ? ld_tagged(r + (size_t)g * D + d) : fill;
               }
             }
           }
@@ -974,9 +1003,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
           for (int i = 0; i < MC; ++i)
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-              ready = ready && mv[i][g] != 0u && lv[i][g] != 0u;
+              ready = ready && tag_is(mv[i][g], ep) && tag_is(lv[i][g], ep);
 #pragma unroll
-              for (int k = 0; k < DPL; ++k) ready = ready && av[i][g][k] != 0u;
+              for (int k = 0; k < DPL; ++k) ready = ready && tag_is(av[i][g][k], ep);
             }
           if (__all(ready)) break;
         }
@@ -988,27 +1017,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
             for (int g = 0; g < G; ++g)
 #pragma unroll
               for (int k = 0; k < DPL; ++k)
-                lse_combine(M[g][k], Ls[g][k], A[g][k], rec_decode(mv[i][g]), rec_decode(lv[i][g]),
-                            rec_decode(av[i][g][k]));
+                lse_combine(M[g][k], Ls[g][k], A[g][k], tag_value(mv[i][g]),
+                            tag_value(lv[i][g]), tag_value(av[i][g][k]));
       }
-      for (int j = 0; j < np; ++j) {
-        uint32_t* r = record(j);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-#pragma unroll
-          for (int k = 0; k < DPL; ++k) {
-            const int d = lane + 64 * k;
-            if (d < D) st_word(r + (size_t)g * D + d, 0u);
-          }
-          if (lane == 0) {
-            st_word(r + G * D + g, 0u);
-            st_word(r + G * D + G + g, 0u);
-          }
-        }
-      }
+      if (!ok && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_MERGE_TIMEOUT);
     }
     // Output of a row inside the group's range or merged above (NaN if a
-    // partial never arrived within kMergeWaitTicks).
+    // partial did not arrive within the wait bound).
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -1021,6 +1036,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
         }
       }
   }
+  end_epoch(ep);
 }
 
 // Launches one instantiation of the kernel on stream (defined here, instantiated

@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -56,8 +57,38 @@ int device_cu_count(int* cus) {
   return RLSE_OK;
 }
 
+static std::atomic<unsigned long long> g_wait_ticks{10000000ull};  // 100 ms at 100 MHz
+
+unsigned long long merge_wait_ticks() { return g_wait_ticks.load(std::memory_order_relaxed); }
+
+int read_and_clear_ws_flags(void* workspace, hipStream_t stream, unsigned* flags) {
+  hipError_t e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return fail((int)e, "workspace_check: %s", hipGetErrorString(e));
+  unsigned word = 0;
+  e = hipMemcpyAsync(&word, workspace, sizeof(word), hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return fail((int)e, "workspace_check: read: %s", hipGetErrorString(e));
+  if (flags) *flags = word;
+  if (word == 0) return RLSE_OK;
+  e = hipMemsetAsync(workspace, 0, sizeof(word), stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return fail((int)e, "workspace_check: clear: %s", hipGetErrorString(e));
+  if (word & RLSE_WS_ERR_MERGE_TIMEOUT)
+    return fail(RLSE_ERR_DEVICE_TIMEOUT,
+                "a merge on the device gave up waiting for a partial (flags 0x%x)", word);
+  if (word & RLSE_WS_ERR_LENGTH)
+    return fail(RLSE_ERR_TOKEN_LIMIT,
+                "a sequence length exceeded its block table (flags 0x%x)", word);
+  return fail(RLSE_ERR_DEVICE_TIMEOUT, "unknown device error flags 0x%x", word);
+}
+
 }  // namespace rlse
+
+extern "C" int rlse_set_merge_wait_ns(unsigned long long ns) {
+  rlse::g_wait_ticks.store(ns / 10, std::memory_order_relaxed);  // 100 MHz: 10 ns per tick
+  return RLSE_OK;
+}
 
 extern "C" const char* rlse_last_error(void) { return rlse::g_last_error; }
 
-extern "C" int rlse_version(void) { return 100; /* 0.1.0 */ }
+extern "C" int rlse_version(void) { return 200; /* 0.2.0 */ }

@@ -24,4 +24,13 @@ int device_cu_count(int* cus);
 
 inline hipStream_t as_stream(rlse_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Current bound on a cross-workgroup merge's wait, in 100 MHz wall-clock
+// ticks (rlse_set_merge_wait_ns).
+unsigned long long merge_wait_ticks();
+
+// Synchronises `stream`, reads the sticky error flags in word 0 of a
+// workspace into *flags (may be NULL), clears them when set, and maps them
+// to a status: RLSE_ERR_DEVICE_TIMEOUT, RLSE_ERR_TOKEN_LIMIT or 0.
+int read_and_clear_ws_flags(void* workspace, hipStream_t stream, unsigned* flags);
+
 }  // namespace rlse

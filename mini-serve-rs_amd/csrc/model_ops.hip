@@ -6,7 +6,9 @@
 // the logits to the host for sample_token, src/backends/candle.rs:737-751).
 //
 // Element-wise rounding follows Candle's per-op order on bf16/f16 tensors:
-// every op computes in f32 and rounds its result to the tensor dtype.
+// every op computes in f32 and rounds its result to the tensor dtype, with
+// no multiply-add contraction (a Candle op rounds its product before the
+// next op adds to it).
 #include <math.h>
 #include <rocblas/rocblas.h>
 
@@ -16,6 +18,8 @@
 
 #include "common.cuh"
 #include "host_common.h"
+
+#pragma clang fp contract(off)
 
 namespace rlse {
 namespace {
@@ -320,7 +324,13 @@ struct DenseParams {
   void* out0;        // y [rows][N] | q [rows][n1] | x_res [rows][N] | act [rows][n1]
   void* out1;        // k [rows][n2 - n1] (kEpiQkv)
   void* out2;        // v [rows][N - n2] (kEpiQkv)
-  uint32_t* ws;      // KS > 1: (tile groups) x (KS - 1) records of FT*RT*256 words
+  // KS > 1: sticky error flags, one launch counter per wave slot
+  // (kDenseCtrWords) and (tile groups) x (KS - 1) records of FT*RT*256
+  // tagged 64-bit words.
+  uint32_t* ws_err;
+  uint32_t* ws_ctr;
+  uint64_t* ws_rec;
+  unsigned long long wait_ticks;
   int rows, K, N, n1, n2;
   int ksplit;        // KS
   int steps;         // 32-wide k steps per wave
@@ -329,6 +339,11 @@ struct DenseParams {
 constexpr int kDenseWaves = 4;
 constexpr int kDenseMaxRows = 64;
 constexpr int kDenseMaxSplit = 8;
+// Launch counters of a K-split workspace: one per wave of the largest split
+// grid. A split grid has fewer than 512 workgroups: an output is split only
+// when it has fewer than 256 tile groups, into ceil(256 / groups) slices.
+constexpr int kDenseCtrWords = 512 * kDenseWaves;
+constexpr int kDenseHeaderWords = 64;
 
 template <typename T>
 __device__ __forceinline__ void load4(const T* p, float* v) {
@@ -365,6 +380,19 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
   const int KS = p.ksplit;
   const int grp = blockIdx.x / KS;
   const int ks = blockIdx.x - grp * KS;
+  // K split: this wave's launch counter (its epoch tags the records it
+  // publishes and is expected on those it merges); the wave also advances
+  // the counters of the wave slots this grid does not cover, so every
+  // counter moves once per launch.
+  const int gw = blockIdx.x * kDenseWaves + wave;
+  uint32_t ep = 0;
+  if (KS > 1)
+    ep = next_epoch(__hip_atomic_load(p.ws_ctr + gw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  auto end_epoch = [&]() __attribute__((always_inline)) {
+    if (KS > 1 && lane == 0)
+      for (int c = gw; c < kDenseCtrWords; c += gridDim.x * kDenseWaves)
+        __hip_atomic_store(p.ws_ctr + c, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   const T* wr[FT];
 #pragma unroll
   for (int f = 0; f < FT; ++f) {
@@ -463,15 +491,10 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
 
   bool ok = true;
   if (KS > 1) {
-    // Record of slice sl: kItems items of kPair*4 words, as 64-bit halves.
-    constexpr int kHalves = kPair * 2;
-    auto half_ptr = [&](int slice, int it, int h) {
-      return reinterpret_cast<unsigned long long*>(
-                 p.ws + ((size_t)grp * (KS - 1) + slice) * kRecWords) +
-             (size_t)it * kHalves + h;
-    };
-    auto enc2 = [](float a, float b) {
-      return (unsigned long long)rec_encode(a) | ((unsigned long long)rec_encode(b) << 32);
+    // Record of slice sl: kItems items of kPair*4 tagged words.
+    constexpr int kWords = kPair * 4;
+    auto word_ptr = [&](int slice, int it, int j) {
+      return p.ws_rec + ((size_t)grp * (KS - 1) + slice) * kRecWords + (size_t)it * kWords + j;
     };
     if (ks < KS - 1) {
 #pragma unroll
@@ -479,40 +502,37 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
         const int it = threadIdx.x + k * 64 * kDenseWaves;
         if (it < kItems)
 #pragma unroll
-          for (int h = 0; h < kHalves; ++h)
-            __hip_atomic_store(half_ptr(ks, it, h),
-                               enc2(v[k][h >> 1][2 * (h & 1)], v[k][h >> 1][2 * (h & 1) + 1]),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          for (int j = 0; j < kWords; ++j) st_tagged(word_ptr(ks, it, j), ep, v[k][j >> 2][j & 3]);
       }
+      end_epoch();
       return;
     }
     // The merging workgroup: every slice's words are requested together,
-    // then only the missing ones again; the sum runs in slice order.
+    // then only those without this launch's epoch again; the sum runs in
+    // slice order.
     const unsigned long long t0 = wall_clock64();
 #pragma unroll
     for (int k = 0; k < kItemsPerThread; ++k) {
       const int it = threadIdx.x + k * 64 * kDenseWaves;
       if (it >= kItems) continue;
-      unsigned long long r[kDenseMaxSplit - 1][kHalves];
+      uint64_t r[kDenseMaxSplit - 1][kWords];
 #pragma unroll
       for (int sl = 0; sl < kDenseMaxSplit - 1; ++sl)
 #pragma unroll
-        for (int h = 0; h < kHalves; ++h) r[sl][h] = 0ull;
+        for (int j = 0; j < kWords; ++j) r[sl][j] = 0ull;
       for (;;) {
         bool all = true;
 #pragma unroll
         for (int sl = 0; sl < kDenseMaxSplit - 1; ++sl) {
           if (sl >= KS - 1) break;
 #pragma unroll
-          for (int h = 0; h < kHalves; ++h) {
-            if ((uint32_t)r[sl][h] == 0u || (uint32_t)(r[sl][h] >> 32) == 0u)
-              r[sl][h] = __hip_atomic_load(half_ptr(sl, it, h), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-            all = all && (uint32_t)r[sl][h] != 0u && (uint32_t)(r[sl][h] >> 32) != 0u;
+          for (int j = 0; j < kWords; ++j) {
+            if (!tag_is(r[sl][j], ep)) r[sl][j] = ld_tagged(word_ptr(sl, it, j));
+            all = all && tag_is(r[sl][j], ep);
           }
         }
         if (all) break;
-        if (wall_clock64() - t0 > kMergeWaitTicks) {
+        if (wall_clock64() - t0 > p.wait_ticks) {
           ok = false;
           break;
         }
@@ -523,15 +543,9 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
       for (int sl = 0; sl < kDenseMaxSplit - 1; ++sl) {
         if (sl >= KS - 1) break;
 #pragma unroll
-        for (int h = 0; h < kHalves; ++h) {
-          const float lo = rec_decode((uint32_t)r[sl][h]);
-          const float hi = rec_decode((uint32_t)(r[sl][h] >> 32));
-          float& a = sum[h >> 1][2 * (h & 1)];
-          float& c = sum[h >> 1][2 * (h & 1) + 1];
-          a = sl == 0 ? lo : a + lo;
-          c = sl == 0 ? hi : c + hi;
-          __hip_atomic_store(half_ptr(sl, it, h), 0ull, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < kWords; ++j) {
+          float& a = sum[j >> 2][j & 3];
+          a = sl == 0 ? tag_value(r[sl][j]) : a + tag_value(r[sl][j]);
         }
       }
 #pragma unroll
@@ -539,6 +553,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[k][q][e] = sum[q][e] + v[k][q][e];
     }
+    if (!ok) ws_raise(p.ws_err, RLSE_WS_ERR_MERGE_TIMEOUT);
   }
 
 #pragma unroll
@@ -581,6 +596,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
       store4<T>(dst, o);
     }
   }
+  end_epoch();
 }
 
 template <typename F>
@@ -615,6 +631,9 @@ int dense_tiles_per_group(bool plain_store, int rows, int tiles) {
   return 1;
 }
 
+// Header and launch-counter words at the start of a K-split workspace.
+constexpr size_t dense_ws_fixed_words() { return kDenseHeaderWords + kDenseCtrWords; }
+
 // K slices per output tile group: enough workgroups to cover every compute
 // unit (256 on MI355X) when the output has few 16-feature tiles, each slice
 // at least 4 k steps of 32. Outputs with 256 or more tiles are not split:
@@ -640,7 +659,7 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
   const int ft = dense_tiles_per_group(EPI == kEpiStore, total_rows, tiles);
   const bool wide = ft == 4;
   const int groups = tiles / ft;
-  const int ks = p.ws ? dense_split(groups, p.K) : 1;
+  const int ks = p.ws_rec ? dense_split(groups, p.K) : 1;
   const int steps_total = p.K / 32;
   const int slice = (steps_total + ks - 1) / ks;
   p.ksplit = ks;
@@ -657,8 +676,11 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
     q.out1 = base1 ? (void*)(base1 + (size_t)r0 * o1_stride * sizeof(T)) : nullptr;
     q.out2 = base2 ? (void*)(base2 + (size_t)r0 * o2_stride * sizeof(T)) : nullptr;
     const int rt = (q.rows + 15) / 16;
-    if (ks > 1 && (size_t)groups * (ks - 1) * ft * rt * 256 > ws_words)
+    if (ks > 1 && dense_ws_fixed_words() + (size_t)groups * (ks - 1) * ft * rt * 256 * 2 >
+                      ws_words)
       return fail(RLSE_ERR_INVALID_VALUE, "dense: workspace too small");
+    if (ks > 1 && groups * ks * kDenseWaves > kDenseCtrWords)
+      return fail(RLSE_ERR_INVALID_VALUE, "dense: K-split grid larger than its counters");
     const dim3 block(64 * kDenseWaves);
     const dim3 grid(groups * ks);
     auto run = [&](auto rt_c) {
@@ -687,13 +709,16 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
   return RLSE_OK;
 }
 
-// Workspace words a fused projection needs for its K split (0: none).
+// Workspace words a fused projection needs for its K split (0: none): the
+// header and the launch counters, then the tagged records (two 32-bit words
+// each).
 size_t dense_ws_words(int rows, int tiles, int K) {
   if (rows <= 0 || tiles <= 0 || K < 32) return 0;
   const int ft = dense_tiles_per_group(false, rows, tiles);
   const int ks = dense_split(tiles / ft, K);
   const int rt = (std::min(rows, kDenseMaxRows) + 15) / 16;
-  return ks > 1 ? (size_t)(tiles / ft) * (ks - 1) * ft * rt * 256 : 0;
+  return ks > 1 ? dense_ws_fixed_words() + (size_t)(tiles / ft) * (ks - 1) * ft * rt * 256 * 2
+                : 0;
 }
 
 // Shape and alignment checks shared by the MFMA entry points.
@@ -730,14 +755,19 @@ int dense_by_dtype(int dtype, const DenseParams& p, size_t xs, size_t s0, size_t
 int dense_workspace(const char* what, DenseParams& p, void* workspace, size_t workspace_bytes,
                     size_t* words) {
   *words = 0;
-  p.ws = nullptr;
+  p.ws_err = p.ws_ctr = nullptr;
+  p.ws_rec = nullptr;
   if (!workspace) return RLSE_OK;
   const size_t need = dense_ws_words(p.rows, p.N / 16, p.K);
   if (need == 0) return RLSE_OK;
-  if (workspace_bytes < need * 4 || !aligned(workspace, 4))
-    return fail(RLSE_ERR_INVALID_VALUE, "%s: workspace of %zu bytes (4-byte aligned) needed, %zu "
+  if (workspace_bytes < need * 4 || !aligned(workspace, 8))
+    return fail(RLSE_ERR_INVALID_VALUE, "%s: workspace of %zu bytes (8-byte aligned) needed, %zu "
                                         "given", what, need * 4, workspace_bytes);
-  p.ws = (uint32_t*)workspace;
+  uint32_t* base = (uint32_t*)workspace;
+  p.ws_err = base;
+  p.ws_ctr = base + kDenseHeaderWords;
+  p.ws_rec = reinterpret_cast<uint64_t*>(base + dense_ws_fixed_words());
+  p.wait_ticks = merge_wait_ticks();
   *words = need;
   return RLSE_OK;
 }

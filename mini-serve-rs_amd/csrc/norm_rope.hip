@@ -2,14 +2,14 @@
 // that forms the front half of Attention::forward
 // (src/backends/qwen2.rs:291-313).
 //
-// Numerics follow Candle's op sequence on the reference's CPU path so the
-// outputs match it to the last bit wherever the operation order is fixed:
+// Numerics follow Candle's op sequence on the reference's CPU path:
 //   RmsNorm::forward (qwen2.rs:68-75): x -> f32; var = sum(x^2) * (1/n);
 //     x / sqrt(var + eps) -> dtype; then * weight in dtype.
 //   apply_rope (qwen2.rs:133-142): x*cos and rotate_half(x)*sin are each
 //     rounded to dtype, then added and rounded, with no fused multiply-add.
-// Only the sum of squares differs in order (a wave reduction instead of a
-// sequential sum), which moves the result by at most a few ulps.
+// The sum of squares follows one fixed order (sumsq_tree: 16-byte packets,
+// then a pairwise tree), the order of the fused decode step's q/k norm too,
+// so cached K holds the same bytes whichever entry point wrote it.
 //
 // One wave handles one (token, head) row. For RoPE lane i holds the pair
 // (x[i], x[i + d/2]) that rotate_half mixes, so no cross-lane traffic is
@@ -17,6 +17,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <type_traits>
 #include <vector>
 
 #include "common.cuh"
@@ -38,8 +39,9 @@ __device__ __forceinline__ void st(T* p, size_t i, float v) {
   p[i] = Elem<T>::from_f32(v);
 }
 
-// RMSNorm of one row held by one wave.
-template <typename T>
+// RMSNorm of one row held by one wave (M packets per lane in the sum of
+// squares, see sumsq_tree).
+template <typename T, int M>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void rmsnorm_kernel(
     const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ out, int rows, int n,
     float inv_n, float eps) {
@@ -48,12 +50,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void rmsnorm_kernel(
   if (row >= rows) return;
   const T* xr = x + row * n;
   T* orow = out + row * n;
-  float ss = 0.f;
-  for (int i = lane; i < n; i += 64) {
-    const float v = ld(xr, i);
-    ss += v * v;
-  }
-  ss = wave_sum(ss);
+  const float ss = sumsq_tree<T, M>(xr, n);
   const float norm = sqrtf(ss * inv_n + eps);
   for (int i = lane; i < n; i += 64) {
     const float xn = round_to<T>(ld(xr, i) / norm);
@@ -79,9 +76,9 @@ __device__ __forceinline__ void norm_rope_row(const T* __restrict__ src, T* __re
     x2[k] = ld(src, i + half);
   }
   if (nw) {
-    float ss = 0.f;
-    for (int k = 0; k < np; ++k) ss += x1[k] * x1[k] + x2[k] * x2[k];
-    ss = wave_sum(ss);
+    // d <= 512: at most 128 packets (f32), two per lane
+    const float ss = d * (int)sizeof(T) <= 1024 ? sumsq_tree<T, 1>(src, d)
+                                                 : sumsq_tree<T, 2>(src, d);
     const float norm = sqrtf(ss * inv_d + eps);
     for (int k = 0; k < np; ++k) {
       const int i = lane + 64 * k;
@@ -187,25 +184,38 @@ extern "C" int rlse_rmsnorm(const void* x, const void* weight, void* out, int ro
   if (rows <= 0 || n <= 0) return fail(RLSE_ERR_INVALID_VALUE, "rmsnorm: rows %d n %d", rows, n);
   if (!x || !weight || !out) return fail(RLSE_ERR_INVALID_VALUE, "rmsnorm: null pointer");
   if (!(eps >= 0.f)) return fail(RLSE_ERR_INVALID_VALUE, "rmsnorm: eps must be >= 0");
+  const size_t es = dtype_size(dtype);
+  if (es == 0) return fail(RLSE_ERR_INVALID_VALUE, "rmsnorm: bad dtype %d", dtype);
+  const int m = sumsq_lane_packets(n, (int)es);
+  if (m == 0)
+    return fail(RLSE_ERR_INVALID_VALUE, "rmsnorm: n %d above %d elements", n,
+                64 * 64 * (int)(16 / es));
   const float inv_n = (float)(1.0 / (double)n);
   const dim3 grid(row_grid(rows)), block(64 * kRowsPerBlock);
   hipStream_t s = as_stream(stream);
-  switch (dtype) {
-    case RLSE_DTYPE_F32:
-      hipLaunchKernelGGL(rmsnorm_kernel<float>, grid, block, 0, s, (const float*)x,
-                         (const float*)weight, (float*)out, rows, n, inv_n, eps);
-      break;
-    case RLSE_DTYPE_BF16:
-      hipLaunchKernelGGL(rmsnorm_kernel<bf16>, grid, block, 0, s, (const bf16*)x,
-                         (const bf16*)weight, (bf16*)out, rows, n, inv_n, eps);
-      break;
-    case RLSE_DTYPE_F16:
-      hipLaunchKernelGGL(rmsnorm_kernel<f16>, grid, block, 0, s, (const f16*)x,
-                         (const f16*)weight, (f16*)out, rows, n, inv_n, eps);
-      break;
-    default:
-      return fail(RLSE_ERR_INVALID_VALUE, "rmsnorm: bad dtype %d", dtype);
-  }
+  auto run = [&](auto t) {
+    using T = decltype(t);
+    auto go = [&](auto mc) {
+      constexpr int M = decltype(mc)::value;
+      hipLaunchKernelGGL((rmsnorm_kernel<T, M>), grid, block, 0, s, (const T*)x,
+                         (const T*)weight, (T*)out, rows, n, inv_n, eps);
+    };
+    switch (m) {
+      case 1: go(std::integral_constant<int, 1>{}); break;
+      case 2: go(std::integral_constant<int, 2>{}); break;
+      case 4: go(std::integral_constant<int, 4>{}); break;
+      case 8: go(std::integral_constant<int, 8>{}); break;
+      case 16: go(std::integral_constant<int, 16>{}); break;
+      case 32: go(std::integral_constant<int, 32>{}); break;
+      default: go(std::integral_constant<int, 64>{}); break;
+    }
+  };
+  if (dtype == RLSE_DTYPE_F32)
+    run(float{});
+  else if (dtype == RLSE_DTYPE_BF16)
+    run(bf16{});
+  else
+    run(f16{});
   return launch_status("rmsnorm");
 }
 

@@ -124,6 +124,24 @@ extern "C" int rlse_st_prepare(rlse_step_tables* st, rlse_block_manager* bm,
     return fail(RLSE_ERR_INVALID_VALUE, "st_prepare: batch %d > max_batch %d", batch,
                 st->max_batch);
   const int mbps = st->mbps;
+  // Triples still pending from an earlier prepare (no upload since): a row
+  // prepared again supersedes its pending triples from the column it now
+  // starts at, so one upload never carries two pages for one table cell.
+  const size_t prev = st->deltas.size() / 3;
+  std::vector<std::vector<size_t>> pending_of_row;
+  if (prev > 0) {
+    pending_of_row.resize(st->max_batch);
+    for (size_t t = 0; t < prev; ++t) pending_of_row[st->deltas[3 * t]].push_back(t);
+  }
+  bool dropped = false;
+  auto drop_pending = [&](int row, int from_col) {
+    if (prev == 0) return;
+    for (size_t t : pending_of_row[row])
+      if (st->deltas[3 * t + 1] >= from_col) {
+        st->deltas[3 * t] = -1;  // removed below
+        dropped = true;
+      }
+  };
   for (int i = 0; i < batch; ++i) {
     st->lens[i] = 0;
     status[i] = RLSE_OK;
@@ -168,12 +186,22 @@ extern "C" int rlse_st_prepare(rlse_step_tables* st, rlse_block_manager* bm,
       st->row_version[i] = ver;
       from = 0;
     }
+    drop_pending(i, from);
     int32_t* row = st->tables.data() + (size_t)i * mbps;
     for (int j = from; j < count; ++j) {
       row[j] = pages[(size_t)j];
       st->deltas.insert(st->deltas.end(), {(int32_t)i, (int32_t)j, (int32_t)pages[(size_t)j]});
     }
     st->row_count[i] = count;
+  }
+  if (dropped) {
+    size_t w = 0;
+    for (size_t t = 0; t < st->deltas.size() / 3; ++t) {
+      if (st->deltas[3 * t] < 0) continue;
+      for (int c = 0; c < 3; ++c) st->deltas[3 * w + c] = st->deltas[3 * t + c];
+      ++w;
+    }
+    st->deltas.resize(3 * w);
   }
   st->batch = batch;
   return RLSE_OK;

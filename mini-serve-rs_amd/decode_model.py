@@ -160,14 +160,14 @@ class DecodeModel:
         self.arg_ws = torch.zeros(max(kv.argmax_workspace_size(B, cfg.vocab), 8),
                                   dtype=torch.uint8, device=dev)
         # One workspace for the K split of every fused projection (they run
-        # one after another on the step's stream); zero-filled once, as each
-        # call leaves it.
+        # one after another on the step's stream); zero-filled once, then
+        # kept consistent by the kernels (epoch-tagged records).
         dense_ws = max([kv.dense_workspace_size(B, n, k) for n, k in (
             (nq + 2 * nkv, cfg.hidden), (cfg.hidden, nq), (2 * cfg.inter, cfg.hidden),
             (cfg.hidden, cfg.inter))] + [4])
         self.dense_ws = torch.zeros(dense_ws, dtype=torch.uint8, device=dev)
         ws = kv.decode_workspace_size(B, cfg.heads, cfg.kv_heads, cfg.head_dim)
-        # Zero once: every launch of the decode kernel leaves it zero again.
+        # Zero once: the decode kernels keep it consistent from then on.
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=dev)
         # The step's decode plan: built once per step, read by every layer.
         self.plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=dev)
@@ -193,8 +193,8 @@ class DecodeModel:
         launches at once instead of one host call each. With feed_back the
         graph ends by copying the greedy ids into ids_in, so successive
         replays decode greedily on the device alone. No launch of the step
-        records a memset: every workspace it uses is left zero by the kernels
-        themselves."""
+        records a memset: the workspaces need no clearing between launches
+        (their records carry a per-launch epoch)."""
         torch.cuda.synchronize(self.device)
         # One eager run first, outside the capture, with every length zero
         # (nothing is appended or attended), then the inputs are restored.

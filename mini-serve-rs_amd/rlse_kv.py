@@ -42,6 +42,9 @@ ERR_CACHE_PRESSURE = 10001
 ERR_UNKNOWN_REQUEST = 10002
 ERR_BUFFER_TOO_SMALL = 10003
 ERR_TOKEN_LIMIT = 10004
+ERR_DEVICE_TIMEOUT = 10005
+WS_ERR_MERGE_TIMEOUT = 1
+WS_ERR_LENGTH = 2
 BLOCK_SIZE = 16
 
 # Every extern "C" symbol of include/rlse_kv.h (checked by the CPU tests).
@@ -70,7 +73,7 @@ EXPORTED = (
     "rlse_embedding", "rlse_add_rmsnorm", "rlse_silu_mul", "rlse_argmax", "rlse_linear",
     "rlse_argmax_workspace_size", "rlse_qkv_proj", "rlse_linear_residual", "rlse_gate_up_silu",
     "rlse_dense_workspace_size", "rlse_decode_plan_size", "rlse_decode_plan",
-    "rlse_decode_step_planned",
+    "rlse_decode_step_planned", "rlse_workspace_check", "rlse_set_merge_wait_ns",
 )
 
 
@@ -89,6 +92,12 @@ class CachePressure(RlseError):
 
 class TokenLimitExceeded(RlseError):
     """RLSE_ERR_TOKEN_LIMIT, the reference's EngineError::TokenLimitExceeded."""
+
+
+class DeviceTimeout(RlseError):
+    """RLSE_ERR_DEVICE_TIMEOUT: a merge on the device gave up waiting; the
+    caller treats it as the reference's BackendError (quarantine,
+    src/backends/candle.rs:689-696)."""
 
 
 class _MemoryStats(ctypes.Structure):
@@ -245,6 +254,8 @@ _SIGS = {
     "rlse_qkv_proj": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_linear_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_gate_up_silu": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "rlse_workspace_check": (_i, [_vp, _vp, ctypes.POINTER(ctypes.c_uint)]),
+    "rlse_set_merge_wait_ns": (_i, [ctypes.c_ulonglong]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -279,6 +290,8 @@ def _check(status: int) -> None:
             raise CachePressure(status, msg)
         if status == ERR_TOKEN_LIMIT:
             raise TokenLimitExceeded(status, msg)
+        if status == ERR_DEVICE_TIMEOUT:
+            raise DeviceTimeout(status, msg)
         raise RlseError(status, msg)
 
 
@@ -882,3 +895,30 @@ def gate_up_silu(x, w_gate_up, act, rows: int, hidden: int, inter: int, dtype, w
     wp, wb = _ws(workspace)
     _check(load().rlse_gate_up_silu(_ptr(x), _ptr(w_gate_up), _ptr(act), rows, hidden, inter,
                                     _dt(dtype), wp, wb, _stream(stream)))
+
+
+# --------------------------------------------------------------------------
+# Device-side failures
+# --------------------------------------------------------------------------
+def workspace_flags(workspace=None, stream=None) -> int:
+    """Synchronises the stream, then reads and clears the sticky error flags
+    of a decode or projection workspace (None: the library-owned decode
+    workspace). Returns them without raising (WS_ERR_* bits)."""
+    flags = ctypes.c_uint(0)
+    load().rlse_workspace_check(_ptr(workspace), _stream(stream), ctypes.byref(flags))
+    return int(flags.value)
+
+
+def workspace_check(workspace=None, stream=None) -> None:
+    """As workspace_flags, raising DeviceTimeout (a merge gave up) or
+    TokenLimitExceeded (a length exceeded its block table) when a flag was
+    set -- the point where a serving loop turns a device failure into the
+    reference's BackendError."""
+    flags = ctypes.c_uint(0)
+    _check(load().rlse_workspace_check(_ptr(workspace), _stream(stream), ctypes.byref(flags)))
+
+
+def set_merge_wait_ns(ns: int) -> None:
+    """Bound on a cross-workgroup merge's wait for launches queued after the
+    call (default 100 ms; 0 gives up at the first miss)."""
+    _check(load().rlse_set_merge_wait_ns(int(ns)))

@@ -58,6 +58,7 @@ def load() -> ctypes.CDLL:
         "orc_prefill_f32": (None, [vp, vp, vp, i, i, i, i, i, i, f, vp, i]),
         "orc_rmsnorm_f32": (None, [vp, vp, vp, i, i, f]),
         "orc_rmsnorm_bf16": (None, [vp, vp, vp, i, i, f]),
+        "orc_sumsq_tree_rows": (None, [vp, i, i, i, vp]),
         "orc_rope_tables_f32": (None, [d, i, i, vp, vp]),
         "orc_apply_rope_f32": (None, [vp, vp, vp, vp, i, i]),
         "orc_apply_rope_bf16": (None, [vp, vp, vp, vp, i, i]),
@@ -214,6 +215,30 @@ def rmsnorm_bf16(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarr
     out = np.empty_like(x)
     load().orc_rmsnorm_bf16(_p(x), _p(w), _p(out), rows, n, eps)
     return out
+
+
+def sumsq_tree(x: np.ndarray, epl: int) -> np.ndarray:
+    """orc_sumsq_tree per row of x [..., n] (f32): the sum of squares in the
+    order every K-writing RMSNorm follows (packets of epl elements summed in
+    order, then a balanced pairwise tree over the packets)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    rows = x.size // n
+    out = np.empty(rows, np.float32)
+    load().orc_sumsq_tree_rows(_p(x), rows, n, epl, _p(out))
+    return out.reshape(x.shape[:-1])
+
+
+def rmsnorm_f16(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """RmsNorm::forward on f16 storage (qwen2.rs:68-75): f32 arithmetic with
+    the sum of squares in the 8-element packet order of orc_sumsq_tree,
+    x / norm rounded to f16, then the weight product rounded to f16."""
+    xf = np.asarray(x, np.float16).astype(np.float32)
+    n = xf.shape[-1]
+    ss = sumsq_tree(xf, 8)
+    norm = np.sqrt(ss * np.float32(1.0 / n) + np.float32(eps)).astype(np.float32)
+    xn = (xf / norm[..., None]).astype(np.float16).astype(np.float32)
+    return (xn * np.asarray(w, np.float16).astype(np.float32)).astype(np.float16)
 
 
 def rope_tables_f32(theta: float, d: int, max_pos: int):
@@ -502,9 +527,7 @@ def rmsnorm_ref(x: np.ndarray, w: np.ndarray, eps: float, dt: str) -> np.ndarray
     product in the dtype."""
     x = np.asarray(x, dtype=np.float32)
     n = x.shape[-1]
-    ss = np.zeros(x.shape[:-1], dtype=np.float32)
-    for i in range(n):                      # sequential f32 sum, as the C oracle
-        ss = ss + x[..., i] * x[..., i]
+    ss = sumsq_tree(x, 4 if dt == "f32" else 8)   # the C oracle's order (orc_sumsq_tree)
     norm = np.sqrt(ss * np.float32(1.0 / n) + np.float32(eps)).astype(np.float32)
     xn = round_to(x / norm[..., None], dt)
     return round_to(xn * np.asarray(w, np.float32), dt)

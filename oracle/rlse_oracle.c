@@ -215,13 +215,47 @@ void orc_prefill_f32(const float* q, const float* k, const float* v, int Hq, int
 /* ---- RmsNorm::forward (src/backends/qwen2.rs:68-75) ----
  * x_f32 = x; variance = mean_keepdim(x^2) = sum * (1/n) (candle's mean is a
  * sum scaled by 1/n); norm = sqrt(variance + eps); x_normed = (x / norm) cast
- * to dtype; out = x_normed * weight in dtype. */
+ * to dtype; out = x_normed * weight in dtype.
+ *
+ * Summation order of sum(x^2). Candle's own order inside its reduction is
+ * not reproducible without building it, so this restatement fixes one order,
+ * which every RMSNorm kernel of the build that writes cached K follows too:
+ * the row is cut into packets of epl consecutive elements (epl = 16 bytes /
+ * element size: 4 for f32, 8 for bf16 and f16), each packet's squares are
+ * summed in element order starting from 0, and the packet sums are added by
+ * a balanced pairwise tree over the next power of two of packets, the missing
+ * ones counting as 0 (level k adds the sums of blocks 2j and 2j+1 of 2^k
+ * packets). Elements past n in the last packet count as 0. */
+float orc_sumsq_tree(const float* x, int n, int epl) {
+  const int np = (n + epl - 1) / epl;
+  int p2 = 1;
+  while (p2 < np) p2 <<= 1;
+  float* ps = (float*)calloc((size_t)p2, sizeof(float));
+  for (int j = 0; j < np; ++j) {
+    float a = 0.f;
+    for (int e = 0; e < epl; ++e) {
+      const int i = j * epl + e;
+      const float v = i < n ? x[i] : 0.f;
+      a = a + v * v;
+    }
+    ps[j] = a;
+  }
+  for (int span = 1; span < p2; span <<= 1)
+    for (int j = 0; j < p2; j += 2 * span) ps[j] = ps[j] + ps[j + span];
+  const float ss = ps[0];
+  free(ps);
+  return ss;
+}
+
+void orc_sumsq_tree_rows(const float* x, int rows, int n, int epl, float* out) {
+  for (int r = 0; r < rows; ++r) out[r] = orc_sumsq_tree(x + (size_t)r * n, n, epl);
+}
+
 void orc_rmsnorm_f32(const float* x, const float* w, float* out, int rows, int n, float eps) {
   const float inv_n = (float)(1.0 / (double)n);
   for (int r = 0; r < rows; ++r) {
     const float* xr = x + (size_t)r * n;
-    float ss = 0.f;
-    for (int i = 0; i < n; ++i) ss += xr[i] * xr[i];
+    const float ss = orc_sumsq_tree(xr, n, 4);
     const float var = ss * inv_n;
     const float norm = sqrtf(var + eps);
     for (int i = 0; i < n; ++i) out[(size_t)r * n + i] = (xr[i] / norm) * w[i];
@@ -231,19 +265,18 @@ void orc_rmsnorm_f32(const float* x, const float* w, float* out, int rows, int n
 void orc_rmsnorm_bf16(const uint16_t* x, const uint16_t* w, uint16_t* out, int rows, int n,
                       float eps) {
   const float inv_n = (float)(1.0 / (double)n);
+  float* xf = (float*)malloc(sizeof(float) * (size_t)n);
   for (int r = 0; r < rows; ++r) {
     const uint16_t* xr = x + (size_t)r * n;
-    float ss = 0.f;
-    for (int i = 0; i < n; ++i) {
-      const float v = orc_bf16_to_f32(xr[i]);
-      ss += v * v;
-    }
+    for (int i = 0; i < n; ++i) xf[i] = orc_bf16_to_f32(xr[i]);
+    const float ss = orc_sumsq_tree(xf, n, 8);
     const float norm = sqrtf(ss * inv_n + eps);
     for (int i = 0; i < n; ++i) {
-      const float xn = rbf(orc_bf16_to_f32(xr[i]) / norm);
+      const float xn = rbf(xf[i] / norm);
       out[(size_t)r * n + i] = orc_f32_to_bf16(xn * orc_bf16_to_f32(w[i]));
     }
   }
+  free(xf);
 }
 
 /* ---- RotaryEmbedding::new (src/backends/qwen2.rs:90-108) ----

@@ -10,8 +10,12 @@ reference for this path, and the reference cannot be built here):
 * prefill_f32 (qwen2.rs:329-345, 476-503): float64 textbook; a one-token
   chunk equals decode over offset+1 keys; with offset 0 the first query sees
   only key 0; golden vectors.
-* rmsnorm_f32/bf16 (qwen2.rs:68-75): constant-row closed form; float64 form;
-  scale invariance; golden vectors.
+* rmsnorm_f32/bf16/f16 (qwen2.rs:68-75): constant-row closed form; float64
+  form; scale invariance; golden vectors. The sum of squares follows one
+  fixed order (sumsq_tree: 16-byte packets, then a pairwise tree), pinned by
+  exact integer rows, a row built so that the packet split and the tree
+  decide the rounded result (a sequential sum or another packet size gives
+  other bits), a float64 error bound and an independent numpy restatement.
 * rope tables / apply_rope (qwen2.rs:90-142): position 0 is the identity
   (bit-exact); rotations preserve the pair norms; inv_freq against
   theta^(-2i/d); float64 rotation; golden vectors.
@@ -159,6 +163,55 @@ def test_rmsnorm_matches_float64_and_is_scale_invariant():
         np.testing.assert_allclose(out, O.rmsnorm_f64(x, w, 1e-6), rtol=2e-6, atol=2e-6)
         out4 = O.rmsnorm_f32(x * np.float32(4.0), w, 0.0)
         np.testing.assert_allclose(out4, O.rmsnorm_f32(x, w, 0.0), rtol=1e-6, atol=1e-6)
+
+
+def _sumsq_tree_numpy(x, epl):
+    """The packet-then-tree order written with numpy array operations."""
+    x = np.asarray(x, np.float32)
+    n = x.shape[-1]
+    np_ = -(-n // epl)
+    p2 = 1 << (np_ - 1).bit_length()
+    pad = np.zeros(x.shape[:-1] + (p2 * epl,), np.float32)
+    pad[..., :n] = x
+    sq = (pad * pad).reshape(x.shape[:-1] + (p2, epl))
+    acc = np.zeros(x.shape[:-1] + (p2,), np.float32)
+    for e in range(epl):
+        acc = acc + sq[..., e]
+    while acc.shape[-1] > 1:
+        acc = acc[..., 0::2] + acc[..., 1::2]
+    return acc[..., 0]
+
+
+@pytest.mark.parametrize("epl", [4, 8])
+def test_sumsq_tree_order(epl):
+    rng = _rng(40 + epl)
+    for n in (1, 3, 8, 9, 64, 100, 128, 896, 1024, 5000):
+        x = (rng.standard_normal((6, n)) * rng.uniform(0.1, 30, (6, 1))).astype(np.float32)
+        got = O.sumsq_tree(x, epl)
+        np.testing.assert_array_equal(got, _sumsq_tree_numpy(x, epl))
+        exact = (x.astype(np.float64) ** 2).sum(-1)
+        # pairwise summation error bound: (epl + log2(packets)) ulps of the sum
+        depth = epl + int(np.ceil(np.log2(max(1, -(-n // epl))))) + 1
+        assert np.all(np.abs(got - exact) <= depth * 2.0 ** -24 * exact)
+        ints = rng.integers(-5, 6, (3, n)).astype(np.float32)   # every partial sum exact
+        np.testing.assert_array_equal(O.sumsq_tree(ints, epl), (ints.astype(np.int64) ** 2).sum(-1))
+
+
+def test_sumsq_tree_packet_split_decides_rounding():
+    # x^2 = 2^24 then ones: inside a packet each 1 is lost to 2^24 (ties to
+    # even), across packets the tree adds the other packets' sums exactly.
+    x = np.ones(16, np.float32)
+    x[0] = 4096.0
+    assert O.sumsq_tree(x, 4) == 2.0 ** 24 + 12   # packets [2^24, 4, 4, 4]
+    assert O.sumsq_tree(x, 8) == 2.0 ** 24 + 8    # packets [2^24, 8]
+    seq = np.float32(0)
+    for v in x:
+        seq = np.float32(seq + v * v)
+    assert seq == 2.0 ** 24                      # a sequential sum loses all 15
+    # the f32 norm uses 4-element packets, the 16-bit norms 8-element ones
+    w = np.ones(16, np.float32)
+    assert O.rmsnorm_f32(x[None], w, 0.0)[0, 1] == np.float32(1.0) / np.sqrt(
+        np.float32(2.0 ** 24 + 12) * np.float32(1.0 / 16))
 
 
 def test_rmsnorm_bf16_within_bf16_rounding():

@@ -135,3 +135,35 @@ def test_change_only_plan_keeps_a_device_mirror_exact(kv):
     assert sent_total < 0.2 * full_total, (sent_total, full_total)
     bm.release_all()
     assert bm.free_count() == 160
+
+
+def test_reprepared_rows_leave_one_page_per_cell(kv):
+    """A step abandoned after prepare and prepared again (no upload between)
+    must not leave two pending triples for one (row, col): a row that
+    restarts -- another request now sits in it -- supersedes its earlier
+    pending triples, and one upload applies exactly the latest pages."""
+    bm = kv.BlockManager(64)
+    st = kv.StepTables(3, 8)
+    for r, n in (("a", 40), ("b", 20), ("c", 70)):
+        bm.allocate(r, n)
+    st.prepare(bm, ["a", "b", "c"], [41, 21, 71])
+    # abandoned: row 0 now holds c, row 1 a, row 2 b (no upload in between)
+    st.prepare(bm, ["c", "a", "b"], [71, 41, 22])
+    _, _, batch, pend = st.host()
+    cells = [(int(r), int(c)) for r, c, _ in pend.tolist()]
+    assert len(cells) == len(set(cells)), "two pages pending for one cell"
+    mirror = {}
+    for row, col, page in pend.tolist():
+        mirror[(row, col)] = page
+    for i, r in enumerate(["c", "a", "b"]):
+        bt = bm.block_table(r)
+        assert [mirror[(i, j)] for j in range(len(bt))] == bt
+    # the same request prepared twice keeps its first triples and adds the growth
+    st.mark_uploaded()
+    st.prepare(bm, ["c", "a", "b"], [81, 41, 22])
+    st.prepare(bm, ["c", "a", "b"], [97, 41, 22])
+    _, _, _, pend = st.host()
+    cells = [(int(r), int(c)) for r, c, _ in pend.tolist()]
+    assert len(cells) == len(set(cells))
+    assert sorted(c for r, c in cells if r == 0) == list(range(5, 7))
+    assert [p for r, c, p in sorted(pend.tolist()) if r == 0] == bm.block_table("c")[5:7]
