@@ -65,8 +65,10 @@ int rlse_version(void);
 #define RLSE_WS_ERR_MERGE_TIMEOUT 1u
 #define RLSE_WS_ERR_LENGTH 2u
 /* Synchronises stream, then reads and clears the flags of a decode or
- * projection workspace (NULL: the library-owned decode workspace of the
- * current device). *flags (may be NULL) receives them. Returns
+ * projection workspace (NULL: the library's own decode workspaces of the
+ * current device -- the one used by calls without a workspace and the
+ * static one of rlse_decode_step_noalloc). *flags (may be NULL) receives
+ * them. Returns
  * RLSE_ERR_DEVICE_TIMEOUT if a merge timed out, else RLSE_ERR_TOKEN_LIMIT
  * if a length exceeded its table, else 0 (or a hip error). No counterpart
  * in the reference: its CPU/Candle ops return errors synchronously. */
@@ -218,6 +220,24 @@ int rlse_decode_step_planned(const void* q, const void* k_new, const void* v_new
                              int num_kv_heads, int head_dim, int max_blocks_per_seq,
                              int num_blocks, float scale, int dtype, void* workspace,
                              size_t workspace_bytes, const void* plan, rlse_stream_t stream);
+
+/* rlse_decode_step for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Same arguments and results
+ * as rlse_decode_step, without a workspace: the split-K records live in a
+ * static device array of 8.5 MB per device (room for 512 workgroups -- two
+ * per compute unit on up to 256 CUs -- at group size <= 8, head_dim <= 128;
+ * RLSE_ERR_INVALID_VALUE beyond that). The call allocates nothing and
+ * calls no allocating routine. Every call on a device shares that array:
+ * calls that overlap on one device (different streams or host threads)
+ * race. Its error flags are read by rlse_workspace_check(NULL, ...). */
+int rlse_decode_step_noalloc(const void* q, const void* k_new, const void* v_new,
+                             const void* q_norm_weight, const void* k_norm_weight, float eps,
+                             const void* cos_table, const void* sin_table, int max_pos,
+                             void* k_pool, void* v_pool, const int32_t* block_tables,
+                             const int32_t* seq_lens, void* out, int batch, int num_heads,
+                             int num_kv_heads, int head_dim, int max_blocks_per_seq,
+                             int num_blocks, float scale, int dtype, rlse_stream_t stream);
 
 /* Chunked-prefill attention of one sequence: the prefill branch of
  * Attention::forward (src/backends/qwen2.rs:329-345) with the causal mask

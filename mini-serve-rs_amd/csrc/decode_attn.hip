@@ -370,16 +370,104 @@ extern "C" int launch_paged_gqa_decode_tiled_bf16(const void* d_q, const void* d
                        num_heads, num_kv_heads, max_blocks_per_seq, scale, RLSE_DTYPE_BF16);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free fused decode step (rlse_decode_step_noalloc). Its
+// workspace is `scratch`, a file-scope device array sized for the largest
+// decode workspace it serves: kStaticMaxGroups workgroups (2 per compute
+// unit on a device of up to 256 CUs) and records of group size <= 8 at
+// head_dim <= 128 -- 8.5 MB, held by every device the library runs on until
+// the process ends. Like every static-storage object it starts zero-filled
+// (error flags clear, launch counters equal, no record carrying an epoch);
+// the kernels keep it consistent from then on. Host code never passes
+// `scratch` itself to a kernel: each device holds its own copy at its own
+// address, taken once per device with hipGetSymbolAddress and kept in
+// g_scratch_ptr. Calls on one device share it, so calls that overlap on one
+// device (different streams, different host threads) race.
+// ---------------------------------------------------------------------------
+constexpr int kStaticMaxGroups = 512;
+constexpr size_t kScratchWords = kWsHeaderWords + decode_ctr_words(kStaticMaxGroups) +
+                                 (size_t)kStaticMaxGroups * 2 * rec_words(8, 128) * 2;
+static __device__ __align__(256) uint32_t scratch[kScratchWords];
+
+static void* g_scratch_ptr[64] = {nullptr};
+static std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch` (set up on the first call per
+// device, with that device current).
+static int scratch_address(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_step_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(e != hipSuccess ? (int)e : RLSE_ERR_INVALID_VALUE,
+                  "decode_step_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return RLSE_OK;
+}
+
+extern "C" int rlse_decode_step_noalloc(
+    const void* q, const void* k_new, const void* v_new, const void* q_norm_weight,
+    const void* k_norm_weight, float eps, const void* cos_table, const void* sin_table,
+    int max_pos, void* k_pool, void* v_pool, const int32_t* block_tables,
+    const int32_t* seq_lens, void* out, int batch, int num_heads, int num_kv_heads, int head_dim,
+    int max_blocks_per_seq, int num_blocks, float scale, int dtype, rlse_stream_t stream) {
+  int st = validate_decode(batch, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                           num_blocks, dtype);
+  if (st) return st;
+  int W = 0;
+  st = decode_groups(&W);
+  if (st) return st;
+  if (W > kStaticMaxGroups)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "decode_step_noalloc: %d workgroups exceed the static scratch's %d", W,
+                kStaticMaxGroups);
+  const size_t need = decode_ws_bytes(W, num_heads / num_kv_heads, head_dim);
+  if (need > sizeof(scratch))
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "decode_step_noalloc: workspace of %zu bytes exceeds the static scratch (%zu)",
+                need, sizeof(scratch));
+  void* ws = nullptr;
+  st = scratch_address(&ws);
+  if (st) return st;
+  return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
+                          sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
+                          num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
+                          scale, dtype, ws, need, nullptr, stream);
+}
+
 extern "C" int rlse_workspace_check(void* workspace, rlse_stream_t stream, unsigned* flags) {
   if (flags) *flags = 0;
   hipStream_t s = as_stream(stream);
-  if (!workspace) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-      return fail(RLSE_ERR_INVALID_VALUE, "workspace_check: no current device");
+  if (workspace) return read_and_clear_ws_flags(workspace, s, flags);
+  // The library's own decode workspaces of the current device: the
+  // allocated one and the static scratch, each if a call has used it.
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(RLSE_ERR_INVALID_VALUE, "workspace_check: no current device");
+  void* own[2] = {nullptr, nullptr};
+  {
     std::lock_guard<std::mutex> lock(g_ws_mu);
-    if (!g_ws_ptr[dev]) return RLSE_OK;  // no library-owned decode has run on this device
-    workspace = g_ws_ptr[dev];
+    own[0] = g_ws_ptr[dev];
   }
-  return read_and_clear_ws_flags(workspace, s, flags);
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    own[1] = g_scratch_ptr[dev];
+  }
+  int rc = RLSE_OK;
+  for (void* w : own) {
+    if (!w) continue;
+    unsigned f = 0;
+    const int r = read_and_clear_ws_flags(w, s, &f);
+    if (flags) *flags |= f;
+    if (rc == RLSE_OK || r == RLSE_ERR_DEVICE_TIMEOUT) rc = r ? r : rc;
+  }
+  return rc;
 }

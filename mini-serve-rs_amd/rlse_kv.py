@@ -74,6 +74,7 @@ EXPORTED = (
     "rlse_argmax_workspace_size", "rlse_qkv_proj", "rlse_linear_residual", "rlse_gate_up_silu",
     "rlse_dense_workspace_size", "rlse_decode_plan_size", "rlse_decode_plan",
     "rlse_decode_step_planned", "rlse_workspace_check", "rlse_set_merge_wait_ns",
+    "rlse_decode_step_noalloc",
 )
 
 
@@ -255,6 +256,8 @@ _SIGS = {
     "rlse_linear_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_gate_up_silu": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_workspace_check": (_i, [_vp, _vp, ctypes.POINTER(ctypes.c_uint)]),
+    "rlse_decode_step_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp,
+                                      _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp]),
     "rlse_set_merge_wait_ns": (_i, [ctypes.c_ulonglong]),
 }
 
@@ -719,6 +722,20 @@ def paged_gqa_decode(q, k_pool, v_pool, block_tables, seq_lens, out, batch: int,
                                         num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
                                         scale, _dt(dtype), _ptr(workspace), workspace_bytes,
                                         _stream(stream)))
+
+
+def decode_step_noalloc(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: float, cos_table,
+                        sin_table, max_pos: int, k_pool, v_pool, block_tables, seq_lens, out,
+                        batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                        max_blocks_per_seq: int, num_blocks: int, scale: float, dtype,
+                        stream=None) -> None:
+    """decode_step without a workspace: the split-K records live in the
+    library's static device scratch; nothing is allocated."""
+    _check(load().rlse_decode_step_noalloc(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(q_norm_weight), _ptr(k_norm_weight), eps,
+        _ptr(cos_table), _ptr(sin_table), max_pos, _ptr(k_pool), _ptr(v_pool),
+        _ptr(block_tables), _ptr(seq_lens), _ptr(out), batch, num_heads, num_kv_heads, head_dim,
+        max_blocks_per_seq, num_blocks, scale, _dt(dtype), _stream(stream)))
 
 
 def decode_step(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: float, cos_table, sin_table,
