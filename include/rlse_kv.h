@@ -578,7 +578,7 @@ typedef struct rlse_model_shape {    /* the Config fields memory_charge reads */
   int dtype_bytes, context_length, block_size;
 } rlse_model_shape;
 
-/* TensorMemoryBudget::new (:48-67): 0 < headroom < budget, else
+/* TensorMemoryBudget::new (:48-67): 0 <= headroom < budget, else
  * RLSE_ERR_INVALID_VALUE; the headroom is reserved from the start. */
 int rlse_mb_create(long long budget_bytes, long long headroom_bytes, rlse_memory_budget** out);
 int rlse_mb_destroy(rlse_memory_budget* mb);

@@ -4,7 +4,7 @@
 //
 // Kept from the reference, so an admission path sees the same accounting:
 //   - a budget with a headroom reserved at creation, refused unless
-//     0 < headroom < budget (tensor_memory.rs:48-67);
+//     0 <= headroom < budget (tensor_memory.rs:48-67);
 //   - three reserved classes (active KV, execution, retained prefix), the
 //     peak of the reserved bytes and a rejection count (:28-39);
 //   - try_reserve is all-or-nothing and refuses a charge whose total overflows

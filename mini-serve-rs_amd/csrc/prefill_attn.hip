@@ -475,8 +475,10 @@ int launch_prefill(PrefillParams& pp, hipStream_t stream) {
   return launch_status("prefill_merge_kernel");
 }
 
-// Library-owned workspace per device, for callers that pass none; the
-// mutex serialises its growth across host threads.
+// Library-owned workspace per device, for callers that pass none. The mutex
+// is held from the lookup until the launches are queued, so a thread that
+// grows (frees and reallocates) the buffer never frees one another thread
+// is about to launch on; hipFree waits for launches already queued.
 void* g_pws_ptr[64] = {nullptr};
 size_t g_pws_size[64] = {0};
 std::mutex g_pws_mu;
@@ -536,13 +538,14 @@ extern "C" int rlse_prefill_attn(const void* q, const void* k_pool, const void* 
   PrefillPlan plan;
   st = plan_prefill(num_tokens, ctx_len, num_heads, num_kv_heads, head_dim, &plan);
   if (st) return st;
+  std::unique_lock<std::mutex> lock;
   if (plan.ws_bytes > 0) {
     if (workspace == nullptr) {
       int dev = 0;
       hipError_t e = hipGetDevice(&dev);
       if (e != hipSuccess || dev < 0 || dev >= 64)
         return fail(RLSE_ERR_INVALID_VALUE, "prefill: no current device");
-      std::lock_guard<std::mutex> lock(g_pws_mu);
+      lock = std::unique_lock<std::mutex>(g_pws_mu);
       if (g_pws_size[dev] < plan.ws_bytes) {
         if (g_pws_ptr[dev]) (void)hipFree(g_pws_ptr[dev]);
         g_pws_ptr[dev] = nullptr;
