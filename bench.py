@@ -377,6 +377,8 @@ def fork_bench(args):
         if evs is not None:
             evs[0].record(stream)
         for layer in range(layers):
+            # The prefix pages are read by all b rows: they stay cacheable (no
+            # RLSE_DECODE_STREAM), so their re-reads hit the caches.
             kv.decode_step_planned(q_in[layer], k_in[layer], v_in[layer], qw, kw, 1e-6, cos_t,
                                    sin_t, max_pos, ptrs[layer][0], ptrs[layer][1], t_dev,
                                    lens_dev, out, b, hq, hkv, d, mbps, nb, scale, "bf16", plan,
@@ -497,7 +499,8 @@ def e2e_bench(args):
             w.update({p + "q_b": vec(nq, 0), p + "k_b": vec(nkv, 0), p + "v_b": vec(nkv, 0)})
         if cfg.qk_norm:
             w.update({p + "q_norm": vec(d), p + "k_norm": vec(d)})
-    model = DecodeModel(cfg, w, "bf16", nb, b, mbps, dev)
+    # The table is a permutation: no page is shared, so attention streams.
+    model = DecodeModel(cfg, w, "bf16", nb, b, mbps, dev, stream_pages=True)
     del w
     t_dev = torch.from_numpy(tables).to(dev)
     for i, n in enumerate(cached):   # cached context: N(0,1) K/V in every layer
@@ -695,10 +698,13 @@ def main():
                 kv.paged_gqa_decode(q_rot, k_pools[layer], v_pools[layer], t_dev, lens_dev, out,
                                     b, hq, hkv, d, mbps, nb, scale, "bf16", ws, ws_bytes, stream)
             else:
+                # The table is a permutation: no page is read by two rows, so the
+                # pages stream (RLSE_DECODE_STREAM).
                 kv.decode_step_planned(q_in[layer], k_in[layer], v_in[layer], qw[layer],
                                        kw[layer], 1e-6, cos_t, sin_t, max_pos, k_pools[layer],
                                        v_pools[layer], t_dev, lens_dev, out, b, hq, hkv, d, mbps,
-                                       nb, scale, "bf16", plan, ws, ws_bytes, stream)
+                                       nb, scale, "bf16", plan, ws, ws_bytes, stream,
+                                       stream_pages=True)
             if args.unfused and timed_index is not None:
                 ev_b[timed_index * layers + layer].record(stream)
         if not args.unfused and timed_index is not None:

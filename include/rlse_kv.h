@@ -210,8 +210,16 @@ int rlse_decode_plan(const int32_t* block_tables, const int32_t* seq_lens, int b
 /* rlse_decode_step with a plan that rlse_decode_plan built from the same
  * block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq and
  * num_blocks (every layer of a decode step shares them): each wave's page
- * ids then arrive with its first load instead of after a table walk.
- * Results are identical to rlse_decode_step's. */
+ * ids then arrive with its first load, and its first pages are requested
+ * right after. Results are identical to rlse_decode_step's.
+ * flags: RLSE_DECODE_STREAM when no page of the batch is read by more than
+ * one row (no sequence shares pages with another -- the caller's block
+ * manager knows: no page with a refcount above 1): the pages are then read
+ * with non-temporal loads that keep the per-launch data in the caches.
+ * Without it (e.g. sequences forked from one cached prefix) the pages stay
+ * cacheable, so a page read by many rows is served from the caches. Either
+ * way the results are the same. */
+#define RLSE_DECODE_STREAM 1
 int rlse_decode_step_planned(const void* q, const void* k_new, const void* v_new,
                              const void* q_norm_weight, const void* k_norm_weight, float eps,
                              const void* cos_table, const void* sin_table, int max_pos,
@@ -219,7 +227,8 @@ int rlse_decode_step_planned(const void* q, const void* k_new, const void* v_new
                              const int32_t* seq_lens, void* out, int batch, int num_heads,
                              int num_kv_heads, int head_dim, int max_blocks_per_seq,
                              int num_blocks, float scale, int dtype, void* workspace,
-                             size_t workspace_bytes, const void* plan, rlse_stream_t stream);
+                             size_t workspace_bytes, const void* plan, int flags,
+                             rlse_stream_t stream);
 
 /* rlse_decode_step for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -342,6 +342,9 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // is at or past the descriptor's record count returns zeros without
 // accessing memory.
 constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of a buffer load that streams data read once: the
+// non-temporal bit (bit 1), so the lines do not displace reused data in L2.
+constexpr int kLoadNonTemporal = 2;
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima), fenced
 // against compiler reordering on both sides.

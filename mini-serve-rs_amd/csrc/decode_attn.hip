@@ -9,12 +9,18 @@
 
 namespace rlse {
 
-RLSE_DECODE_INSTANCES(extern template, float, false)
-RLSE_DECODE_INSTANCES(extern template, float, true)
-RLSE_DECODE_INSTANCES(extern template, bf16, false)
-RLSE_DECODE_INSTANCES(extern template, bf16, true)
-RLSE_DECODE_INSTANCES(extern template, f16, false)
-RLSE_DECODE_INSTANCES(extern template, f16, true)
+RLSE_DECODE_INSTANCES(extern template, float, kModePlain)
+RLSE_DECODE_INSTANCES(extern template, float, kModeFused)
+RLSE_DECODE_INSTANCES(extern template, float, kModePlanned)
+RLSE_DECODE_INSTANCES(extern template, float, kModePlannedStream)
+RLSE_DECODE_INSTANCES(extern template, bf16, kModePlain)
+RLSE_DECODE_INSTANCES(extern template, bf16, kModeFused)
+RLSE_DECODE_INSTANCES(extern template, bf16, kModePlanned)
+RLSE_DECODE_INSTANCES(extern template, bf16, kModePlannedStream)
+RLSE_DECODE_INSTANCES(extern template, f16, kModePlain)
+RLSE_DECODE_INSTANCES(extern template, f16, kModeFused)
+RLSE_DECODE_INSTANCES(extern template, f16, kModePlanned)
+RLSE_DECODE_INSTANCES(extern template, f16, kModePlannedStream)
 
 // Per-step plan: for every wave of every workgroup of a decode launch, the
 // descriptors of its first 64 blocks -- exactly what the wave would compute
@@ -24,12 +30,12 @@ RLSE_DECODE_INSTANCES(extern template, f16, true)
 __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __restrict__ tables,
                                                                const int* __restrict__ seq_lens,
                                                                int B, int Hkv, int mbps,
-                                                               int num_blocks, int W,
+                                                               int num_blocks, int W, int w1,
                                                                int4* __restrict__ plan) {
   extern __shared__ int s_pref[];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  if (wave == 0) block_prefix(seq_lens, B, mbps, s_pref);
+  if (wave == 0) block_prefix(seq_lens, B, mbps, s_pref, lane < B ? seq_lens[lane] : 0);
   __syncthreads();
   const long long w = blockIdx.x;
   const long long total = (long long)Hkv * s_pref[B];
@@ -37,8 +43,8 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __rest
   if (total > 0) {
     const long long we = effective_groups(total, W);
     if (w < we) {
-      const long long glo = range_lo(w, total, we);
-      const long long ghi = range_lo(w + 1, total, we);
+      const long long glo = range_lo(w, total, we, W, w1);
+      const long long ghi = range_lo(w + 1, total, we, W, w1);
       const long long wlo = glo + (ghi - glo) * wave / kWaves;
       const long long whi = glo + (ghi - glo) * (wave + 1) / kWaves;
       d = block_desc(wlo + lane, whi, s_pref, tables, seq_lens, B, Hkv, mbps, num_blocks);
@@ -73,36 +79,36 @@ static void set_workspace(DecodeParams& p, void* workspace, int W) {
   p.wait_ticks = merge_wait_ticks();
 }
 
-template <typename T, int D, bool FUSED>
+template <typename T, int D, int MODE>
 static int launch_decode_g(int G, const DecodeParams& p, hipStream_t s) {
   switch (G) {
-    case 1: return launch_decode_t<T, D, 1, FUSED>(p, s);
-    case 2: return launch_decode_t<T, D, 2, FUSED>(p, s);
-    case 3: return launch_decode_t<T, D, 3, FUSED>(p, s);
-    case 4: return launch_decode_t<T, D, 4, FUSED>(p, s);
-    case 5: return launch_decode_t<T, D, 5, FUSED>(p, s);
-    case 6: return launch_decode_t<T, D, 6, FUSED>(p, s);
-    case 7: return launch_decode_t<T, D, 7, FUSED>(p, s);
-    case 8: return launch_decode_t<T, D, 8, FUSED>(p, s);
+    case 1: return launch_decode_t<T, D, 1, MODE>(p, s);
+    case 2: return launch_decode_t<T, D, 2, MODE>(p, s);
+    case 3: return launch_decode_t<T, D, 3, MODE>(p, s);
+    case 4: return launch_decode_t<T, D, 4, MODE>(p, s);
+    case 5: return launch_decode_t<T, D, 5, MODE>(p, s);
+    case 6: return launch_decode_t<T, D, 6, MODE>(p, s);
+    case 7: return launch_decode_t<T, D, 7, MODE>(p, s);
+    case 8: return launch_decode_t<T, D, 8, MODE>(p, s);
   }
   return fail(RLSE_ERR_INVALID_VALUE, "decode: unsupported group size %d", G);
 }
 
-template <typename T, bool FUSED>
+template <typename T, int MODE>
 static int launch_decode_d(int D, int G, const DecodeParams& p, hipStream_t s) {
   switch (D) {
-    case 64: return launch_decode_g<T, 64, FUSED>(G, p, s);
-    case 128: return launch_decode_g<T, 128, FUSED>(G, p, s);
+    case 64: return launch_decode_g<T, 64, MODE>(G, p, s);
+    case 128: return launch_decode_g<T, 128, MODE>(G, p, s);
   }
   return fail(RLSE_ERR_INVALID_VALUE, "decode: unsupported head_dim %d", D);
 }
 
-template <bool FUSED>
+template <int MODE>
 static int launch_decode_dtype(int dtype, int D, int G, const DecodeParams& p, hipStream_t s) {
   switch (dtype) {
-    case RLSE_DTYPE_F32: return launch_decode_d<float, FUSED>(D, G, p, s);
-    case RLSE_DTYPE_BF16: return launch_decode_d<bf16, FUSED>(D, G, p, s);
-    case RLSE_DTYPE_F16: return launch_decode_d<f16, FUSED>(D, G, p, s);
+    case RLSE_DTYPE_F32: return launch_decode_d<float, MODE>(D, G, p, s);
+    case RLSE_DTYPE_BF16: return launch_decode_d<bf16, MODE>(D, G, p, s);
+    case RLSE_DTYPE_F16: return launch_decode_d<f16, MODE>(D, G, p, s);
   }
   return fail(RLSE_ERR_INVALID_VALUE, "decode: bad dtype %d", dtype);
 }
@@ -211,6 +217,7 @@ static int prepare_decode(DecodeParams& p, std::unique_lock<std::mutex>& lock, c
   p.mbps = max_blocks_per_seq;
   p.num_blocks = num_blocks;
   p.W = W;
+  p.w1 = kSlot1Weight;
   p.c = scale * 1.4426950408889634f;
   return RLSE_OK;
 }
@@ -227,8 +234,8 @@ extern "C" int rlse_paged_gqa_decode(const void* q, const void* k_pool, const vo
                                 num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
                                 num_blocks, scale, dtype, workspace, workspace_bytes);
   if (st) return st;
-  return launch_decode_dtype<false>(dtype, head_dim, num_heads / num_kv_heads, p,
-                                    as_stream(stream));
+  return launch_decode_dtype<kModePlain>(dtype, head_dim, num_heads / num_kv_heads, p,
+                                         as_stream(stream));
 }
 
 extern "C" int rlse_decode_plan_size(size_t* bytes) {
@@ -261,7 +268,7 @@ extern "C" int rlse_decode_plan(const int32_t* block_tables, const int32_t* seq_
   const size_t lds = (size_t)(batch + 1) * sizeof(int);
   hipLaunchKernelGGL(decode_plan_kernel, dim3(W), dim3(kThreads), lds, as_stream(stream),
                      block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq, num_blocks,
-                     W, reinterpret_cast<int4*>(plan));
+                     W, kSlot1Weight, reinterpret_cast<int4*>(plan));
   return launch_status("decode_plan_kernel");
 }
 
@@ -272,7 +279,10 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
                                 const int32_t* seq_lens, void* out, int batch, int num_heads,
                                 int num_kv_heads, int head_dim, int max_blocks_per_seq,
                                 int num_blocks, float scale, int dtype, void* workspace,
-                                size_t workspace_bytes, const void* plan, rlse_stream_t stream) {
+                                size_t workspace_bytes, const void* plan, int flags,
+                                rlse_stream_t stream) {
+  if (flags & ~RLSE_DECODE_STREAM)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_step: unknown flags 0x%x", flags);
   DecodeParams p;
   std::unique_lock<std::mutex> lock;
   const int st = prepare_decode(p, lock, q, k_pool, v_pool, block_tables, seq_lens, out, batch,
@@ -298,8 +308,12 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
   if (plan && (uintptr_t)plan % 16)
     return fail(RLSE_ERR_INVALID_VALUE, "decode_step: plan must be 16-byte aligned");
   p.plan = reinterpret_cast<const int4*>(plan);
-  return launch_decode_dtype<true>(dtype, head_dim, num_heads / num_kv_heads, p,
-                                   as_stream(stream));
+  const int G = num_heads / num_kv_heads;
+  const hipStream_t s = as_stream(stream);
+  if (!plan) return launch_decode_dtype<kModeFused>(dtype, head_dim, G, p, s);
+  return (flags & RLSE_DECODE_STREAM)
+             ? launch_decode_dtype<kModePlannedStream>(dtype, head_dim, G, p, s)
+             : launch_decode_dtype<kModePlanned>(dtype, head_dim, G, p, s);
 }
 
 extern "C" int rlse_decode_step(const void* q, const void* k_new, const void* v_new,
@@ -313,7 +327,7 @@ extern "C" int rlse_decode_step(const void* q, const void* k_new, const void* v_
   return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
                           sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
                           num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
-                          scale, dtype, workspace, workspace_bytes, nullptr, stream);
+                          scale, dtype, workspace, workspace_bytes, nullptr, 0, stream);
 }
 
 extern "C" int rlse_decode_step_planned(
@@ -322,12 +336,12 @@ extern "C" int rlse_decode_step_planned(
     int max_pos, void* k_pool, void* v_pool, const int32_t* block_tables,
     const int32_t* seq_lens, void* out, int batch, int num_heads, int num_kv_heads, int head_dim,
     int max_blocks_per_seq, int num_blocks, float scale, int dtype, void* workspace,
-    size_t workspace_bytes, const void* plan, rlse_stream_t stream) {
+    size_t workspace_bytes, const void* plan, int flags, rlse_stream_t stream) {
   if (!plan) return fail(RLSE_ERR_INVALID_VALUE, "decode_step_planned: null plan");
   return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
                           sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
                           num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
-                          scale, dtype, workspace, workspace_bytes, plan, stream);
+                          scale, dtype, workspace, workspace_bytes, plan, flags, stream);
 }
 
 static int compat_decode(const void* q, const void* k, const void* v, const int* tables,
@@ -440,7 +454,7 @@ extern "C" int rlse_decode_step_noalloc(
   return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
                           sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
                           num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
-                          scale, dtype, ws, need, nullptr, stream);
+                          scale, dtype, ws, need, nullptr, 0, stream);
 }
 
 extern "C" int rlse_workspace_check(void* workspace, rlse_stream_t stream, unsigned* flags) {

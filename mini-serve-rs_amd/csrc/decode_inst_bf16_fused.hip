@@ -2,5 +2,5 @@
 #include "decode_kernel.cuh"
 
 namespace rlse {
-RLSE_DECODE_INSTANCES(template, bf16, true)
+RLSE_DECODE_INSTANCES(template, bf16, kModeFused)
 }  // namespace rlse

@@ -2,5 +2,5 @@
 #include "decode_kernel.cuh"
 
 namespace rlse {
-RLSE_DECODE_INSTANCES(template, bf16, false)
+RLSE_DECODE_INSTANCES(template, bf16, kModePlain)
 }  // namespace rlse

@@ -2,5 +2,5 @@
 #include "decode_kernel.cuh"
 
 namespace rlse {
-RLSE_DECODE_INSTANCES(template, f16, false)
+RLSE_DECODE_INSTANCES(template, f16, kModePlain)
 }  // namespace rlse

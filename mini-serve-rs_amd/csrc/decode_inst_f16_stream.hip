@@ -1,0 +1,7 @@
+// Decode kernel instantiations: f16 K/V, fused decode step with a per-step plan,
+// pages streamed with non-temporal loads.
+#include "decode_kernel.cuh"
+
+namespace rlse {
+RLSE_DECODE_INSTANCES(template, f16, kModePlannedStream)
+}  // namespace rlse

@@ -2,5 +2,5 @@
 #include "decode_kernel.cuh"
 
 namespace rlse {
-RLSE_DECODE_INSTANCES(template, float, true)
+RLSE_DECODE_INSTANCES(template, float, kModeFused)
 }  // namespace rlse

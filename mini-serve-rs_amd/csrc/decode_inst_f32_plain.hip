@@ -2,5 +2,5 @@
 #include "decode_kernel.cuh"
 
 namespace rlse {
-RLSE_DECODE_INSTANCES(template, float, false)
+RLSE_DECODE_INSTANCES(template, float, kModePlain)
 }  // namespace rlse

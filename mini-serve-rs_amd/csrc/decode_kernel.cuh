@@ -50,6 +50,14 @@ constexpr int kGroupsPerCU = 2;         // workgroups launched per compute unit
 constexpr int kMinBlocksPerGroup = 8;   // smallest share of blocks per workgroup
 constexpr int kMaxDecodeBatch = 8192;   // prefix table lives in LDS
 constexpr int kMaxDecodeRows = 65536;   // batch * num_kv_heads
+// Share of the block stream taken by the second workgroup of each compute
+// unit, in sixteenths of the first's (16: equal shares; see share_cum).
+constexpr int kSlot1Weight = 16;
+// Kernel modes: the paged decode (rlse_paged_gqa_decode), the fused step
+// (rlse_decode_step), the fused step with a plan (rlse_decode_step_planned),
+// and the same streaming its pages with non-temporal loads (flag
+// RLSE_DECODE_STREAM: no page is read by more than one row of the batch).
+enum : int { kModePlain = 0, kModeFused = 1, kModePlanned = 2, kModePlannedStream = 3 };
 // The running max of a softmax moves only when a score exceeds it by more
 // than this many powers of two.
 constexpr float kLazyLog2 = 8.f;
@@ -73,14 +81,16 @@ __device__ __forceinline__ int valid_len(int L, int mbps) {
 }
 
 // Exclusive prefix of per-sequence block counts into s_pref[0..B] (one wave).
-__device__ void block_prefix(const int* __restrict__ seq_lens, int B, int mbps, int* s_pref) {
+// first: seq_lens[lane] for lane < B, requested by the caller beforehand.
+// (The first chunk issues no load, so a caller with loads in flight does not
+// wait for them here.)
+__device__ void block_prefix(const int* __restrict__ seq_lens, int B, int mbps, int* s_pref,
+                             int first) {
   const int lane = threadIdx.x & 63;
   int carry = 0;
-  for (int base = 0; base < B; base += 64) {
+  auto chunk = [&](int base, int len) __attribute__((always_inline)) {
     const int b = base + lane;
-    int nb = 0;
-    if (b < B) nb = (valid_len(seq_lens[b], mbps) + 15) >> 4;
-    int x = nb;
+    int x = b < B ? (valid_len(len, mbps) + 15) >> 4 : 0;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const int y = __shfl_up(x, o, 64);
@@ -88,7 +98,10 @@ __device__ void block_prefix(const int* __restrict__ seq_lens, int B, int mbps, 
     }
     if (b < B) s_pref[b + 1] = carry + x;
     carry += __shfl(x, 63, 64);
-  }
+  };
+  chunk(0, first);
+  for (int base = 64; base < B; base += 64)
+    chunk(base, base + lane < B ? seq_lens[base + lane] : 0);
   if (lane == 0) s_pref[0] = 0;
 }
 
@@ -98,8 +111,35 @@ __device__ __forceinline__ long long effective_groups(long long total, int W) {
   return we < W ? we : W;
 }
 
-__device__ __forceinline__ long long range_lo(long long w, long long total, long long we) {
-  return (w * total) / we;
+// Shares of the block stream. With the full grid, workgroups [0, W/2) --
+// dispatched first, one per compute unit -- weigh 16 and the second
+// workgroup of each compute unit weighs w1 (a per-launch constant): the
+// second workgroup's waves start later and lose issue arbitration to the
+// first's, so an equal share would leave its compute units streaming alone
+// at the end. Fewer groups (small batches) share evenly.
+__device__ __forceinline__ long long share_cum(long long w, long long we, int W, int w1) {
+  if (we < W || w1 == 16) return w * 16;
+  const long long h = W / 2;
+  return w <= h ? w * 16 : h * 16 + (w - h) * w1;
+}
+__device__ __forceinline__ long long range_lo(long long w, long long total, long long we, int W,
+                                              int w1) {
+  return total * share_cum(w, we, W, w1) / share_cum(we, we, W, w1);
+}
+// The workgroup whose range holds block f: the largest w with
+// range_lo(w) <= f.
+__device__ __forceinline__ long long group_of(long long f, long long total, long long we, int W,
+                                              int w1) {
+  if (we < W || w1 == 16) return ((f + 1) * we - 1) / total;
+  long long lo = 0, hi = we - 1;
+  while (lo < hi) {
+    const long long mid = (lo + hi + 1) >> 1;
+    if (range_lo(mid, total, we, W, w1) <= f)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
 }
 
 // Largest b in [0, B) with Hkv*s_pref[b] <= g (that sequence is non-empty).
@@ -171,6 +211,7 @@ struct DecodeParams {
   int mbps;
   int num_blocks;
   int W;    // workgroups launched
+  int w1;   // weight of the second workgroup per compute unit (16 = even shares)
   float c;  // scale * log2(e)
   // Fused decode step only (rlse_decode_step): raw new-token k/v
   // [B][Hkv][D], q/k RMSNorm weights [D] (null: no norm), RoPE tables
@@ -299,8 +340,38 @@ __device__ __forceinline__ uint4 norm_rope_packet(uint4 x, bool norm, uint4 w, f
   return pack_packet<T>(y);
 }
 
+// Appended rows per wave kept in LDS: the blocks of a wave's first kNewCap
+// appends take the new row from there, so their loads never wait for the
+// append stores.
+template <typename T>
+__host__ __device__ constexpr int new_row_cap() { return sizeof(T) == 2 ? 4 : 2; }
+
+// Static LDS of one decode workgroup (the block prefix is dynamic LDS).
 template <typename T, int D, int G, bool FUSED>
-__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
+struct DecodeLds {
+  static constexpr int LPR = DecodeShape<T, D>::LPR;
+  static constexpr int QR = q_stage_rows<T, D, G>();
+  static constexpr int kNew = new_row_cap<T>();
+  float part[2 * kWaves][G][D + 2];  // wave partials: acc[D], m, l per head
+  int part_row[2 * kWaves];          // their rows (-1 = unused)
+  uint4 q[kWaves][QR][G][LPR];       // staged query packets per wave
+  uint4 nw[FUSED ? kWaves : 1][FUSED ? kNew : 1][2][LPR];  // appended k, v rows
+};
+
+// The decode of one workgroup. POL is the cache-policy operand of the page
+// loads: kLoadNonTemporal when every page is read by one row only (streamed
+// once: the lines do not displace the small per-launch data -- plan, tables,
+// queries, records -- from L2); 0 otherwise, so that a page shared by many
+// rows (a forked prefix) is served from the caches after its first read.
+// plan_d, ctr0 and len_t0 were requested by decode_kernel: the wave's plan
+// descriptors (planned modes), its launch counter and seq_lens[tid].
+template <typename T, int D, int G, int MODE, int POL>
+__device__ __forceinline__ void decode_body(const DecodeParams& p,
+                                            DecodeLds<T, D, G, MODE != kModePlain>& lds,
+                                            int* s_pref, int4 plan_d, uint32_t ctr0,
+                                            int len_t0) {
+  constexpr bool FUSED = MODE != kModePlain;
+  constexpr bool PLANNED = MODE >= kModePlanned;
   using S = DecodeShape<T, D>;
   constexpr int EPL = S::EPL, LPR = S::LPR, RPL = S::RPL, NR = S::NR;
   constexpr int REC = rec_words(G, D);
@@ -312,17 +383,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   // With 2 * kWaves waves per compute unit that is enough bytes in flight to
   // keep HBM streaming; deeper buffering only lengthens the memory queues,
   // which the publication chain at the end of the launch then waits behind.
-  constexpr int kPreIssued = 1;  // blocks issued before the prologue's appends
-  // Appended rows per wave kept in LDS: the blocks of a wave's first kNewCap
-  // appends take the new row from there, so their loads never wait for the
-  // append stores.
-  constexpr int kNewCap = sizeof(T) == 2 ? 4 : 2;
+  constexpr int kPreIssued = 2;  // blocks issued before the prologue's appends
+  constexpr int kNewCap = new_row_cap<T>();
   static_assert(kNewCap >= kPreIssued, "pre-issued blocks must find their new rows in LDS");
-  extern __shared__ int s_pref[];             // [B + 1]; fused step: then s_len[B]
-  __shared__ float s_part[NPART][G][D + 2];   // wave partials: acc[D], m, l per head
-  __shared__ int s_part_row[NPART];           // their rows (-1 = unused)
-  __shared__ uint4 s_q[kWaves][QR][G][LPR];   // staged query packets per wave
-  __shared__ uint4 s_new[FUSED ? kWaves : 1][FUSED ? kNewCap : 1][2][LPR];  // appended k, v rows
+  auto& s_part = lds.part;
+  auto& s_part_row = lds.part_row;
+  auto& s_q = lds.q;
+  auto& s_new = lds.nw;
 
   const int tid = threadIdx.x;
   // The wave index and everything derived from LDS-held prefixes below are
@@ -336,21 +403,54 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   T* __restrict__ ob = reinterpret_cast<T*>(p.out);
 
   int* s_len = s_pref + B + 1;  // fused step: valid sequence lengths
-  // With a plan the wave's first descriptors are requested first of all:
-  // they then arrive while wave 0 computes the block prefix, instead of a
-  // page-table walk starting after it.
-  int4 plan_d = make_int4(0, 0, -1, 0);
-  if (p.plan) plan_d = p.plan[((size_t)blockIdx.x * kWaves + wave) * 64 + lane];
-  // This wave's launch counter: the epoch tags its records and is expected
-  // on the records it merges; stored back on every exit path.
+  const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
+  const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
+  const size_t tile = (size_t)16 * D;  // elements of one (block, head) tile
+  const int voff = (int)(((size_t)rsub * D + (size_t)col * EPL) * sizeof(T));
+  // K and V packets of one block, as raw buffer loads through a descriptor
+  // of the block's tile: a block not fetched (past the wave's end, or an
+  // invalid page) gets a descriptor of zero records, which returns zeros
+  // without a memory access. With loads under a branch instead the compiler
+  // cannot count the loads in flight and waits for every earlier block
+  // before reusing a buffer's registers, which would serialize the pipeline.
+  // (POL: see above.)
+  auto load_pages = [&](Buf<T, D>& bf, int id, int kvh, bool fetch) __attribute__((always_inline)) {
+    const size_t tb = ((size_t)(fetch ? id : 0) * Hkv + kvh) * tile;
+    const int nrec = fetch ? (int)(tile * sizeof(T)) : 0;
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kp + tb), 0, nrec,
+                                                      kBufferWord3);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vp + tb), 0, nrec,
+                                                      kBufferWord3);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int o = voff + r * RPL * D * (int)sizeof(T);
+      const u32x4_t kx = __builtin_amdgcn_raw_buffer_load_b128(rk, o, 0, POL);
+      const u32x4_t vx = __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, POL);
+      bf.k[r] = make_uint4(kx.x, kx.y, kx.z, kx.w);
+      bf.v[r] = make_uint4(vx.x, vx.y, vx.z, vx.w);
+    }
+  };
+  Buf<T, D> b0, b1;
+  // With a plan the wave's first kPreIssued blocks are requested as soon as
+  // its descriptors arrive: HBM starts streaming one round trip into the
+  // launch, while the prefix, the query staging and the appends run.
   uint32_t* const ctr = p.ws_ctr + (size_t)blockIdx.x * kWaves + wave;
-  const uint32_t ctr0 = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   auto end_epoch = [&](uint32_t ep) __attribute__((always_inline)) {
     if (lane == 0) __hip_atomic_store(ctr, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref);
+  if constexpr (PLANNED) {
+#pragma unroll
+    for (int k = 0; k < kPreIssued; ++k) {
+      const int nv = __builtin_amdgcn_readlane(plan_d.y, k) & 255;
+      const int row = __builtin_amdgcn_readlane(plan_d.z, k);
+      const int kvh = nv > 0 ? row % Hkv : 0;
+      load_pages(k == 0 ? b0 : b1, __builtin_amdgcn_readlane(plan_d.x, k), kvh, nv > 0);
+    }
+  }
+  if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref, len_t0);
   if constexpr (FUSED) {
-    for (int b = tid; b < B; b += kThreads) s_len[b] = valid_len(p.seq_lens[b], mbps);
+    if (tid < B) s_len[tid] = valid_len(len_t0, mbps);
+    for (int b = tid + kThreads; b < B; b += kThreads) s_len[b] = valid_len(p.seq_lens[b], mbps);
   }
   if (tid < NPART) s_part_row[tid] = -1;
   __syncthreads();
@@ -374,8 +474,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     end_epoch(ep);
     return;
   }
-  const long long glo = range_lo(w, total, we);
-  const long long ghi = range_lo(w + 1, total, we);
+  const long long glo = range_lo(w, total, we, p.W, p.w1);
+  const long long ghi = range_lo(w + 1, total, we, p.W, p.w1);
   // This wave's contiguous share of the group's range.
   const long long wlo = glo + (ghi - glo) * wave / kWaves;
   const long long whi = glo + (ghi - glo) * (wave + 1) / kWaves;
@@ -390,10 +490,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
 
   if (nblk > 0) {
     const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
-    const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
-    const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
-    const size_t tile = (size_t)16 * D;  // elements of one (block, head) tile
-    const size_t lane_off = (size_t)rsub * D + (size_t)col * EPL;
 
     // Descriptors of 64 consecutive blocks, one per lane: page id, valid
     // rows and row, read back with readlane when the block is issued.
@@ -403,7 +499,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     auto load_chunk = [&](int base) __attribute__((always_inline)) {
       cbase = base;
       int4 d;
-      if (base == 0 && p.plan)  // the plan's copy, loaded before the barrier
+      if (PLANNED && base == 0)  // the plan's copy, loaded before the barrier
         d = plan_d;
       else
         d = block_desc(wlo + base + lane, whi, s_pref, p.tables, p.seq_lens, B, Hkv, mbps,
@@ -609,15 +705,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
 
     int issued_row = -1;
     int n_last = 0;  // last blocks of rows issued so far = their append ordinal
-    const int voff = (int)(lane_off * sizeof(T));
-    // Block j of the wave's range (j >= nblk: past the end, never computed).
-    // The loads are issued for every j, as raw buffer loads through a
-    // descriptor of the block's tile: a block past the end or on an invalid
-    // page gets a descriptor of zero records, which returns zeros without a
-    // memory access. With loads under a branch instead the compiler cannot
-    // count the loads in flight and waits for every earlier block before
-    // reusing a buffer's registers, which would serialize the pipeline.
-    auto issue = [&](Buf<T, D>& bf, int j) __attribute__((always_inline)) {
+    // Block j of the wave's range (j >= nblk: past the end, never computed):
+    // its bookkeeping, then (unless the plan's early requests already made
+    // them) its loads, issued for every j (load_pages).
+    auto issue = [&](Buf<T, D>& bf, int j, bool loads) __attribute__((always_inline)) {
       const bool real = j < nblk;
       j = real ? j : nblk - 1;
       if (j - cbase >= 64) load_chunk(cbase + 64);
@@ -636,21 +727,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
         if (row_end) ++n_last;
         issued_row = row;
       }
-      const bool fetch = real && nv > 0;
-      const size_t tb = ((size_t)(fetch ? id : 0) * Hkv + kvh) * tile;
-      const int nrec = fetch ? (int)(tile * sizeof(T)) : 0;
-      const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kp + tb), 0, nrec,
-                                                        kBufferWord3);
-      const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vp + tb), 0, nrec,
-                                                        kBufferWord3);
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const int o = voff + r * RPL * D * (int)sizeof(T);
-        const u32x4_t kx = __builtin_amdgcn_raw_buffer_load_b128(rk, o, 0, 0);
-        const u32x4_t vx = __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, 0);
-        bf.k[r] = make_uint4(kx.x, kx.y, kx.z, kx.w);
-        bf.v[r] = make_uint4(vx.x, vx.y, vx.z, vx.w);
-      }
+      if (loads) load_pages(bf, id, kvh, real && nv > 0);
     };
 
     // nms[g] is the exponent offset -m[g] (0 while m[g] is -inf), kept
@@ -844,18 +921,20 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       }
     };
 
-    // The next block is issued before the current one is computed (an index
-    // past the end loads nothing and is never computed).
-    Buf<T, D> b0, b1;
-    issue(b0, 0);
+    // While block i is computed, block i + 1 is in flight (an index past the
+    // end loads nothing and is never computed). With a plan, blocks 0 and 1
+    // were requested at the start of the launch.
+    issue(b0, 0, !PLANNED);
+    if constexpr (PLANNED) issue(b1, 1, false);
     after_pre_issue();
+    if constexpr (!PLANNED) issue(b1, 1, true);
     for (int i = 0;;) {
-      issue(b1, i + 1);
       compute(b0);
       if (++i == nblk) break;
-      issue(b0, i + 1);
+      issue(b0, i + 1, true);
       compute(b1);
       if (++i == nblk) break;
+      issue(b1, i + 1, true);
     }
     finalize();
   }
@@ -932,9 +1011,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       // earlier groups wa .. w-1 with this one's, each record once all of its
       // words carry this launch's epoch. Group wa used slot 0 only if its
       // range starts exactly at the row start.
-      const long long wa = ((R + 1) * we - 1) / total;
+      const long long wa = group_of(R, total, we, p.W, p.w1);
       const int np = (int)(w - wa);
-      const bool wa_slot1 = range_lo(wa, total, we) != R;
+      const bool wa_slot1 = range_lo(wa, total, we, p.W, p.w1) != R;
       auto record = [&](int j) __attribute__((always_inline)) {
         const int slot = (j == 0 && wa_slot1) ? 1 : 0;
         return p.ws_rec + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
@@ -1039,30 +1118,56 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   end_epoch(ep);
 }
 
+template <typename T, int D, int G, int MODE>
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
+  constexpr bool PLANNED = MODE >= kModePlanned;
+  extern __shared__ int s_pref[];  // [B + 1]; fused step: then s_len[B]
+  __shared__ DecodeLds<T, D, G, MODE != kModePlain> lds;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  // Requested first of all: with a plan, the wave's first descriptors; its
+  // launch counter (the epoch tags its records and is expected on those it
+  // merges); seq_lens[tid] (0 past the batch) for the block prefix's first
+  // chunk and the fused step's first pass over the lengths -- a raw buffer
+  // load over the B lengths, so no exec-masked branch and no copy at a join
+  // that would wait for it early. The lengths arrive with the descriptors,
+  // so the prefix never waits behind the first blocks.
+  int4 plan_d = make_int4(0, 0, -1, 0);
+  if constexpr (PLANNED) plan_d = p.plan[((size_t)blockIdx.x * kWaves + wave) * 64 + lane];
+  const uint32_t ctr0 = __hip_atomic_load(p.ws_ctr + (size_t)blockIdx.x * kWaves + wave,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int len_t0 = (int)__builtin_amdgcn_raw_buffer_load_b32(
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(p.seq_lens), 0, p.B * 4, kBufferWord3),
+      tid * 4, 0, 0);
+  (void)lane;
+  decode_body<T, D, G, MODE, MODE == kModePlannedStream ? kLoadNonTemporal : 0>(
+      p, lds, s_pref, plan_d, ctr0, len_t0);
+}
+
+
 // Launches one instantiation of the kernel on stream (defined here, instantiated
 // explicitly per element type and mode in the decode_inst_*.hip units so they
 // compile in parallel).
-template <typename T, int D, int G, bool FUSED>
+template <typename T, int D, int G, int MODE>
 int launch_decode_t(const DecodeParams& p, hipStream_t stream) {
   // Dynamic LDS: block prefix [B + 1], then (fused step) lengths [B].
-  const size_t lds = (size_t)(p.B + 1 + (FUSED ? p.B : 0)) * sizeof(int);
-  hipLaunchKernelGGL((decode_kernel<T, D, G, FUSED>), dim3(p.W), dim3(kThreads), lds, stream,
-                     p);
+  const size_t lds = (size_t)(p.B + 1 + (MODE != kModePlain ? p.B : 0)) * sizeof(int);
+  hipLaunchKernelGGL((decode_kernel<T, D, G, MODE>), dim3(p.W), dim3(kThreads), lds, stream, p);
   return launch_status("decode_kernel");
 }
 
-#define RLSE_DECODE_INST_G(PREFIX, T, D, FUSED)                              \
-  PREFIX int launch_decode_t<T, D, 1, FUSED>(const DecodeParams&, hipStream_t); \
-  PREFIX int launch_decode_t<T, D, 2, FUSED>(const DecodeParams&, hipStream_t); \
-  PREFIX int launch_decode_t<T, D, 3, FUSED>(const DecodeParams&, hipStream_t); \
-  PREFIX int launch_decode_t<T, D, 4, FUSED>(const DecodeParams&, hipStream_t); \
-  PREFIX int launch_decode_t<T, D, 5, FUSED>(const DecodeParams&, hipStream_t); \
-  PREFIX int launch_decode_t<T, D, 6, FUSED>(const DecodeParams&, hipStream_t); \
-  PREFIX int launch_decode_t<T, D, 7, FUSED>(const DecodeParams&, hipStream_t); \
-  PREFIX int launch_decode_t<T, D, 8, FUSED>(const DecodeParams&, hipStream_t);
+#define RLSE_DECODE_INST_G(PREFIX, T, D, MODE)                              \
+  PREFIX int launch_decode_t<T, D, 1, MODE>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 2, MODE>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 3, MODE>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 4, MODE>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 5, MODE>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 6, MODE>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 7, MODE>(const DecodeParams&, hipStream_t); \
+  PREFIX int launch_decode_t<T, D, 8, MODE>(const DecodeParams&, hipStream_t);
 // Every supported (head_dim, group size) of one element type and mode.
-#define RLSE_DECODE_INSTANCES(PREFIX, T, FUSED) \
-  RLSE_DECODE_INST_G(PREFIX, T, 64, FUSED)      \
-  RLSE_DECODE_INST_G(PREFIX, T, 128, FUSED)
+#define RLSE_DECODE_INSTANCES(PREFIX, T, MODE) \
+  RLSE_DECODE_INST_G(PREFIX, T, 64, MODE)      \
+  RLSE_DECODE_INST_G(PREFIX, T, 128, MODE)
 
 }  // namespace rlse

@@ -111,9 +111,14 @@ class DecodeModel:
     """
 
     def __init__(self, cfg: ModelConfig, weights: Dict[str, object], dtype: str,
-                 num_blocks: int, max_batch: int, max_blocks_per_seq: int, device="cuda:0"):
+                 num_blocks: int, max_batch: int, max_blocks_per_seq: int, device="cuda:0",
+                 stream_pages: bool = False):
         if dtype not in _TORCH:
             raise ValueError(f"dtype {dtype!r}")
+        # RLSE_DECODE_STREAM for every step: the caller guarantees that no
+        # page is read by two sequences (no forked prefixes), so attention
+        # reads its pages with non-temporal loads.
+        self.stream_pages = stream_pages
         kv.load()
         self.cfg, self.dtype, self.device = cfg, dtype, torch.device(device)
         self.max_batch, self.mbps, self.num_blocks = max_batch, max_blocks_per_seq, num_blocks
@@ -274,7 +279,8 @@ class DecodeModel:
                                    block_tables, seq_lens, self.attn, batch, cfg.heads,
                                    cfg.kv_heads, cfg.head_dim, self.mbps, self.num_blocks,
                                    self.scale, dt, self.plan, self.workspace,
-                                   self.workspace.numel(), stream)
+                                   self.workspace.numel(), stream,
+                                   stream_pages=self.stream_pages)
             nxt = self.layers[l + 1]["in_norm"] if l + 1 < cfg.layers else self.norm
             if self.fused:
                 kv.linear_residual(self.attn, L["o_w"], self.x, batch, H, nq, dt, self.dense_ws,

@@ -43,6 +43,7 @@ ERR_UNKNOWN_REQUEST = 10002
 ERR_BUFFER_TOO_SMALL = 10003
 ERR_TOKEN_LIMIT = 10004
 ERR_DEVICE_TIMEOUT = 10005
+DECODE_STREAM = 1
 WS_ERR_MERGE_TIMEOUT = 1
 WS_ERR_LENGTH = 2
 BLOCK_SIZE = 16
@@ -185,7 +186,7 @@ _SIGS = {
     "rlse_decode_step": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                               _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp]),
     "rlse_decode_step_planned": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp,
-                              _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _vp]),
+                              _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _i, _vp]),
     "rlse_prefill_workspace_size": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz)]),
     "rlse_prefill_attn": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp,
                                _sz, _vp]),
@@ -772,15 +773,18 @@ def decode_step_planned(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: floa
                         sin_table, max_pos: int, k_pool, v_pool, block_tables, seq_lens, out,
                         batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
                         max_blocks_per_seq: int, num_blocks: int, scale: float, dtype, plan,
-                        workspace=None, workspace_bytes: int = 0, stream=None) -> None:
+                        workspace=None, workspace_bytes: int = 0, stream=None,
+                        stream_pages: bool = False) -> None:
     """decode_step with a plan built by decode_plan from the same tables and
-    lengths; the results are the same bit for bit."""
+    lengths; the results are the same bit for bit. stream_pages
+    (RLSE_DECODE_STREAM): no page is read by more than one row of the batch,
+    so pages are read with non-temporal loads."""
     _check(load().rlse_decode_step_planned(
         _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(q_norm_weight), _ptr(k_norm_weight), eps,
         _ptr(cos_table), _ptr(sin_table), max_pos, _ptr(k_pool), _ptr(v_pool),
         _ptr(block_tables), _ptr(seq_lens), _ptr(out), batch, num_heads, num_kv_heads, head_dim,
         max_blocks_per_seq, num_blocks, scale, _dt(dtype), _ptr(workspace), workspace_bytes,
-        _ptr(plan), _stream(stream)))
+        _ptr(plan), DECODE_STREAM if stream_pages else 0, _stream(stream)))
 
 
 def prefill_workspace_size(num_tokens: int, ctx_len: int, num_heads: int, num_kv_heads: int,

@@ -487,8 +487,9 @@ def test_fused_decode_step_matches_two_kernel_path_and_oracle(kv, dtype, hq, hkv
     (2, 2, 64, [16384] * 72),                                   # > 64 blocks per wave
 ])
 def test_planned_step_equals_unplanned(kv, hq, hkv, d, lens):
-    """rlse_decode_step_planned with a plan from rlse_decode_plan gives the
-    outputs and pool contents of rlse_decode_step bit for bit, including rows
+    """rlse_decode_step_planned with a plan from rlse_decode_plan, with
+    cacheable or streamed (RLSE_DECODE_STREAM) pages, gives the outputs and
+    pool contents of rlse_decode_step bit for bit, including rows
     of length 0, idle workgroups and waves whose range spans several 64-block
     chunks."""
     dtype = "bf16"
@@ -516,20 +517,21 @@ def test_planned_step_equals_unplanned(kv, hq, hkv, d, lens):
     scale = 1.0 / math.sqrt(d)
     outs, pools = [], []
     plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=DEV)
-    for planned in (False, True, True):
+    # unplanned; planned with cacheable pages; planned streaming (twice)
+    for planned, stream_pages in ((False, False), (True, False), (True, True), (True, True)):
         kp_i, vp_i = kp.clone(), vp.clone()
         out = torch.full((b, hq, d), 3.0, dtype=bf, device=DEV)
         args = (q, kn, vn, qw, kw, 1e-6, c, s, max_pos, kp_i, vp_i, t_dev, l_dev, out, b, hq, hkv,
                 d, mbps, nb, scale, "bf16")
         if planned:
             kv.decode_plan(t_dev, l_dev, b, hkv, mbps, nb, plan, plan.numel())
-            kv.decode_step_planned(*args, plan)
+            kv.decode_step_planned(*args, plan, stream_pages=stream_pages)
         else:
             kv.decode_step(*args)
         torch.cuda.synchronize()
         outs.append(out)
         pools.append((kp_i, vp_i))
-    for i in (1, 2):
+    for i in (1, 2, 3):
         assert torch.equal(outs[0].view(torch.int16), outs[i].view(torch.int16)), i
         assert torch.equal(pools[0][0].view(torch.int16), pools[i][0].view(torch.int16)), i
         assert torch.equal(pools[0][1].view(torch.int16), pools[i][1].view(torch.int16)), i

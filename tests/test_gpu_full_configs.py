@@ -87,11 +87,13 @@ def test_qwen3_8b_long_context_decode_step_full_batch(kv):
         print(f"qwen3-8b decode: planned fused step, launch {rep}", flush=True)
         kv.decode_plan(t_dev, l_dev, b, hkv, mbps, nb, plan, plan.numel())
         kv.decode_step_planned(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp, vp, t_dev, l_dev,
-                               out, b, hq, hkv, d, mbps, nb, scale, "bf16", plan, ws, ws.numel())
+                               out, b, hq, hkv, d, mbps, nb, scale, "bf16", plan, ws, ws.numel(),
+                               stream_pages=rep == 1)
         torch.cuda.synchronize()
         assert kv.workspace_flags(ws) == 0
         outs.append(out)
-    # the second launch re-appends the same token bits at the same positions
+    # the second launch (streamed pages) re-appends the same token bits at the
+    # same positions and gives the first's output
     assert torch.equal(_bits(outs[0]), _bits(outs[1]))
 
     rows = [int(np.argmax(lens)), int(np.argmin(lens))]
@@ -201,6 +203,21 @@ def test_prefix_fork_decode_full_size(kv, prefix_len):
     torch.cuda.synchronize()
     assert torch.equal(_bits(outs[0]), _bits(outs[1]))
     assert kv.workspace_flags() == 0
+    # Planned steps over the same inputs (the appended token is rewritten with
+    # the same bits): the forked layout shares pages, so they stay cacheable;
+    # the private layout streams them (RLSE_DECODE_STREAM). Both give the
+    # unplanned output bit for bit.
+    plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=DEV)
+    for (k0, v0), tab, streams in (((ka, va), ta, False), ((kb, vb), tb, True)):
+        t_dev = to_dev(tab)
+        kv.decode_plan(t_dev, l_dev, b, hkv, mbps, nb, plan, plan.numel())
+        out = torch.empty((b, hq, d), dtype=BF, device=DEV)
+        print(f"fork full size: planned step, {'private' if streams else 'forked'}", flush=True)
+        kv.decode_step_planned(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, k0, v0, t_dev, l_dev,
+                               out, b, hq, hkv, d, mbps, nb, 1.0 / math.sqrt(d), "bf16", plan,
+                               stream_pages=streams)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(out), _bits(outs[0]))
     # every sequence, its appended token included, reads back identically
     for i in range(b):
         n = int(lens[i])
