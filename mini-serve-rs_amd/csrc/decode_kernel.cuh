@@ -730,16 +730,20 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       if (loads) load_pages(bf, id, kvh, real && nv > 0);
     };
 
-    // nms[g] is the exponent offset -m[g] (0 while m[g] is -inf), kept
-    // beside m[g] as it changes only when the running max moves.
-    float m[G], l[G], acc[G][EPL], nms[G];
+    // nms[g] is the exponent offset -m[g] (0 while m[g] is -inf) and thr[g]
+    // the raw score above which the running max must move, (m[g] +
+    // kLazyLog2) / c (-inf while m[g] is -inf); both are kept beside m[g],
+    // as they change only when the running max moves.
+    float m[G], l[G], acc[G][EPL], nms[G], thr[G];
     uint4 qv[G];
     int cur_row = -1;
+    const float inv_c = 1.f / p.c;
     auto reset = [&]() __attribute__((always_inline)) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
         nms[g] = 0.f;
+        thr[g] = -INFINITY;
         l[g] = 0.f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
@@ -875,24 +879,35 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
 #pragma unroll
         for (int r = 0; r < NR; ++r) Packet<T>::unpack(vr[r], vf[r]);
       }
+      // Lazy rescaling: a running max moves only when a scaled score exceeds
+      // it by more than kLazyLog2 (probabilities then stay below
+      // 2^kLazyLog2). The test compares raw scores with thr (c > 0), every
+      // head at once; when any lane of the wave needs it, every head's max
+      // moves to its largest score so far.
+      float cand[G];
+      bool move = false;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        // The largest scaled score (c > 0, so this is the largest score
-        // times c; products need no NaN canonicalisation before the max).
-        float cand = s[g][0] * p.c;
+        cand[g] = s[g][0];
 #pragma unroll
-        for (int r = 1; r < NR; ++r) cand = fmaxf(cand, s[g][r] * p.c);
-        // Lazy rescaling: the running max moves only when a score exceeds it
-        // by more than kLazyLog2 (probabilities then stay below 2^kLazyLog2).
-        if (__any(cand > m[g] + kLazyLog2)) {
-          const float mn = fmaxf(m[g], cand);
+        for (int r = 1; r < NR; ++r) cand[g] = fmaxf(cand[g], s[g][r]);
+        move = move || cand[g] > thr[g];
+      }
+      if (__any(move)) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float mn = fmaxf(m[g], cand[g] * p.c);
           const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m[g] - mn);
           l[g] *= alpha;
 #pragma unroll
           for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
           m[g] = mn;
           nms[g] = (mn == -INFINITY) ? 0.f : -mn;
+          thr[g] = (mn == -INFINITY) ? -INFINITY : (mn + kLazyLog2) * inv_c;
         }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
         float pr[NR];
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
