@@ -378,7 +378,8 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   constexpr int NPART = 2 * kWaves;
   constexpr int DPL = (D + 63) / 64;  // output dims per lane in the row epilogue
   constexpr int QR = q_stage_rows<T, D, G>();
-  constexpr int MC = 16 / G > 2 ? 16 / G : 2;  // partial records loaded per batch in a merge
+  // Partial records loaded per batch in a merge: G*DPL + 1 words per lane each.
+  constexpr int MC = 64 / (G * DPL + 1) > 8 ? 8 : (64 / (G * DPL + 1) < 2 ? 2 : 64 / (G * DPL + 1));
   // Two register buffers per wave: one block loading while one is computed.
   // With 2 * kWaves waves per compute unit that is enough bytes in flight to
   // keep HBM streaming; deeper buffering only lengthens the memory queues,
@@ -955,23 +956,26 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   }
   __syncthreads();
 
-  // Rows this group holds in pieces. The wave holding the group's last piece
-  // of a row finishes it: it combines the pieces parked by earlier waves
-  // (waves own consecutive ranges, so a row's pieces sit in consecutive
-  // waves), then writes the output (row inside the group's range), publishes
-  // one group partial (the row continues in a later group) or, in the group
-  // holding the row's last block, merges the partials of the earlier groups
-  // as they arrive. Waves handle their rows independently. A wave's later
-  // piece (slot 1) is handled first: if it is a row continuing into the next
-  // group its publication must not wait behind a merge of the wave's first
-  // piece, or merges would chain from group to group.
+  // Rows this group holds in pieces. A row that started in an earlier group
+  // and ends in this one is finished by wave 0, which merges the partials of
+  // the earlier groups as they arrive; every other row is finished by the
+  // wave holding its last piece in the group, which writes the output (row
+  // inside the group's range) or publishes one group partial (the row
+  // continues in a later group: always the group's last wave). The finishing
+  // wave first combines the pieces parked by the group's waves (a row's
+  // pieces sit in consecutive waves), from the last piece down. No wave both
+  // publishes and merges: a wave's waits count its own stores too, so a
+  // merge in the publishing wave would stand behind the publication's write
+  // round trip, and a publication behind a merge would chain merges from
+  // group to group.
   for (int s = 1; s >= 0; --s) {
     const int row = s_part_row[2 * wave + s];
     if (row < 0) continue;
     long long R;
     int nb;
     row_extent(row, R, nb);
-    if (R + nb > whi && whi < ghi) continue;  // a later wave holds more of the row
+    const bool merge = R < glo && R + nb <= ghi;  // only ever wave 0's slot 0 in wave 0
+    if (merge ? wave != 0 : (R + nb > whi && whi < ghi)) continue;
     const int b = row / Hkv, kvh = row - b * Hkv;
     float M[G][DPL], Ls[G][DPL], A[G][DPL];
 #pragma unroll
@@ -982,7 +986,8 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         Ls[g][k] = 0.f;
         A[g][k] = 0.f;
       }
-    for (int wv = wave; wv >= 0; --wv) {
+    bool seen = false;
+    for (int wv = merge ? kWaves - 1 : wave; wv >= 0; --wv) {
       bool any = false;
       for (int s2 = 1; s2 >= 0; --s2) {
         const int slot = 2 * wv + s2;
@@ -998,7 +1003,10 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
                           s_part[slot][g][d]);
           }
       }
-      if (!any) break;
+      if (any)
+        seen = true;
+      else if (seen)
+        break;
     }
     if (R + nb > ghi) {
       // The row continues in a later group: publish this group's piece
@@ -1011,13 +1019,15 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
           const int d = lane + 64 * k;
           if (d < D) st_tagged(rec + (size_t)g * D + d, ep, A[g][k]);
         }
-      if (lane == 0) {
+      // m and l of every head (the same in every lane): lane j < 2G stores
+      // word G*D + j, m[j] then l[j - G].
+      float ml = 0.f;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          st_tagged(rec + G * D + g, ep, M[g][0]);
-          st_tagged(rec + G * D + G + g, ep, Ls[g][0]);  // l of head G-1 last
-        }
+      for (int g = 0; g < G; ++g) {
+        ml = lane == g ? M[g][0] : ml;
+        ml = lane == G + g ? Ls[g][0] : ml;
       }
+      if (lane < 2 * G) st_tagged(rec + G * D + lane, ep, ml);
       continue;
     }
     bool ok = true;
@@ -1037,82 +1047,65 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       auto timed_out = [&]() __attribute__((always_inline)) {
         return wall_clock64() - t0 > p.wait_ticks;
       };
+      // Records are loaded MC at a time, each as G*DPL words of acc per lane
+      // plus one word of m/l per lane j < 2G, and loaded again (after a
+      // short sleep) until every word carries this launch's epoch.
       for (int c = 0; c < np && ok; c += MC) {
-        uint64_t mv[MC][G], lv[MC][G], av[MC][G][DPL];
-        // With at most two records pending, polling the records themselves
-        // costs little and sees them one round trip sooner.
-        const bool poll_full = np - c <= 2;
+        uint64_t mt[MC], av[MC][G][DPL];
         for (int attempt = 0;; ++attempt) {
-          if (attempt > 0 && poll_full) {
+          if (attempt > 0) {
             if (timed_out()) {
               ok = false;
               break;
             }
             __builtin_amdgcn_s_sleep(2);
-          } else if (attempt > 0) {
-            // Not all there yet: wait on one word per record, l of the last
-            // head (stored last), with one broadcast load each, before loading
-            // the records again (stores to different words may land out of
-            // order, so every word is checked after each load).
-            for (;;) {
-              if (timed_out()) {
-                ok = false;
-                break;
-              }
-              __builtin_amdgcn_s_sleep(2);
-              bool seen = true;
-#pragma unroll
-              for (int i = 0; i < MC; ++i)
-                if (c + i < np) seen = seen && tag_is(ld_tagged(record(c + i) + G * D + 2 * G - 1), ep);
-              if (__all(seen)) break;
-            }
-            if (!ok) break;
           }
-          bool ready = true;
+          const uint64_t fill = (uint64_t)ep << 32;  // words not loaded count as arrived
 #pragma unroll
-          for (int i = 0; i < MC; ++i) {  // issue the chunk's loads together
-            const uint64_t fill = (uint64_t)ep << 32;  // slots past the end count as arrived
+          for (int i = 0; i < MC; ++i) {  // issue the batch's loads together
             if (c + i >= np) {
+              mt[i] = fill;
 #pragma unroll
-              for (int g = 0; g < G; ++g) {
-                mv[i][g] = lv[i][g] = fill;
+              for (int g = 0; g < G; ++g)
 #pragma unroll
                 for (int k = 0; k < DPL; ++k) av[i][g][k] = fill;
-              }
               continue;
             }
             const uint64_t* r = record(c + i);
+            mt[i] = lane < 2 * G ? ld_tagged(r + G * D + lane) : fill;
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-              mv[i][g] = ld_tagged(r + G * D + g);
-              lv[i][g] = ld_tagged(r + G * D + G + g);
+            for (int g = 0; g < G; ++g)
 #pragma unroll
               for (int k = 0; k < DPL; ++k) {
                 const int d = lane + 64 * k;
                 av[i][g][k] = d < D ? ld_tagged(r + (size_t)g * D + d) : fill;
               }
-            }
           }
+          bool ready = true;
 #pragma unroll
-          for (int i = 0; i < MC; ++i)
+          for (int i = 0; i < MC; ++i) {
+            ready = ready && tag_is(mt[i], ep);
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-              ready = ready && tag_is(mv[i][g], ep) && tag_is(lv[i][g], ep);
+            for (int g = 0; g < G; ++g)
 #pragma unroll
               for (int k = 0; k < DPL; ++k) ready = ready && tag_is(av[i][g][k], ep);
-            }
+          }
           if (__all(ready)) break;
         }
         if (!ok) break;
 #pragma unroll
         for (int i = 0; i < MC; ++i)
-          if (c + i < np)
+          if (c + i < np) {
+            const int mlw = (int)(uint32_t)mt[i];
 #pragma unroll
-            for (int g = 0; g < G; ++g)
+            for (int g = 0; g < G; ++g) {
+              const float mo = __int_as_float(__builtin_amdgcn_readlane(mlw, g));
+              const float lo_ = __int_as_float(__builtin_amdgcn_readlane(mlw, G + g));
 #pragma unroll
               for (int k = 0; k < DPL; ++k)
-                lse_combine(M[g][k], Ls[g][k], A[g][k], tag_value(mv[i][g]),
-                            tag_value(lv[i][g]), tag_value(av[i][g][k]));
+                lse_combine(M[g][k], Ls[g][k], A[g][k], mo, lo_, tag_value(av[i][g][k]));
+            }
+          }
       }
       if (!ok && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_MERGE_TIMEOUT);
     }
