@@ -380,10 +380,15 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   constexpr int QR = q_stage_rows<T, D, G>();
   // Partial records loaded per batch in a merge: G*DPL + 1 words per lane each.
   constexpr int MC = 64 / (G * DPL + 1) > 8 ? 8 : (64 / (G * DPL + 1) < 2 ? 2 : 64 / (G * DPL + 1));
-  // Two register buffers per wave: one block loading while one is computed.
-  // With 2 * kWaves waves per compute unit that is enough bytes in flight to
-  // keep HBM streaming; deeper buffering only lengthens the memory queues,
-  // which the publication chain at the end of the launch then waits behind.
+  // Register buffers per wave: while one block is computed, NBUF - 1 are in
+  // flight. 16-bit K/V at head_dim 128 with up to 4 heads per group take
+  // three (the third, 32 VGPRs, still leaves two waves per SIMD): the bytes
+  // in flight then also cover the stretches in which the compute unit's other
+  // workgroup is not streaming (its late start, the end of the launch). At
+  // head_dim 64 a third buffer measured slower (G = 7: the wave is VALU-bound
+  // and the longer register live ranges cost more than the extra block in
+  // flight), and 32-bit K/V and wider groups lack the registers.
+  constexpr int NBUF = (sizeof(T) == 2 && D == 128 && G <= 4) ? 3 : 2;
   constexpr int kPreIssued = 2;  // blocks issued before the prologue's appends
   constexpr int kNewCap = new_row_cap<T>();
   static_assert(kNewCap >= kPreIssued, "pre-issued blocks must find their new rows in LDS");
@@ -431,7 +436,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       bf.v[r] = make_uint4(vx.x, vx.y, vx.z, vx.w);
     }
   };
-  Buf<T, D> b0, b1;
+  Buf<T, D> b0, b1, b2;
   // With a plan the wave's first kPreIssued blocks are requested as soon as
   // its descriptors arrive: HBM starts streaming one round trip into the
   // launch, while the prefix, the query staging and the appends run.
@@ -937,20 +942,26 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       }
     };
 
-    // While block i is computed, block i + 1 is in flight (an index past the
-    // end loads nothing and is never computed). With a plan, blocks 0 and 1
-    // were requested at the start of the launch.
+    // While block i is computed, blocks i + 1 .. i + NBUF - 1 are in flight
+    // (an index past the end loads nothing and is never computed). With a
+    // plan, blocks 0 and 1 were requested at the start of the launch.
     issue(b0, 0, !PLANNED);
     if constexpr (PLANNED) issue(b1, 1, false);
     after_pre_issue();
     if constexpr (!PLANNED) issue(b1, 1, true);
+    if constexpr (NBUF == 3) issue(b2, 2, true);
     for (int i = 0;;) {
       compute(b0);
       if (++i == nblk) break;
-      issue(b0, i + 1, true);
+      issue(b0, i + NBUF - 1, true);
       compute(b1);
       if (++i == nblk) break;
-      issue(b1, i + 1, true);
+      issue(b1, i + NBUF - 1, true);
+      if constexpr (NBUF == 3) {
+        compute(b2);
+        if (++i == nblk) break;
+        issue(b2, i + 2, true);
+      }
     }
     finalize();
   }
