@@ -199,7 +199,8 @@ int rlse_decode_step(const void* q, const void* k_new, const void* v_new,
 
 /* Per-step plan for rlse_decode_step_planned: the first block descriptors
  * of every wave of a decode launch (page id, valid rows, row, new-token
- * position), computed once from the step's block tables and lengths instead
+ * position) and the new-token positions of the rows its first query stage
+ * covers, computed once from the step's block tables and lengths instead
  * of by every layer's launch. No counterpart in the reference: its decode
  * runs per sequence on contiguous buffers, with no page tables to walk.
  * plan: rlse_decode_plan_size bytes, 16-byte aligned. */
@@ -210,8 +211,8 @@ int rlse_decode_plan(const int32_t* block_tables, const int32_t* seq_lens, int b
 /* rlse_decode_step with a plan that rlse_decode_plan built from the same
  * block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq and
  * num_blocks (every layer of a decode step shares them): each wave's page
- * ids then arrive with its first load, and its first pages are requested
- * right after. Results are identical to rlse_decode_step's.
+ * ids then arrive with its first load, its query and append loads go out
+ * next and its first pages right after. Results are identical to rlse_decode_step's.
  * flags: RLSE_DECODE_STREAM when no page of the batch is read by more than
  * one row (no sequence shares pages with another -- the caller's block
  * manager knows: no page with a refcount above 1): the pages are then read

@@ -24,9 +24,11 @@ RLSE_DECODE_INSTANCES(extern template, f16, kModePlannedStream)
 
 // Per-step plan: for every wave of every workgroup of a decode launch, the
 // descriptors of its first 64 blocks -- exactly what the wave would compute
-// with the same lengths and tables (same prefix, ranges and block_desc).
-// One launch serves every layer of a step: the tables and lengths are the
-// same in each.
+// with the same lengths and tables (same prefix, ranges and block_desc) --
+// followed, in a second array, by the new-token positions of the 64 rows
+// from the wave's first row on (0 past the last row or for a wave without
+// blocks), which rope its first query stage. One launch serves every layer
+// of a step: the tables and lengths are the same in each.
 __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __restrict__ tables,
                                                                const int* __restrict__ seq_lens,
                                                                int B, int Hkv, int mbps,
@@ -50,7 +52,15 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __rest
       d = block_desc(wlo + lane, whi, s_pref, tables, seq_lens, B, Hkv, mbps, num_blocks);
     }
   }
-  plan[((size_t)w * kWaves + wave) * 64 + lane] = d;
+  const size_t at = ((size_t)w * kWaves + wave) * 64 + lane;
+  plan[at] = d;
+  const int row0 = __shfl(d.z, 0, 64);
+  int pos = 0;
+  if (row0 >= 0 && row0 + lane < B * Hkv) {
+    const int L = valid_len(seq_lens[(row0 + lane) / Hkv], mbps);
+    pos = L > 0 ? L - 1 : 0;
+  }
+  reinterpret_cast<int*>(plan + (size_t)gridDim.x * kWaves * 64)[at] = pos;
 }
 
 static int decode_groups(int* W) {
@@ -243,7 +253,7 @@ extern "C" int rlse_decode_plan_size(size_t* bytes) {
   int W = 0;
   const int st = decode_groups(&W);
   if (st) return st;
-  *bytes = (size_t)W * kWaves * 64 * sizeof(int4);
+  *bytes = (size_t)W * kWaves * 64 * (sizeof(int4) + sizeof(int));
   return RLSE_OK;
 }
 

@@ -368,8 +368,8 @@ struct DecodeLds {
 template <typename T, int D, int G, int MODE, int POL>
 __device__ __forceinline__ void decode_body(const DecodeParams& p,
                                             DecodeLds<T, D, G, MODE != kModePlain>& lds,
-                                            int* s_pref, int4 plan_d, uint32_t ctr0,
-                                            int len_t0) {
+                                            int* s_pref, int4 plan_d, int plan_pos,
+                                            uint32_t ctr0, int len_t0) {
   constexpr bool FUSED = MODE != kModePlain;
   constexpr bool PLANNED = MODE >= kModePlanned;
   using S = DecodeShape<T, D>;
@@ -444,7 +444,108 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   auto end_epoch = [&](uint32_t ep) __attribute__((always_inline)) {
     if (lane == 0) __hip_atomic_store(ctr, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
+  const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
+  // Descriptors of 64 consecutive blocks, one per lane: page id, valid
+  // rows and row, read back with readlane when the block is issued.
+  // d_nv holds the valid rows in bits 0-7 and "last block of its row" in
+  // bit 8; d_pos is the row's new-token position (fused step).
+  int d_id = 0, d_nv = 0, d_row = -1, d_pos = 0, cbase = 0;
+  // RoPE cos/sin packets of position pos for lane column col: rotate_half
+  // pairs element i with i + D/2, so both halves use table columns
+  // (col % (LPR/2)) * EPL onwards.
+  auto rope_packets = [&](int pos, uint4& cs, uint4& sn) __attribute__((always_inline)) {
+    const size_t to = (size_t)pos * (D / 2) + (size_t)(col % (LPR / 2)) * EPL;
+    cs = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.cos_t) + to);
+    sn = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.sin_t) + to);
+  };
+  // RMSNorm weight packet of lane column col (zeros when w is null), read
+  // where it is used (an L1 hit) rather than held across the streaming loop.
+  // RMSNorm weight packet of lane column col, read where it is used (an L1
+  // hit) rather than held across the streaming loop. A null weight (no
+  // norm) reads q instead, which norm_rope_packet then ignores.
+  auto load_weight = [&](const void* w) __attribute__((always_inline)) {
+    const T* wp = reinterpret_cast<const T*>(w ? w : p.q);
+    return *reinterpret_cast<const uint4*>(wp + col * EPL);
+  };
+  // Query packets of QR consecutive rows from q_base on, staged in this
+  // wave's LDS slice (fused step: q_norm + RoPE at the row's new position).
+  // Staging is split into loads and then math + LDS stores, so the first
+  // stage's loads are in flight together with the first blocks' loads.
+  constexpr int QITEMS = QR * G;
+  constexpr int QPASSES = (QITEMS + RPL - 1) / RPL;
+  int q_base = 0, q_top = 0;  // staged rows [q_base, q_top)
+  uint4 sq_q[QPASSES], sq_c[QPASSES], sq_s[QPASSES], sq_w;
+  // Every staging load is unconditional, with its indices clamped into
+  // range (items past the end re-read a valid row and are never used): a
+  // load under a branch with a zero default would make the compiler copy
+  // its result at the join and wait for it right after issue.
+  // Issues the query staging loads of QR rows from row0 on (items past the
+  // last row re-read a clamped row and are never stored). The fused step
+  // ropes each query at its row's new position: from the plan (lane t holds
+  // row row0 + t's) when it is loaded before the barrier, else from s_len.
+  auto stage_q_load = [&](int row0) __attribute__((always_inline)) {
+    const int nrows = B * Hkv;
+    q_base = row0;
+    if constexpr (FUSED) sq_w = load_weight(p.qw);
+#pragma unroll
+    for (int ps = 0; ps < QPASSES; ++ps) {
+      const int item = ps * RPL + rsub;
+      const int t = item / G, g = item - t * G;
+      const int r = row0 + t < nrows ? row0 + t : nrows - 1;
+      const int b = r / Hkv, kvh = r - b * Hkv;
+      sq_q[ps] = *reinterpret_cast<const uint4*>(
+          qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
+      if constexpr (FUSED) {
+        const int pos = PLANNED ? __shfl(plan_pos, t, 64) : s_len[b] - 1;
+        rope_packets(pos > 0 ? pos : 0, sq_c[ps], sq_s[ps]);
+      }
+    }
+  };
+  uint64_t amask = 0;
+  int a_src = -1, a_slot = -1;
+  int a_ord = 0;  // appends started so far (wave-uniform)
+  uint4 a_k, a_v, a_c, a_s, a_w;  // one pass's loads (append_load)
+  auto append_load = [&]() __attribute__((always_inline)) {
+    int src = -1, ord = -1;
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) {
+      if (amask) {
+        const int k = __builtin_ctzll(amask);
+        amask &= amask - 1;
+        if (rsub == i) {
+          src = k;
+          ord = a_ord;
+        }
+        ++a_ord;
+      }
+    }
+    a_src = src;
+    a_slot = ord;
+    // Lane groups without a row load lane 0's (a valid block of the chunk)
+    // and store nothing.
+    const int sl = src >= 0 ? src : 0;
+    const int rw = __shfl(d_row, sl, 64), pos = __shfl(d_pos, sl, 64);
+    const int row = rw > 0 ? rw : 0;  // a wave without blocks loads row 0
+    a_w = load_weight(p.kw);
+    const size_t no = (size_t)row * D + (size_t)col * EPL;
+    a_k = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.k_new) + no);
+    a_v = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.v_new) + no);
+    rope_packets(pos, a_c, a_s);
+  };
   if constexpr (PLANNED) {
+    // The plan gives the first row and the appends of the first 64 blocks:
+    // their query and append loads go out ahead of the first blocks', so the
+    // prologue's math waits for them alone and not behind the launch's first
+    // wave of block loads (loads complete in order).
+    d_id = plan_d.x;
+    d_nv = plan_d.y;
+    d_row = plan_d.z;
+    d_pos = plan_d.w;
+    const int row0 = __builtin_amdgcn_readfirstlane(plan_d.z);
+    stage_q_load(row0 > 0 ? row0 : 0);
+    amask = __ballot((d_nv & 256) != 0);
+    append_load();
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < kPreIssued; ++k) {
       const int nv = __builtin_amdgcn_readlane(plan_d.y, k) & 255;
@@ -495,13 +596,10 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   };
 
   if (nblk > 0) {
-    const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
-
     // Descriptors of 64 consecutive blocks, one per lane: page id, valid
     // rows and row, read back with readlane when the block is issued.
     // d_nv holds the valid rows in bits 0-7 and "last block of its row" in
     // bit 8; d_pos is the row's new-token position (fused step).
-    int d_id = 0, d_nv = 0, d_row = -1, d_pos = 0, cbase = 0;
     auto load_chunk = [&](int base) __attribute__((always_inline)) {
       cbase = base;
       int4 d;
@@ -517,35 +615,6 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     };
     load_chunk(0);
 
-    // RoPE cos/sin packets of position pos for lane column col: rotate_half
-    // pairs element i with i + D/2, so both halves use table columns
-    // (col % (LPR/2)) * EPL onwards.
-    auto rope_packets = [&](int pos, uint4& cs, uint4& sn) __attribute__((always_inline)) {
-      const size_t to = (size_t)pos * (D / 2) + (size_t)(col % (LPR / 2)) * EPL;
-      cs = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.cos_t) + to);
-      sn = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.sin_t) + to);
-    };
-    // RMSNorm weight packet of lane column col (zeros when w is null), read
-    // where it is used (an L1 hit) rather than held across the streaming loop.
-    // RMSNorm weight packet of lane column col, read where it is used (an L1
-    // hit) rather than held across the streaming loop. A null weight (no
-    // norm) reads q instead, which norm_rope_packet then ignores.
-    auto load_weight = [&](const void* w) __attribute__((always_inline)) {
-      const T* wp = reinterpret_cast<const T*>(w ? w : p.q);
-      return *reinterpret_cast<const uint4*>(wp + col * EPL);
-    };
-    // Query packets of QR consecutive rows from q_base on, staged in this
-    // wave's LDS slice (fused step: q_norm + RoPE at the row's new position).
-    // Staging is split into loads and then math + LDS stores, so the first
-    // stage's loads are in flight together with the first blocks' loads.
-    constexpr int QITEMS = QR * G;
-    constexpr int QPASSES = (QITEMS + RPL - 1) / RPL;
-    int q_base = 0, q_top = 0;  // staged rows [q_base, q_top)
-    uint4 sq_q[QPASSES], sq_c[QPASSES], sq_s[QPASSES], sq_w;
-    // Every staging load is unconditional, with its indices clamped into
-    // range (items past the end re-read a valid row and are never used): a
-    // load under a branch with a zero default would make the compiler copy
-    // its result at the join and wait for it right after issue.
     // The wave's last row; staging never goes past it.
     int last_row;
     {
@@ -559,24 +628,6 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       q_base = row0;
       q_top = row0 + QR < last_row + 1 ? row0 + QR : last_row + 1;
       q_items = (q_top - q_base) * G;
-    };
-    auto stage_q_load = [&](int row0) __attribute__((always_inline)) {
-      const int nrows = B * Hkv;
-      stage_bounds(row0);
-      if constexpr (FUSED) sq_w = load_weight(p.qw);
-#pragma unroll
-      for (int ps = 0; ps < QPASSES; ++ps) {
-        const int item = ps * RPL + rsub;
-        const int t = item / G, g = item - t * G;
-        const int r = row0 + t < nrows ? row0 + t : nrows - 1;
-        const int b = r / Hkv, kvh = r - b * Hkv;
-        sq_q[ps] = *reinterpret_cast<const uint4*>(
-            qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
-        if constexpr (FUSED) {
-          const int pos = s_len[b] - 1;
-          rope_packets(pos > 0 ? pos : 0, sq_c[ps], sq_s[ps]);
-        }
-      }
     };
     // In-loop restaging (a wave whose range holds more than QR rows): one
     // pass at a time in a rolled loop, which keeps the streaming loop's code
@@ -629,36 +680,6 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     // them to its loads -- and only blocks issued after that wait can hold an
     // append past the first kNewCap. A pass appends up to RPL rows, one per
     // lane group.
-    uint64_t amask = 0;
-    int a_src = -1, a_slot = -1;
-    int a_ord = 0;  // appends started so far (wave-uniform)
-    uint4 a_k, a_v, a_c, a_s, a_w;  // one pass's loads (append_load)
-    auto append_load = [&]() __attribute__((always_inline)) {
-      int src = -1, ord = -1;
-#pragma unroll
-      for (int i = 0; i < RPL; ++i) {
-        if (amask) {
-          const int k = __builtin_ctzll(amask);
-          amask &= amask - 1;
-          if (rsub == i) {
-            src = k;
-            ord = a_ord;
-          }
-          ++a_ord;
-        }
-      }
-      a_src = src;
-      a_slot = ord;
-      // Lane groups without a row load lane 0's (a valid block of the chunk)
-      // and store nothing.
-      const int sl = src >= 0 ? src : 0;
-      const int row = __shfl(d_row, sl, 64), pos = __shfl(d_pos, sl, 64);
-      a_w = load_weight(p.kw);
-      const size_t no = (size_t)row * D + (size_t)col * EPL;
-      a_k = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.k_new) + no);
-      a_v = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.v_new) + no);
-      rope_packets(pos, a_c, a_s);
-    };
     auto append_store = [&]() __attribute__((always_inline)) {
       const int sl = a_src >= 0 ? a_src : 0;
       const int row = __shfl(d_row, sl, 64), pos = __shfl(d_pos, sl, 64);
@@ -677,13 +698,16 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       }
     };
 
-    // Before the first blocks are issued: the first row's query loads and
-    // the first append pass's loads.
-    stage_q_load(__builtin_amdgcn_readfirstlane(d_row));
-    if constexpr (FUSED) {
-      amask = __ballot((d_nv & 256) != 0);
-      append_load();
+    // Before the first blocks are issued (planned launches: at the start):
+    // the first row's query loads and the first append pass's loads.
+    if constexpr (!PLANNED) {
+      stage_q_load(__builtin_amdgcn_readfirstlane(d_row));
+      if constexpr (FUSED) {
+        amask = __ballot((d_nv & 256) != 0);
+        append_load();
+      }
     }
+    stage_bounds(q_base);
     // Keep these loads ahead of the block loads: the math after the first
     // issues waits for them, and a wait for a load issued after the blocks
     // would wait for the blocks too (loads complete in order).
@@ -1152,7 +1176,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   // that would wait for it early. The lengths arrive with the descriptors,
   // so the prefix never waits behind the first blocks.
   int4 plan_d = make_int4(0, 0, -1, 0);
-  if constexpr (PLANNED) plan_d = p.plan[((size_t)blockIdx.x * kWaves + wave) * 64 + lane];
+  int plan_pos = 0;
+  if constexpr (PLANNED) {
+    const size_t at = ((size_t)blockIdx.x * kWaves + wave) * 64 + lane;
+    plan_d = p.plan[at];
+    plan_pos = reinterpret_cast<const int*>(p.plan + (size_t)p.W * kWaves * 64)[at];
+  }
   const uint32_t ctr0 = __hip_atomic_load(p.ws_ctr + (size_t)blockIdx.x * kWaves + wave,
                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int len_t0 = (int)__builtin_amdgcn_raw_buffer_load_b32(
@@ -1160,7 +1189,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       tid * 4, 0, 0);
   (void)lane;
   decode_body<T, D, G, MODE, MODE == kModePlannedStream ? kLoadNonTemporal : 0>(
-      p, lds, s_pref, plan_d, ctr0, len_t0);
+      p, lds, s_pref, plan_d, plan_pos, ctr0, len_t0);
 }
 
 
