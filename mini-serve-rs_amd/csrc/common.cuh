@@ -346,6 +346,13 @@ constexpr int kBufferWord3 = 0x00020000;
 // non-temporal bit (bit 1), so the lines do not displace reused data in L2.
 constexpr int kLoadNonTemporal = 2;
 
+// Marks a loaded packet as used here (an empty asm reading its registers):
+// the compiler waits for its load at this point, in straight-line code where
+// it can count the loads issued since, instead of later inside a loop.
+__device__ __forceinline__ void consume(const uint4& x) {
+  asm volatile("" ::"v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w));
+}
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima), fenced
 // against compiler reordering on both sides.
 __device__ __forceinline__ void wait_vm_stores() {

@@ -127,19 +127,16 @@ __device__ __forceinline__ long long range_lo(long long w, long long total, long
   return total * share_cum(w, we, W, w1) / share_cum(we, we, W, w1);
 }
 // The workgroup whose range holds block f: the largest w with
-// range_lo(w) <= f.
+// range_lo(w) <= f, i.e. with total * share_cum(w) < (f + 1) * S (S the
+// whole stream's share): the largest w whose share_cum is at most
+// c = ((f + 1) * S - 1) / total. One division, on the merge's critical path.
 __device__ __forceinline__ long long group_of(long long f, long long total, long long we, int W,
                                               int w1) {
-  if (we < W || w1 == 16) return ((f + 1) * we - 1) / total;
-  long long lo = 0, hi = we - 1;
-  while (lo < hi) {
-    const long long mid = (lo + hi + 1) >> 1;
-    if (range_lo(mid, total, we, W, w1) <= f)
-      lo = mid;
-    else
-      hi = mid - 1;
-  }
-  return lo;
+  const long long S = share_cum(we, we, W, w1);
+  const long long c = ((f + 1) * S - 1) / total;
+  if (we < W || w1 == 16) return c / 16;
+  const long long h16 = (long long)(W / 2) * 16;
+  return c <= h16 ? c / 16 : W / 2 + (c - h16) / w1;
 }
 
 // Largest b in [0, B) with Hkv*s_pref[b] <= g (that sequence is non-empty).
@@ -644,10 +641,13 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         const int b = r / Hkv, kvh = r - b * Hkv;
         uint4 x = *reinterpret_cast<const uint4*>(
             qb + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL);
+        consume(x);  // every load used on every path (see after_pre_issue)
         if constexpr (FUSED) {
           const int pos = s_len[b] - 1;
           uint4 cs, sn;
           rope_packets(pos > 0 ? pos : 0, cs, sn);
+          consume(cs);
+          consume(sn);
           x = norm_rope_packet<T, D>(x, p.qw != nullptr, w, p.inv_d, p.eps, cs, sn, col);
         }
         if (item < q_items) s_q[wave][t][g][col] = x;
@@ -716,8 +716,27 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     // and every append.
     auto after_pre_issue = [&]() __attribute__((always_inline)) {
       stage_q_store();
+      if constexpr (FUSED) append_store();
+      // Every prologue load is consumed here, in straight-line code: a
+      // staging pass past the staged items, or an append pass with nothing to
+      // store, would otherwise leave its load pending into the streaming loop,
+      // where the compiler cannot count the loads issued since and drains
+      // every block in flight (vmcnt(0)) before it first reuses the register.
+#pragma unroll
+      for (int ps = 0; ps < QPASSES; ++ps) {
+        consume(sq_q[ps]);
+        if constexpr (FUSED) {
+          consume(sq_c[ps]);
+          consume(sq_s[ps]);
+        }
+      }
       if constexpr (FUSED) {
-        append_store();
+        consume(sq_w);
+        consume(a_k);
+        consume(a_v);
+        consume(a_c);
+        consume(a_s);
+        consume(a_w);
         for (int base = 0; base < nblk; base += 64) {
           if (base) {
             load_chunk(base);
