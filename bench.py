@@ -149,6 +149,14 @@ def measured_traffic(workload, fused):
     return rec["traffic_bytes_per_launch"], os.path.relpath(path, ROOT)
 
 
+# What every cpu_baseline times: the oracle's scalar C restatement of the
+# reference's Candle CPU path (gcc -O2, no fast-math, no contraction,
+# sequential dot products; OpenMP over "cores" threads), not Candle itself,
+# whose matmuls use the SIMD gemm crate. "nproc" is the host's CPU count.
+ORACLE_IMPL = ("scalar C restatement of the reference CPU path (-O2, no SIMD gemm), "
+               "OpenMP over 'cores' threads")
+
+
 def cpu_baseline(args, lens, hq, hkv, d, layers):
     """The oracle (C restatement of the reference's Candle CPU path: contiguous
     per-sequence f32 buffers, KvCache append, per-KV-head matmul / softmax /
@@ -179,6 +187,7 @@ def cpu_baseline(args, lens, hq, hkv, d, layers):
             break
     steps = n / layers
     return {"value": b * steps / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "nproc": os.cpu_count(), "impl": ORACLE_IMPL,
             "sample": f"{n} layer-steps (append + decode of all {b} sequences, f32, one "
                       f"layer's contiguous buffers reused) in {el:.2f} s = {steps:.2f} "
                       f"decode steps of {layers} layers"}
@@ -286,6 +295,7 @@ def prefill_cpu_baseline(args, hq, hkv, d, tq, offset):
             break
     flops = prefill_flops(g, d, tq, offset) * n
     return {"value": flops / el / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "nproc": os.cpu_count(), "impl": ORACLE_IMPL,
             "sample": f"{n} KV head(s) of the chunk ({g} query heads each, f32) in {el:.2f} s"}
 
 
@@ -403,6 +413,7 @@ def fork_bench(args):
         2 * b * row + b * d * 2 + 2 * d * 2
     compulsory = plen * row + int(sum(int(n) - plen for n in lens)) * row + extra
     logical = int(sum(int(n) for n in lens)) * row + extra
+    traffic, traffic_src = measured_traffic(args.workload, True)
     achieved = compulsory / (avg_ms * 1e-3) / 1e9
     result = {
         "metric": "prefix-fork decode tokens/sec and compulsory HBM GB/s at Qwen3-0.6B shape, "
@@ -415,13 +426,20 @@ def fork_bench(args):
                    "mean_keys": float(np.mean(lens)), "fork_ms": fork_ms,
                    "cow_pages_per_layer": len(src), "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
-                     "kernel": "decode_kernel fused step (rlse_decode_step)",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "kernel": "decode_kernel planned fused step "
+                               "(rlse_decode_step_planned, cacheable pages)",
                      "bytes_per_launch": compulsory, "logical_bytes_per_launch": logical,
                      "effective_GBps": logical / (avg_ms * 1e-3) / 1e9,
                      "avg_launch_ms": avg_ms, "timed_launches": ev_steps * layers},
         "cpu_baseline": None,
     }
+    if not args.no_cpu:
+        # The reference holds every forked sequence in its own contiguous
+        # buffers (prefix copied in), so its decode step is the plain one over
+        # prefix + suffix keys.
+        result["cpu_baseline"] = cpu_baseline(args, lens, hq, hkv, d, layers)
     print(json.dumps(result))
     pool.close()
 
@@ -596,6 +614,7 @@ def e2e_cpu_baseline(args, cfg, cached):
         if el >= args.cpu_seconds or steps >= max_steps:
             break
     return {"value": len(sub) * steps / el, "unit": "tokens/s", "cores": O.max_threads(),
+            "nproc": os.cpu_count(), "impl": ORACLE_IMPL,
             "kind": "port",
             "sample": f"{steps} whole step(s) of {len(sub)} of the sequences (cached "
                       f"{sub}), f32, in {el:.2f} s"}
@@ -748,7 +767,8 @@ def main():
                      "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "traffic_source": traffic_src,
                      "kernel": ("decode_kernel (rlse_paged_gqa_decode)" if args.unfused else
-                                "decode_kernel fused step (rlse_decode_step)"),
+                                "decode_kernel planned fused step (rlse_decode_step_planned, "
+                                "streamed pages)"),
                      "bytes_per_launch": per_launch, "avg_launch_ms": avg_ms,
                      "timed_launches": ev_steps * layers,
                      "event_spans": ("one per timed step around its back-to-back decode "
