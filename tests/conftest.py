@@ -10,6 +10,12 @@ for sub in ("mini-serve-rs_amd", "oracle", ""):
     if p not in sys.path:
         sys.path.insert(0, p)
 
+# A sanitized build of the library (mini-serve-rs_amd/csrc: make sanitize;
+# sanitize_tests.sh runs the CPU tests against it) replaces the product one.
+if os.environ.get("RLSE_KV_TEST_LIB"):
+    import rlse_kv  # noqa: E402
+    rlse_kv.LIB_PATH = os.environ["RLSE_KV_TEST_LIB"]
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
