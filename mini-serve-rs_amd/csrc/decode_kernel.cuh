@@ -787,6 +787,21 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     uint4 qv[G];
     int cur_row = -1;
     const float inv_c = 1.f / p.c;
+    // Own-head softmax (16-bit K/V at head_dim 64, three or more heads per
+    // group: eight lanes per key row, two rows per lane). After the row sums
+    // every lane of a row group holds the same G x NR scores, so the softmax
+    // of head g is computed once, by lane g of the group: m_o, l_o, nms_o and
+    // thr_o are that lane's running max, sum, exponent offset and rescale
+    // threshold (lanes past G hold none), and the packed probability pair of
+    // each head, and a rescale's factor, reach the other lanes through
+    // ds_bpermute. m[g] and l[g] are gathered from the owners at the row's end.
+    constexpr bool kOwn = sizeof(T) == 2 && D == 64 && G >= 3;
+    static_assert(!kOwn || (LPR == 8 && NR == 2 && G <= LPR), "own-head layout");
+    float m_o = -INFINITY, l_o = 0.f, nms_o = 0.f, thr_o = -INFINITY;
+    const int gaddr = (lane & ~(LPR - 1)) * 4;  // ds_bpermute address of the group's lane 0
+    auto from_head = [&](uint32_t v, int g) __attribute__((always_inline)) {
+      return (uint32_t)__builtin_amdgcn_ds_bpermute(gaddr + 4 * g, (int)v);
+    };
     auto reset = [&]() __attribute__((always_inline)) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -797,10 +812,21 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
       }
+      m_o = -INFINITY;
+      l_o = 0.f;
+      nms_o = 0.f;
+      thr_o = -INFINITY;
     };
     // Ends the wave's part of cur_row: merge the lane groups, then write the
     // output (row wholly inside this wave) or park the state in LDS.
     auto finalize = [&]() __attribute__((always_inline)) {
+      if constexpr (kOwn) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          m[g] = __uint_as_float(from_head(__float_as_uint(m_o), g));
+          l[g] = __uint_as_float(from_head(__float_as_uint(l_o), g));
+        }
+      }
 #pragma unroll
       for (int off = LPR; off < 64; off <<= 1) {
 #pragma unroll
@@ -927,6 +953,47 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       } else {
 #pragma unroll
         for (int r = 0; r < NR; ++r) Packet<T>::unpack(vr[r], vf[r]);
+      }
+      if constexpr (kOwn) {
+        // This lane's head: its scores of the lane's two rows (-inf past G).
+        float so[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          float v = -INFINITY;
+#pragma unroll
+          for (int g = 0; g < G; ++g) v = col == g ? s[g][r] : v;
+          so[r] = v;
+        }
+        const float cand = fmaxf(so[0], so[1]);
+        if (__any(cand > thr_o)) {  // lazy rescaling, as below, per owning lane
+          const float mn = fmaxf(m_o, cand * p.c);
+          const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_o - mn);
+          l_o *= alpha;
+          m_o = mn;
+          nms_o = (mn == -INFINITY) ? 0.f : -mn;
+          thr_o = (mn == -INFINITY) ? -INFINITY : (mn + kLazyLog2) * inv_c;
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float a = __uint_as_float(from_head(__float_as_uint(alpha), g));
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[g][e] *= a;
+          }
+        }
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(so[0], p.c, nms_o));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(so[1], p.c, nms_o));
+        l_o += p0;
+        l_o += p1;
+        const uint32_t pp_o = Packet<T>::pack2(p0, p1);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const uint32_t pp = from_head(pp_o, g);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            acc[g][2 * k] = Packet<T>::dot2(vpair[0][k][0], pp, acc[g][2 * k]);
+            acc[g][2 * k + 1] = Packet<T>::dot2(vpair[0][k][1], pp, acc[g][2 * k + 1]);
+          }
+        }
+        return;
       }
       // Lazy rescaling: a running max moves only when a scaled score exceeds
       // it by more than kLazyLog2 (probabilities then stay below
