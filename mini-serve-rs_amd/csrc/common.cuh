@@ -104,6 +104,9 @@ struct Packet<float> {
     c = fmaf(__uint_as_float(a.w), __uint_as_float(b.w), c);
     return c;
   }
+  static __device__ __forceinline__ float dot0(const uint4& a, const uint4& b) {
+    return dot(a, b, 0.f);
+  }
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -126,6 +129,17 @@ struct Packet<bf16> {
   }
   static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float c) {
     c = dot2(a.x, b.x, c);
+    c = dot2(a.y, b.y, c);
+    c = dot2(a.z, b.z, c);
+    c = dot2(a.w, b.w, c);
+    return c;
+  }
+  // dot(a, b, 0) with the chain's first step in the three-operand encoding
+  // and its accumulator an inline 0: the compiler otherwise emits the
+  // two-operand form, which needs its accumulator register zeroed first.
+  static __device__ __forceinline__ float dot0(const uint4& a, const uint4& b) {
+    float c;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(c) : "v"(a.x), "v"(b.x));
     c = dot2(a.y, b.y, c);
     c = dot2(a.z, b.z, c);
     c = dot2(a.w, b.w, c);
@@ -161,6 +175,15 @@ struct Packet<f16> {
   }
   static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float c) {
     c = dot2(a.x, b.x, c);
+    c = dot2(a.y, b.y, c);
+    c = dot2(a.z, b.z, c);
+    c = dot2(a.w, b.w, c);
+    return c;
+  }
+  // dot(a, b, 0); see Packet<bf16>::dot0.
+  static __device__ __forceinline__ float dot0(const uint4& a, const uint4& b) {
+    float c;
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(c) : "v"(a.x), "v"(b.x));
     c = dot2(a.y, b.y, c);
     c = dot2(a.z, b.z, c);
     c = dot2(a.w, b.w, c);

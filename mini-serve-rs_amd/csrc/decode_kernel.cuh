@@ -917,7 +917,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-          for (int r = 0; r < NR; ++r) part[g * NR + r] = Packet<T>::dot(qv[g], kr[r], 0.f);
+          for (int r = 0; r < NR; ++r) part[g * NR + r] = Packet<T>::dot0(qv[g], kr[r]);
         group_sum_n<LPR>(part);
 #pragma unroll
         for (int g = 0; g < G; ++g)
