@@ -784,7 +784,6 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     // kLazyLog2) / c (-inf while m[g] is -inf); both are kept beside m[g],
     // as they change only when the running max moves.
     float m[G], l[G], acc[G][EPL], nms[G], thr[G];
-    uint4 qv[G];
     int cur_row = -1;
     const float inv_c = 1.f / p.c;
     // Own-head softmax (16-bit K/V at head_dim 64, three or more heads per
@@ -797,6 +796,17 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     // ds_bpermute. m[g] and l[g] are gathered from the owners at the row's end.
     constexpr bool kOwn = sizeof(T) == 2 && D == 64 && G >= 3;
     static_assert(!kOwn || (LPR == 8 && NR == 2 && G <= LPR), "own-head layout");
+    // With six or more heads the row sums are a reduce-scatter instead: the
+    // lane in column i of a row group holds the queries of its eight head
+    // slots in the order sig_i(s) = i ^ s (s < 4), (7 - i) ^ (s - 4) (s >= 4)
+    // (a zero query past G). Then three DPP steps -- slots s += slots s+4 of
+    // the mirrored lane 7-i, s += s+2 of lane i^2, s += s+1 of lane i^1 --
+    // leave in slot 0 the full row sums of head i, each exchange adding the
+    // partner's slot that holds the same head: 14 adds instead of an
+    // all-reduce of 14 values (42) and the owner's pick (14).
+    constexpr bool kScatter = kOwn && G >= 6;
+    constexpr int QS = kScatter ? 8 : G;  // query slots per lane
+    uint4 qv[QS];
     float m_o = -INFINITY, l_o = 0.f, nms_o = 0.f, thr_o = -INFINITY;
     const int gaddr = (lane & ~(LPR - 1)) * 4;  // ds_bpermute address of the group's lane 0
     auto from_head = [&](uint32_t v, int g) __attribute__((always_inline)) {
@@ -883,7 +893,15 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         cur_row = bf.row;
         if (cur_row < q_base || cur_row >= q_top) stage_q_refill(cur_row);
 #pragma unroll
-        for (int g = 0; g < G; ++g) qv[g] = s_q[wave][cur_row - q_base][g][col];
+        for (int g = 0; g < QS; ++g) {
+          if constexpr (kScatter) {
+            const int hd = g < 4 ? (col ^ g) : ((7 - col) ^ (g - 4));
+            const uint4 v = s_q[wave][cur_row - q_base][hd < G ? hd : G - 1][col];
+            qv[g] = hd < G ? v : make_uint4(0, 0, 0, 0);
+          } else {
+            qv[g] = s_q[wave][cur_row - q_base][g][col];
+          }
+        }
       }
       // A skipped block (nv = 0) runs the same math with every row masked,
       // which leaves m, l and acc unchanged; consuming its registers on every
@@ -912,7 +930,30 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       // Raw scores q.k, summed over the LPR lanes of each row (all G*NR
       // partial dots first, then the reduction steps across all of them).
       float s[G][NR];
-      {
+      float sc[NR];  // reduce-scatter: this lane's head's row sums (-inf past G)
+      if constexpr (kScatter) {
+        float x[8][NR];
+#pragma unroll
+        for (int g = 0; g < 8; ++g)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) x[g][r] = Packet<T>::dot0(qv[g], kr[r]);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) x[g][r] += dpp_f32<0x141>(x[g + 4][r]);
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) x[g][r] += dpp_f32<0x4E>(x[g + 2][r]);
+        // The last step in every lane (a DPP source lane switched off by a
+        // branch would read as 0), and only then the pick of lanes past G.
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          float t = x[0][r] + dpp_f32<0xB1>(x[1][r]);
+          asm volatile("" : "+v"(t));
+          sc[r] = col < G ? t : -INFINITY;
+        }
+      } else {
         float part[G * NR];
 #pragma unroll
         for (int g = 0; g < G; ++g)
@@ -928,8 +969,12 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
           if (r * RPL + rsub >= nv) {
+            if constexpr (kScatter) {
+              sc[r] = -INFINITY;
+            } else {
 #pragma unroll
-            for (int g = 0; g < G; ++g) s[g][r] = -INFINITY;
+              for (int g = 0; g < G; ++g) s[g][r] = -INFINITY;
+            }
             vr[r] = make_uint4(0, 0, 0, 0);
           }
         }
@@ -960,8 +1005,12 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
           float v = -INFINITY;
+          if constexpr (kScatter) {
+            v = sc[r];
+          } else {
 #pragma unroll
-          for (int g = 0; g < G; ++g) v = col == g ? s[g][r] : v;
+            for (int g = 0; g < G; ++g) v = col == g ? s[g][r] : v;
+          }
           so[r] = v;
         }
         const float cand = fmaxf(so[0], so[1]);
