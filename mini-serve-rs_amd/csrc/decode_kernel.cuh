@@ -592,6 +592,12 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     R = (long long)Hkv * s_pref[b] + (long long)kvh * nb;
   };
 
+  // This wave's parked pieces (slot 0: the row that started before the
+  // wave's range, 1: the row that continues after it), kept in registers
+  // beside the LDS copy the group reads: row (-1 = none), start and blocks.
+  int part_row0 = -1, part_row1 = -1, part_nb0 = 0, part_nb1 = 0;
+  long long part_R0 = 0, part_R1 = 0;
+
   if (nblk > 0) {
     // Descriptors of 64 consecutive blocks, one per lane: page id, valid
     // rows and row, read back with readlane when the block is issued.
@@ -866,12 +872,23 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
           for (int g = 0; g < G; ++g) {
             const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;  // all pages skipped -> zeros
             T* dst = ob + ((size_t)b * Hq + (size_t)kvh * G + g) * D + (size_t)col * EPL;
+            float y[EPL];
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) dst[e] = Elem<T>::from_f32(acc[g][e] * inv);
+            for (int e = 0; e < EPL; ++e) y[e] = acc[g][e] * inv;
+            *reinterpret_cast<uint4*>(dst) = pack_packet<T>(y);
           }
         }
       } else {
         const int slot = 2 * wave + (R < wlo ? 0 : 1);
+        if (R < wlo) {
+          part_row0 = cur_row;
+          part_R0 = R;
+          part_nb0 = nb;
+        } else {
+          part_row1 = cur_row;
+          part_R1 = R;
+          part_nb1 = nb;
+        }
         if (rsub == 0) {
 #pragma unroll
           for (int g = 0; g < G; ++g) {
@@ -1137,13 +1154,16 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   // publishes and merges: a wave's waits count its own stores too, so a
   // merge in the publishing wave would stand behind the publication's write
   // round trip, and a publication behind a merge would chain merges from
-  // group to group.
+  // group to group. Every slot's row is read once (lane j < NPART holds slot
+  // j's), so the pieces of a row are found with one ballot and their LDS
+  // reads issued together.
+  const int prow = lane < NPART ? s_part_row[lane] : -1;
+#pragma unroll 1
   for (int s = 1; s >= 0; --s) {
-    const int row = s_part_row[2 * wave + s];
+    const int row = s ? part_row1 : part_row0;
     if (row < 0) continue;
-    long long R;
-    int nb;
-    row_extent(row, R, nb);
+    const long long R = s ? part_R1 : part_R0;
+    const int nb = s ? part_nb1 : part_nb0;
     const bool merge = R < glo && R + nb <= ghi;  // only ever wave 0's slot 0 in wave 0
     if (merge ? wave != 0 : (R + nb > whi && whi < ghi)) continue;
     const int b = row / Hkv, kvh = row - b * Hkv;
@@ -1156,27 +1176,36 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         Ls[g][k] = 0.f;
         A[g][k] = 0.f;
       }
-    bool seen = false;
-    for (int wv = merge ? kWaves - 1 : wave; wv >= 0; --wv) {
-      bool any = false;
-      for (int s2 = 1; s2 >= 0; --s2) {
-        const int slot = 2 * wv + s2;
-        if ((wv == wave && s2 != s) || s_part_row[slot] != row) continue;
-        any = true;
+    // Slots holding pieces of the row: this wave's slot s and, in the waves
+    // below it (every wave when merging), the slot naming the same row. A
+    // row's pieces sit in consecutive waves, at most one slot per wave.
+    const int top = merge ? kWaves - 1 : wave;
+    const uint64_t hit = __ballot(lane < 2 * top + 2 && prow == row &&
+                                  ((lane >> 1) != wave || (lane & 1) == s));
+    float pm[kWaves][G], pl[kWaves][G], pa[kWaves][G][DPL];
 #pragma unroll
-        for (int g = 0; g < G; ++g)
+    for (int wv = 0; wv < kWaves; ++wv) {
+      const int slot = 2 * wv + (int)((hit >> (2 * wv + 1)) & 1);
 #pragma unroll
-          for (int k = 0; k < DPL; ++k) {
-            const int d = lane + 64 * k;
-            if (d < D)
-              lse_combine(M[g][k], Ls[g][k], A[g][k], s_part[slot][g][D], s_part[slot][g][D + 1],
-                          s_part[slot][g][d]);
-          }
+      for (int g = 0; g < G; ++g) {
+        pm[wv][g] = s_part[slot][g][D];
+        pl[wv][g] = s_part[slot][g][D + 1];
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) {
+          const int d = lane + 64 * k;
+          pa[wv][g][k] = d < D ? s_part[slot][g][d] : 0.f;
+        }
       }
-      if (any)
-        seen = true;
-      else if (seen)
-        break;
+    }
+#pragma unroll
+    for (int wv = kWaves - 1; wv >= 0; --wv) {
+      if (((hit >> (2 * wv)) & 3) == 0) continue;
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < DPL; ++k)
+          if (lane + 64 * k < D)
+            lse_combine(M[g][k], Ls[g][k], A[g][k], pm[wv][g], pl[wv][g], pa[wv][g][k]);
     }
     if (R + nb > ghi) {
       // The row continues in a later group: publish this group's piece

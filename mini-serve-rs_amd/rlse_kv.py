@@ -29,7 +29,9 @@ from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "librlse_kv.so")
+# RLSE_KV_LIB names another build of the library (a sanitized one, or one
+# built from other sources for a before/after measurement).
+LIB_PATH = os.environ.get("RLSE_KV_LIB") or os.path.join(_HERE, "librlse_kv.so")
 
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 DTYPE_NAMES = {"f32": DTYPE_F32, "float32": DTYPE_F32, "bf16": DTYPE_BF16,

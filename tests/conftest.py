@@ -10,11 +10,9 @@ for sub in ("mini-serve-rs_amd", "oracle", ""):
     if p not in sys.path:
         sys.path.insert(0, p)
 
-# A sanitized build of the library (mini-serve-rs_amd/csrc: make sanitize;
-# sanitize_tests.sh runs the CPU tests against it) replaces the product one.
-if os.environ.get("RLSE_KV_TEST_LIB"):
-    import rlse_kv  # noqa: E402
-    rlse_kv.LIB_PATH = os.environ["RLSE_KV_TEST_LIB"]
+# RLSE_KV_LIB (read by rlse_kv) swaps in another build of the library, such
+# as a sanitized one (mini-serve-rs_amd/csrc: make sanitize; sanitize_tests.sh
+# runs the CPU tests against it).
 
 
 def pytest_configure(config):
