@@ -259,6 +259,50 @@ __host__ __device__ constexpr int q_stage_rows() {
                                                       : 1;
 }
 
+// Matrix-core decode: 16-bit K/V at head_dim 64 with three or more query
+// heads per KV head. Per 16-key block, S^T = K . Q^T on 16x16x32 MFMAs (keys
+// x heads, the heads padded to 16 with zero queries) and O^T += V^T . P^T on
+// 16x16x16 MFMAs; the q.k and p.V dot products leave the VALU.
+template <typename T, int D, int G>
+__host__ __device__ constexpr bool decode_mma() {
+  return sizeof(T) == 2 && D == 64 && G >= 3;
+}
+
+typedef float mma_f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 mma_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 mma_f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 mma_f16x4_t __attribute__((ext_vector_type(4)));
+typedef short mma_i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) mma_i16x4_t mma_lds_i16x4_t;
+
+// 16x16 MFMAs on 16-bit operands (lane l: A[l%16][k], B[k][l%16] for its
+// k-slots, accumulator rows 4*(l/16) .. +3 of column l%16). k32: eight
+// elements per lane and operand; k16: four.
+template <typename T>
+struct Mma16;
+template <>
+struct Mma16<bf16> {
+  static __device__ __forceinline__ mma_f32x4_t k32(uint4 a, uint4 b, mma_f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mma_bf16x8_t, a),
+                                                   __builtin_bit_cast(mma_bf16x8_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ mma_f32x4_t k16(mma_i16x4_t a, uint2 b, mma_f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(mma_i16x4_t, b), c, 0,
+                                                     0, 0);
+  }
+};
+template <>
+struct Mma16<f16> {
+  static __device__ __forceinline__ mma_f32x4_t k32(uint4 a, uint4 b, mma_f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mma_f16x8_t, a),
+                                                  __builtin_bit_cast(mma_f16x8_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ mma_f32x4_t k16(mma_i16x4_t a, uint2 b, mma_f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(mma_f16x4_t, a),
+                                                 __builtin_bit_cast(mma_f16x4_t, b), c, 0, 0, 0);
+  }
+};
+
 // Rounding to T for the prologue's element-wise math: bf16 uses the
 // select-form conversion (same result as round_to).
 template <typename T>
@@ -353,6 +397,10 @@ struct DecodeLds {
   int part_row[2 * kWaves];          // their rows (-1 = unused)
   uint4 q[kWaves][QR][G][LPR];       // staged query packets per wave
   uint4 nw[FUSED ? kWaves : 1][FUSED ? kNew : 1][2][LPR];  // appended k, v rows
+  // Matrix-core decode: the V block of each wave, row-major with 16 elements
+  // of padding per row (transposing reads free of bank conflicts).
+  static constexpr bool kMma = decode_mma<T, D, G>();
+  uint4 vt[kMma ? kWaves : 1][kMma ? 16 : 1][(D + 16) / 8];
 };
 
 // The decode of one workgroup. POL is the cache-policy operand of the page
@@ -369,6 +417,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
                                             uint32_t ctr0, int len_t0) {
   constexpr bool FUSED = MODE != kModePlain;
   constexpr bool PLANNED = MODE >= kModePlanned;
+  constexpr bool kMma = decode_mma<T, D, G>();
   using S = DecodeShape<T, D>;
   constexpr int EPL = S::EPL, LPR = S::LPR, RPL = S::RPL, NR = S::NR;
   constexpr int REC = rec_words(G, D);
@@ -384,8 +433,9 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   // workgroup is not streaming (its late start, the end of the launch). At
   // head_dim 64 a third buffer measured slower (G = 7: the wave is VALU-bound
   // and the longer register live ranges cost more than the extra block in
-  // flight), and 32-bit K/V and wider groups lack the registers.
-  constexpr int NBUF = (sizeof(T) == 2 && D == 128 && G <= 4) ? 3 : 2;
+  // flight), and 32-bit K/V and wider groups lack the registers. The
+  // matrix-core decode holds far fewer registers per head and takes three.
+  constexpr int NBUF = ((sizeof(T) == 2 && D == 128 && G <= 4) || kMma) ? 3 : 2;
   constexpr int kPreIssued = 2;  // blocks issued before the prologue's appends
   constexpr int kNewCap = new_row_cap<T>();
   static_assert(kNewCap >= kPreIssued, "pre-issued blocks must find their new rows in LDS");
@@ -393,6 +443,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   auto& s_part_row = lds.part_row;
   auto& s_q = lds.q;
   auto& s_new = lds.nw;
+  auto& s_vt = lds.vt;
 
   const int tid = threadIdx.x;
   // The wave index and everything derived from LDS-held prefixes below are
@@ -410,6 +461,13 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
   const size_t tile = (size_t)16 * D;  // elements of one (block, head) tile
   const int voff = (int)(((size_t)rsub * D + (size_t)col * EPL) * sizeof(T));
+  // Matrix-core decode: K is read straight into the MFMA operand layout --
+  // lane l takes key row l%16, elements 32r + 8*(l/16) .. +8 in its r-th
+  // load; the four lanes of a key read 64 contiguous bytes per load, so the
+  // requests are those of the coalesced load. V keeps the coalesced layout
+  // (it is transposed through LDS).
+  const int koff =
+      kMma ? (int)(((size_t)(lane & 15) * D + (size_t)(lane >> 4) * EPL) * sizeof(T)) : voff;
   // K and V packets of one block, as raw buffer loads through a descriptor
   // of the block's tile: a block not fetched (past the wave's end, or an
   // invalid page) gets a descriptor of zero records, which returns zeros
@@ -427,7 +485,8 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const int o = voff + r * RPL * D * (int)sizeof(T);
-      const u32x4_t kx = __builtin_amdgcn_raw_buffer_load_b128(rk, o, 0, POL);
+      const int ok = kMma ? koff + r * 32 * (int)sizeof(T) : o;
+      const u32x4_t kx = __builtin_amdgcn_raw_buffer_load_b128(rk, ok, 0, POL);
       const u32x4_t vx = __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, POL);
       bf.k[r] = make_uint4(kx.x, kx.y, kx.z, kx.w);
       bf.v[r] = make_uint4(vx.x, vx.y, vx.z, vx.w);
@@ -800,7 +859,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     // threshold (lanes past G hold none), and the packed probability pair of
     // each head, and a rescale's factor, reach the other lanes through
     // ds_bpermute. m[g] and l[g] are gathered from the owners at the row's end.
-    constexpr bool kOwn = sizeof(T) == 2 && D == 64 && G >= 3;
+    constexpr bool kOwn = sizeof(T) == 2 && D == 64 && G >= 3 && !kMma;
     static_assert(!kOwn || (LPR == 8 && NR == 2 && G <= LPR), "own-head layout");
     // With six or more heads the row sums are a reduce-scatter instead: the
     // lane in column i of a row group holds the queries of its eight head
@@ -818,7 +877,26 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     auto from_head = [&](uint32_t v, int g) __attribute__((always_inline)) {
       return (uint32_t)__builtin_amdgcn_ds_bpermute(gaddr + 4 * g, (int)v);
     };
+    // Matrix-core decode state: lane l works for head l%16 (heads past G have
+    // zero queries and are never stored) and holds keys 4*(l/16) .. +3 of
+    // each block's S^T column and rows 16t + 4*(l/16) .. +3 of O^T tile t;
+    // m1, nms1 and thr1 are the head's running max, exponent offset and
+    // rescale threshold (equal in the head's four lanes), l1 the lane's part
+    // of the head's sum. mqv holds the head's query in the K operand layout.
+    const int mh = lane & 15, mq = lane >> 4;
+    uint4 mqv[kMma ? NR : 1];
+    mma_f32x4_t macc[kMma ? D / 16 : 1];
+    float m1 = -INFINITY, l1 = 0.f, nms1 = 0.f, thr1 = -INFINITY;
     auto reset = [&]() __attribute__((always_inline)) {
+      if constexpr (kMma) {
+        m1 = -INFINITY;
+        l1 = 0.f;
+        nms1 = 0.f;
+        thr1 = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) macc[t] = mma_f32x4_t{0.f, 0.f, 0.f, 0.f};
+        return;
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
@@ -836,6 +914,52 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     // Ends the wave's part of cur_row: merge the lane groups, then write the
     // output (row wholly inside this wave) or park the state in LDS.
     auto finalize = [&]() __attribute__((always_inline)) {
+      if constexpr (kMma) {
+        // The head's sum over its four lanes; m1 is already common to them.
+        float lt = l1 + __shfl_xor(l1, 16, 64);
+        lt = lt + __shfl_xor(lt, 32, 64);
+        long long R;
+        int nb;
+        row_extent(cur_row, R, nb);
+        const int b = cur_row / Hkv, kvh = cur_row - b * Hkv;
+        if (R >= wlo && R + nb <= whi) {
+          if (mh < G) {
+            const float inv = lt > 0.f ? 1.f / lt : 0.f;  // all pages skipped -> zeros
+            T* dst = ob + ((size_t)b * Hq + (size_t)kvh * G + mh) * D + 4 * mq;
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t) {
+              const uint32_t w0 = (uint32_t)bits_sel<T>(macc[t][0] * inv) |
+                                  ((uint32_t)bits_sel<T>(macc[t][1] * inv) << 16);
+              const uint32_t w1 = (uint32_t)bits_sel<T>(macc[t][2] * inv) |
+                                  ((uint32_t)bits_sel<T>(macc[t][3] * inv) << 16);
+              *reinterpret_cast<uint2*>(dst + 16 * t) = make_uint2(w0, w1);
+            }
+          }
+        } else {
+          const int slot = 2 * wave + (R < wlo ? 0 : 1);
+          if (R < wlo) {
+            part_row0 = cur_row;
+            part_R0 = R;
+            part_nb0 = nb;
+          } else {
+            part_row1 = cur_row;
+            part_R1 = R;
+            part_nb1 = nb;
+          }
+          if (mh < G) {
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) s_part[slot][mh][16 * t + 4 * mq + i] = macc[t][i];
+            if (mq == 0) {
+              s_part[slot][mh][D] = m1;
+              s_part[slot][mh][D + 1] = lt;
+            }
+          }
+          if (lane == 0) s_part_row[slot] = cur_row;
+        }
+        return;
+      }
       if constexpr (kOwn) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -904,6 +1028,95 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       }
     };
     auto compute = [&](const Buf<T, D>& bf) __attribute__((always_inline)) {
+      if constexpr (kMma) {
+        if (bf.newrow) {
+          if (cur_row >= 0) finalize();
+          reset();
+          cur_row = bf.row;
+          if (cur_row < q_base || cur_row >= q_top) stage_q_refill(cur_row);
+          const int hq = mh < G ? mh : G - 1;
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            const uint4 x = s_q[wave][cur_row - q_base][hq][4 * r + mq];
+            mqv[r] = mh < G ? x : make_uint4(0, 0, 0, 0);
+          }
+        }
+        const int nv = bf.nvalid;
+        uint4 kr[NR], vr[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          kr[r] = bf.k[r];
+          vr[r] = bf.v[r];
+        }
+        if constexpr (FUSED) {
+          if (bf.sub >= 0) {  // the new token (slot nv-1) may not be stored yet: take it from LDS
+            const int slot = nv - 1;
+            if (mh == slot) {
+#pragma unroll
+              for (int r = 0; r < NR; ++r) kr[r] = s_new[wave][bf.sub][0][4 * r + mq];
+            }
+            if (rsub == slot % RPL) {
+              const uint4 vn = s_new[wave][bf.sub][1][col];
+#pragma unroll
+              for (int r = 0; r < NR; ++r)
+                if (r == slot / RPL) vr[r] = vn;
+            }
+          }
+        }
+        // Rows past the sequence end: V = 0 (their p is 0, and 0 * garbage
+        // could be NaN), scores -inf below.
+        if (nv < 16) {
+#pragma unroll
+          for (int r = 0; r < NR; ++r)
+            if (r * RPL + rsub >= nv) vr[r] = make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) s_vt[wave][r * RPL + rsub][col] = vr[r];
+        // S^T (keys x heads) = K . Q^T
+        mma_f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < NR; ++r) sacc = Mma16<T>::k32(kr[r], mqv[r], sacc);
+        float sv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = 4 * mq + i < nv ? sacc[i] : -INFINITY;
+        // Lazy rescaling (as below): the head's new max is taken over its
+        // four lanes.
+        const float cand = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        if (__any(cand > thr1)) {
+          float cm = fmaxf(cand, __shfl_xor(cand, 16, 64));
+          cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+          const float mn = fmaxf(m1, cm * p.c);
+          const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m1 - mn);
+          l1 *= alpha;
+#pragma unroll
+          for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) macc[t][i] *= alpha;
+          m1 = mn;
+          nms1 = (mn == -INFINITY) ? 0.f : -mn;
+          thr1 = (mn == -INFINITY) ? -INFINITY : (mn + kLazyLog2) * inv_c;
+        }
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pr[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.c, nms1));
+          l1 += pr[i];
+        }
+        // P^T in the accumulator layout is the B operand of O^T += V^T . P^T;
+        // V^T tile t comes from LDS by transposing reads: within each 16-lane
+        // group, lane 4j+a points at key row 4*(l/16)+j, columns 16t+4a .. +3,
+        // and lane 4a+e receives column 16t+4a+e of those four keys.
+        const uint2 pp = make_uint2(Packet<T>::pack2(pr[0], pr[1]), Packet<T>::pack2(pr[2], pr[3]));
+        const uint16_t* vrow =
+            reinterpret_cast<const uint16_t*>(&s_vt[wave][4 * mq + ((lane & 15) >> 2)][0]) +
+            4 * (lane & 3);
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) {
+          const mma_i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mma_lds_i16x4_t*)(vrow + 16 * t));
+          macc[t] = Mma16<T>::k16(a, pp, macc[t]);
+        }
+        return;
+      }
       if (bf.newrow) {
         if (cur_row >= 0) finalize();
         reset();
