@@ -35,6 +35,12 @@
 // double-buffered in registers so the next block's loads -- and the query of
 // a new row -- are in flight during the math, and no barrier is taken while
 // streaming.
+//
+// The matrix-core variant (decode_mma) keeps the decomposition, the loads of
+// K and the merges, and replaces the lane-group math: per block, MFMAs give
+// S^T (16 keys x the heads padded to 16) and accumulate O^T = V^T . P^T; a
+// lane then holds one head's scores of four keys and 16 of its output
+// dimensions, and only the softmax runs on the VALU.
 #pragma once
 
 #include <math.h>
@@ -259,13 +265,14 @@ __host__ __device__ constexpr int q_stage_rows() {
                                                       : 1;
 }
 
-// Matrix-core decode: 16-bit K/V at head_dim 64 with three or more query
-// heads per KV head. Per 16-key block, S^T = K . Q^T on 16x16x32 MFMAs (keys
-// x heads, the heads padded to 16 with zero queries) and O^T += V^T . P^T on
-// 16x16x16 MFMAs; the q.k and p.V dot products leave the VALU.
+// Matrix-core decode for 16-bit K/V: per 16-key block, S^T = K . Q^T on
+// 16x16x32 MFMAs (keys x heads, the heads padded to 16 with zero queries) and
+// O^T += V^T . P^T on 16x16x16 MFMAs, so the q.k and p.V dot products leave
+// the VALU. Every mode takes it, so the cache-policy flag never changes a
+// result.
 template <typename T, int D, int G>
 __host__ __device__ constexpr bool decode_mma() {
-  return sizeof(T) == 2 && D == 64 && G >= 3;
+  return sizeof(T) == 2;
 }
 
 typedef float mma_f32x4_t __attribute__((ext_vector_type(4)));
