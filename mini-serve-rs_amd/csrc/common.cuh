@@ -134,17 +134,6 @@ struct Packet<bf16> {
     c = dot2(a.w, b.w, c);
     return c;
   }
-  // dot(a, b, 0) with the chain's first step in the three-operand encoding
-  // and its accumulator an inline 0: the compiler otherwise emits the
-  // two-operand form, which needs its accumulator register zeroed first.
-  static __device__ __forceinline__ float dot0(const uint4& a, const uint4& b) {
-    float c;
-    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(c) : "v"(a.x), "v"(b.x));
-    c = dot2(a.y, b.y, c);
-    c = dot2(a.z, b.z, c);
-    c = dot2(a.w, b.w, c);
-    return c;
-  }
   // Two floats rounded to nearest-even bf16, lo in the low half.
   static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
     const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
@@ -175,15 +164,6 @@ struct Packet<f16> {
   }
   static __device__ __forceinline__ float dot(const uint4& a, const uint4& b, float c) {
     c = dot2(a.x, b.x, c);
-    c = dot2(a.y, b.y, c);
-    c = dot2(a.z, b.z, c);
-    c = dot2(a.w, b.w, c);
-    return c;
-  }
-  // dot(a, b, 0); see Packet<bf16>::dot0.
-  static __device__ __forceinline__ float dot0(const uint4& a, const uint4& b) {
-    float c;
-    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(c) : "v"(a.x), "v"(b.x));
     c = dot2(a.y, b.y, c);
     c = dot2(a.z, b.z, c);
     c = dot2(a.w, b.w, c);

@@ -25,22 +25,20 @@
 // and a merge that gives up writes NaN and raises a sticky error flag in the
 // workspace. A workspace only needs zero-filling once, before first use.
 //
-// Inside a wave a K/V block is read as 16-byte packets: LPR lanes cover one
-// 16-token row's head_dim, RPL = 64/LPR rows are read per instruction and each
-// lane owns NR = 16/RPL rows of the block. Scores are reduced over the LPR
-// lanes of a row with DPP adds (bf16/f16 dot products with v_dot2); each lane
-// group keeps its own online-softmax state (running max m in log2 units, sum
-// l, acc) and the groups are merged when the wave's part of a row ends. The
-// page ids of 64 blocks are fetched at once (one per lane), blocks are
-// double-buffered in registers so the next block's loads -- and the query of
-// a new row -- are in flight during the math, and no barrier is taken while
-// streaming.
-//
-// The matrix-core variant (decode_mma) keeps the decomposition, the loads of
-// K and the merges, and replaces the lane-group math: per block, MFMAs give
-// S^T (16 keys x the heads padded to 16) and accumulate O^T = V^T . P^T; a
-// lane then holds one head's scores of four keys and 16 of its output
-// dimensions, and only the softmax runs on the VALU.
+// Inside a wave a K/V block is read as 16-byte packets (16 rows of head_dim
+// elements); the page ids of 64 blocks are fetched at once (one per lane),
+// NBUF blocks are buffered in registers so the next blocks' loads -- and the
+// query of a new row -- are in flight during the math, and no barrier is
+// taken while streaming. The math per block:
+//  - 16-bit K/V (decode_mma): MFMAs give S^T = K . Q^T (16 keys x the G heads
+//    padded to 16) and accumulate O^T += V^T . P^T, V transposed through LDS;
+//    a lane holds one head's scores of four keys and 16 of its output
+//    dimensions, and only the online softmax runs on the VALU;
+//  - 32-bit K/V: LPR lanes cover one row's head_dim, RPL = 64/LPR rows are
+//    read per instruction and each lane owns NR = 16/RPL rows of the block;
+//    scores are reduced over the LPR lanes of a row with DPP adds, each lane
+//    group keeps its own online-softmax state (running max m in log2 units,
+//    sum l, acc) and the groups are merged when the wave's part of a row ends.
 #pragma once
 
 #include <math.h>
@@ -434,15 +432,12 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   // Partial records loaded per batch in a merge: G*DPL + 1 words per lane each.
   constexpr int MC = 64 / (G * DPL + 1) > 8 ? 8 : (64 / (G * DPL + 1) < 2 ? 2 : 64 / (G * DPL + 1));
   // Register buffers per wave: while one block is computed, NBUF - 1 are in
-  // flight. 16-bit K/V at head_dim 128 with up to 4 heads per group take
-  // three (the third, 32 VGPRs, still leaves two waves per SIMD): the bytes
-  // in flight then also cover the stretches in which the compute unit's other
-  // workgroup is not streaming (its late start, the end of the launch). At
-  // head_dim 64 a third buffer measured slower (G = 7: the wave is VALU-bound
-  // and the longer register live ranges cost more than the extra block in
-  // flight), and 32-bit K/V and wider groups lack the registers. The
-  // matrix-core decode holds far fewer registers per head and takes three.
-  constexpr int NBUF = ((sizeof(T) == 2 && D == 128 && G <= 4) || kMma) ? 3 : 2;
+  // flight. The matrix-core decode (16-bit K/V) takes three: the bytes in
+  // flight then also cover the stretches in which the compute unit's other
+  // workgroup is not streaming (its late start, the end of the launch), and
+  // its state per head is small enough to keep two waves per SIMD. 32-bit
+  // K/V lacks the registers for a third.
+  constexpr int NBUF = kMma ? 3 : 2;
   constexpr int kPreIssued = 2;  // blocks issued before the prologue's appends
   constexpr int kNewCap = new_row_cap<T>();
   static_assert(kNewCap >= kPreIssued, "pre-issued blocks must find their new rows in LDS");
@@ -858,32 +853,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     float m[G], l[G], acc[G][EPL], nms[G], thr[G];
     int cur_row = -1;
     const float inv_c = 1.f / p.c;
-    // Own-head softmax (16-bit K/V at head_dim 64, three or more heads per
-    // group: eight lanes per key row, two rows per lane). After the row sums
-    // every lane of a row group holds the same G x NR scores, so the softmax
-    // of head g is computed once, by lane g of the group: m_o, l_o, nms_o and
-    // thr_o are that lane's running max, sum, exponent offset and rescale
-    // threshold (lanes past G hold none), and the packed probability pair of
-    // each head, and a rescale's factor, reach the other lanes through
-    // ds_bpermute. m[g] and l[g] are gathered from the owners at the row's end.
-    constexpr bool kOwn = sizeof(T) == 2 && D == 64 && G >= 3 && !kMma;
-    static_assert(!kOwn || (LPR == 8 && NR == 2 && G <= LPR), "own-head layout");
-    // With six or more heads the row sums are a reduce-scatter instead: the
-    // lane in column i of a row group holds the queries of its eight head
-    // slots in the order sig_i(s) = i ^ s (s < 4), (7 - i) ^ (s - 4) (s >= 4)
-    // (a zero query past G). Then three DPP steps -- slots s += slots s+4 of
-    // the mirrored lane 7-i, s += s+2 of lane i^2, s += s+1 of lane i^1 --
-    // leave in slot 0 the full row sums of head i, each exchange adding the
-    // partner's slot that holds the same head: 14 adds instead of an
-    // all-reduce of 14 values (42) and the owner's pick (14).
-    constexpr bool kScatter = kOwn && G >= 6;
-    constexpr int QS = kScatter ? 8 : G;  // query slots per lane
-    uint4 qv[QS];
-    float m_o = -INFINITY, l_o = 0.f, nms_o = 0.f, thr_o = -INFINITY;
-    const int gaddr = (lane & ~(LPR - 1)) * 4;  // ds_bpermute address of the group's lane 0
-    auto from_head = [&](uint32_t v, int g) __attribute__((always_inline)) {
-      return (uint32_t)__builtin_amdgcn_ds_bpermute(gaddr + 4 * g, (int)v);
-    };
+    uint4 qv[G];
     // Matrix-core decode state: lane l works for head l%16 (heads past G have
     // zero queries and are never stored) and holds keys 4*(l/16) .. +3 of
     // each block's S^T column and rows 16t + 4*(l/16) .. +3 of O^T tile t;
@@ -913,10 +883,6 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
       }
-      m_o = -INFINITY;
-      l_o = 0.f;
-      nms_o = 0.f;
-      thr_o = -INFINITY;
     };
     // Ends the wave's part of cur_row: merge the lane groups, then write the
     // output (row wholly inside this wave) or park the state in LDS.
@@ -966,13 +932,6 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
           if (lane == 0) s_part_row[slot] = cur_row;
         }
         return;
-      }
-      if constexpr (kOwn) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          m[g] = __uint_as_float(from_head(__float_as_uint(m_o), g));
-          l[g] = __uint_as_float(from_head(__float_as_uint(l_o), g));
-        }
       }
 #pragma unroll
       for (int off = LPR; off < 64; off <<= 1) {
@@ -1122,211 +1081,103 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
           const mma_i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mma_lds_i16x4_t*)(vrow + 16 * t));
           macc[t] = Mma16<T>::k16(a, pp, macc[t]);
         }
-        return;
-      }
-      if (bf.newrow) {
-        if (cur_row >= 0) finalize();
-        reset();
-        cur_row = bf.row;
-        if (cur_row < q_base || cur_row >= q_top) stage_q_refill(cur_row);
-#pragma unroll
-        for (int g = 0; g < QS; ++g) {
-          if constexpr (kScatter) {
-            const int hd = g < 4 ? (col ^ g) : ((7 - col) ^ (g - 4));
-            const uint4 v = s_q[wave][cur_row - q_base][hd < G ? hd : G - 1][col];
-            qv[g] = hd < G ? v : make_uint4(0, 0, 0, 0);
-          } else {
-            qv[g] = s_q[wave][cur_row - q_base][g][col];
-          }
-        }
-      }
-      // A skipped block (nv = 0) runs the same math with every row masked,
-      // which leaves m, l and acc unchanged; consuming its registers on every
-      // path keeps the compiler's count of loads in flight exact.
-      const int nv = bf.nvalid;
-      uint4 kr[NR], vr[NR];
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        kr[r] = bf.k[r];
-        vr[r] = bf.v[r];
-      }
-      if constexpr (FUSED) {
-        if (bf.sub >= 0) {  // the new token (slot nv-1) may not be stored yet: take it from LDS
-          const int slot = nv - 1;
-          if (rsub == slot % RPL) {
-            const uint4 kn = s_new[wave][bf.sub][0][col], vn = s_new[wave][bf.sub][1][col];
-#pragma unroll
-            for (int r = 0; r < NR; ++r)
-              if (r == slot / RPL) {
-                kr[r] = kn;
-                vr[r] = vn;
-              }
-          }
-        }
-      }
-      // Raw scores q.k, summed over the LPR lanes of each row (all G*NR
-      // partial dots first, then the reduction steps across all of them).
-      float s[G][NR];
-      float sc[NR];  // reduce-scatter: this lane's head's row sums (-inf past G)
-      if constexpr (kScatter) {
-        float x[8][NR];
-#pragma unroll
-        for (int g = 0; g < 8; ++g)
-#pragma unroll
-          for (int r = 0; r < NR; ++r) x[g][r] = Packet<T>::dot0(qv[g], kr[r]);
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int r = 0; r < NR; ++r) x[g][r] += dpp_f32<0x141>(x[g + 4][r]);
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
-#pragma unroll
-          for (int r = 0; r < NR; ++r) x[g][r] += dpp_f32<0x4E>(x[g + 2][r]);
-        // The last step in every lane (a DPP source lane switched off by a
-        // branch would read as 0), and only then the pick of lanes past G.
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          float t = x[0][r] + dpp_f32<0xB1>(x[1][r]);
-          asm volatile("" : "+v"(t));
-          sc[r] = col < G ? t : -INFINITY;
-        }
       } else {
-        float part[G * NR];
+        // 32-bit K/V: the lane-group math on the VALU.
+        if (bf.newrow) {
+          if (cur_row >= 0) finalize();
+          reset();
+          cur_row = bf.row;
+          if (cur_row < q_base || cur_row >= q_top) stage_q_refill(cur_row);
 #pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int r = 0; r < NR; ++r) part[g * NR + r] = Packet<T>::dot0(qv[g], kr[r]);
-        group_sum_n<LPR>(part);
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int r = 0; r < NR; ++r) s[g][r] = part[g * NR + r];
-      }
-      if (nv < 16) {  // tail block: rows past the sequence end get p = 0 and V = 0
+          for (int g = 0; g < G; ++g) qv[g] = s_q[wave][cur_row - q_base][g][col];
+        }
+        // A skipped block (nv = 0) runs the same math with every row masked,
+        // which leaves m, l and acc unchanged; consuming its registers on every
+        // path keeps the compiler's count of loads in flight exact.
+        const int nv = bf.nvalid;
+        uint4 kr[NR], vr[NR];
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-          if (r * RPL + rsub >= nv) {
-            if constexpr (kScatter) {
-              sc[r] = -INFINITY;
-            } else {
+          kr[r] = bf.k[r];
+          vr[r] = bf.v[r];
+        }
+        if constexpr (FUSED) {
+          if (bf.sub >= 0) {  // the new token (slot nv-1) may not be stored yet: take it from LDS
+            const int slot = nv - 1;
+            if (rsub == slot % RPL) {
+              const uint4 kn = s_new[wave][bf.sub][0][col], vn = s_new[wave][bf.sub][1][col];
+#pragma unroll
+              for (int r = 0; r < NR; ++r)
+                if (r == slot / RPL) {
+                  kr[r] = kn;
+                  vr[r] = vn;
+                }
+            }
+          }
+        }
+        // Raw scores q.k, summed over the LPR lanes of each row (all G*NR
+        // partial dots first, then the reduction steps across all of them).
+        float s[G][NR];
+        {
+          float part[G * NR];
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) part[g * NR + r] = Packet<T>::dot0(qv[g], kr[r]);
+          group_sum_n<LPR>(part);
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) s[g][r] = part[g * NR + r];
+        }
+        if (nv < 16) {  // tail block: rows past the sequence end get p = 0 and V = 0
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            if (r * RPL + rsub >= nv) {
 #pragma unroll
               for (int g = 0; g < G; ++g) s[g][r] = -INFINITY;
+              vr[r] = make_uint4(0, 0, 0, 0);
             }
-            vr[r] = make_uint4(0, 0, 0, 0);
           }
         }
-      }
-      // 16-bit V: pair rows (r, r+1) element-wise so one v_dot2 applies two
-      // probabilities; the pairing is shared by all G heads.
-      constexpr bool kPacked = sizeof(T) == 2;
-      uint32_t vpair[kPacked ? NR / 2 : 1][4][2];
-      float vf[kPacked ? 1 : NR][EPL];
-      if constexpr (kPacked) {
-#pragma unroll
-        for (int r = 0; r < NR; r += 2) {
-          const uint32_t w0[4] = {vr[r].x, vr[r].y, vr[r].z, vr[r].w};
-          const uint32_t w1[4] = {vr[r + 1].x, vr[r + 1].y, vr[r + 1].z, vr[r + 1].w};
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            vpair[r / 2][k][0] = __builtin_amdgcn_perm(w1[k], w0[k], 0x05040100u);  // low halves
-            vpair[r / 2][k][1] = __builtin_amdgcn_perm(w1[k], w0[k], 0x07060302u);  // high halves
-          }
-        }
-      } else {
+        float vf[NR][EPL];
 #pragma unroll
         for (int r = 0; r < NR; ++r) Packet<T>::unpack(vr[r], vf[r]);
-      }
-      if constexpr (kOwn) {
-        // This lane's head: its scores of the lane's two rows (-inf past G).
-        float so[NR];
+        // Lazy rescaling: a running max moves only when a scaled score exceeds
+        // it by more than kLazyLog2 (probabilities then stay below
+        // 2^kLazyLog2). The test compares raw scores with thr (c > 0), every
+        // head at once; when any lane of the wave needs it, every head's max
+        // moves to its largest score so far.
+        float cand[G];
+        bool move = false;
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          float v = -INFINITY;
-          if constexpr (kScatter) {
-            v = sc[r];
-          } else {
+        for (int g = 0; g < G; ++g) {
+          cand[g] = s[g][0];
 #pragma unroll
-            for (int g = 0; g < G; ++g) v = col == g ? s[g][r] : v;
-          }
-          so[r] = v;
+          for (int r = 1; r < NR; ++r) cand[g] = fmaxf(cand[g], s[g][r]);
+          move = move || cand[g] > thr[g];
         }
-        const float cand = fmaxf(so[0], so[1]);
-        if (__any(cand > thr_o)) {  // lazy rescaling, as below, per owning lane
-          const float mn = fmaxf(m_o, cand * p.c);
-          const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_o - mn);
-          l_o *= alpha;
-          m_o = mn;
-          nms_o = (mn == -INFINITY) ? 0.f : -mn;
-          thr_o = (mn == -INFINITY) ? -INFINITY : (mn + kLazyLog2) * inv_c;
+        if (__any(move)) {
 #pragma unroll
           for (int g = 0; g < G; ++g) {
-            const float a = __uint_as_float(from_head(__float_as_uint(alpha), g));
+            const float mn = fmaxf(m[g], cand[g] * p.c);
+            const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m[g] - mn);
+            l[g] *= alpha;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[g][e] *= a;
+            for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
+            m[g] = mn;
+            nms[g] = (mn == -INFINITY) ? 0.f : -mn;
+            thr[g] = (mn == -INFINITY) ? -INFINITY : (mn + kLazyLog2) * inv_c;
           }
         }
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(so[0], p.c, nms_o));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(so[1], p.c, nms_o));
-        l_o += p0;
-        l_o += p1;
-        const uint32_t pp_o = Packet<T>::pack2(p0, p1);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const uint32_t pp = from_head(pp_o, g);
+          float pr[NR];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            acc[g][2 * k] = Packet<T>::dot2(vpair[0][k][0], pp, acc[g][2 * k]);
-            acc[g][2 * k + 1] = Packet<T>::dot2(vpair[0][k][1], pp, acc[g][2 * k + 1]);
+          for (int r = 0; r < NR; ++r) {
+            pr[r] = __builtin_amdgcn_exp2f(fmaf(s[g][r], p.c, nms[g]));
+            l[g] += pr[r];
           }
-        }
-        return;
-      }
-      // Lazy rescaling: a running max moves only when a scaled score exceeds
-      // it by more than kLazyLog2 (probabilities then stay below
-      // 2^kLazyLog2). The test compares raw scores with thr (c > 0), every
-      // head at once; when any lane of the wave needs it, every head's max
-      // moves to its largest score so far.
-      float cand[G];
-      bool move = false;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        cand[g] = s[g][0];
-#pragma unroll
-        for (int r = 1; r < NR; ++r) cand[g] = fmaxf(cand[g], s[g][r]);
-        move = move || cand[g] > thr[g];
-      }
-      if (__any(move)) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float mn = fmaxf(m[g], cand[g] * p.c);
-          const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m[g] - mn);
-          l[g] *= alpha;
-#pragma unroll
-          for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
-          m[g] = mn;
-          nms[g] = (mn == -INFINITY) ? 0.f : -mn;
-          thr[g] = (mn == -INFINITY) ? -INFINITY : (mn + kLazyLog2) * inv_c;
-        }
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float pr[NR];
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          pr[r] = __builtin_amdgcn_exp2f(fmaf(s[g][r], p.c, nms[g]));
-          l[g] += pr[r];
-        }
-        if constexpr (kPacked) {
-#pragma unroll
-          for (int r = 0; r < NR; r += 2) {
-            const uint32_t pp = Packet<T>::pack2(pr[r], pr[r + 1]);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              acc[g][2 * k] = Packet<T>::dot2(vpair[r / 2][k][0], pp, acc[g][2 * k]);
-              acc[g][2 * k + 1] = Packet<T>::dot2(vpair[r / 2][k][1], pp, acc[g][2 * k + 1]);
-            }
-          }
-        } else {
 #pragma unroll
           for (int e = 0; e < EPL; ++e) {
             float a = acc[g][e];
