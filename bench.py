@@ -99,6 +99,10 @@ def parse():
     ap.add_argument("--eager", action="store_true",
                     help="whole-step workloads: launch every op from the host each step "
                          "instead of replaying the step captured as a HIP graph")
+    ap.add_argument("--no-cascade", action="store_true",
+                    help="fork workload: decode every sequence's prefix pages in the decode "
+                         "launch (rlse_decode_step_planned) instead of once per batch "
+                         "(rlse_decode_step_cascade)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 1 GiB (HBM counter calibration)")
     return ap.parse_args()
@@ -304,9 +308,13 @@ def fork_bench(args):
     layers in one allocation, one block id spanning the layers), 64 requests
     forked from it by the block manager (full pages shared, the trailing
     partial page copied on write), each with a private suffix. The fork runs
-    once per request and is timed on its own; one step = one rlse_decode_step
+    once per request and is timed on its own; one step = one fused decode step
     per layer for the 64 forked sequences (append of the new token + decode
-    over shared prefix pages and private suffix pages)."""
+    over shared prefix pages and private suffix pages): by default the
+    cascade step (rlse_decode_step_cascade: the shared full pages attended once
+    for the batch, then each sequence's own pages, streamed), with
+    --no-cascade the planned step over every sequence's whole table (prefix
+    pages cacheable, re-read by every row)."""
     import numpy as np
     import torch
 
@@ -380,19 +388,36 @@ def fork_bench(args):
     stream = torch.cuda.current_stream()
     scale = 1.0 / math.sqrt(d)
     ptrs = [pool.layer(layer) for layer in range(layers)]
+    cascade = not args.no_cascade
+    shared = plen // 16      # full prefix pages, the same in every table
+    pre_bytes = kv.decode_prefix_size(b, hq, d, shared)
+    pre = torch.zeros(pre_bytes, dtype=torch.uint8, device=dev)
 
     def step(evs=None):
         # evs: one event pair around the step's back-to-back decode launches.
-        kv.decode_plan(t_dev, lens_dev, b, hkv, mbps, nb, plan, plan_bytes, stream)
+        if cascade:
+            kv.decode_plan_cascade(t_dev, lens_dev, b, hkv, mbps, nb, shared, plan, plan_bytes,
+                                   stream)
+        else:
+            kv.decode_plan(t_dev, lens_dev, b, hkv, mbps, nb, plan, plan_bytes, stream)
         if evs is not None:
             evs[0].record(stream)
         for layer in range(layers):
-            # The prefix pages are read by all b rows: they stay cacheable (no
-            # RLSE_DECODE_STREAM), so their re-reads hit the caches.
-            kv.decode_step_planned(q_in[layer], k_in[layer], v_in[layer], qw, kw, 1e-6, cos_t,
-                                   sin_t, max_pos, ptrs[layer][0], ptrs[layer][1], t_dev,
-                                   lens_dev, out, b, hq, hkv, d, mbps, nb, scale, "bf16", plan,
-                                   ws, ws_bytes, stream)
+            if cascade:
+                # The shared pages are attended once for the batch; the
+                # launch after it reads each page once (streamed).
+                kv.decode_step_cascade(q_in[layer], k_in[layer], v_in[layer], qw, kw, 1e-6,
+                                       cos_t, sin_t, max_pos, ptrs[layer][0], ptrs[layer][1],
+                                       t_dev, lens_dev, out, b, hq, hkv, d, mbps, nb, scale,
+                                       "bf16", plan, shared, pre, pre_bytes, ws, ws_bytes,
+                                       stream, stream_pages=True)
+            else:
+                # The prefix pages are read by all b rows: they stay cacheable
+                # (no RLSE_DECODE_STREAM), so their re-reads hit the caches.
+                kv.decode_step_planned(q_in[layer], k_in[layer], v_in[layer], qw, kw, 1e-6,
+                                       cos_t, sin_t, max_pos, ptrs[layer][0], ptrs[layer][1],
+                                       t_dev, lens_dev, out, b, hq, hkv, d, mbps, nb, scale,
+                                       "bf16", plan, ws, ws_bytes, stream)
         if evs is not None:
             evs[1].record(stream)
 
@@ -423,13 +448,17 @@ def fork_bench(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic N(0,1) prefix/suffix K/V and q, block-manager page placement",
         "config": {"workload": desc, "batch": b, "layers": layers, "prefix": plen,
+                   "cascade_pages": shared if cascade else 0,
                    "mean_keys": float(np.mean(lens)), "fork_ms": fork_ms,
                    "cow_pages_per_layer": len(src), "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "decode_kernel planned fused step "
-                               "(rlse_decode_step_planned, cacheable pages)",
+                     "kernel": ("decode_prefix_kernel + decode_kernel cascade step "
+                                "(rlse_decode_step_cascade, the batch's shared pages attended "
+                                "once, the rest streamed)" if cascade else
+                                "decode_kernel planned fused step "
+                                "(rlse_decode_step_planned, cacheable pages)"),
                      "bytes_per_launch": compulsory, "logical_bytes_per_launch": logical,
                      "effective_GBps": logical / (avg_ms * 1e-3) / 1e9,
                      "avg_launch_ms": avg_ms, "timed_launches": ev_steps * layers},

@@ -58,19 +58,25 @@ int rlse_version(void);
 /*   RLSE_WS_ERR_LENGTH: a sequence length exceeded its block table    */
 /*     (max_blocks_per_seq*16); its output row is zeros and nothing was */
 /*     appended for it.                                                 */
+/*   RLSE_WS_ERR_PREFIX: a cascade step's batch broke its contract (a   */
+/*     sequence's first prefix_pages table entries differ from sequence */
+/*     0's, or its new token lies inside them); the step's outputs are  */
+/*     not its attention.                                               */
 /* The reference turns a failed step into BackendError and quarantines */
 /* the backend (src/backends/candle.rs:689-696); a caller maps a       */
 /* nonzero rlse_workspace_check to the same.                           */
 /* ------------------------------------------------------------------ */
 #define RLSE_WS_ERR_MERGE_TIMEOUT 1u
 #define RLSE_WS_ERR_LENGTH 2u
+#define RLSE_WS_ERR_PREFIX 4u
 /* Synchronises stream, then reads and clears the flags of a decode or
  * projection workspace (NULL: the library's own decode workspaces of the
  * current device -- the one used by calls without a workspace and the
  * static one of rlse_decode_step_noalloc). *flags (may be NULL) receives
  * them. Returns
  * RLSE_ERR_DEVICE_TIMEOUT if a merge timed out, else RLSE_ERR_TOKEN_LIMIT
- * if a length exceeded its table, else 0 (or a hip error). No counterpart
+ * if a length exceeded its table, else RLSE_ERR_INVALID_VALUE if a cascade
+ * step's batch broke its contract, else 0 (or a hip error). No counterpart
  * in the reference: its CPU/Candle ops return errors synchronously. */
 int rlse_workspace_check(void* workspace, rlse_stream_t stream, unsigned* flags);
 /* Bound on a merge's wait for an earlier workgroup's partial, in
@@ -229,6 +235,45 @@ int rlse_decode_step_planned(const void* q, const void* k_new, const void* v_new
                              int num_kv_heads, int head_dim, int max_blocks_per_seq,
                              int num_blocks, float scale, int dtype, void* workspace,
                              size_t workspace_bytes, const void* plan, int flags,
+                             rlse_stream_t stream);
+
+/* Shared-prefix (cascade) decode step. No counterpart in the reference: its
+ * decode attends every sequence's keys separately (src/backends/qwen2.rs:
+ * 177-203), also when sequences were forked from one cached prefix
+ * (src/backends/candle.rs:437-478). When the first prefix_pages entries of
+ * every block table are the same pages and every new token lies past them
+ * (seq_lens[b] - 1 >= 16 * prefix_pages), the prefix's keys are attended
+ * once for all sequences -- a matrix-core tile of 16 query heads per KV head
+ * -- into prefix_buf, and the decode launch that follows streams only each
+ * sequence's own pages and combines the two softmax states per row. Same
+ * arguments and results as rlse_decode_step_planned (within rounding: the
+ * order of the sums over the keys changes), with a plan from
+ * rlse_decode_plan_cascade for the same prefix_pages (or NULL: the
+ * descriptors are derived in the launch, as in rlse_decode_step).
+ * bf16/f16 only; 0 <= prefix_pages <= min(max_blocks_per_seq, 512), 0 being
+ * the plain step. prefix_buf: rlse_decode_prefix_size bytes for the same
+ * batch, num_heads, head_dim and prefix_pages, 16-byte aligned, overwritten
+ * by every call (calls sharing one must be ordered: same stream). Pages of
+ * the prefix are read by one workgroup per slice of about 16 pages and 16
+ * query heads; with more than one slice a second small launch combines the
+ * slices before the decode launch. A batch that breaks the contract
+ * raises RLSE_WS_ERR_PREFIX in the workspace; its outputs are then not its
+ * attention. */
+int rlse_decode_prefix_size(int batch, int num_heads, int head_dim, int prefix_pages,
+                            size_t* bytes);
+int rlse_decode_plan_cascade(const int32_t* block_tables, const int32_t* seq_lens, int batch,
+                             int num_kv_heads, int max_blocks_per_seq, int num_blocks,
+                             int prefix_pages, void* plan, size_t plan_bytes,
+                             rlse_stream_t stream);
+int rlse_decode_step_cascade(const void* q, const void* k_new, const void* v_new,
+                             const void* q_norm_weight, const void* k_norm_weight, float eps,
+                             const void* cos_table, const void* sin_table, int max_pos,
+                             void* k_pool, void* v_pool, const int32_t* block_tables,
+                             const int32_t* seq_lens, void* out, int batch, int num_heads,
+                             int num_kv_heads, int head_dim, int max_blocks_per_seq,
+                             int num_blocks, float scale, int dtype, void* workspace,
+                             size_t workspace_bytes, const void* plan, int flags,
+                             int prefix_pages, void* prefix_buf, size_t prefix_bytes,
                              rlse_stream_t stream);
 
 /* rlse_decode_step for callers that cannot allocate device memory (code

@@ -33,11 +33,12 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __rest
                                                                const int* __restrict__ seq_lens,
                                                                int B, int Hkv, int mbps,
                                                                int num_blocks, int W, int w1,
+                                                               int prefix,
                                                                int4* __restrict__ plan) {
   extern __shared__ int s_pref[];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  if (wave == 0) block_prefix(seq_lens, B, mbps, s_pref, lane < B ? seq_lens[lane] : 0);
+  if (wave == 0) block_prefix(seq_lens, B, mbps, s_pref, lane < B ? seq_lens[lane] : 0, prefix);
   __syncthreads();
   const long long w = blockIdx.x;
   const long long total = (long long)Hkv * s_pref[B];
@@ -49,7 +50,7 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __rest
       const long long ghi = range_lo(w + 1, total, we, W, w1);
       const long long wlo = glo + (ghi - glo) * wave / kWaves;
       const long long whi = glo + (ghi - glo) * (wave + 1) / kWaves;
-      d = block_desc(wlo + lane, whi, s_pref, tables, seq_lens, B, Hkv, mbps, num_blocks);
+      d = block_desc(wlo + lane, whi, s_pref, tables, seq_lens, B, Hkv, mbps, num_blocks, prefix);
     }
   }
   const size_t at = ((size_t)w * kWaves + wave) * 64 + lane;
@@ -257,9 +258,12 @@ extern "C" int rlse_decode_plan_size(size_t* bytes) {
   return RLSE_OK;
 }
 
-extern "C" int rlse_decode_plan(const int32_t* block_tables, const int32_t* seq_lens, int batch,
-                                int num_kv_heads, int max_blocks_per_seq, int num_blocks,
-                                void* plan, size_t plan_bytes, rlse_stream_t stream) {
+static int decode_plan_impl(const int32_t* block_tables, const int32_t* seq_lens, int batch,
+                            int num_kv_heads, int max_blocks_per_seq, int num_blocks, int prefix,
+                            void* plan, size_t plan_bytes, rlse_stream_t stream) {
+  if (prefix < 0 || prefix > max_blocks_per_seq || prefix > kMaxPrefixPages)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_plan: prefix_pages %d outside [0, min(%d, %d)]",
+                prefix, max_blocks_per_seq, kMaxPrefixPages);
   if (batch <= 0 || batch > kMaxDecodeBatch || num_kv_heads <= 0 ||
       (long long)batch * num_kv_heads > kMaxDecodeRows || max_blocks_per_seq <= 0 ||
       num_blocks <= 0 || (long long)max_blocks_per_seq * 16 > 0x7fffffffLL)
@@ -278,8 +282,35 @@ extern "C" int rlse_decode_plan(const int32_t* block_tables, const int32_t* seq_
   const size_t lds = (size_t)(batch + 1) * sizeof(int);
   hipLaunchKernelGGL(decode_plan_kernel, dim3(W), dim3(kThreads), lds, as_stream(stream),
                      block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq, num_blocks,
-                     W, kSlot1Weight, reinterpret_cast<int4*>(plan));
+                     W, kSlot1Weight, prefix, reinterpret_cast<int4*>(plan));
   return launch_status("decode_plan_kernel");
+}
+
+extern "C" int rlse_decode_plan(const int32_t* block_tables, const int32_t* seq_lens, int batch,
+                                int num_kv_heads, int max_blocks_per_seq, int num_blocks,
+                                void* plan, size_t plan_bytes, rlse_stream_t stream) {
+  return decode_plan_impl(block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq,
+                          num_blocks, 0, plan, plan_bytes, stream);
+}
+
+extern "C" int rlse_decode_plan_cascade(const int32_t* block_tables, const int32_t* seq_lens,
+                                        int batch, int num_kv_heads, int max_blocks_per_seq,
+                                        int num_blocks, int prefix_pages, void* plan,
+                                        size_t plan_bytes, rlse_stream_t stream) {
+  return decode_plan_impl(block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq,
+                          num_blocks, prefix_pages, plan, plan_bytes, stream);
+}
+
+extern "C" int rlse_decode_prefix_size(int batch, int num_heads, int head_dim,
+                                       int prefix_pages, size_t* bytes) {
+  if (!bytes) return fail(RLSE_ERR_INVALID_VALUE, "decode_prefix_size: null output");
+  if (batch <= 0 || num_heads <= 0 || head_dim <= 0 || prefix_pages < 0 ||
+      prefix_pages > kMaxPrefixPages)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_prefix_size: bad shape");
+  // The slices' states, then (with more than one slice) their combination.
+  *bytes = (size_t)prefix_regions(prefix_pages) * batch * num_heads *
+           prefix_row_floats(head_dim) * sizeof(float);
+  return RLSE_OK;
 }
 
 static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
@@ -290,6 +321,7 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
                                 int num_kv_heads, int head_dim, int max_blocks_per_seq,
                                 int num_blocks, float scale, int dtype, void* workspace,
                                 size_t workspace_bytes, const void* plan, int flags,
+                                int prefix, void* prefix_buf, size_t prefix_bytes,
                                 rlse_stream_t stream) {
   if (flags & ~RLSE_DECODE_STREAM)
     return fail(RLSE_ERR_INVALID_VALUE, "decode_step: unknown flags 0x%x", flags);
@@ -320,6 +352,46 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
   p.plan = reinterpret_cast<const int4*>(plan);
   const int G = num_heads / num_kv_heads;
   const hipStream_t s = as_stream(stream);
+  if (prefix > 0) {
+    // Cascade step: the shared prefix's partials first, on the same stream.
+    if (dtype != RLSE_DTYPE_BF16 && dtype != RLSE_DTYPE_F16)
+      return fail(RLSE_ERR_INVALID_VALUE, "decode_step_cascade: dtype %d (bf16/f16 only)", dtype);
+    if (prefix > max_blocks_per_seq || prefix > kMaxPrefixPages)
+      return fail(RLSE_ERR_INVALID_VALUE,
+                  "decode_step_cascade: prefix_pages %d above min(max_blocks_per_seq %d, %d)",
+                  prefix, max_blocks_per_seq, kMaxPrefixPages);
+    size_t need = 0;
+    int st2 = rlse_decode_prefix_size(batch, num_heads, head_dim, prefix, &need);
+    if (st2) return st2;
+    if (!prefix_buf || prefix_bytes < need || (uintptr_t)prefix_buf % 16)
+      return fail(RLSE_ERR_BUFFER_TOO_SMALL,
+                  "decode_step_cascade: prefix buffer of %zu bytes (16-byte aligned) needed, %zu "
+                  "given", need, prefix_bytes);
+    PrefixParams pp;
+    pp.q = q;
+    pp.k_pool = k_pool;
+    pp.v_pool = v_pool;
+    pp.tables = block_tables;
+    pp.seq_lens = seq_lens;
+    pp.qw = q_norm_weight;
+    pp.cos_t = cos_table;
+    pp.sin_t = sin_table;
+    pp.eps = eps;
+    pp.inv_d = p.inv_d;
+    pp.c = p.c;
+    pp.B = batch;
+    pp.Hkv = num_kv_heads;
+    pp.mbps = max_blocks_per_seq;
+    pp.num_blocks = num_blocks;
+    pp.prefix = prefix;
+    pp.pre = reinterpret_cast<float*>(prefix_buf);
+    pp.ws_err = p.ws_err;
+    st2 = launch_decode_prefix(dtype, head_dim, G, pp, s);
+    if (st2) return st2;
+    p.prefix = prefix;
+    p.pre = pp.pre + (size_t)(prefix_regions(prefix) - 1) * batch * num_heads *
+                         prefix_row_floats(head_dim);
+  }
   if (!plan) return launch_decode_dtype<kModeFused>(dtype, head_dim, G, p, s);
   return (flags & RLSE_DECODE_STREAM)
              ? launch_decode_dtype<kModePlannedStream>(dtype, head_dim, G, p, s)
@@ -337,7 +409,8 @@ extern "C" int rlse_decode_step(const void* q, const void* k_new, const void* v_
   return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
                           sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
                           num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
-                          scale, dtype, workspace, workspace_bytes, nullptr, 0, stream);
+                          scale, dtype, workspace, workspace_bytes, nullptr, 0, 0, nullptr, 0,
+                          stream);
 }
 
 extern "C" int rlse_decode_step_planned(
@@ -351,7 +424,25 @@ extern "C" int rlse_decode_step_planned(
   return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
                           sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
                           num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
-                          scale, dtype, workspace, workspace_bytes, plan, flags, stream);
+                          scale, dtype, workspace, workspace_bytes, plan, flags, 0, nullptr, 0,
+                          stream);
+}
+
+extern "C" int rlse_decode_step_cascade(
+    const void* q, const void* k_new, const void* v_new, const void* q_norm_weight,
+    const void* k_norm_weight, float eps, const void* cos_table, const void* sin_table,
+    int max_pos, void* k_pool, void* v_pool, const int32_t* block_tables,
+    const int32_t* seq_lens, void* out, int batch, int num_heads, int num_kv_heads, int head_dim,
+    int max_blocks_per_seq, int num_blocks, float scale, int dtype, void* workspace,
+    size_t workspace_bytes, const void* plan, int flags, int prefix_pages, void* prefix_buf,
+    size_t prefix_bytes, rlse_stream_t stream) {
+  if (prefix_pages < 0)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_step_cascade: prefix_pages %d < 0", prefix_pages);
+  return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
+                          sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
+                          num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
+                          scale, dtype, workspace, workspace_bytes, plan, flags, prefix_pages,
+                          prefix_buf, prefix_bytes, stream);
 }
 
 static int compat_decode(const void* q, const void* k, const void* v, const int* tables,
@@ -464,7 +555,7 @@ extern "C" int rlse_decode_step_noalloc(
   return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
                           sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
                           num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
-                          scale, dtype, ws, need, nullptr, 0, stream);
+                          scale, dtype, ws, need, nullptr, 0, 0, nullptr, 0, stream);
 }
 
 extern "C" int rlse_workspace_check(void* workspace, rlse_stream_t stream, unsigned* flags) {

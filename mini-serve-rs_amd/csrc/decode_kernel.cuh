@@ -87,14 +87,16 @@ __device__ __forceinline__ int valid_len(int L, int mbps) {
 // Exclusive prefix of per-sequence block counts into s_pref[0..B] (one wave).
 // first: seq_lens[lane] for lane < B, requested by the caller beforehand.
 // (The first chunk issues no load, so a caller with loads in flight does not
-// wait for them here.)
+// wait for them here.) prefix: leading blocks of every sequence left out of
+// the stream (a shared prefix attended separately; 0 = none).
 __device__ void block_prefix(const int* __restrict__ seq_lens, int B, int mbps, int* s_pref,
-                             int first) {
+                             int first, int prefix) {
   const int lane = threadIdx.x & 63;
   int carry = 0;
   auto chunk = [&](int base, int len) __attribute__((always_inline)) {
     const int b = base + lane;
     int x = b < B ? (valid_len(len, mbps) + 15) >> 4 : 0;
+    x = x > prefix ? x - prefix : 0;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const int y = __shfl_up(x, o, 64);
@@ -160,10 +162,11 @@ __device__ __forceinline__ int locate_seq(const int* s_pref, int B, int Hkv, lon
 // the valid rows in bits 0-7 (0 for a page id outside the pool) with bit 8
 // set on the last block of its row, the (sequence, KV head) row and the
 // row's new-token position. Blocks past the wave's end get {0, 0, -1, 0}.
+// A row's stream starts at table entry `prefix` (block_prefix).
 __device__ __forceinline__ int4 block_desc(long long f, long long whi, const int* s_pref,
                                            const int* __restrict__ tables,
                                            const int* __restrict__ seq_lens, int B, int Hkv,
-                                           int mbps, int num_blocks) {
+                                           int mbps, int num_blocks, int prefix) {
   int4 d = make_int4(0, 0, -1, 0);
   if (f < whi) {
     const int b = locate_seq(s_pref, B, Hkv, f);
@@ -171,9 +174,9 @@ __device__ __forceinline__ int4 block_desc(long long f, long long whi, const int
     const long long o = f - (long long)Hkv * s_pref[b];
     const int kvh = (int)(o / nb), blk = (int)(o % nb);
     d.z = b * Hkv + kvh;
-    d.x = tables[(size_t)b * mbps + blk];
+    d.x = tables[(size_t)b * mbps + prefix + blk];
     const int L = valid_len(seq_lens[b], mbps);
-    const int nv = L - blk * 16;
+    const int nv = L - (prefix + blk) * 16;
     d.y = nv > 16 ? 16 : nv;
     d.w = L - 1;
     if ((unsigned)d.x >= (unsigned)num_blocks)
@@ -229,7 +232,57 @@ struct DecodeParams {
   // descriptors of every wave, as block_desc computes them. Null: each wave
   // derives them from the lengths and the block tables.
   const int4* plan;
+  // Shared-prefix (cascade) step, 16-bit K/V only: the first `prefix` table
+  // entries of every sequence are left out of the stream, and every row's
+  // result is combined with `pre`, the softmax state of its query heads over
+  // those pages ([B][Hq][D + 4] floats: acc[D], m, l in log2 units), when the
+  // row is finished. prefix 0 and pre null: none.
+  int prefix;
+  const float* pre;
 };
+
+// Floats per (sequence, query head) of a prefix partial: acc[D], m, l, and
+// two of padding so that rows stay 16-byte aligned.
+__host__ __device__ constexpr int prefix_row_floats(int D) { return D + 4; }
+
+// Shared-prefix partial attention of a cascade decode step
+// (decode_prefix.hip): the softmax state of every query head over the first
+// `prefix` table entries, which every sequence of the batch shares.
+struct PrefixParams {
+  const void* q;  // [B][Hq][D] raw queries (q_norm + RoPE applied here, as the decode does)
+  const void* k_pool;
+  const void* v_pool;
+  const int* tables;  // [B][mbps]; sequence 0's first `prefix` entries are the shared pages
+  const int* seq_lens;
+  const void* qw;  // q RMSNorm weight [D] (null: no norm)
+  const void* cos_t;
+  const void* sin_t;
+  float eps;
+  float inv_d;
+  float c;  // scale * log2(e)
+  int B;
+  int Hkv;
+  int mbps;
+  int num_blocks;
+  int prefix;
+  float* pre;        // prefix_regions(prefix) x [B][Hq][prefix_row_floats(D)]
+  uint32_t* ws_err;  // sticky flags: RLSE_WS_ERR_PREFIX
+};
+// Longest shared prefix a cascade step takes, in pages (8192 tokens).
+constexpr int kMaxPrefixPages = 512;
+// Slices of the prefix attended by separate workgroups (each leaves its own
+// softmax state, a second launch combines them): about 16 pages per slice,
+// at most 8 slices.
+__host__ __device__ constexpr int prefix_splits(int prefix) {
+  return prefix <= 16 ? 1 : ((prefix + 15) / 16 > 8 ? 8 : (prefix + 15) / 16);
+}
+// Prefix partial regions of a cascade step: one per slice, then (with more
+// than one slice) the combined states, which the decode reads.
+__host__ __device__ constexpr int prefix_regions(int prefix) {
+  return prefix_splits(prefix) > 1 ? prefix_splits(prefix) + 1 : 1;
+}
+
+int launch_decode_prefix(int dtype, int D, int G, const PrefixParams& p, hipStream_t s);
 
 // Combines (m, l, a) with (mo, lo, ao), all in log2 units; -inf maxima mean
 // "empty" and never produce NaN.
@@ -612,7 +665,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       load_pages(k == 0 ? b0 : b1, __builtin_amdgcn_readlane(plan_d.x, k), kvh, nv > 0);
     }
   }
-  if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref, len_t0);
+  if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref, len_t0, p.prefix);
   if constexpr (FUSED) {
     if (tid < B) s_len[tid] = valid_len(len_t0, mbps);
     for (int b = tid + kThreads; b < B; b += kThreads) s_len[b] = valid_len(p.seq_lens[b], mbps);
@@ -671,7 +724,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         d = plan_d;
       else
         d = block_desc(wlo + base + lane, whi, s_pref, p.tables, p.seq_lens, B, Hkv, mbps,
-                       p.num_blocks);
+                       p.num_blocks, p.prefix);
       d_id = d.x;
       d_nv = d.y;
       d_row = d.z;
@@ -896,6 +949,23 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         row_extent(cur_row, R, nb);
         const int b = cur_row / Hkv, kvh = cur_row - b * Hkv;
         if (R >= wlo && R + nb <= whi) {
+          if (p.pre) {  // cascade step: the row's softmax state over the shared prefix
+            const float* pr = p.pre + ((size_t)b * Hq + (size_t)kvh * G + (mh < G ? mh : 0)) *
+                                          prefix_row_floats(D);
+            const float pm = pr[D], pl = pr[D + 1];
+            const float M = fmaxf(m1, pm);
+            const float Ms = (M == -INFINITY) ? 0.f : M;
+            const float sa = __builtin_amdgcn_exp2f(m1 - Ms), sb = __builtin_amdgcn_exp2f(pm - Ms);
+            lt = lt * sa + pl * sb;
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t) {
+              const float4 pa = *reinterpret_cast<const float4*>(pr + 16 * t + 4 * mq);
+              macc[t][0] = macc[t][0] * sa + pa.x * sb;
+              macc[t][1] = macc[t][1] * sa + pa.y * sb;
+              macc[t][2] = macc[t][2] * sa + pa.z * sb;
+              macc[t][3] = macc[t][3] * sa + pa.w * sb;
+            }
+          }
           if (mh < G) {
             const float inv = lt > 0.f ? 1.f / lt : 0.f;  // all pages skipped -> zeros
             T* dst = ob + ((size_t)b * Hq + (size_t)kvh * G + mh) * D + 4 * mq;
@@ -1378,6 +1448,17 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
           }
       }
       if (!ok && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_MERGE_TIMEOUT);
+    }
+    if (p.pre) {  // cascade step: the row's softmax state over the shared prefix
+      constexpr int PF = prefix_row_floats(D);
+      const float* pr = p.pre + ((size_t)b * Hq + (size_t)kvh * G) * PF;
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < DPL; ++k)
+          if (lane + 64 * k < D)
+            lse_combine(M[g][k], Ls[g][k], A[g][k], pr[g * PF + D], pr[g * PF + D + 1],
+                        pr[g * PF + lane + 64 * k]);
     }
     // Output of a row inside the group's range or merged above (NaN if a
     // partial did not arrive within the wait bound).

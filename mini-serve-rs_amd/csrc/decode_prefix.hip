@@ -1,0 +1,382 @@
+// Shared-prefix (cascade) attention of a decode step, 16-bit K/V.
+//
+// When every sequence of a batch was forked from one cached prefix, the first
+// P entries of all block tables are the same pages (refcounted, see
+// rlse_bm_fork / rlse_pc_fork). Attending them once per sequence reads each
+// prefix page B times; here they are attended once for the whole batch: per
+// KV head h, the B*G query vectors of h are taken 16 at a time as the columns
+// of the decode's matrix-core block math (S^T = K . Q^T on 16x16x32 MFMAs,
+// O^T += V^T . P^T on 16x16x16 MFMAs with V transposed through LDS). The
+// prefix is cut into NS = prefix_splits(P) slices of about 16 pages, one
+// workgroup per (column tile, KV head, slice), and each wave of a workgroup
+// takes its own pages of the slice. The waves' partial softmax states are
+// combined in LDS (pairwise, in a fixed order) into the slice's state; with
+// more than one slice a second launch combines the slices' states in slice
+// order into each query's state over the whole prefix -- acc[D], m, l in the
+// decode's log2 units -- which the decode launch combines into each row it
+// finishes; it leaves the prefix out of its page stream. Workgroups are
+// numbered so that the column tiles reading one slice's pages run on one XCD
+// and share its L2.
+// The queries get q_norm + RoPE at their sequence's new position exactly as
+// the decode stages them, so both launches see the same query bytes.
+//
+// Reference semantics are those of decode_attention_gqa_zero_copy
+// (src/backends/qwen2.rs:177-203) over the sequence's full key range; the
+// split of the keys into prefix and suffix changes only the order of the
+// softmax sums.
+#include "decode_kernel.cuh"
+
+namespace rlse {
+namespace {
+
+constexpr int kPrefixWaves = 8;
+static_assert(kMaxPrefixPages <= 64 * kPrefixWaves, "a wave holds the page ids of 64 blocks");
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(PrefixParams p) {
+  using S = DecodeShape<T, D>;
+  constexpr int EPL = S::EPL, LPR = S::LPR, RPL = S::RPL, NR = S::NR;
+  constexpr int NT = D / 16;                   // O^T tiles
+  constexpr int PF = prefix_row_floats(D);     // floats per stored (sequence, head)
+  constexpr int PL = 2 + 4 * NT;               // a lane's partial: m, l, acc
+  struct Lds {
+    uint4 q[16][LPR];  // the tile's 16 queries, normed and roped
+    union {
+      uint4 vt[kPrefixWaves][16][(D + 16) / 8];  // each wave's V block (padded rows)
+      float part[kPrefixWaves / 2][PL][64];      // partials handed between waves
+    } u;
+  };
+  __shared__ Lds lds;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int col = lane % LPR, rsub = lane / LPR;
+  const int mh = lane & 15, mq = lane >> 4;
+  const int B = p.B, Hkv = p.Hkv, Hq = Hkv * G, ncols = B * G, P = p.prefix;
+  // Workgroup id -> (slice set ps = h * NS + sp, column tile c): the tiles of
+  // one slice set share id % 8, i.e. one XCD (workgroups are dealt to the
+  // XCDs round-robin); ids past the last slice set have no work.
+  const int NS = prefix_splits(P), NC = (ncols + 15) / 16;
+  const int id = blockIdx.x, xq = id >> 3;
+  const int ps = (xq / NC) * 8 + (id & 7), c = xq % NC;
+  if (ps >= Hkv * NS) return;
+  const int h = ps / NS, sp = ps - h * NS, c0 = c * 16;
+  const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
+  const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
+  const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
+
+
+  // This wave's pages: slice sp of the prefix, then the wave's share of it.
+  const int PS = (P + NS - 1) / NS;
+  const int slo = sp * PS < P ? sp * PS : P, shi = slo + PS < P ? slo + PS : P;
+  const int per = (shi - slo + kPrefixWaves - 1) / kPrefixWaves;
+  const int lo = slo + wave * per < shi ? slo + wave * per : shi;
+  const int hi = lo + per < shi ? lo + per : shi;
+  // Lane i holds the page id of block lo + i (a wave takes at most 64).
+  const int ids = lo + lane < hi ? p.tables[lo + lane] : 0;
+
+  // The tile's queries: column j = c0 + i is (sequence j / G, head h*G + j % G).
+  // Their loads go out with the page ids, ahead of the first blocks' loads
+  // (loads complete in order); their math follows those.
+  constexpr int QPASS = 16 / RPL;  // staging passes, one per wave
+  const bool stager = wave < QPASS;
+  const int it = wave * RPL + rsub;
+  const int qj = c0 + it;
+  uint4 sq_x = make_uint4(0, 0, 0, 0), sq_c = sq_x, sq_s = sq_x, sq_w = sq_x;
+  if (stager) {
+    const int jj = qj < ncols ? qj : ncols - 1;
+    const int b = jj / G, g = jj - b * G;
+    sq_x = *reinterpret_cast<const uint4*>(qb + ((size_t)b * Hq + (size_t)h * G + g) * D +
+                                           (size_t)col * EPL);
+    const int L = valid_len(p.seq_lens[b], p.mbps);
+    const int pos = L > 0 ? L - 1 : 0;
+    const size_t to = (size_t)pos * (D / 2) + (size_t)(col % (LPR / 2)) * EPL;
+    sq_c = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.cos_t) + to);
+    sq_s = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.sin_t) + to);
+    const T* wp = reinterpret_cast<const T*>(p.qw ? p.qw : p.q);
+    sq_w = *reinterpret_cast<const uint4*>(wp + col * EPL);
+  }
+
+  uint4 qv[NR];
+  float m1 = -INFINITY, l1 = 0.f, nms1 = 0.f, thr1 = -INFINITY;
+  const float inv_c = 1.f / p.c;
+  mma_f32x4_t macc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) macc[t] = mma_f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  {
+    // K in the MFMA operand layout, V coalesced (as the decode loads them);
+    // a block past the range or on an id outside the pool gets a descriptor
+    // of zero records (zeros, no memory access) and is masked.
+    const size_t tile = (size_t)16 * D;
+    const int koff = (int)(((size_t)(lane & 15) * D + (size_t)(lane >> 4) * EPL) * sizeof(T));
+    const int voff = (int)(((size_t)rsub * D + (size_t)col * EPL) * sizeof(T));
+    struct PBuf {
+      uint4 k[NR];
+      uint4 v[NR];
+      int nv;
+    };
+    auto load = [&](PBuf& bf, int i) __attribute__((always_inline)) {
+      const bool real = i < hi;
+      const int id = __builtin_amdgcn_readlane(ids, real ? i - lo : 0);
+      const bool fetch = real && (unsigned)id < (unsigned)p.num_blocks;
+      bf.nv = fetch ? 16 : 0;
+      const size_t tb = ((size_t)(fetch ? id : 0) * Hkv + h) * tile;
+      const int nrec = fetch ? (int)(tile * sizeof(T)) : 0;
+      const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kp + tb), 0, nrec,
+                                                        kBufferWord3);
+      const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vp + tb), 0, nrec,
+                                                        kBufferWord3);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const u32x4_t kx =
+            __builtin_amdgcn_raw_buffer_load_b128(rk, koff + r * 32 * (int)sizeof(T), 0, 0);
+        const u32x4_t vx =
+            __builtin_amdgcn_raw_buffer_load_b128(rv, voff + r * RPL * D * (int)sizeof(T), 0, 0);
+        bf.k[r] = make_uint4(kx.x, kx.y, kx.z, kx.w);
+        bf.v[r] = make_uint4(vx.x, vx.y, vx.z, vx.w);
+      }
+    };
+    PBuf b0, b1, b2;
+    load(b0, lo);
+    load(b1, lo + 1);
+    load(b2, lo + 2);
+    // The queries' math, then the barrier that publishes them.
+    if (stager) {
+      const uint4 y = norm_rope_packet<T, D>(sq_x, p.qw != nullptr, sq_w, p.inv_d, p.eps, sq_c,
+                                             sq_s, col);
+      lds.q[it][col] = qj < ncols ? y : make_uint4(0, 0, 0, 0);
+    }
+    consume(sq_x);
+    consume(sq_c);
+    consume(sq_s);
+    consume(sq_w);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) qv[r] = lds.q[mh][4 * r + mq];
+    // The decode's block math (decode_body, matrix-core path) on one block.
+    auto compute = [&](const PBuf& bf) __attribute__((always_inline)) {
+      const int nv = bf.nv;
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+        lds.u.vt[wave][r * RPL + rsub][col] = nv > 0 ? bf.v[r] : make_uint4(0, 0, 0, 0);
+      mma_f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < NR; ++r) sacc = Mma16<T>::k32(bf.k[r], qv[r], sacc);
+      float sv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = 4 * mq + i < nv ? sacc[i] : -INFINITY;
+      const float cand = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      if (__any(cand > thr1)) {
+        float cm = fmaxf(cand, __shfl_xor(cand, 16, 64));
+        cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+        const float mn = fmaxf(m1, cm * p.c);
+        const float alpha = (mn == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m1 - mn);
+        l1 *= alpha;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) macc[t][i] *= alpha;
+        m1 = mn;
+        nms1 = (mn == -INFINITY) ? 0.f : -mn;
+        thr1 = (mn == -INFINITY) ? -INFINITY : (mn + kLazyLog2) * inv_c;
+      }
+      float pr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], p.c, nms1));
+        l1 += pr[i];
+      }
+      const uint2 pp = make_uint2(Packet<T>::pack2(pr[0], pr[1]), Packet<T>::pack2(pr[2], pr[3]));
+      const uint16_t* vrow =
+          reinterpret_cast<const uint16_t*>(&lds.u.vt[wave][4 * mq + ((lane & 15) >> 2)][0]) +
+          4 * (lane & 3);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const mma_i16x4_t a =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((mma_lds_i16x4_t*)(vrow + 16 * t));
+        macc[t] = Mma16<T>::k16(a, pp, macc[t]);
+      }
+    };
+    // Blocks i + 1 and i + 2 in flight while block i is computed.
+    for (int i = lo; i < hi;) {
+      compute(b0);
+      if (++i == hi) break;
+      load(b0, i + 2);
+      compute(b1);
+      if (++i == hi) break;
+      load(b1, i + 2);
+      compute(b2);
+      if (++i == hi) break;
+      load(b2, i + 2);
+    }
+  }
+
+  // Pairwise combine of the waves' partials, wave w + half into wave w,
+  // halving until wave 0 holds the tile's state over the whole prefix. The V
+  // blocks are dead here: the partials take their LDS.
+  __syncthreads();
+#pragma unroll
+  for (int half = kPrefixWaves / 2; half >= 1; half >>= 1) {
+    if (wave >= half && wave < 2 * half) {
+      float(&dst)[PL][64] = lds.u.part[wave - half];
+      dst[0][lane] = m1;
+      dst[1][lane] = l1;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[2 + 4 * t + i][lane] = macc[t][i];
+    }
+    __syncthreads();
+    if (wave < half) {
+      const float(&src)[PL][64] = lds.u.part[wave];
+      const float pm = src[0][lane], pl = src[1][lane];
+      const float M = fmaxf(m1, pm);
+      const float Ms = (M == -INFINITY) ? 0.f : M;
+      const float sa = __builtin_amdgcn_exp2f(m1 - Ms), sb = __builtin_amdgcn_exp2f(pm - Ms);
+      l1 = l1 * sa + pl * sb;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) macc[t][i] = macc[t][i] * sa + src[2 + 4 * t + i][lane] * sb;
+      m1 = M;
+    }
+    __syncthreads();
+  }
+
+  if (wave == 0) {
+    // The head's sum over its four lanes; m1 is common to them.
+    float lt = l1 + __shfl_xor(l1, 16, 64);
+    lt = lt + __shfl_xor(lt, 32, 64);
+    const int j = c0 + mh;
+    const int jj = j < ncols ? j : ncols - 1;
+    const int b = jj / G, g = jj - b * G;
+    // This slice's states, in region sp (with one slice, the final ones).
+    const size_t slice = (size_t)B * Hq * PF;  // floats of one region
+    float* dst = p.pre + (size_t)sp * slice + ((size_t)b * Hq + (size_t)h * G + g) * PF;
+    if (j < ncols) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        *reinterpret_cast<float4*>(dst + 16 * t + 4 * mq) =
+            make_float4(macc[t][0], macc[t][1], macc[t][2], macc[t][3]);
+      if (mq == 0) {
+        dst[D] = m1;
+        dst[D + 1] = lt;
+      }
+    }
+  } else if (wave == 1) {
+    // Wave 1 of each workgroup checks a slice of the batch against the
+    // contract: every sequence's first P table entries are sequence 0's, and
+    // its new token (position L - 1) lies past them.
+    const int nwork = Hkv * NS * NC;
+    bool bad = false;
+    for (int b = ps * NC + c; b < B; b += nwork) {
+      const int L = p.seq_lens[b];
+      bad = bad || L <= 16 * P || L > p.mbps * 16;
+      for (int i = lane; i < P; i += 64)
+        bad = bad || p.tables[(size_t)b * p.mbps + i] != p.tables[i];
+    }
+    if (__any(bad) && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
+  }
+}
+
+// The slices' states of every (sequence, query head) combined in slice order
+// into the final state, stored after them. Thread t: row t / (D/4 + 1), its
+// float4 of acc, or (the row's last thread) m and l. NS is a template
+// parameter so that every slice's loads go out together.
+template <int D, int NS>
+__global__ __launch_bounds__(256) void decode_prefix_merge_kernel(float* pre, int rows) {
+  constexpr int PF = prefix_row_floats(D), TPR = D / 4 + 1;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long long)rows * TPR) return;
+  const long long row = t / TPR;
+  const int k = (int)(t - row * TPR);
+  const size_t slice = (size_t)rows * PF;
+  const float* src = pre + (size_t)row * PF;
+  float M = -INFINITY, L = 0.f;
+  float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int s2 = 0; s2 < NS; ++s2) {
+    const float* r = src + (size_t)s2 * slice;
+    const float pm = r[D], pl = r[D + 1];
+    const float Mn = fmaxf(M, pm);
+    const float Ms = (Mn == -INFINITY) ? 0.f : Mn;
+    const float sa = __builtin_amdgcn_exp2f(M - Ms), sb = __builtin_amdgcn_exp2f(pm - Ms);
+    L = L * sa + pl * sb;
+    if (k < D / 4) {
+      const float4 pa = *reinterpret_cast<const float4*>(r + 4 * k);
+      A.x = A.x * sa + pa.x * sb;
+      A.y = A.y * sa + pa.y * sb;
+      A.z = A.z * sa + pa.z * sb;
+      A.w = A.w * sa + pa.w * sb;
+    }
+    M = Mn;
+  }
+  float* dst = pre + (size_t)NS * slice + (size_t)row * PF;
+  if (k < D / 4) {
+    *reinterpret_cast<float4*>(dst + 4 * k) = A;
+  } else {
+    dst[D] = M;
+    dst[D + 1] = L;
+  }
+}
+
+template <typename T, int D, int G>
+int launch_prefix_t(const PrefixParams& p, hipStream_t s) {
+  // 8 ids per group of 8 slice sets and column tile (see the kernel).
+  const int nc = (p.B * G + 15) / 16, nps = p.Hkv * prefix_splits(p.prefix);
+  const unsigned grid = (unsigned)(8 * nc * ((nps + 7) / 8));
+  hipLaunchKernelGGL((decode_prefix_kernel<T, D, G>), dim3(grid), dim3(64 * kPrefixWaves), 0, s, p);
+  int st = launch_status("decode_prefix_kernel");
+  const int ns = prefix_splits(p.prefix);
+  if (st || ns == 1) return st;
+  const int rows = p.B * p.Hkv * G;
+  const long long threads = (long long)rows * (D / 4 + 1);
+  const dim3 mg((unsigned)((threads + 255) / 256));
+  switch (ns) {
+    case 2: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 2>), mg, dim3(256), 0, s, p.pre, rows); break;
+    case 3: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 3>), mg, dim3(256), 0, s, p.pre, rows); break;
+    case 4: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 4>), mg, dim3(256), 0, s, p.pre, rows); break;
+    case 5: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 5>), mg, dim3(256), 0, s, p.pre, rows); break;
+    case 6: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 6>), mg, dim3(256), 0, s, p.pre, rows); break;
+    case 7: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 7>), mg, dim3(256), 0, s, p.pre, rows); break;
+    default: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 8>), mg, dim3(256), 0, s, p.pre, rows); break;
+  }
+  return launch_status("decode_prefix_merge_kernel");
+}
+
+template <typename T, int D>
+int launch_prefix_g(int G, const PrefixParams& p, hipStream_t s) {
+  switch (G) {
+    case 1: return launch_prefix_t<T, D, 1>(p, s);
+    case 2: return launch_prefix_t<T, D, 2>(p, s);
+    case 3: return launch_prefix_t<T, D, 3>(p, s);
+    case 4: return launch_prefix_t<T, D, 4>(p, s);
+    case 5: return launch_prefix_t<T, D, 5>(p, s);
+    case 6: return launch_prefix_t<T, D, 6>(p, s);
+    case 7: return launch_prefix_t<T, D, 7>(p, s);
+    case 8: return launch_prefix_t<T, D, 8>(p, s);
+  }
+  return fail(RLSE_ERR_INVALID_VALUE, "decode_prefix: unsupported group size %d", G);
+}
+
+template <typename T>
+int launch_prefix_d(int D, int G, const PrefixParams& p, hipStream_t s) {
+  switch (D) {
+    case 64: return launch_prefix_g<T, 64>(G, p, s);
+    case 128: return launch_prefix_g<T, 128>(G, p, s);
+  }
+  return fail(RLSE_ERR_INVALID_VALUE, "decode_prefix: unsupported head_dim %d", D);
+}
+
+}  // namespace
+
+int launch_decode_prefix(int dtype, int D, int G, const PrefixParams& p, hipStream_t s) {
+  switch (dtype) {
+    case RLSE_DTYPE_BF16: return launch_prefix_d<bf16>(D, G, p, s);
+    case RLSE_DTYPE_F16: return launch_prefix_d<f16>(D, G, p, s);
+  }
+  return fail(RLSE_ERR_INVALID_VALUE, "decode_prefix: dtype %d (16-bit K/V only)", dtype);
+}
+
+}  // namespace rlse

@@ -79,6 +79,10 @@ int read_and_clear_ws_flags(void* workspace, hipStream_t stream, unsigned* flags
   if (word & RLSE_WS_ERR_LENGTH)
     return fail(RLSE_ERR_TOKEN_LIMIT,
                 "a sequence length exceeded its block table (flags 0x%x)", word);
+  if (word & RLSE_WS_ERR_PREFIX)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "a cascade step's batch does not share its prefix pages, or a new token lies "
+                "inside them (flags 0x%x)", word);
   return fail(RLSE_ERR_DEVICE_TIMEOUT, "unknown device error flags 0x%x", word);
 }
 

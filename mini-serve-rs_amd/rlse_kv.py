@@ -48,6 +48,7 @@ ERR_DEVICE_TIMEOUT = 10005
 DECODE_STREAM = 1
 WS_ERR_MERGE_TIMEOUT = 1
 WS_ERR_LENGTH = 2
+WS_ERR_PREFIX = 4
 BLOCK_SIZE = 16
 
 # Every extern "C" symbol of include/rlse_kv.h (checked by the CPU tests).
@@ -77,7 +78,8 @@ EXPORTED = (
     "rlse_argmax_workspace_size", "rlse_qkv_proj", "rlse_linear_residual", "rlse_gate_up_silu",
     "rlse_dense_workspace_size", "rlse_decode_plan_size", "rlse_decode_plan",
     "rlse_decode_step_planned", "rlse_workspace_check", "rlse_set_merge_wait_ns",
-    "rlse_decode_step_noalloc",
+    "rlse_decode_step_noalloc", "rlse_decode_prefix_size", "rlse_decode_plan_cascade",
+    "rlse_decode_step_cascade",
 )
 
 
@@ -189,6 +191,11 @@ _SIGS = {
                               _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp]),
     "rlse_decode_step_planned": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                               _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _i, _vp]),
+    "rlse_decode_prefix_size": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
+    "rlse_decode_plan_cascade": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "rlse_decode_step_cascade": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp,
+                                      _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _i,
+                                      _i, _vp, _sz, _vp]),
     "rlse_prefill_workspace_size": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz)]),
     "rlse_prefill_attn": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp,
                                _sz, _vp]),
@@ -787,6 +794,43 @@ def decode_step_planned(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: floa
         _ptr(block_tables), _ptr(seq_lens), _ptr(out), batch, num_heads, num_kv_heads, head_dim,
         max_blocks_per_seq, num_blocks, scale, _dt(dtype), _ptr(workspace), workspace_bytes,
         _ptr(plan), DECODE_STREAM if stream_pages else 0, _stream(stream)))
+
+
+def decode_prefix_size(batch: int, num_heads: int, head_dim: int, prefix_pages: int) -> int:
+    """Bytes of the prefix partials of a cascade step (rlse_decode_prefix_size)."""
+    n = _sz(0)
+    _check(load().rlse_decode_prefix_size(batch, num_heads, head_dim, prefix_pages,
+                                          ctypes.byref(n)))
+    return n.value
+
+
+def decode_plan_cascade(block_tables, seq_lens, batch: int, num_kv_heads: int,
+                        max_blocks_per_seq: int, num_blocks: int, prefix_pages: int, plan,
+                        plan_bytes: int, stream=None) -> None:
+    """decode_plan for a cascade step: every row's page stream starts after
+    the first prefix_pages table entries."""
+    _check(load().rlse_decode_plan_cascade(_ptr(block_tables), _ptr(seq_lens), batch,
+                                           num_kv_heads, max_blocks_per_seq, num_blocks,
+                                           prefix_pages, _ptr(plan), plan_bytes, _stream(stream)))
+
+
+def decode_step_cascade(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: float, cos_table,
+                        sin_table, max_pos: int, k_pool, v_pool, block_tables, seq_lens, out,
+                        batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                        max_blocks_per_seq: int, num_blocks: int, scale: float, dtype, plan,
+                        prefix_pages: int, prefix_buf, prefix_bytes: int, workspace=None,
+                        workspace_bytes: int = 0, stream=None, stream_pages: bool = False) -> None:
+    """The shared-prefix (cascade) decode step: the first prefix_pages pages,
+    common to every sequence, attended once for the batch, then each
+    sequence's own pages, the two softmax states combined per row. plan: from
+    decode_plan_cascade with the same prefix_pages, or None."""
+    _check(load().rlse_decode_step_cascade(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(q_norm_weight), _ptr(k_norm_weight), eps,
+        _ptr(cos_table), _ptr(sin_table), max_pos, _ptr(k_pool), _ptr(v_pool),
+        _ptr(block_tables), _ptr(seq_lens), _ptr(out), batch, num_heads, num_kv_heads, head_dim,
+        max_blocks_per_seq, num_blocks, scale, _dt(dtype), _ptr(workspace), workspace_bytes,
+        _ptr(plan), DECODE_STREAM if stream_pages else 0, prefix_pages, _ptr(prefix_buf),
+        prefix_bytes, _stream(stream)))
 
 
 def prefill_workspace_size(num_tokens: int, ctx_len: int, num_heads: int, num_kv_heads: int,

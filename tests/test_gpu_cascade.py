@@ -1,0 +1,191 @@
+"""Shared-prefix (cascade) decode step on the GPU.
+
+rlse_decode_step_cascade attends the first prefix_pages pages -- the same
+pages in every sequence's block table, as after a prefix fork
+(src/cache/prefix_cache.rs:250-345, src/backends/candle.rs:437-478) -- once
+for the whole batch and then each sequence's own pages, combining the two
+softmax states per row. Its result is decode_attention_gqa_zero_copy
+(src/backends/qwen2.rs:177-203) over each sequence's full key range, checked
+here against the oracle on the appended pool (bar 2e-2 for bf16/f16, as for
+every decode), against rlse_decode_step_planned (the same attention with
+another sum order), and for the pool bytes and the error flags.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import DEV, TOL, err_report, to_dev
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+
+
+def _host16(t):
+    torch.cuda.synchronize()
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _to_f32(bits, dtype):
+    return O.bf16_bits_to_f32(bits) if dtype == "bf16" else bits.view(np.float16).astype(np.float32)
+
+
+def _fork_batch(rng, b, prefix_pages, suffix_lo, suffix_hi, hkv, d, dtype, seed):
+    """A pool in which every sequence's first prefix_pages pages are one
+    shared set and the rest are private (shuffled page ids)."""
+    suffix = rng.integers(suffix_lo, suffix_hi + 1, b).astype(np.int32)
+    lens = (16 * prefix_pages + suffix + 1).astype(np.int32)   # keys after the append
+    own = (lens + 15) // 16 - prefix_pages
+    nb = prefix_pages + int(own.sum()) + 3
+    perm = rng.permutation(nb).astype(np.int32)
+    shared = perm[:prefix_pages]
+    mbps = int(prefix_pages + own.max())
+    tables = np.zeros((b, mbps), np.int32)
+    used = prefix_pages
+    for i in range(b):
+        tables[i, :prefix_pages] = shared
+        tables[i, prefix_pages:prefix_pages + own[i]] = perm[used:used + own[i]]
+        used += int(own[i])
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    tdt = BF if dtype == "bf16" else torch.float16
+    kp = torch.randn((nb, hkv, 16, d), generator=g, device=DEV).to(tdt)
+    vp = torch.randn((nb, hkv, 16, d), generator=g, device=DEV).to(tdt)
+    return lens, tables, nb, mbps, kp, vp, g, tdt
+
+
+def _step_inputs(kv, g, tdt, b, hq, hkv, d, mbps, dtype):
+    q = torch.randn((b, hq, d), generator=g, device=DEV).to(tdt)
+    kn = torch.randn((b, hkv, d), generator=g, device=DEV).to(tdt)
+    vn = torch.randn((b, hkv, d), generator=g, device=DEV).to(tdt)
+    qw = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(tdt)
+    kw = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(tdt)
+    max_pos = mbps * 16
+    cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, dtype)
+    c_h = np.frombuffer(cos_b, np.uint16).reshape(max_pos, d // 2).copy()
+    s_h = np.frombuffer(sin_b, np.uint16).reshape(max_pos, d // 2).copy()
+    c_d = torch.from_numpy(c_h.view(np.int16)).to(DEV).view(tdt)
+    s_d = torch.from_numpy(s_h.view(np.int16)).to(DEV).view(tdt)
+    return q, kn, vn, qw, kw, max_pos, c_h, s_h, c_d, s_d
+
+
+@pytest.mark.parametrize("hq,hkv,d,b,prefix_pages,dtype", [
+    (16, 8, 128, 64, 64, "bf16"),   # Qwen3-0.6B fork workload: 1024-token prefix, 64 sequences
+    (14, 2, 64, 9, 5, "bf16"),      # G = 7, a tile of 16 queries cut by the batch end
+    (32, 8, 128, 3, 1, "f16"),      # G = 4, one shared page, f16
+    (8, 8, 64, 2, 17, "bf16"),      # G = 1, two slices, waves with unequal page shares
+    (16, 8, 128, 2, 130, "bf16"),   # eight slices of 17 pages, idle waves in each
+])
+def test_cascade_step_matches_oracle_and_planned(kv, hq, hkv, d, b, prefix_pages, dtype):
+    rng = np.random.default_rng(prefix_pages * 31 + b)
+    lens, tables, nb, mbps, kp, vp, g, tdt = _fork_batch(rng, b, prefix_pages, 0, 300, hkv, d,
+                                                        dtype, seed=prefix_pages + b)
+    q, kn, vn, qw, kw, max_pos, c_h, s_h, c_d, s_d = _step_inputs(kv, g, tdt, b, hq, hkv, d,
+                                                                  mbps, dtype)
+    print(f"cascade: Hq={hq} Hkv={hkv} d={d} B={b} prefix {prefix_pages} pages, keys "
+          f"{int(lens.min())}..{int(lens.max())}, {dtype}", flush=True)
+    t_dev, l_dev = to_dev(tables), to_dev(lens)
+    scale = 1.0 / math.sqrt(d)
+    ws = torch.zeros(kv.decode_workspace_size(b, hq, hkv, d), dtype=torch.uint8, device=DEV)
+    plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=DEV)
+    pre = torch.zeros(kv.decode_prefix_size(b, hq, d, prefix_pages), dtype=torch.uint8,
+                      device=DEV)
+    results = {}
+    for name in ("planned", "cascade", "cascade_unplanned", "cascade_stream"):
+        kp_i, vp_i = kp.clone(), vp.clone()
+        out = torch.full((b, hq, d), 3.0, dtype=tdt, device=DEV)
+        args = (q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp_i, vp_i, t_dev, l_dev, out, b, hq,
+                hkv, d, mbps, nb, scale, dtype)
+        if name == "planned":
+            kv.decode_plan(t_dev, l_dev, b, hkv, mbps, nb, plan, plan.numel())
+            kv.decode_step_planned(*args, plan, ws, ws.numel())
+        else:
+            p_ = None
+            if name != "cascade_unplanned":
+                kv.decode_plan_cascade(t_dev, l_dev, b, hkv, mbps, nb, prefix_pages, plan,
+                                       plan.numel())
+                p_ = plan
+            kv.decode_step_cascade(*args, p_, prefix_pages, pre, pre.numel(), ws, ws.numel(),
+                                   stream_pages=name == "cascade_stream")
+        torch.cuda.synchronize()
+        assert kv.workspace_flags(ws) == 0, name
+        results[name] = (_host16(out), _host16(kp_i), _host16(vp_i))
+    ref_out, ref_k, ref_v = results["planned"]
+    for name in ("cascade", "cascade_unplanned", "cascade_stream"):
+        out_h, k_h, v_h = results[name]
+        # the append is the same bytes; the output differs only by the sum order
+        np.testing.assert_array_equal(k_h, ref_k, err_msg=name)
+        np.testing.assert_array_equal(v_h, ref_v, err_msg=name)
+        mx, rel = err_report(_to_f32(out_h, dtype), _to_f32(ref_out, dtype))
+        print(f"[{name} vs planned] max_abs={mx:.3e} rel={rel:.3e}")
+        assert mx <= 1e-2, (name, mx)
+    # planned and unplanned cascade steps, cacheable or streamed pages: one result
+    for name in ("cascade_unplanned", "cascade_stream"):
+        np.testing.assert_array_equal(results[name][0], results["cascade"][0], err_msg=name)
+
+    # against the oracle over each row's full key range, on the appended pool
+    out_c, k_h, v_h = results["cascade"]
+    got = _to_f32(out_c, dtype)
+    kf, vf = _to_f32(k_h, dtype), _to_f32(v_h, dtype)
+    qh, qwh = _host16(q), _host16(qw)
+    rows = sorted(set([0, b - 1, int(np.argmax(lens))] + list(rng.choice(b, min(b, 5), False))))
+    worst = 0.0
+    for r in rows:
+        n = int(lens[r])
+        pos = np.full(hq, n - 1, np.int32)
+        if dtype == "bf16":
+            q_ref = O.bf16_bits_to_f32(O.apply_rope_bf16(O.rmsnorm_bf16(qh[r], qwh, 1e-6), pos,
+                                                          c_h, s_h))
+        else:
+            qn = O.rmsnorm_f16(qh[r].view(np.float16), qwh.view(np.float16), 1e-6)
+            q_ref = O.rope_ref(qn.astype(np.float32), pos, c_h.view(np.float16).astype(np.float32),
+                               s_h.view(np.float16).astype(np.float32), "f16").astype(np.float32)
+        kc = O.paged_to_contiguous(kf, tables[r], n)
+        vc = O.paged_to_contiguous(vf, tables[r], n)
+        want = O.decode_batch_f32(q_ref[None], kc[None], vc[None], np.array([n], np.int32), scale)
+        mx, rel = err_report(got[r], want[0])
+        worst = max(worst, mx)
+        assert np.isfinite(got[r]).all()
+        assert mx <= TOL[dtype], (r, mx)
+    print(f"cascade: rows {rows} within {worst:.3e} of the oracle (bar {TOL[dtype]})")
+
+
+def test_cascade_contract_violations_raise_the_prefix_flag(kv):
+    """A sequence whose first prefix_pages table entries are not sequence
+    0's, or whose new token lies inside the prefix, breaks the cascade
+    contract: the step raises RLSE_WS_ERR_PREFIX (rlse_workspace_check maps
+    it to RLSE_ERR_INVALID_VALUE). Host-side limits are errors at the call."""
+    hq, hkv, d, b, pp = 16, 8, 128, 4, 3
+    rng = np.random.default_rng(77)
+    lens, tables, nb, mbps, kp, vp, g, tdt = _fork_batch(rng, b, pp, 20, 60, hkv, d, "bf16", 7)
+    q, kn, vn, qw, kw, max_pos, _, _, c_d, s_d = _step_inputs(kv, g, tdt, b, hq, hkv, d, mbps,
+                                                              "bf16")
+    ws = torch.zeros(kv.decode_workspace_size(b, hq, hkv, d), dtype=torch.uint8, device=DEV)
+    pre = torch.zeros(kv.decode_prefix_size(b, hq, d, pp), dtype=torch.uint8, device=DEV)
+    out = torch.empty((b, hq, d), dtype=tdt, device=DEV)
+
+    def step(tables_, lens_, prefix_pages=pp, pre_bytes=pre.numel(), dtype="bf16"):
+        kv.decode_step_cascade(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp.clone(), vp.clone(),
+                               to_dev(tables_), to_dev(lens_), out, b, hq, hkv, d, mbps, nb,
+                               1.0 / math.sqrt(d), dtype, None, prefix_pages, pre, pre_bytes, ws,
+                               ws.numel())
+        torch.cuda.synchronize()
+        return kv.workspace_flags(ws)
+
+    assert step(tables, lens) == 0
+    bad_t = tables.copy()
+    bad_t[2, 1] = tables[2, pp]          # a private page inside sequence 2's prefix
+    print("cascade contract: prefix tables differ", flush=True)
+    assert step(bad_t, lens) == kv.WS_ERR_PREFIX
+    bad_l = lens.copy()
+    bad_l[1] = 16 * pp                   # the new token at the prefix's last position
+    print("cascade contract: new token inside the prefix", flush=True)
+    assert step(tables, bad_l) == kv.WS_ERR_PREFIX
+    assert step(tables, lens) == 0       # flags cleared by the check, next step clean
+    for kwargs in ({"prefix_pages": mbps + 1}, {"prefix_pages": -1},
+                   {"pre_bytes": pre.numel() - 16}, {"dtype": "f32"}):
+        with pytest.raises(kv.RlseError):
+            step(tables, lens, **kwargs)
