@@ -438,7 +438,8 @@ def fork_bench(args):
         2 * b * row + b * d * 2 + 2 * d * 2
     compulsory = plen * row + int(sum(int(n) - plen for n in lens)) * row + extra
     logical = int(sum(int(n) for n in lens)) * row + extra
-    traffic, traffic_src = measured_traffic(args.workload, True)
+    # The committed counters are those of the cascade step's three kernels.
+    traffic, traffic_src = measured_traffic(args.workload, cascade)
     achieved = compulsory / (avg_ms * 1e-3) / 1e9
     result = {
         "metric": "prefix-fork decode tokens/sec and compulsory HBM GB/s at Qwen3-0.6B shape, "
@@ -454,7 +455,8 @@ def fork_bench(args):
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": ("decode_prefix_kernel + decode_kernel cascade step "
+                     "kernel": ("decode_prefix_kernel + decode_prefix_merge_kernel + "
+                                "decode_kernel cascade step "
                                 "(rlse_decode_step_cascade, the batch's shared pages attended "
                                 "once, the rest streamed)" if cascade else
                                 "decode_kernel planned fused step "
