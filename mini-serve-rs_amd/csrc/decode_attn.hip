@@ -389,8 +389,9 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
     st2 = launch_decode_prefix(dtype, head_dim, G, pp, s);
     if (st2) return st2;
     p.prefix = prefix;
-    p.pre = pp.pre + (size_t)(prefix_regions(prefix) - 1) * batch * num_heads *
-                         prefix_row_floats(head_dim);
+    p.pre = pp.pre;
+    p.pre_slices = prefix_regions(prefix);
+    p.pre_stride = (long long)batch * num_heads * prefix_row_floats(head_dim);
   }
   if (!plan) return launch_decode_dtype<kModeFused>(dtype, head_dim, G, p, s);
   return (flags & RLSE_DECODE_STREAM)

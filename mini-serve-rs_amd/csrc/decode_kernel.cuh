@@ -238,7 +238,9 @@ struct DecodeParams {
   // those pages ([B][Hq][D + 4] floats: acc[D], m, l in log2 units), when the
   // row is finished. prefix 0 and pre null: none.
   int prefix;
-  const float* pre;
+  const float* pre;      // cascade step: pre_slices states over the shared prefix
+  int pre_slices;        // (regions pre_stride floats apart), combined in order
+  long long pre_stride;
 };
 
 // Floats per (sequence, query head) of a prefix partial: acc[D], m, l, and
@@ -271,16 +273,13 @@ struct PrefixParams {
 // Longest shared prefix a cascade step takes, in pages (8192 tokens).
 constexpr int kMaxPrefixPages = 512;
 // Slices of the prefix attended by separate workgroups (each leaves its own
-// softmax state, a second launch combines them): about 16 pages per slice,
-// at most 8 slices.
+// softmax state; the decode combines them into each row): about 16 pages per
+// slice, at most 8 slices.
 __host__ __device__ constexpr int prefix_splits(int prefix) {
   return prefix <= 16 ? 1 : ((prefix + 15) / 16 > 8 ? 8 : (prefix + 15) / 16);
 }
-// Prefix partial regions of a cascade step: one per slice, then (with more
-// than one slice) the combined states, which the decode reads.
-__host__ __device__ constexpr int prefix_regions(int prefix) {
-  return prefix_splits(prefix) > 1 ? prefix_splits(prefix) + 1 : 1;
-}
+// Prefix partial regions of a cascade step: one per slice.
+__host__ __device__ constexpr int prefix_regions(int prefix) { return prefix_splits(prefix); }
 
 int launch_decode_prefix(int dtype, int D, int G, const PrefixParams& p, hipStream_t s);
 
@@ -949,21 +948,41 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         row_extent(cur_row, R, nb);
         const int b = cur_row / Hkv, kvh = cur_row - b * Hkv;
         if (R >= wlo && R + nb <= whi) {
-          if (p.pre) {  // cascade step: the row's softmax state over the shared prefix
+          if (p.pre) {  // cascade step: the row's softmax states over the prefix slices
+            // acc = acc * 2^(m - M) + sum_s acc_s * 2^(m_s - M), M the largest
+            // maximum, one accumulator tile at a time over the slices (few
+            // registers live beside the page buffers).
             const float* pr = p.pre + ((size_t)b * Hq + (size_t)kvh * G + (mh < G ? mh : 0)) *
                                           prefix_row_floats(D);
-            const float pm = pr[D], pl = pr[D + 1];
-            const float M = fmaxf(m1, pm);
+            const int ns = p.pre_slices;
+            const long long st = p.pre_stride;
+            float M = m1;
+#pragma unroll 1
+            for (int sl = 0; sl < ns; ++sl) M = fmaxf(M, pr[sl * st + D]);
             const float Ms = (M == -INFINITY) ? 0.f : M;
-            const float sa = __builtin_amdgcn_exp2f(m1 - Ms), sb = __builtin_amdgcn_exp2f(pm - Ms);
-            lt = lt * sa + pl * sb;
+            const float wo = __builtin_amdgcn_exp2f(m1 - Ms);
+            lt *= wo;
+#pragma unroll 1
+            for (int sl = 0; sl < ns; ++sl)
+              lt += pr[sl * st + D + 1] * __builtin_amdgcn_exp2f(pr[sl * st + D] - Ms);
 #pragma unroll
             for (int t = 0; t < D / 16; ++t) {
-              const float4 pa = *reinterpret_cast<const float4*>(pr + 16 * t + 4 * mq);
-              macc[t][0] = macc[t][0] * sa + pa.x * sb;
-              macc[t][1] = macc[t][1] * sa + pa.y * sb;
-              macc[t][2] = macc[t][2] * sa + pa.z * sb;
-              macc[t][3] = macc[t][3] * sa + pa.w * sb;
+              float a0 = macc[t][0] * wo, a1 = macc[t][1] * wo, a2 = macc[t][2] * wo,
+                    a3 = macc[t][3] * wo;
+#pragma unroll 1
+              for (int sl = 0; sl < ns; ++sl) {
+                const float* r = pr + sl * st;
+                const float w = __builtin_amdgcn_exp2f(r[D] - Ms);
+                const float4 pa = *reinterpret_cast<const float4*>(r + 16 * t + 4 * mq);
+                a0 += pa.x * w;
+                a1 += pa.y * w;
+                a2 += pa.z * w;
+                a3 += pa.w * w;
+              }
+              macc[t][0] = a0;
+              macc[t][1] = a1;
+              macc[t][2] = a2;
+              macc[t][3] = a3;
             }
           }
           if (mh < G) {
@@ -1449,16 +1468,18 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       }
       if (!ok && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_MERGE_TIMEOUT);
     }
-    if (p.pre) {  // cascade step: the row's softmax state over the shared prefix
+    if (p.pre) {  // cascade step: the row's softmax states over the prefix slices
       constexpr int PF = prefix_row_floats(D);
       const float* pr = p.pre + ((size_t)b * Hq + (size_t)kvh * G) * PF;
+#pragma unroll 1
+      for (int sl = 0; sl < p.pre_slices; ++sl, pr += p.pre_stride)
 #pragma unroll
-      for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int k = 0; k < DPL; ++k)
-          if (lane + 64 * k < D)
-            lse_combine(M[g][k], Ls[g][k], A[g][k], pr[g * PF + D], pr[g * PF + D + 1],
-                        pr[g * PF + lane + 64 * k]);
+          for (int k = 0; k < DPL; ++k)
+            if (lane + 64 * k < D)
+              lse_combine(M[g][k], Ls[g][k], A[g][k], pr[g * PF + D], pr[g * PF + D + 1],
+                          pr[g * PF + lane + 64 * k]);
     }
     // Output of a row inside the group's range or merged above (NaN if a
     // partial did not arrive within the wait bound).

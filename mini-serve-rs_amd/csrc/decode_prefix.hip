@@ -10,10 +10,9 @@
 // prefix is cut into NS = prefix_splits(P) slices of about 16 pages, one
 // workgroup per (column tile, KV head, slice), and each wave of a workgroup
 // takes its own pages of the slice. The waves' partial softmax states are
-// combined in LDS (pairwise, in a fixed order) into the slice's state; with
-// more than one slice a second launch combines the slices' states in slice
-// order into each query's state over the whole prefix -- acc[D], m, l in the
-// decode's log2 units -- which the decode launch combines into each row it
+// combined in LDS (pairwise, in a fixed order) into the slice's state --
+// acc[D], m, l of each query in the decode's log2 units -- and the decode
+// launch combines the slices' states, in slice order, into each row it
 // finishes; it leaves the prefix out of its page stream. Workgroups are
 // numbered so that the column tiles reading one slice's pages run on one XCD
 // and share its L2.
@@ -251,7 +250,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     const int j = c0 + mh;
     const int jj = j < ncols ? j : ncols - 1;
     const int b = jj / G, g = jj - b * G;
-    // This slice's states, in region sp (with one slice, the final ones).
+    // This slice's states, in region sp.
     const size_t slice = (size_t)B * Hq * PF;  // floats of one region
     float* dst = p.pre + (size_t)sp * slice + ((size_t)b * Hq + (size_t)h * G + g) * PF;
     if (j < ncols) {
@@ -280,69 +279,13 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
   }
 }
 
-// The slices' states of every (sequence, query head) combined in slice order
-// into the final state, stored after them. Thread t: row t / (D/4 + 1), its
-// float4 of acc, or (the row's last thread) m and l. NS is a template
-// parameter so that every slice's loads go out together.
-template <int D, int NS>
-__global__ __launch_bounds__(256) void decode_prefix_merge_kernel(float* pre, int rows) {
-  constexpr int PF = prefix_row_floats(D), TPR = D / 4 + 1;
-  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (t >= (long long)rows * TPR) return;
-  const long long row = t / TPR;
-  const int k = (int)(t - row * TPR);
-  const size_t slice = (size_t)rows * PF;
-  const float* src = pre + (size_t)row * PF;
-  float M = -INFINITY, L = 0.f;
-  float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int s2 = 0; s2 < NS; ++s2) {
-    const float* r = src + (size_t)s2 * slice;
-    const float pm = r[D], pl = r[D + 1];
-    const float Mn = fmaxf(M, pm);
-    const float Ms = (Mn == -INFINITY) ? 0.f : Mn;
-    const float sa = __builtin_amdgcn_exp2f(M - Ms), sb = __builtin_amdgcn_exp2f(pm - Ms);
-    L = L * sa + pl * sb;
-    if (k < D / 4) {
-      const float4 pa = *reinterpret_cast<const float4*>(r + 4 * k);
-      A.x = A.x * sa + pa.x * sb;
-      A.y = A.y * sa + pa.y * sb;
-      A.z = A.z * sa + pa.z * sb;
-      A.w = A.w * sa + pa.w * sb;
-    }
-    M = Mn;
-  }
-  float* dst = pre + (size_t)NS * slice + (size_t)row * PF;
-  if (k < D / 4) {
-    *reinterpret_cast<float4*>(dst + 4 * k) = A;
-  } else {
-    dst[D] = M;
-    dst[D + 1] = L;
-  }
-}
-
 template <typename T, int D, int G>
 int launch_prefix_t(const PrefixParams& p, hipStream_t s) {
   // 8 ids per group of 8 slice sets and column tile (see the kernel).
   const int nc = (p.B * G + 15) / 16, nps = p.Hkv * prefix_splits(p.prefix);
   const unsigned grid = (unsigned)(8 * nc * ((nps + 7) / 8));
   hipLaunchKernelGGL((decode_prefix_kernel<T, D, G>), dim3(grid), dim3(64 * kPrefixWaves), 0, s, p);
-  int st = launch_status("decode_prefix_kernel");
-  const int ns = prefix_splits(p.prefix);
-  if (st || ns == 1) return st;
-  const int rows = p.B * p.Hkv * G;
-  const long long threads = (long long)rows * (D / 4 + 1);
-  const dim3 mg((unsigned)((threads + 255) / 256));
-  switch (ns) {
-    case 2: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 2>), mg, dim3(256), 0, s, p.pre, rows); break;
-    case 3: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 3>), mg, dim3(256), 0, s, p.pre, rows); break;
-    case 4: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 4>), mg, dim3(256), 0, s, p.pre, rows); break;
-    case 5: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 5>), mg, dim3(256), 0, s, p.pre, rows); break;
-    case 6: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 6>), mg, dim3(256), 0, s, p.pre, rows); break;
-    case 7: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 7>), mg, dim3(256), 0, s, p.pre, rows); break;
-    default: hipLaunchKernelGGL((decode_prefix_merge_kernel<D, 8>), mg, dim3(256), 0, s, p.pre, rows); break;
-  }
-  return launch_status("decode_prefix_merge_kernel");
+  return launch_status("decode_prefix_kernel");
 }
 
 template <typename T, int D>
