@@ -307,7 +307,7 @@ extern "C" int rlse_decode_prefix_size(int batch, int num_heads, int head_dim,
   if (batch <= 0 || num_heads <= 0 || head_dim <= 0 || prefix_pages < 0 ||
       prefix_pages > kMaxPrefixPages)
     return fail(RLSE_ERR_INVALID_VALUE, "decode_prefix_size: bad shape");
-  // The slices' states, then (with more than one slice) their combination.
+  // The slices' states, then the decode's parked row states.
   *bytes = (size_t)prefix_regions(prefix_pages) * batch * num_heads *
            prefix_row_floats(head_dim) * sizeof(float);
   return RLSE_OK;
@@ -390,8 +390,9 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
     if (st2) return st2;
     p.prefix = prefix;
     p.pre = pp.pre;
-    p.pre_slices = prefix_regions(prefix);
+    p.pre_slices = prefix_splits(prefix);
     p.pre_stride = (long long)batch * num_heads * prefix_row_floats(head_dim);
+    p.pre_own = pp.pre + (size_t)p.pre_slices * p.pre_stride;
   }
   if (!plan) return launch_decode_dtype<kModeFused>(dtype, head_dim, G, p, s);
   return (flags & RLSE_DECODE_STREAM)

@@ -241,6 +241,10 @@ struct DecodeParams {
   const float* pre;      // cascade step: pre_slices states over the shared prefix
   int pre_slices;        // (regions pre_stride floats apart), combined in order
   long long pre_stride;
+  // Cascade step: rows finished inside one wave's range park their state
+  // here ([B][Hq][prefix_row_floats(D)] floats) and are combined with the
+  // prefix states after the wave's stream, all slices' loads at once.
+  float* pre_own;
 };
 
 // Floats per (sequence, query head) of a prefix partial: acc[D], m, l, and
@@ -267,7 +271,7 @@ struct PrefixParams {
   int mbps;
   int num_blocks;
   int prefix;
-  float* pre;        // prefix_regions(prefix) x [B][Hq][prefix_row_floats(D)]
+  float* pre;        // prefix_splits(prefix) x [B][Hq][prefix_row_floats(D)] floats
   uint32_t* ws_err;  // sticky flags: RLSE_WS_ERR_PREFIX
 };
 // Longest shared prefix a cascade step takes, in pages (8192 tokens).
@@ -278,8 +282,9 @@ constexpr int kMaxPrefixPages = 512;
 __host__ __device__ constexpr int prefix_splits(int prefix) {
   return prefix <= 16 ? 1 : ((prefix + 15) / 16 > 8 ? 8 : (prefix + 15) / 16);
 }
-// Prefix partial regions of a cascade step: one per slice.
-__host__ __device__ constexpr int prefix_regions(int prefix) { return prefix_splits(prefix); }
+// Regions of a cascade step's prefix buffer: one state per slice, then the
+// decode's parked row states.
+__host__ __device__ constexpr int prefix_regions(int prefix) { return prefix_splits(prefix) + 1; }
 
 int launch_decode_prefix(int dtype, int D, int G, const PrefixParams& p, hipStream_t s);
 
@@ -710,6 +715,9 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   // beside the LDS copy the group reads: row (-1 = none), start and blocks.
   int part_row0 = -1, part_row1 = -1, part_nb0 = 0, part_nb1 = 0;
   long long part_R0 = 0, part_R1 = 0;
+  // Cascade step: the first and last row finished inside this wave's range
+  // (consecutive rows, their states parked in pre_own).
+  int def_lo = -1, def_hi = -1;
 
   if (nblk > 0) {
     // Descriptors of 64 consecutive blocks, one per lane: page id, valid
@@ -948,44 +956,21 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         row_extent(cur_row, R, nb);
         const int b = cur_row / Hkv, kvh = cur_row - b * Hkv;
         if (R >= wlo && R + nb <= whi) {
-          if (p.pre) {  // cascade step: the row's softmax states over the prefix slices
-            // acc = acc * 2^(m - M) + sum_s acc_s * 2^(m_s - M), M the largest
-            // maximum, one accumulator tile at a time over the slices (few
-            // registers live beside the page buffers).
-            const float* pr = p.pre + ((size_t)b * Hq + (size_t)kvh * G + (mh < G ? mh : 0)) *
-                                          prefix_row_floats(D);
-            const int ns = p.pre_slices;
-            const long long st = p.pre_stride;
-            float M = m1;
-#pragma unroll 1
-            for (int sl = 0; sl < ns; ++sl) M = fmaxf(M, pr[sl * st + D]);
-            const float Ms = (M == -INFINITY) ? 0.f : M;
-            const float wo = __builtin_amdgcn_exp2f(m1 - Ms);
-            lt *= wo;
-#pragma unroll 1
-            for (int sl = 0; sl < ns; ++sl)
-              lt += pr[sl * st + D + 1] * __builtin_amdgcn_exp2f(pr[sl * st + D] - Ms);
+          if (p.pre) {
+            // Cascade step: park the row's state; the prefix states are
+            // combined into it after the stream.
+            if (mh < G) {
+              float* dst = p.pre_own + ((size_t)b * Hq + (size_t)kvh * G + mh) *
+                                           prefix_row_floats(D);
 #pragma unroll
-            for (int t = 0; t < D / 16; ++t) {
-              float a0 = macc[t][0] * wo, a1 = macc[t][1] * wo, a2 = macc[t][2] * wo,
-                    a3 = macc[t][3] * wo;
-#pragma unroll 1
-              for (int sl = 0; sl < ns; ++sl) {
-                const float* r = pr + sl * st;
-                const float w = __builtin_amdgcn_exp2f(r[D] - Ms);
-                const float4 pa = *reinterpret_cast<const float4*>(r + 16 * t + 4 * mq);
-                a0 += pa.x * w;
-                a1 += pa.y * w;
-                a2 += pa.z * w;
-                a3 += pa.w * w;
-              }
-              macc[t][0] = a0;
-              macc[t][1] = a1;
-              macc[t][2] = a2;
-              macc[t][3] = a3;
+              for (int t = 0; t < D / 16; ++t)
+                *reinterpret_cast<float4*>(dst + 16 * t + 4 * mq) =
+                    make_float4(macc[t][0], macc[t][1], macc[t][2], macc[t][3]);
+              if (mq == 0) *reinterpret_cast<float2*>(dst + D) = make_float2(m1, lt);
             }
-          }
-          if (mh < G) {
+            def_lo = def_lo < 0 ? cur_row : def_lo;
+            def_hi = cur_row;
+          } else if (mh < G) {
             const float inv = lt > 0.f ? 1.f / lt : 0.f;  // all pages skipped -> zeros
             T* dst = ob + ((size_t)b * Hq + (size_t)kvh * G + mh) * D + 4 * mq;
 #pragma unroll
@@ -1317,6 +1302,58 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   // group to group. Every slot's row is read once (lane j < NPART holds slot
   // j's), so the pieces of a row are found with one ballot and their LDS
   // reads issued together.
+  // Cascade step: combines the prefix slices' states of row (b, kvh) into
+  // (M, Ls, A) in slice order, the loads of SB slices in flight at once
+  // (a slice index past the last reloads the first of the batch, unused).
+  constexpr int SB = 32 / (G * DPL) < 1 ? 1 : (32 / (G * DPL) > 8 ? 8 : 32 / (G * DPL));
+  auto combine_prefix = [&](int b, int kvh, float(&M)[G][DPL], float(&Ls)[G][DPL],
+                            float(&A)[G][DPL]) __attribute__((always_inline)) {
+    constexpr int PF = prefix_row_floats(D);
+    const float* pr = p.pre + ((size_t)b * Hq + (size_t)kvh * G) * PF;
+    const int ns = p.pre_slices;
+#pragma unroll 1
+    for (int s0 = 0; s0 < ns; s0 += SB) {
+      float sm[SB][G], sl[SB][G], sa[SB][G][DPL];
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const float* r = pr + (size_t)(s0 + i < ns ? s0 + i : s0) * (size_t)p.pre_stride;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          sm[i][g] = r[g * PF + D];
+          sl[i][g] = r[g * PF + D + 1];
+#pragma unroll
+          for (int k = 0; k < DPL; ++k)
+            sa[i][g][k] = lane + 64 * k < D ? r[g * PF + lane + 64 * k] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < SB; ++i)
+        if (s0 + i < ns) {
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int k = 0; k < DPL; ++k)
+              if (lane + 64 * k < D)
+                lse_combine(M[g][k], Ls[g][k], A[g][k], sm[i][g], sl[i][g], sa[i][g][k]);
+        }
+    }
+  };
+  // Output of a finished row (NaN if a partial did not arrive within the
+  // wait bound).
+  auto write_row = [&](int b, int kvh, bool ok, const float(&Ls)[G][DPL],
+                       const float(&A)[G][DPL]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        const int d = lane + 64 * k;
+        if (d < D) {
+          const float inv = Ls[g][k] > 0.f ? 1.f / Ls[g][k] : 0.f;
+          ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] =
+              Elem<T>::from_f32(ok ? A[g][k] * inv : __builtin_nanf(""));
+        }
+      }
+  };
   const int prow = lane < NPART ? s_part_row[lane] : -1;
 #pragma unroll 1
   for (int s = 1; s >= 0; --s) {
@@ -1468,32 +1505,36 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       }
       if (!ok && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_MERGE_TIMEOUT);
     }
-    if (p.pre) {  // cascade step: the row's softmax states over the prefix slices
+    if (p.pre) combine_prefix(b, kvh, M, Ls, A);  // cascade step
+    write_row(b, kvh, ok, Ls, A);
+  }
+  if constexpr (kMma) {
+    // Cascade step: the rows this wave finished inside its range, their
+    // states parked in pre_own, combined with the prefix states.
+    if (p.pre && def_lo >= 0) {
       constexpr int PF = prefix_row_floats(D);
-      const float* pr = p.pre + ((size_t)b * Hq + (size_t)kvh * G) * PF;
 #pragma unroll 1
-      for (int sl = 0; sl < p.pre_slices; ++sl, pr += p.pre_stride)
+      for (int row = def_lo; row <= def_hi; ++row) {
+        long long R;
+        int nb;
+        row_extent(row, R, nb);
+        if (nb == 0) continue;  // no keys of its own: written by group 0
+        const int b = row / Hkv, kvh = row - b * Hkv;
+        float M[G][DPL], Ls[G][DPL], A[G][DPL];
+        const float* own = p.pre_own + ((size_t)b * Hq + (size_t)kvh * G) * PF;
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-          for (int k = 0; k < DPL; ++k)
-            if (lane + 64 * k < D)
-              lse_combine(M[g][k], Ls[g][k], A[g][k], pr[g * PF + D], pr[g * PF + D + 1],
-                          pr[g * PF + lane + 64 * k]);
-    }
-    // Output of a row inside the group's range or merged above (NaN if a
-    // partial did not arrive within the wait bound).
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int k = 0; k < DPL; ++k) {
-        const int d = lane + 64 * k;
-        if (d < D) {
-          const float inv = Ls[g][k] > 0.f ? 1.f / Ls[g][k] : 0.f;
-          ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] =
-              Elem<T>::from_f32(ok ? A[g][k] * inv : __builtin_nanf(""));
-        }
+          for (int k = 0; k < DPL; ++k) {
+            const int d = lane + 64 * k;
+            M[g][k] = own[g * PF + D];
+            Ls[g][k] = own[g * PF + D + 1];
+            A[g][k] = d < D ? own[g * PF + d] : 0.f;
+          }
+        combine_prefix(b, kvh, M, Ls, A);
+        write_row(b, kvh, true, Ls, A);
       }
+    }
   }
   end_epoch(ep);
 }

@@ -72,17 +72,19 @@ def _step_inputs(kv, g, tdt, b, hq, hkv, d, mbps, dtype):
     return q, kn, vn, qw, kw, max_pos, c_h, s_h, c_d, s_d
 
 
-@pytest.mark.parametrize("hq,hkv,d,b,prefix_pages,dtype", [
-    (16, 8, 128, 64, 64, "bf16"),   # Qwen3-0.6B fork workload: 1024-token prefix, 64 sequences
-    (14, 2, 64, 9, 5, "bf16"),      # G = 7, a tile of 16 queries cut by the batch end
-    (32, 8, 128, 3, 1, "f16"),      # G = 4, one shared page, f16
-    (8, 8, 64, 2, 17, "bf16"),      # G = 1, two slices, waves with unequal page shares
-    (16, 8, 128, 2, 130, "bf16"),   # eight slices of 17 pages, idle waves in each
+@pytest.mark.parametrize("hq,hkv,d,b,prefix_pages,dtype,suffix_hi", [
+    (16, 8, 128, 64, 64, "bf16", 300),  # Qwen3-0.6B fork workload: 1024-token prefix, 64 sequences
+    (16, 8, 128, 64, 64, "bf16", 20),   # short suffixes: rows finish inside one wave's range
+    (14, 2, 64, 9, 5, "bf16", 300),     # G = 7, a tile of 16 queries cut by the batch end
+    (32, 8, 128, 3, 1, "f16", 300),     # G = 4, one shared page, f16
+    (8, 8, 64, 2, 17, "bf16", 300),     # G = 1, two slices, waves with unequal page shares
+    (16, 8, 128, 2, 130, "bf16", 300),  # eight slices of 17 pages, idle waves in each
 ])
-def test_cascade_step_matches_oracle_and_planned(kv, hq, hkv, d, b, prefix_pages, dtype):
-    rng = np.random.default_rng(prefix_pages * 31 + b)
-    lens, tables, nb, mbps, kp, vp, g, tdt = _fork_batch(rng, b, prefix_pages, 0, 300, hkv, d,
-                                                        dtype, seed=prefix_pages + b)
+def test_cascade_step_matches_oracle_and_planned(kv, hq, hkv, d, b, prefix_pages, dtype,
+                                                 suffix_hi):
+    rng = np.random.default_rng(prefix_pages * 31 + b + suffix_hi)
+    lens, tables, nb, mbps, kp, vp, g, tdt = _fork_batch(rng, b, prefix_pages, 0, suffix_hi, hkv,
+                                                        d, dtype, seed=prefix_pages + b)
     q, kn, vn, qw, kw, max_pos, c_h, s_h, c_d, s_d = _step_inputs(kv, g, tdt, b, hq, hkv, d,
                                                                   mbps, dtype)
     print(f"cascade: Hq={hq} Hkv={hkv} d={d} B={b} prefix {prefix_pages} pages, keys "
