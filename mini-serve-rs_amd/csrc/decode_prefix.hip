@@ -42,7 +42,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     uint4 q[16][LPR];  // the tile's 16 queries, normed and roped
     union {
       uint4 vt[kPrefixWaves][16][(D + 16) / 8];  // each wave's V block (padded rows)
-      float part[kPrefixWaves / 2][PL][64];      // partials handed between waves
+      float part[kPrefixWaves][PL][64];          // every wave's partial
     } u;
   };
   __shared__ Lds lds;
@@ -73,6 +73,25 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
   const int hi = lo + per < shi ? lo + per : shi;
   // Lane i holds the page id of block lo + i (a wave takes at most 64).
   const int ids = lo + lane < hi ? p.tables[lo + lane] : 0;
+  // Wave 1 of each workgroup checks a share of the batch against the
+  // contract: every sequence's first P table entries are sequence 0's, and
+  // its new token (position L - 1) lies past them. The first sequence's
+  // entries are requested here, ahead of the page loads, and compared once
+  // those are issued (further sequences, when the batch outnumbers the
+  // workgroups, are read at the end).
+  constexpr int kChk = kMaxPrefixPages / 64;
+  const int nwork = Hkv * NS * NC, bchk = ps * NC + c;
+  int chk_len = 0, chk_t[kChk], chk_0[kChk];
+  bool bad = false;
+  if (wave == 1 && bchk < B) {
+    chk_len = p.seq_lens[bchk];
+#pragma unroll
+    for (int k = 0; k < kChk; ++k) {
+      const int i = lane + 64 * k;
+      chk_t[k] = i < P ? p.tables[(size_t)bchk * p.mbps + i] : 0;
+      chk_0[k] = i < P ? p.tables[i] : 0;
+    }
+  }
 
   // The tile's queries: column j = c0 + i is (sequence j / G, head h*G + j % G).
   // Their loads go out with the page ids, ahead of the first blocks' loads
@@ -140,6 +159,11 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     load(b0, lo);
     load(b1, lo + 1);
     load(b2, lo + 2);
+    if (wave == 1 && bchk < B) {
+      bad = chk_len <= 16 * P || chk_len > p.mbps * 16;
+#pragma unroll
+      for (int k = 0; k < kChk; ++k) bad = bad || chk_t[k] != chk_0[k];
+    }
     // The queries' math, then the barrier that publishes them.
     if (stager) {
       const uint4 y = norm_rope_packet<T, D>(sq_x, p.qw != nullptr, sq_w, p.inv_d, p.eps, sq_c,
@@ -211,65 +235,48 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     }
   }
 
-  // Pairwise combine of the waves' partials, wave w + half into wave w,
-  // halving until wave 0 holds the tile's state over the whole prefix. The V
-  // blocks are dead here: the partials take their LDS.
+  // Every wave parks its partial in LDS (the V blocks are dead here); after
+  // one barrier wave t combines accumulator tile t of all waves, in wave
+  // order, and stores it in region sp; wave 0 also stores m and l.
   __syncthreads();
+  {
+    float(&dst)[PL][64] = lds.u.part[wave];
+    dst[0][lane] = m1;
+    dst[1][lane] = l1;
 #pragma unroll
-  for (int half = kPrefixWaves / 2; half >= 1; half >>= 1) {
-    if (wave >= half && wave < 2 * half) {
-      float(&dst)[PL][64] = lds.u.part[wave - half];
-      dst[0][lane] = m1;
-      dst[1][lane] = l1;
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[2 + 4 * t + i][lane] = macc[t][i];
-    }
-    __syncthreads();
-    if (wave < half) {
-      const float(&src)[PL][64] = lds.u.part[wave];
-      const float pm = src[0][lane], pl = src[1][lane];
-      const float M = fmaxf(m1, pm);
-      const float Ms = (M == -INFINITY) ? 0.f : M;
-      const float sa = __builtin_amdgcn_exp2f(m1 - Ms), sb = __builtin_amdgcn_exp2f(pm - Ms);
-      l1 = l1 * sa + pl * sb;
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) macc[t][i] = macc[t][i] * sa + src[2 + 4 * t + i][lane] * sb;
-      m1 = M;
-    }
-    __syncthreads();
+      for (int i = 0; i < 4; ++i) dst[2 + 4 * t + i][lane] = macc[t][i];
   }
-
-  if (wave == 0) {
-    // The head's sum over its four lanes; m1 is common to them.
-    float lt = l1 + __shfl_xor(l1, 16, 64);
-    lt = lt + __shfl_xor(lt, 32, 64);
-    const int j = c0 + mh;
-    const int jj = j < ncols ? j : ncols - 1;
-    const int b = jj / G, g = jj - b * G;
-    // This slice's states, in region sp.
+  __syncthreads();
+  const int j = c0 + mh;
+  if (wave < NT && j < ncols) {
+    float pm[kPrefixWaves], M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kPrefixWaves; ++v) {
+      pm[v] = lds.u.part[v][0][lane];
+      M = fmaxf(M, pm[v]);
+    }
+    const float Ms = (M == -INFINITY) ? 0.f : M;
+    float l = 0.f, a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < kPrefixWaves; ++v) {
+      const float sc = __builtin_amdgcn_exp2f(pm[v] - Ms);
+      l += lds.u.part[v][1][lane] * sc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] += lds.u.part[v][2 + 4 * wave + i][lane] * sc;
+    }
+    // The head's sum over its four lanes; M is common to them.
+    l = l + __shfl_xor(l, 16, 64);
+    l = l + __shfl_xor(l, 32, 64);
+    const int b = j / G, g = j - b * G;
     const size_t slice = (size_t)B * Hq * PF;  // floats of one region
     float* dst = p.pre + (size_t)sp * slice + ((size_t)b * Hq + (size_t)h * G + g) * PF;
-    if (j < ncols) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        *reinterpret_cast<float4*>(dst + 16 * t + 4 * mq) =
-            make_float4(macc[t][0], macc[t][1], macc[t][2], macc[t][3]);
-      if (mq == 0) {
-        dst[D] = m1;
-        dst[D + 1] = lt;
-      }
-    }
-  } else if (wave == 1) {
-    // Wave 1 of each workgroup checks a slice of the batch against the
-    // contract: every sequence's first P table entries are sequence 0's, and
-    // its new token (position L - 1) lies past them.
-    const int nwork = Hkv * NS * NC;
-    bool bad = false;
-    for (int b = ps * NC + c; b < B; b += nwork) {
+    *reinterpret_cast<float4*>(dst + 16 * wave + 4 * mq) = make_float4(a[0], a[1], a[2], a[3]);
+    if (wave == 0 && mq == 0) *reinterpret_cast<float2*>(dst + D) = make_float2(M, l);
+  }
+  if (wave == 1 && bchk < B) {
+    for (int b = bchk + nwork; b < B; b += nwork) {
       const int L = p.seq_lens[b];
       bad = bad || L <= 16 * P || L > p.mbps * 16;
       for (int i = lane; i < P; i += 64)
