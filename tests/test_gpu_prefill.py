@@ -148,6 +148,22 @@ def test_prefill_qwen3_8b_chunk(kv):
     want = oracle_prefill(q, kp, vp, table, L, hq, hkv, d, dtype, 1 / math.sqrt(d), heads=[0, 7])
     sub = np.concatenate([got[:, 0:g], got[:, 7 * g:8 * g]], axis=1)
     check("qwen3-8b chunk heads 0,7", sub, want, dtype)
+    # Every KV head (each one's row tiles on their own XCD and key splits) on
+    # the tokens at the edges of the 64-token row tiles and at the chunk ends.
+    tq = q.shape[0]
+    kc = as_f32(O.paged_to_contiguous(kp, table, L), dtype)
+    vc = as_f32(O.paged_to_contiguous(vp, table, L), dtype)
+    qf = as_f32(q, dtype)
+    toks = [0, 1, 63, 64, 127, 128, 191, 255, 256, 319, 383, 384, 447, 448, 510, 511]
+    worst = 0.0
+    for h in range(hkv):
+        for t in toks:
+            qh = np.ascontiguousarray(qf[t:t + 1, h * g:(h + 1) * g, :].transpose(1, 0, 2))
+            o = O.prefill_f32(qh, kc[h:h + 1], vc[h:h + 1], L - tq + t, 1 / math.sqrt(d))
+            mx, _ = err_report(got[t, h * g:(h + 1) * g], o[:, 0, :])
+            worst = max(worst, mx)
+            assert mx <= TOL[dtype], (h, t, mx)
+    print(f"qwen3-8b chunk: all {hkv} KV heads x {len(toks)} tokens within {worst:.3e}")
 
 
 def test_prefill_single_token_equals_decode(kv):
