@@ -455,8 +455,7 @@ def fork_bench(args):
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": ("decode_prefix_kernel + decode_prefix_merge_kernel + "
-                                "decode_kernel cascade step "
+                     "kernel": ("decode_prefix_kernel + decode_kernel cascade step "
                                 "(rlse_decode_step_cascade, the batch's shared pages attended "
                                 "once, the rest streamed)" if cascade else
                                 "decode_kernel planned fused step "

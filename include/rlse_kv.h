@@ -255,8 +255,8 @@ int rlse_decode_step_planned(const void* q, const void* k_new, const void* v_new
  * batch, num_heads, head_dim and prefix_pages, 16-byte aligned, overwritten
  * by every call (calls sharing one must be ordered: same stream). Pages of
  * the prefix are read by one workgroup per slice of about 16 pages and 16
- * query heads; with more than one slice a second small launch combines the
- * slices before the decode launch. A batch that breaks the contract
+ * query heads, in a launch ahead of the decode launch; the decode combines
+ * the slices' states into each row. A batch that breaks the contract
  * raises RLSE_WS_ERR_PREFIX in the workspace; its outputs are then not its
  * attention. */
 int rlse_decode_prefix_size(int batch, int num_heads, int head_dim, int prefix_pages,
