@@ -262,9 +262,9 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
 #pragma unroll
     for (int v = 0; v < kPrefixWaves; ++v) {
       const float sc = __builtin_amdgcn_exp2f(pm[v] - Ms);
-      l += lds.u.part[v][1][lane] * sc;
+      l = fmaf(lds.u.part[v][1][lane], sc, l);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] += lds.u.part[v][2 + 4 * wave + i][lane] * sc;
+      for (int i = 0; i < 4; ++i) a[i] = fmaf(lds.u.part[v][2 + 4 * wave + i][lane], sc, a[i]);
     }
     // The head's sum over its four lanes; M is common to them.
     l = l + __shfl_xor(l, 16, 64);
