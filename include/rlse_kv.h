@@ -421,6 +421,24 @@ int rlse_argmax(const void* logits, int32_t* out, int rows, int vocab, int dtype
  * go through rocBLAS gemm_ex. */
 int rlse_linear(const void* x, const void* weight, const void* bias, void* y, int rows,
                 int out_features, int in_features, int dtype, rlse_stream_t stream);
+/* Packed weights (no counterpart in the reference, which multiplies its
+ * row-major weights as loaded). OR-ed into the dtype argument of
+ * rlse_linear, rlse_qkv_proj, rlse_linear_residual and rlse_gate_up_silu
+ * (bf16/f16), it says the weight is in the order rlse_dense_pack writes:
+ * per 16-row tile and 32-element k step, the 64 16-byte packets one MFMA
+ * operand load takes, contiguous. Results are bit-identical to the
+ * row-major weight's; each operand load reads one KiB instead of 64 bytes
+ * from each of 16 rows. Packed, rlse_linear runs every row count on the
+ * MFMA kernel (64 rows at a time). */
+#define RLSE_DENSE_PACKED 0x100
+/* Writes weight [out_features][in_features] (row-major) to packed in that
+ * order (same size, not in place). gate_up_inter > 0: the stacked gate/up
+ * weight of rlse_gate_up_silu ([2*gate_up_inter][in], gate rows then up
+ * rows), whose tiles pair 8 gate rows with the matching 8 up rows; 0: any
+ * other weight (out_features a multiple of 16). in_features a multiple of
+ * 32, both buffers 16-byte aligned. */
+int rlse_dense_pack(const void* weight, void* packed, int out_features, int in_features,
+                    int gate_up_inter, int dtype, rlse_stream_t stream);
 /* The three calls below are the decode step's projections fused with their
  * neighbours on MFMA (bf16/f16; in_features a multiple of 32; any rows,
  * taken 64 at a time; x and weights 16-byte, outputs 8-byte aligned).

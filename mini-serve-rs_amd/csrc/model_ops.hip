@@ -334,6 +334,7 @@ struct DenseParams {
   int rows, K, N, n1, n2;
   int ksplit;        // KS
   int steps;         // 32-wide k steps per wave
+  int packed;        // w in the tile order rlse_dense_pack writes
 };
 
 constexpr int kDenseWaves = 4;
@@ -402,8 +403,12 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
       row = fi < 8 ? tile * 8 + fi : p.n1 + tile * 8 + (fi - 8);
     else
       row = tile * 16 + fi;
-    wr[f] = (const T*)p.w + (size_t)row * K + 8 * g;
+    // Packed weights: tile t's operands of k step s are 64 lanes x 16
+    // bytes at ((t * K/32 + s) * 64 + lane) * 8, one contiguous KiB per load.
+    wr[f] = p.packed ? (const T*)p.w + ((size_t)tile * (K >> 5) * 64 + lane) * 8
+                     : (const T*)p.w + (size_t)row * K + 8 * g;
   }
+  const int wstep = p.packed ? 512 : 32;  // weight elements between k steps
   const T* xr[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t)
@@ -445,7 +450,8 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
       if (s + j < s_end) {
         const int off = 32 * (s + j);
 #pragma unroll
-        for (int f = 0; f < FT; ++f) a[j][f] = *reinterpret_cast<const u32x4_t*>(wr[f] + off);
+        for (int f = 0; f < FT; ++f)
+          a[j][f] = *reinterpret_cast<const u32x4_t*>(wr[f] + (size_t)wstep * (s + j));
 #pragma unroll
         for (int t = 0; t < RT; ++t) b[j][t] = *reinterpret_cast<const u32x4_t*>(xr[t] + off);
       }
@@ -772,6 +778,35 @@ int dense_workspace(const char* what, DenseParams& p, void* workspace, size_t wo
   return RLSE_OK;
 }
 
+// Weights in the tile order of dense_rows_kernel: one 16-byte packet per
+// thread, packet i = ((tile * K/32 + s) * 64 + lane) holding row
+// row(tile, lane % 16), elements 32s + 8(lane / 16) .. +8. Rows of a tile are
+// 16 consecutive rows, or (n1 > 0, gate/up) gate rows 8t .. 8t+7 then up rows
+// n1 + 8t .. n1 + 8t + 7.
+template <typename T>
+__global__ void dense_pack_kernel(const T* __restrict__ w, T* __restrict__ out, int K, int n1,
+                                  long long packets) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= packets) return;
+  const int S = K >> 5;
+  const int lane = (int)(i & 63);
+  const long long ts = i >> 6;
+  const int st = (int)(ts % S);
+  const long long tile = ts / S;
+  const int fi = lane & 15, g = lane >> 4;
+  const long long row = n1 > 0 ? (fi < 8 ? tile * 8 + fi : n1 + tile * 8 + (fi - 8))
+                               : tile * 16 + fi;
+  *reinterpret_cast<uint4*>(out + i * 8) =
+      *reinterpret_cast<const uint4*>(w + row * K + 32 * st + 8 * g);
+}
+
+// Strips RLSE_DENSE_PACKED from a dtype argument.
+bool take_packed(int& dtype) {
+  const bool packed = (dtype & RLSE_DENSE_PACKED) != 0;
+  dtype &= ~RLSE_DENSE_PACKED;
+  return packed;
+}
+
 }  // namespace
 }  // namespace rlse
 
@@ -888,15 +923,22 @@ extern "C" int rlse_argmax(const void* logits, int32_t* out, int rows, int vocab
 extern "C" int rlse_linear(const void* x, const void* weight, const void* bias, void* y,
                            int rows, int out_features, int in_features, int dtype,
                            rlse_stream_t stream) {
+  const bool packed = take_packed(dtype);
   if (!dtype_size(dtype) || rows < 0 || out_features <= 0 || in_features <= 0)
     return fail(RLSE_ERR_INVALID_VALUE, "linear: bad arguments");
   if (rows == 0) return RLSE_OK;
   if (!x || !weight || !y) return fail(RLSE_ERR_INVALID_VALUE, "linear: null pointer");
   hipStream_t s = as_stream(stream);
-  // Decode-shaped products (a few rows, bf16/f16) run on the MFMA kernel.
-  if ((dtype == RLSE_DTYPE_BF16 || dtype == RLSE_DTYPE_F16) && rows <= kDenseMaxRows &&
-      in_features % 32 == 0 && out_features % 16 == 0 && aligned(x, 16) &&
-      aligned(weight, 16) && aligned(y, 8) && (!bias || aligned(bias, 8))) {
+  const bool mfma = (dtype == RLSE_DTYPE_BF16 || dtype == RLSE_DTYPE_F16) &&
+                    in_features % 32 == 0 && out_features % 16 == 0 && aligned(x, 16) &&
+                    aligned(weight, 16) && aligned(y, 8) && (!bias || aligned(bias, 8));
+  if (packed && !mfma)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "linear: packed weights need bf16/f16, in_features %% 32 == 0, out_features %% "
+                "16 == 0 and aligned buffers");
+  // Decode-shaped products (a few rows, bf16/f16) run on the MFMA kernel, as
+  // do products over packed weights (64 rows at a time).
+  if (mfma && (rows <= kDenseMaxRows || packed)) {
     DenseParams p{};
     p.x = x;
     p.w = weight;
@@ -905,6 +947,7 @@ extern "C" int rlse_linear(const void* x, const void* weight, const void* bias, 
     p.rows = rows;
     p.K = in_features;
     p.N = out_features;
+    p.packed = packed;
     return dense_by_dtype<kEpiStore>(dtype, p, in_features, out_features, 0, 0, 0, s);
   }
   int dev = 0;
@@ -953,6 +996,7 @@ extern "C" int rlse_qkv_proj(const void* x, const void* w_qkv, const void* b_qkv
                              void* k, void* v, int rows, int hidden, int q_features,
                              int kv_features, int dtype, void* workspace, size_t workspace_bytes,
                              rlse_stream_t stream) {
+  const bool packed = take_packed(dtype);
   const void* outs[3] = {q, k, v};
   int rc = check_dense("qkv_proj", dtype, rows, hidden, x, w_qkv, outs, 3);
   if (rc || rows == 0) return rc;
@@ -974,6 +1018,7 @@ extern "C" int rlse_qkv_proj(const void* x, const void* w_qkv, const void* b_qkv
   p.n1 = q_features;
   p.n2 = q_features + kv_features;
   p.N = q_features + 2 * kv_features;
+  p.packed = packed;
   size_t words = 0;
   rc = dense_workspace("qkv_proj", p, workspace, workspace_bytes, &words);
   if (rc) return rc;
@@ -985,6 +1030,7 @@ extern "C" int rlse_linear_residual(const void* x, const void* weight, void* res
                                     int out_features, int in_features, int dtype,
                                     void* workspace, size_t workspace_bytes,
                                     rlse_stream_t stream) {
+  const bool packed = take_packed(dtype);
   const void* outs[1] = {residual};
   int rc = check_dense("linear_residual", dtype, rows, in_features, x, weight, outs, 1);
   if (rc || rows == 0) return rc;
@@ -999,6 +1045,7 @@ extern "C" int rlse_linear_residual(const void* x, const void* weight, void* res
   p.rows = rows;
   p.K = in_features;
   p.N = out_features;
+  p.packed = packed;
   size_t words = 0;
   rc = dense_workspace("linear_residual", p, workspace, workspace_bytes, &words);
   if (rc) return rc;
@@ -1009,6 +1056,7 @@ extern "C" int rlse_linear_residual(const void* x, const void* weight, void* res
 extern "C" int rlse_gate_up_silu(const void* x, const void* w_gate_up, void* act, int rows,
                                  int hidden, int inter, int dtype, void* workspace,
                                  size_t workspace_bytes, rlse_stream_t stream) {
+  const bool packed = take_packed(dtype);
   const void* outs[1] = {act};
   int rc = check_dense("gate_up_silu", dtype, rows, hidden, x, w_gate_up, outs, 1);
   if (rc || rows == 0) return rc;
@@ -1023,8 +1071,38 @@ extern "C" int rlse_gate_up_silu(const void* x, const void* w_gate_up, void* act
   p.K = hidden;
   p.N = 2 * inter;
   p.n1 = inter;
+  p.packed = packed;
   size_t words = 0;
   rc = dense_workspace("gate_up_silu", p, workspace, workspace_bytes, &words);
   if (rc) return rc;
   return dense_by_dtype<kEpiSiluMul>(dtype, p, hidden, inter, 0, 0, words, as_stream(stream));
+}
+
+extern "C" int rlse_dense_pack(const void* weight, void* packed, int out_features,
+                               int in_features, int gate_up_inter, int dtype,
+                               rlse_stream_t stream) {
+  if (dtype != RLSE_DTYPE_BF16 && dtype != RLSE_DTYPE_F16)
+    return fail(RLSE_ERR_INVALID_VALUE, "dense_pack: bf16 or f16 only");
+  if (out_features <= 0 || in_features <= 0 || in_features % 32 || gate_up_inter < 0)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "dense_pack: out_features %d, in_features %d (a multiple of 32)", out_features,
+                in_features);
+  if (gate_up_inter > 0 ? (out_features != 2 * gate_up_inter || gate_up_inter % 8)
+                        : out_features % 16)
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "dense_pack: out_features %d must be a multiple of 16, or 2 * gate_up_inter "
+                "with gate_up_inter %d a multiple of 8", out_features, gate_up_inter);
+  if (!weight || !packed || weight == packed)
+    return fail(RLSE_ERR_INVALID_VALUE, "dense_pack: null or in-place buffers");
+  if (!aligned(weight, 16) || !aligned(packed, 16))
+    return fail(RLSE_ERR_INVALID_VALUE, "dense_pack: buffers must be 16-byte aligned");
+  const long long packets = (long long)out_features * in_features / 8;
+  const dim3 grid((unsigned)((packets + 255) / 256));
+  if (dtype == RLSE_DTYPE_BF16)
+    hipLaunchKernelGGL(dense_pack_kernel<bf16>, grid, dim3(256), 0, as_stream(stream),
+                       (const bf16*)weight, (bf16*)packed, in_features, gate_up_inter, packets);
+  else
+    hipLaunchKernelGGL(dense_pack_kernel<f16>, grid, dim3(256), 0, as_stream(stream),
+                       (const f16*)weight, (f16*)packed, in_features, gate_up_inter, packets);
+  return launch_status("dense_pack");
 }

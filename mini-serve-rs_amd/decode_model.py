@@ -112,7 +112,7 @@ class DecodeModel:
 
     def __init__(self, cfg: ModelConfig, weights: Dict[str, object], dtype: str,
                  num_blocks: int, max_batch: int, max_blocks_per_seq: int, device="cuda:0",
-                 stream_pages: bool = False):
+                 stream_pages: bool = False, packed_weights: bool = True):
         if dtype not in _TORCH:
             raise ValueError(f"dtype {dtype!r}")
         # RLSE_DECODE_STREAM for every step: the caller guarantees that no
@@ -144,6 +144,26 @@ class DecodeModel:
             for n in ("q_norm", "k_norm") if cfg.qk_norm else ():
                 L[n] = up(p + n)
             self.layers.append(L)
+        # 16-bit steps: the projection weights in the tile order of the MFMA
+        # kernel (rlse_dense_pack), bit-identical results with one contiguous
+        # KiB per operand load; lm_head too when its shape allows.
+        self.packed = self.fused and packed_weights
+        self.lm_packed = (self.packed and cfg.vocab % 16 == 0 and cfg.hidden % 32 == 0)
+        if self.packed:
+            nq, nkv = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+            shapes = {"qkv_w": (nq + 2 * nkv, cfg.hidden, 0), "o_w": (cfg.hidden, nq, 0),
+                      "gate_up_w": (2 * cfg.inter, cfg.hidden, cfg.inter),
+                      "down_w": (cfg.hidden, cfg.inter, 0)}
+            for L in self.layers:
+                for n, (rows, cols, pair) in shapes.items():
+                    w = torch.empty_like(L[n])
+                    kv.dense_pack(L[n], w, rows, cols, pair, dtype)
+                    L[n] = w
+            if self.lm_packed:
+                w = torch.empty_like(self.lm_head)
+                kv.dense_pack(self.lm_head, w, cfg.vocab, cfg.hidden, 0, dtype)
+                self.lm_head = w
+            torch.cuda.synchronize(dev)
 
         self.pool = kv.KVPool(cfg.layers, num_blocks, cfg.kv_heads, cfg.head_dim, dtype)
         self.max_pos = max_blocks_per_seq * kv.BLOCK_SIZE
@@ -268,7 +288,7 @@ class DecodeModel:
         for l, L in enumerate(self.layers):
             if self.fused:
                 kv.qkv_proj(self.h, L["qkv_w"], L["qkv_b"], self.q, self.k, self.v, batch, H, nq,
-                            nkv, dt, self.dense_ws, stream)
+                            nkv, dt, self.dense_ws, stream, packed=self.packed)
             else:
                 kv.linear(self.h, L["q_w"], L["q_b"], self.q, batch, nq, H, dt, stream)
                 kv.linear(self.h, L["k_w"], L["k_b"], self.k, batch, nkv, H, dt, stream)
@@ -284,13 +304,13 @@ class DecodeModel:
             nxt = self.layers[l + 1]["in_norm"] if l + 1 < cfg.layers else self.norm
             if self.fused:
                 kv.linear_residual(self.attn, L["o_w"], self.x, batch, H, nq, dt, self.dense_ws,
-                                   stream)
+                                   stream, packed=self.packed)
                 kv.add_rmsnorm(None, self.x, L["post_norm"], self.h, batch, H, cfg.eps, dt,
                                stream)
                 kv.gate_up_silu(self.h, L["gate_up_w"], self.act, batch, H, inter, dt,
-                                self.dense_ws, stream)
+                                self.dense_ws, stream, packed=self.packed)
                 kv.linear_residual(self.act, L["down_w"], self.x, batch, H, inter, dt,
-                                   self.dense_ws, stream)
+                                   self.dense_ws, stream, packed=self.packed)
                 kv.add_rmsnorm(None, self.x, nxt, self.h, batch, H, cfg.eps, dt, stream)
             else:
                 kv.linear(self.attn, L["o_w"], None, self.o, batch, H, nq, dt, stream)
@@ -301,7 +321,8 @@ class DecodeModel:
                 kv.silu_mul(self.gu, self.act, batch, inter, dt, stream)
                 kv.linear(self.act, L["down_w"], None, self.o, batch, H, inter, dt, stream)
                 kv.add_rmsnorm(self.o, self.x, nxt, self.h, batch, H, cfg.eps, dt, stream)
-        kv.linear(self.h, self.lm_head, None, self.logits, batch, cfg.vocab, H, dt, stream)
+        kv.linear(self.h, self.lm_head, None, self.logits, batch, cfg.vocab, H, dt, stream,
+                  packed=self.lm_packed)
         kv.argmax(self.logits, self.next_ids, batch, cfg.vocab, dt, self.arg_ws,
                   self.arg_ws.numel(), stream)
         return self.logits[:batch], self.next_ids[:batch]

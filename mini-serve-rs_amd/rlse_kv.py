@@ -76,7 +76,7 @@ EXPORTED = (
     "rlse_st_prepare", "rlse_st_host", "rlse_st_upload", "rlse_st_mark_uploaded",
     "rlse_embedding", "rlse_add_rmsnorm", "rlse_silu_mul", "rlse_argmax", "rlse_linear",
     "rlse_argmax_workspace_size", "rlse_qkv_proj", "rlse_linear_residual", "rlse_gate_up_silu",
-    "rlse_dense_workspace_size", "rlse_decode_plan_size", "rlse_decode_plan",
+    "rlse_dense_workspace_size", "rlse_dense_pack", "rlse_decode_plan_size", "rlse_decode_plan",
     "rlse_decode_step_planned", "rlse_workspace_check", "rlse_set_merge_wait_ns",
     "rlse_decode_step_noalloc", "rlse_decode_prefix_size", "rlse_decode_plan_cascade",
     "rlse_decode_step_cascade",
@@ -265,6 +265,7 @@ _SIGS = {
     "rlse_qkv_proj": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_linear_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_gate_up_silu": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "rlse_dense_pack": (_i, [_vp, _vp, _i, _i, _i, _i, _vp]),
     "rlse_workspace_check": (_i, [_vp, _vp, ctypes.POINTER(ctypes.c_uint)]),
     "rlse_decode_step_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp,
                                       _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp]),
@@ -920,10 +921,28 @@ def argmax(logits, out, rows: int, vocab: int, dtype, workspace, workspace_bytes
                               workspace_bytes, _stream(stream)))
 
 
+# RLSE_DENSE_PACKED: OR-ed into the dtype of the projection calls, the
+# weight is in the tile order dense_pack writes.
+DENSE_PACKED = 0x100
+
+
+def _dtp(dtype, packed: bool) -> int:
+    return _dt(dtype) | (DENSE_PACKED if packed else 0)
+
+
+def dense_pack(weight, packed, out_features: int, in_features: int, gate_up_inter: int, dtype,
+               stream=None) -> None:
+    """rlse_dense_pack: weight [out][in] row-major -> packed (same size) in the
+    order the MFMA projections load; gate_up_inter > 0 for the stacked
+    gate/up weight of gate_up_silu."""
+    _check(load().rlse_dense_pack(_ptr(weight), _ptr(packed), out_features, in_features,
+                                  gate_up_inter, _dt(dtype), _stream(stream)))
+
+
 def linear(x, weight, bias, y, rows: int, out_features: int, in_features: int, dtype,
-           stream=None) -> None:
+           stream=None, packed: bool = False) -> None:
     _check(load().rlse_linear(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), rows, out_features,
-                              in_features, _dt(dtype), _stream(stream)))
+                              in_features, _dtp(dtype, packed), _stream(stream)))
 
 
 def dense_workspace_size(rows: int, out_features: int, in_features: int) -> int:
@@ -942,26 +961,26 @@ def _ws(workspace):
 
 
 def qkv_proj(x, w_qkv, b_qkv, q, k, v, rows: int, hidden: int, q_features: int,
-             kv_features: int, dtype, workspace=None, stream=None) -> None:
+             kv_features: int, dtype, workspace=None, stream=None, packed: bool = False) -> None:
     wp, wb = _ws(workspace)
     _check(load().rlse_qkv_proj(_ptr(x), _ptr(w_qkv), _ptr(b_qkv), _ptr(q), _ptr(k), _ptr(v),
-                                rows, hidden, q_features, kv_features, _dt(dtype), wp, wb,
-                                _stream(stream)))
+                                rows, hidden, q_features, kv_features, _dtp(dtype, packed), wp,
+                                wb, _stream(stream)))
 
 
 def linear_residual(x, weight, residual, rows: int, out_features: int, in_features: int, dtype,
-                    workspace=None, stream=None) -> None:
+                    workspace=None, stream=None, packed: bool = False) -> None:
     wp, wb = _ws(workspace)
     _check(load().rlse_linear_residual(_ptr(x), _ptr(weight), _ptr(residual), rows,
-                                       out_features, in_features, _dt(dtype), wp, wb,
+                                       out_features, in_features, _dtp(dtype, packed), wp, wb,
                                        _stream(stream)))
 
 
 def gate_up_silu(x, w_gate_up, act, rows: int, hidden: int, inter: int, dtype, workspace=None,
-                 stream=None) -> None:
+                 stream=None, packed: bool = False) -> None:
     wp, wb = _ws(workspace)
     _check(load().rlse_gate_up_silu(_ptr(x), _ptr(w_gate_up), _ptr(act), rows, hidden, inter,
-                                    _dt(dtype), wp, wb, _stream(stream)))
+                                    _dtp(dtype, packed), wp, wb, _stream(stream)))
 
 
 # --------------------------------------------------------------------------

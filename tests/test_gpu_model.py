@@ -372,7 +372,7 @@ SPECS = {
 }
 
 
-def _setup(kv, arch, dt, ctx_lens, steps, seed):
+def _setup(kv, arch, dt, ctx_lens, steps, seed, packed=True):
     from decode_model import DecodeModel, ModelConfig
     spec = O.ModelSpec(**SPECS[arch])
     rng = np.random.default_rng(seed)
@@ -381,7 +381,7 @@ def _setup(kv, arch, dt, ctx_lens, steps, seed):
     mbps = max((n + steps + 15) // 16 for n in ctx_lens) + 1
     nb = b * mbps + 5
     tables = build_tables(rng, [mbps * 16] * b, nb, mbps)
-    model = DecodeModel(ModelConfig(**SPECS[arch]), w, dt, nb, b, mbps)
+    model = DecodeModel(ModelConfig(**SPECS[arch]), w, dt, nb, b, mbps, packed_weights=packed)
     # cached context: random K/V (already rotated), the same in pool and oracle
     kc = [[None] * b for _ in range(spec.layers)]
     vc = [[None] * b for _ in range(spec.layers)]
@@ -427,6 +427,124 @@ def test_decode_steps_match_oracle(kv, arch, dt):
             rel_check(f"{arch} K layer {l} seq {i}", host(k[l]), kc[l][i], dt)
             rel_check(f"{arch} V layer {l} seq {i}", host(v[l]), vc[l][i], dt)
     model.close()
+
+
+def _bits(t):
+    torch.cuda.synchronize()
+    return t.contiguous().view(torch.int16).cpu().numpy()
+
+
+def _pack(kv, w, n_out, n_in, pair, dt):
+    packed = torch.empty_like(w)
+    kv.dense_pack(w, packed, n_out, n_in, pair, dt)
+    return packed
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_dense_pack_layout(kv, dt):
+    """rlse_dense_pack against the layout restated in numpy: packet
+    ((tile * K/32 + s) * 64 + lane) = row tile_rows[lane % 16] of the tile,
+    elements 32 s + 8 (lane / 16) .. +8; gate/up tiles take gate rows 8t..8t+7
+    and up rows inter + 8t..+7."""
+    rng = np.random.default_rng(4)
+    for n_out, n_in, pair in ((48, 96, 0), (64, 64, 32)):
+        w = O.round_to(rng.standard_normal((n_out, n_in)), dt)
+        got = host(_pack(kv, dev(w, dt), n_out, n_in, pair, dt)).reshape(-1, 8)
+        tiles = n_out // 16
+        if pair:
+            order = np.concatenate([np.r_[8 * t:8 * t + 8, pair + 8 * t:pair + 8 * t + 8]
+                                    for t in range(tiles)])
+        else:
+            order = np.arange(n_out)
+        want = (w[order].reshape(tiles, 16, n_in // 32, 4, 8)
+                .transpose(0, 2, 3, 1, 4).reshape(-1, 8))
+        np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows", [1, 33, 100])
+def test_packed_weights_give_identical_results(kv, dt, rows):
+    """Every projection over packed weights (RLSE_DENSE_PACKED) returns the
+    row-major weight's bits: q/k/v with bias, o/down_proj with and without
+    the K split, gate/up with SwiGLU, and a wide linear (lm_head-like; more
+    than 64 rows take 64-row chunks, as two row-major calls do)."""
+    rng = np.random.default_rng(rows)
+    r = lambda *s: O.round_to(rng.standard_normal(s) / np.sqrt(s[-1]), dt)  # noqa: E731
+    # q/k/v
+    hidden, nq, nkv = 896, 896, 128
+    x, w, b = dev(r(rows, hidden), dt), dev(r(nq + 2 * nkv, hidden), dt), dev(r(nq + 2 * nkv), dt)
+    pk = _pack(kv, w, nq + 2 * nkv, hidden, 0, dt)
+    res = []
+    for packed, w_ in ((False, w), (True, pk)):
+        outs = [torch.zeros((rows, n), dtype=_T[dt], device=DEV) for n in (nq, nkv, nkv)]
+        ws = _dense_ws(kv, rows, nq + 2 * nkv, hidden, True)
+        kv.qkv_proj(x, w_, b, *outs, rows, hidden, nq, nkv, dt, ws, packed=packed)
+        _assert_clean(ws)
+        res.append([_bits(o) for o in outs])
+    for a, c in zip(*res):
+        np.testing.assert_array_equal(a, c)
+    # o_proj / down_proj, K split and not
+    for n_out, n_in, split in ((1024, 3072, True), (1024, 2048, False), (8192, 128, True)):
+        x, w = dev(r(rows, n_in), dt), dev(r(n_out, n_in), dt)
+        r0 = r(rows, n_out)
+        pk = _pack(kv, w, n_out, n_in, 0, dt)
+        res = []
+        for packed, w_ in ((False, w), (True, pk)):
+            rd = dev(r0, dt)
+            ws = _dense_ws(kv, rows, n_out, n_in, split)
+            kv.linear_residual(x, w_, rd, rows, n_out, n_in, dt, ws, packed=packed)
+            _assert_clean(ws)
+            res.append(_bits(rd))
+        np.testing.assert_array_equal(res[0], res[1])
+    # gate/up + SwiGLU
+    hidden, inter = 1024, 3072
+    x, w = dev(r(rows, hidden), dt), dev(r(2 * inter, hidden), dt)
+    pk = _pack(kv, w, 2 * inter, hidden, inter, dt)
+    res = []
+    for packed, w_ in ((False, w), (True, pk)):
+        act = torch.zeros((rows, inter), dtype=_T[dt], device=DEV)
+        ws = _dense_ws(kv, rows, 2 * inter, hidden, True)
+        kv.gate_up_silu(x, w_, act, rows, hidden, inter, dt, ws, packed=packed)
+        _assert_clean(ws)
+        res.append(_bits(act))
+    np.testing.assert_array_equal(res[0], res[1])
+    # wide linear with bias
+    n_out, n_in = 4096, 1024
+    x, w, b = dev(r(rows, n_in), dt), dev(r(n_out, n_in), dt), dev(r(n_out), dt)
+    pk = _pack(kv, w, n_out, n_in, 0, dt)
+    y0 = torch.zeros((rows, n_out), dtype=_T[dt], device=DEV)
+    for r0 in range(0, rows, 64):
+        n = min(64, rows - r0)
+        kv.linear(x[r0:r0 + n], w, b, y0[r0:r0 + n], n, n_out, n_in, dt)
+    y1 = torch.zeros_like(y0)
+    kv.linear(x, pk, b, y1, rows, n_out, n_in, dt, packed=True)
+    np.testing.assert_array_equal(_bits(y0), _bits(y1))
+
+
+@pytest.mark.parametrize("arch", ["qwen3", "qwen2"])
+def test_decode_model_packed_weights_equal_row_major(kv, arch):
+    """Three steps of DecodeModel over packed weights and over row-major
+    weights (same weights, contexts and ids): logits and greedy ids bit for
+    bit."""
+    ctx, dt = [0, 17, 40], "bf16"
+    runs = []
+    for packed in (True, False):
+        spec, w, model, t_dev, *_rest, rng = _setup(kv, arch, dt, ctx, 3, 9, packed=packed)
+        assert model.packed == packed
+        ids = np.array(rng.integers(0, spec.vocab, len(ctx)), np.int32)
+        lens = np.array(ctx, np.int32)
+        out = []
+        for step in range(3):
+            lens = lens + 1
+            logits, nxt = model.step(torch.from_numpy(ids).to(DEV), t_dev,
+                                     torch.from_numpy(lens).to(DEV), len(ctx))
+            out.append((_bits(logits), nxt.cpu().numpy().copy()))
+            ids = out[-1][1].astype(np.int32)
+        model.close()
+        runs.append(out)
+    for (la, ia), (lb, ib) in zip(*runs):
+        np.testing.assert_array_equal(la, lb)
+        np.testing.assert_array_equal(ia, ib)
 
 
 def test_greedy_loop_on_device_with_step_tables(kv):
