@@ -431,6 +431,15 @@ int rlse_linear(const void* x, const void* weight, const void* bias, void* y, in
  * from each of 16 rows. Packed, rlse_linear runs every row count on the
  * MFMA kernel (64 rows at a time). */
 #define RLSE_DENSE_PACKED 0x100
+/* Packed rows (no counterpart in the reference): OR-ed into the dtype of
+ * rlse_add_rmsnorm, `out` is written, and OR-ed into the dtype of the four
+ * projection calls, `x` is read, in the order of the MFMA kernel's B
+ * operands: per 16-row tile and 32-element k step, 64 16-byte packets
+ * (packet (t * in/32 + s) * 64 + r + 16j holds row 16t + r, elements
+ * 32s + 8j .. +8). bf16/f16, the row length a multiple of 32; the buffer
+ * holds whole 16-row tiles (rows rounded up to 16). Results are the
+ * row-major ones, bit for bit. */
+#define RLSE_PACKED_ROWS 0x200
 /* Writes weight [out_features][in_features] (row-major) to packed in that
  * order (same size, not in place). gate_up_inter > 0: the stacked gate/up
  * weight of rlse_gate_up_silu ([2*gate_up_inter][in], gate rows then up

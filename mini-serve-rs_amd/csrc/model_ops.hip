@@ -71,7 +71,7 @@ constexpr int kNormChunks = 4;
 template <typename T, bool ADD>
 __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
     const T* __restrict__ x, T* __restrict__ residual, const T* __restrict__ w,
-    T* __restrict__ out, int n, float inv_n, float eps) {
+    T* __restrict__ out, int n, float inv_n, float eps, int packed_out) {
   constexpr int E = 16 / sizeof(T);
   __shared__ float s_part[kNormThreads / 64];
   const size_t base = (size_t)blockIdx.x * n;
@@ -112,7 +112,14 @@ __global__ __launch_bounds__(kNormThreads) void norm_rows_kernel(
       Packet<T>::unpack(wp[c], wv);
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] = round_to<T>(h[c][e] / norm) * wv[e];
-      reinterpret_cast<uint4*>(out + base)[ci] = pack_packet<T>(o);
+      // Packed rows (16-bit): row r's packet ci (elements 8ci .. +8) goes to
+      // ((r/16 * n/32 + ci/4) * 64 + r%16 + 16 (ci%4)) * 8, the order in
+      // which dense_rows_kernel loads its B operands.
+      const size_t at =
+          packed_out ? (((size_t)(blockIdx.x >> 4) * (n >> 5) + (ci >> 2)) * 64 + (blockIdx.x & 15) +
+                        16 * (ci & 3)) * 8
+                     : base + (size_t)ci * E;
+      *reinterpret_cast<uint4*>(out + at) = pack_packet<T>(o);
     }
   }
 }
@@ -335,6 +342,7 @@ struct DenseParams {
   int ksplit;        // KS
   int steps;         // 32-wide k steps per wave
   int packed;        // w in the tile order rlse_dense_pack writes
+  int xpacked;       // x in the packed row order (RLSE_PACKED_ROWS)
 };
 
 constexpr int kDenseWaves = 4;
@@ -409,10 +417,15 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
                      : (const T*)p.w + (size_t)row * K + 8 * g;
   }
   const int wstep = p.packed ? 512 : 32;  // weight elements between k steps
+  // x: row-major (rows past the batch read its last row), or packed rows:
+  // row tile t's operands of k step s at ((t * K/32 + s) * 64 + lane) * 8
+  // (the packed buffer holds whole 16-row tiles).
   const T* xr[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t)
-    xr[t] = (const T*)p.x + (size_t)min(16 * t + fi, p.rows - 1) * K + 8 * g;
+    xr[t] = p.xpacked ? (const T*)p.x + ((size_t)t * (K >> 5) * 64 + lane) * 8
+                      : (const T*)p.x + (size_t)min(16 * t + fi, p.rows - 1) * K + 8 * g;
+  const int xstep = p.xpacked ? 512 : 32;  // x elements between k steps
   f32x4_t acc[FT][RT];
 #pragma unroll
   for (int f = 0; f < FT; ++f)
@@ -453,7 +466,8 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
         for (int f = 0; f < FT; ++f)
           a[j][f] = *reinterpret_cast<const u32x4_t*>(wr[f] + (size_t)wstep * (s + j));
 #pragma unroll
-        for (int t = 0; t < RT; ++t) b[j][t] = *reinterpret_cast<const u32x4_t*>(xr[t] + off);
+        for (int t = 0; t < RT; ++t)
+          b[j][t] = *reinterpret_cast<const u32x4_t*>(xr[t] + (size_t)xstep * (s + j));
       }
     }
 #pragma unroll
@@ -800,11 +814,12 @@ __global__ void dense_pack_kernel(const T* __restrict__ w, T* __restrict__ out, 
       *reinterpret_cast<const uint4*>(w + row * K + 32 * st + 8 * g);
 }
 
-// Strips RLSE_DENSE_PACKED from a dtype argument.
-bool take_packed(int& dtype) {
-  const bool packed = (dtype & RLSE_DENSE_PACKED) != 0;
-  dtype &= ~RLSE_DENSE_PACKED;
-  return packed;
+// Strips RLSE_DENSE_PACKED (weight) and RLSE_PACKED_ROWS (x) from a dtype
+// argument into p.
+void take_packed(int& dtype, DenseParams& p) {
+  p.packed = (dtype & RLSE_DENSE_PACKED) != 0;
+  p.xpacked = (dtype & RLSE_PACKED_ROWS) != 0;
+  dtype &= ~(RLSE_DENSE_PACKED | RLSE_PACKED_ROWS);
 }
 
 }  // namespace
@@ -831,6 +846,8 @@ extern "C" int rlse_embedding(const int32_t* ids, const void* table, void* out, 
 
 extern "C" int rlse_add_rmsnorm(const void* x, void* residual, const void* weight, void* out,
                                 int rows, int n, float eps, int dtype, rlse_stream_t stream) {
+  const bool packed_out = (dtype & RLSE_PACKED_ROWS) != 0;
+  dtype &= ~RLSE_PACKED_ROWS;
   const size_t es = dtype_size(dtype);
   if (!es || rows < 0 || n <= 0 || !(eps >= 0.f))
     return fail(RLSE_ERR_INVALID_VALUE, "add_rmsnorm: bad arguments");
@@ -842,6 +859,10 @@ extern "C" int rlse_add_rmsnorm(const void* x, void* residual, const void* weigh
   const bool chunked = (n * es) % 16 == 0 && n * es / 16 <= (size_t)kNormThreads * kNormChunks &&
                        aligned(residual, 16) && aligned(weight, 16) && aligned(out, 16) &&
                        (!x || aligned(x, 16));
+  if (packed_out && (es != 2 || n % 32 || !chunked))
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "add_rmsnorm: packed rows need bf16/f16, n a multiple of 32 (at most %d) and "
+                "16-byte aligned buffers", kNormThreads * kNormChunks * 8);
   return by_dtype(dtype, [&](auto t) {
     using T = decltype(t);
     const T* xp = (const T*)x;
@@ -849,10 +870,10 @@ extern "C" int rlse_add_rmsnorm(const void* x, void* residual, const void* weigh
     if (chunked) {
       if (x)
         hipLaunchKernelGGL((norm_rows_kernel<T, true>), dim3(rows), dim3(kNormThreads), 0, s,
-                           xp, rp, (const T*)weight, (T*)out, n, inv_n, eps);
+                           xp, rp, (const T*)weight, (T*)out, n, inv_n, eps, (int)packed_out);
       else
         hipLaunchKernelGGL((norm_rows_kernel<T, false>), dim3(rows), dim3(kNormThreads), 0, s,
-                           xp, rp, (const T*)weight, (T*)out, n, inv_n, eps);
+                           xp, rp, (const T*)weight, (T*)out, n, inv_n, eps, (int)packed_out);
     } else if (x) {
       hipLaunchKernelGGL((norm_rows_any_kernel<T, true>), dim3((rows + 3) / 4), dim3(256), 0, s,
                          xp, rp, (const T*)weight, (T*)out, rows, n, inv_n, eps);
@@ -923,7 +944,9 @@ extern "C" int rlse_argmax(const void* logits, int32_t* out, int rows, int vocab
 extern "C" int rlse_linear(const void* x, const void* weight, const void* bias, void* y,
                            int rows, int out_features, int in_features, int dtype,
                            rlse_stream_t stream) {
-  const bool packed = take_packed(dtype);
+  DenseParams flags{};
+  take_packed(dtype, flags);
+  const bool packed = flags.packed || flags.xpacked;
   if (!dtype_size(dtype) || rows < 0 || out_features <= 0 || in_features <= 0)
     return fail(RLSE_ERR_INVALID_VALUE, "linear: bad arguments");
   if (rows == 0) return RLSE_OK;
@@ -934,8 +957,8 @@ extern "C" int rlse_linear(const void* x, const void* weight, const void* bias, 
                     aligned(weight, 16) && aligned(y, 8) && (!bias || aligned(bias, 8));
   if (packed && !mfma)
     return fail(RLSE_ERR_INVALID_VALUE,
-                "linear: packed weights need bf16/f16, in_features %% 32 == 0, out_features %% "
-                "16 == 0 and aligned buffers");
+                "linear: packed weights or rows need bf16/f16, in_features %% 32 == 0, "
+                "out_features %% 16 == 0 and aligned buffers");
   // Decode-shaped products (a few rows, bf16/f16) run on the MFMA kernel, as
   // do products over packed weights (64 rows at a time).
   if (mfma && (rows <= kDenseMaxRows || packed)) {
@@ -947,7 +970,8 @@ extern "C" int rlse_linear(const void* x, const void* weight, const void* bias, 
     p.rows = rows;
     p.K = in_features;
     p.N = out_features;
-    p.packed = packed;
+    p.packed = flags.packed;
+    p.xpacked = flags.xpacked;
     return dense_by_dtype<kEpiStore>(dtype, p, in_features, out_features, 0, 0, 0, s);
   }
   int dev = 0;
@@ -996,7 +1020,9 @@ extern "C" int rlse_qkv_proj(const void* x, const void* w_qkv, const void* b_qkv
                              void* k, void* v, int rows, int hidden, int q_features,
                              int kv_features, int dtype, void* workspace, size_t workspace_bytes,
                              rlse_stream_t stream) {
-  const bool packed = take_packed(dtype);
+  DenseParams flags{};
+  take_packed(dtype, flags);
+  const bool packed = flags.packed || flags.xpacked;
   const void* outs[3] = {q, k, v};
   int rc = check_dense("qkv_proj", dtype, rows, hidden, x, w_qkv, outs, 3);
   if (rc || rows == 0) return rc;
@@ -1018,7 +1044,8 @@ extern "C" int rlse_qkv_proj(const void* x, const void* w_qkv, const void* b_qkv
   p.n1 = q_features;
   p.n2 = q_features + kv_features;
   p.N = q_features + 2 * kv_features;
-  p.packed = packed;
+  p.packed = flags.packed;
+  p.xpacked = flags.xpacked;
   size_t words = 0;
   rc = dense_workspace("qkv_proj", p, workspace, workspace_bytes, &words);
   if (rc) return rc;
@@ -1030,7 +1057,9 @@ extern "C" int rlse_linear_residual(const void* x, const void* weight, void* res
                                     int out_features, int in_features, int dtype,
                                     void* workspace, size_t workspace_bytes,
                                     rlse_stream_t stream) {
-  const bool packed = take_packed(dtype);
+  DenseParams flags{};
+  take_packed(dtype, flags);
+  const bool packed = flags.packed || flags.xpacked;
   const void* outs[1] = {residual};
   int rc = check_dense("linear_residual", dtype, rows, in_features, x, weight, outs, 1);
   if (rc || rows == 0) return rc;
@@ -1045,7 +1074,8 @@ extern "C" int rlse_linear_residual(const void* x, const void* weight, void* res
   p.rows = rows;
   p.K = in_features;
   p.N = out_features;
-  p.packed = packed;
+  p.packed = flags.packed;
+  p.xpacked = flags.xpacked;
   size_t words = 0;
   rc = dense_workspace("linear_residual", p, workspace, workspace_bytes, &words);
   if (rc) return rc;
@@ -1056,7 +1086,9 @@ extern "C" int rlse_linear_residual(const void* x, const void* weight, void* res
 extern "C" int rlse_gate_up_silu(const void* x, const void* w_gate_up, void* act, int rows,
                                  int hidden, int inter, int dtype, void* workspace,
                                  size_t workspace_bytes, rlse_stream_t stream) {
-  const bool packed = take_packed(dtype);
+  DenseParams flags{};
+  take_packed(dtype, flags);
+  const bool packed = flags.packed || flags.xpacked;
   const void* outs[1] = {act};
   int rc = check_dense("gate_up_silu", dtype, rows, hidden, x, w_gate_up, outs, 1);
   if (rc || rows == 0) return rc;
@@ -1071,7 +1103,8 @@ extern "C" int rlse_gate_up_silu(const void* x, const void* w_gate_up, void* act
   p.K = hidden;
   p.N = 2 * inter;
   p.n1 = inter;
-  p.packed = packed;
+  p.packed = flags.packed;
+  p.xpacked = flags.xpacked;
   size_t words = 0;
   rc = dense_workspace("gate_up_silu", p, workspace, workspace_bytes, &words);
   if (rc) return rc;

@@ -176,7 +176,10 @@ class DecodeModel:
         B, t = max_batch, _TORCH[dtype]
         nq, nkv = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
         z = lambda *s: torch.zeros(s, dtype=t, device=dev)  # noqa: E731
-        self.x, self.h, self.o = z(B, cfg.hidden), z(B, cfg.hidden), z(B, cfg.hidden)
+        # h (the norms' output, the projections' input) holds whole 16-row
+        # tiles: with packed weights it is written in packed row order.
+        self.x, self.o = z(B, cfg.hidden), z(B, cfg.hidden)
+        self.h = z((B + 15) // 16 * 16, cfg.hidden)
         self.q, self.k, self.v, self.attn = z(B, nq), z(B, nkv), z(B, nkv), z(B, nq)
         self.gu = None if self.fused else z(B, 2 * cfg.inter)
         self.act = z(B, cfg.inter)
@@ -282,13 +285,14 @@ class DecodeModel:
         inter = cfg.inter
         kv.embedding(ids, self.embed, self.x, batch, H, cfg.vocab, dt, stream)
         kv.add_rmsnorm(None, self.x, self.layers[0]["in_norm"], self.h, batch, H, cfg.eps, dt,
-                       stream)
+                       stream, packed_out=self.packed if cfg.layers else self.lm_packed)
         kv.decode_plan(block_tables, seq_lens, batch, cfg.kv_heads, self.mbps, self.num_blocks,
                        self.plan, self.plan.numel(), stream)
         for l, L in enumerate(self.layers):
             if self.fused:
                 kv.qkv_proj(self.h, L["qkv_w"], L["qkv_b"], self.q, self.k, self.v, batch, H, nq,
-                            nkv, dt, self.dense_ws, stream, packed=self.packed)
+                            nkv, dt, self.dense_ws, stream, packed=self.packed,
+                            packed_x=self.packed)
             else:
                 kv.linear(self.h, L["q_w"], L["q_b"], self.q, batch, nq, H, dt, stream)
                 kv.linear(self.h, L["k_w"], L["k_b"], self.k, batch, nkv, H, dt, stream)
@@ -306,12 +310,16 @@ class DecodeModel:
                 kv.linear_residual(self.attn, L["o_w"], self.x, batch, H, nq, dt, self.dense_ws,
                                    stream, packed=self.packed)
                 kv.add_rmsnorm(None, self.x, L["post_norm"], self.h, batch, H, cfg.eps, dt,
-                               stream)
+                               stream, packed_out=self.packed)
                 kv.gate_up_silu(self.h, L["gate_up_w"], self.act, batch, H, inter, dt,
-                                self.dense_ws, stream, packed=self.packed)
+                                self.dense_ws, stream, packed=self.packed, packed_x=self.packed)
                 kv.linear_residual(self.act, L["down_w"], self.x, batch, H, inter, dt,
                                    self.dense_ws, stream, packed=self.packed)
-                kv.add_rmsnorm(None, self.x, nxt, self.h, batch, H, cfg.eps, dt, stream)
+                # lm_head reads the final norm packed only if it runs on the
+                # MFMA kernel (vocab a multiple of 16)
+                last = l + 1 == cfg.layers
+                kv.add_rmsnorm(None, self.x, nxt, self.h, batch, H, cfg.eps, dt, stream,
+                               packed_out=self.lm_packed if last else self.packed)
             else:
                 kv.linear(self.attn, L["o_w"], None, self.o, batch, H, nq, dt, stream)
                 kv.add_rmsnorm(self.o, self.x, L["post_norm"], self.h, batch, H, cfg.eps, dt,
@@ -322,7 +330,7 @@ class DecodeModel:
                 kv.linear(self.act, L["down_w"], None, self.o, batch, H, inter, dt, stream)
                 kv.add_rmsnorm(self.o, self.x, nxt, self.h, batch, H, cfg.eps, dt, stream)
         kv.linear(self.h, self.lm_head, None, self.logits, batch, cfg.vocab, H, dt, stream,
-                  packed=self.lm_packed)
+                  packed=self.lm_packed, packed_x=self.lm_packed)
         kv.argmax(self.logits, self.next_ids, batch, cfg.vocab, dt, self.arg_ws,
                   self.arg_ws.numel(), stream)
         return self.logits[:batch], self.next_ids[:batch]

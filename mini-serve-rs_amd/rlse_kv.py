@@ -899,9 +899,12 @@ def embedding(ids, table, out, batch: int, hidden: int, vocab: int, dtype, strea
 
 
 def add_rmsnorm(x, residual, weight, out, rows: int, n: int, eps: float, dtype,
-                stream=None) -> None:
+                stream=None, packed_out: bool = False) -> None:
+    """packed_out: out in the packed row order (PACKED_ROWS) the projections
+    read with packed_x; out then holds whole 16-row tiles."""
     _check(load().rlse_add_rmsnorm(_ptr(x), _ptr(residual), _ptr(weight), _ptr(out), rows, n,
-                                   eps, _dt(dtype), _stream(stream)))
+                                   eps, _dt(dtype) | (PACKED_ROWS if packed_out else 0),
+                                   _stream(stream)))
 
 
 def silu_mul(gate_up, out, rows: int, inter: int, dtype, stream=None) -> None:
@@ -924,10 +927,13 @@ def argmax(logits, out, rows: int, vocab: int, dtype, workspace, workspace_bytes
 # RLSE_DENSE_PACKED: OR-ed into the dtype of the projection calls, the
 # weight is in the tile order dense_pack writes.
 DENSE_PACKED = 0x100
+# RLSE_PACKED_ROWS: x of a projection (or out of add_rmsnorm) in the packed
+# row order of the MFMA kernel's B operands.
+PACKED_ROWS = 0x200
 
 
-def _dtp(dtype, packed: bool) -> int:
-    return _dt(dtype) | (DENSE_PACKED if packed else 0)
+def _dtp(dtype, packed: bool, packed_x: bool = False) -> int:
+    return _dt(dtype) | (DENSE_PACKED if packed else 0) | (PACKED_ROWS if packed_x else 0)
 
 
 def dense_pack(weight, packed, out_features: int, in_features: int, gate_up_inter: int, dtype,
@@ -940,9 +946,9 @@ def dense_pack(weight, packed, out_features: int, in_features: int, gate_up_inte
 
 
 def linear(x, weight, bias, y, rows: int, out_features: int, in_features: int, dtype,
-           stream=None, packed: bool = False) -> None:
+           stream=None, packed: bool = False, packed_x: bool = False) -> None:
     _check(load().rlse_linear(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), rows, out_features,
-                              in_features, _dtp(dtype, packed), _stream(stream)))
+                              in_features, _dtp(dtype, packed, packed_x), _stream(stream)))
 
 
 def dense_workspace_size(rows: int, out_features: int, in_features: int) -> int:
@@ -961,26 +967,28 @@ def _ws(workspace):
 
 
 def qkv_proj(x, w_qkv, b_qkv, q, k, v, rows: int, hidden: int, q_features: int,
-             kv_features: int, dtype, workspace=None, stream=None, packed: bool = False) -> None:
+             kv_features: int, dtype, workspace=None, stream=None, packed: bool = False,
+             packed_x: bool = False) -> None:
     wp, wb = _ws(workspace)
     _check(load().rlse_qkv_proj(_ptr(x), _ptr(w_qkv), _ptr(b_qkv), _ptr(q), _ptr(k), _ptr(v),
-                                rows, hidden, q_features, kv_features, _dtp(dtype, packed), wp,
-                                wb, _stream(stream)))
+                                rows, hidden, q_features, kv_features,
+                                _dtp(dtype, packed, packed_x), wp, wb, _stream(stream)))
 
 
 def linear_residual(x, weight, residual, rows: int, out_features: int, in_features: int, dtype,
-                    workspace=None, stream=None, packed: bool = False) -> None:
+                    workspace=None, stream=None, packed: bool = False,
+                    packed_x: bool = False) -> None:
     wp, wb = _ws(workspace)
     _check(load().rlse_linear_residual(_ptr(x), _ptr(weight), _ptr(residual), rows,
-                                       out_features, in_features, _dtp(dtype, packed), wp, wb,
-                                       _stream(stream)))
+                                       out_features, in_features, _dtp(dtype, packed, packed_x),
+                                       wp, wb, _stream(stream)))
 
 
 def gate_up_silu(x, w_gate_up, act, rows: int, hidden: int, inter: int, dtype, workspace=None,
-                 stream=None, packed: bool = False) -> None:
+                 stream=None, packed: bool = False, packed_x: bool = False) -> None:
     wp, wb = _ws(workspace)
     _check(load().rlse_gate_up_silu(_ptr(x), _ptr(w_gate_up), _ptr(act), rows, hidden, inter,
-                                    _dtp(dtype, packed), wp, wb, _stream(stream)))
+                                    _dtp(dtype, packed, packed_x), wp, wb, _stream(stream)))
 
 
 # --------------------------------------------------------------------------

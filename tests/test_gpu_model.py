@@ -461,6 +461,76 @@ def test_dense_pack_layout(kv, dt):
         np.testing.assert_array_equal(got, want)
 
 
+def _pack_rows(x):
+    """Rows [rows][K] in the packed row order (RLSE_PACKED_ROWS), padded to
+    whole 16-row tiles with zeros: packet (t * K/32 + s) * 64 + r + 16 j =
+    row 16 t + r, elements 32 s + 8 j .. +8."""
+    rows, k = x.shape
+    rt = (rows + 15) // 16
+    xp = np.zeros((rt * 16, k), x.dtype)
+    xp[:rows] = x
+    return xp.reshape(rt, 16, k // 32, 4, 8).transpose(0, 2, 3, 1, 4).reshape(rt * 16, k)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows", [3, 32, 40])
+def test_add_rmsnorm_packed_rows(kv, dt, rows):
+    """add_rmsnorm with packed output writes the row-major result's bits in
+    the packed row order (with and without the residual add)."""
+    rng = np.random.default_rng(rows)
+    n = 1024
+    x = O.round_to(rng.standard_normal((rows, n)), dt)
+    r = O.round_to(rng.standard_normal((rows, n)), dt)
+    w = O.round_to(1 + 0.1 * rng.standard_normal(n), dt)
+    for add in (False, True):
+        outs = []
+        for packed in (False, True):
+            rd = dev(r, dt)
+            out = torch.zeros(((rows + 15) // 16 * 16, n), dtype=_T[dt], device=DEV)
+            kv.add_rmsnorm(dev(x, dt) if add else None, rd, dev(w, dt), out, rows, n, 1e-6, dt,
+                           packed_out=packed)
+            outs.append(host(out))
+        want = _pack_rows(outs[0][:rows])
+        np.testing.assert_array_equal(outs[1].reshape(-1)[:want.size], want.reshape(-1))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows", [1, 33, 100])
+def test_packed_rows_and_weights_give_identical_results(kv, dt, rows):
+    """q/k/v, gate/up and a wide linear reading packed x (and packed
+    weights) return the row-major call's bits."""
+    rng = np.random.default_rng(rows + 5)
+    r = lambda *s: O.round_to(rng.standard_normal(s) / np.sqrt(s[-1]), dt)  # noqa: E731
+    hidden, nq, nkv, inter, vocab = 1024, 2048, 1024, 3072, 4096
+    x = r(rows, hidden)
+    xd, xpk = dev(x, dt), dev(_pack_rows(x), dt)
+    wq, bq = dev(r(nq + 2 * nkv, hidden), dt), dev(r(nq + 2 * nkv), dt)
+    wg, wl = dev(r(2 * inter, hidden), dt), dev(r(vocab, hidden), dt)
+    pq = _pack(kv, wq, nq + 2 * nkv, hidden, 0, dt)
+    pg = _pack(kv, wg, 2 * inter, hidden, inter, dt)
+    pl = _pack(kv, wl, vocab, hidden, 0, dt)
+    res = []
+    for packed in (False, True):
+        xx = xpk if packed else xd
+        outs = [torch.zeros((rows, n), dtype=_T[dt], device=DEV) for n in (nq, nkv, nkv)]
+        ws = _dense_ws(kv, rows, nq + 2 * nkv, hidden, True)
+        kv.qkv_proj(xx, pq if packed else wq, bq, *outs, rows, hidden, nq, nkv, dt, ws,
+                    packed=packed, packed_x=packed)
+        act = torch.zeros((rows, inter), dtype=_T[dt], device=DEV)
+        kv.gate_up_silu(xx, pg if packed else wg, act, rows, hidden, inter, dt, None,
+                        packed=packed, packed_x=packed)
+        y = torch.zeros((rows, vocab), dtype=_T[dt], device=DEV)
+        if packed:
+            kv.linear(xx, pl, None, y, rows, vocab, hidden, dt, packed=True, packed_x=True)
+        else:
+            for r0 in range(0, rows, 64):
+                n = min(64, rows - r0)
+                kv.linear(xd[r0:r0 + n], wl, None, y[r0:r0 + n], n, vocab, hidden, dt)
+        res.append([_bits(o) for o in outs + [act, y]])
+    for a, c in zip(*res):
+        np.testing.assert_array_equal(a, c)
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("rows", [1, 33, 100])
 def test_packed_weights_give_identical_results(kv, dt, rows):
