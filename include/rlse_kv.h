@@ -440,6 +440,10 @@ int rlse_linear(const void* x, const void* weight, const void* bias, void* y, in
  * holds whole 16-row tiles (rows rounded up to 16). Results are the
  * row-major ones, bit for bit. */
 #define RLSE_PACKED_ROWS 0x200
+/* OR-ed into the dtype of rlse_gate_up_silu: act is written in the packed
+ * row order (inter a multiple of 32; act holds whole 16-row tiles), ready
+ * for rlse_linear_residual's x with RLSE_PACKED_ROWS. */
+#define RLSE_PACKED_OUT 0x400
 /* Writes weight [out_features][in_features] (row-major) to packed in that
  * order (same size, not in place). gate_up_inter > 0: the stacked gate/up
  * weight of rlse_gate_up_silu ([2*gate_up_inter][in], gate rows then up

@@ -343,6 +343,7 @@ struct DenseParams {
   int steps;         // 32-wide k steps per wave
   int packed;        // w in the tile order rlse_dense_pack writes
   int xpacked;       // x in the packed row order (RLSE_PACKED_ROWS)
+  int opacked;       // kEpiSiluMul: act in the packed row order (RLSE_PACKED_OUT)
 };
 
 constexpr int kDenseWaves = 4;
@@ -593,7 +594,12 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
       for (int e = 0; e < 4; ++e)
         o[e] = ok ? silu_mul_rounded<T>(round_to<T>(v[k][0][e]), round_to<T>(v[k][1][e]))
                   : __builtin_nanf("");
-      store4<T>((T*)p.out0 + (size_t)b * p.n1 + tile * 8 + fq, o);
+      const int c = tile * 8 + fq;  // act feature (4 of them)
+      store4<T>((T*)p.out0 +
+                    (p.opacked ? (((size_t)(b >> 4) * (p.n1 >> 5) + (c >> 5)) * 64 + (b & 15) +
+                                  16 * ((c & 31) >> 3)) * 8 + (c & 7)
+                               : (size_t)b * p.n1 + c),
+                o);
     } else if constexpr (EPI == kEpiResidual) {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -814,12 +820,13 @@ __global__ void dense_pack_kernel(const T* __restrict__ w, T* __restrict__ out, 
       *reinterpret_cast<const uint4*>(w + row * K + 32 * st + 8 * g);
 }
 
-// Strips RLSE_DENSE_PACKED (weight) and RLSE_PACKED_ROWS (x) from a dtype
-// argument into p.
+// Strips RLSE_DENSE_PACKED (weight), RLSE_PACKED_ROWS (x) and
+// RLSE_PACKED_OUT (gate/up's act) from a dtype argument into p.
 void take_packed(int& dtype, DenseParams& p) {
   p.packed = (dtype & RLSE_DENSE_PACKED) != 0;
   p.xpacked = (dtype & RLSE_PACKED_ROWS) != 0;
-  dtype &= ~(RLSE_DENSE_PACKED | RLSE_PACKED_ROWS);
+  p.opacked = (dtype & RLSE_PACKED_OUT) != 0;
+  dtype &= ~(RLSE_DENSE_PACKED | RLSE_PACKED_ROWS | RLSE_PACKED_OUT);
 }
 
 }  // namespace
@@ -1095,6 +1102,10 @@ extern "C" int rlse_gate_up_silu(const void* x, const void* w_gate_up, void* act
   if (inter <= 0 || inter % 8)
     return fail(RLSE_ERR_INVALID_VALUE,
                 "gate_up_silu: intermediate size %d must be a positive multiple of 8", inter);
+  if (flags.opacked && (inter % 32 || !aligned(act, 16)))
+    return fail(RLSE_ERR_INVALID_VALUE,
+                "gate_up_silu: packed act needs inter a multiple of 32 (%d) and 16-byte alignment",
+                inter);
   DenseParams p{};
   p.x = x;
   p.w = w_gate_up;
@@ -1105,6 +1116,7 @@ extern "C" int rlse_gate_up_silu(const void* x, const void* w_gate_up, void* act
   p.n1 = inter;
   p.packed = flags.packed;
   p.xpacked = flags.xpacked;
+  p.opacked = flags.opacked;
   size_t words = 0;
   rc = dense_workspace("gate_up_silu", p, workspace, workspace_bytes, &words);
   if (rc) return rc;

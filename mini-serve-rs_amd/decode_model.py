@@ -149,6 +149,7 @@ class DecodeModel:
         # KiB per operand load; lm_head too when its shape allows.
         self.packed = self.fused and packed_weights
         self.lm_packed = (self.packed and cfg.vocab % 16 == 0 and cfg.hidden % 32 == 0)
+        self.act_packed = self.packed and cfg.inter % 32 == 0
         if self.packed:
             nq, nkv = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
             shapes = {"qkv_w": (nq + 2 * nkv, cfg.hidden, 0), "o_w": (cfg.hidden, nq, 0),
@@ -182,7 +183,7 @@ class DecodeModel:
         self.h = z((B + 15) // 16 * 16, cfg.hidden)
         self.q, self.k, self.v, self.attn = z(B, nq), z(B, nkv), z(B, nkv), z(B, nq)
         self.gu = None if self.fused else z(B, 2 * cfg.inter)
-        self.act = z(B, cfg.inter)
+        self.act = z((B + 15) // 16 * 16, cfg.inter)  # whole 16-row tiles (packed rows)
         self.logits = z(B, cfg.vocab)
         self.next_ids = torch.zeros(B, dtype=torch.int32, device=dev)
         self.arg_ws = torch.zeros(max(kv.argmax_workspace_size(B, cfg.vocab), 8),
@@ -312,9 +313,11 @@ class DecodeModel:
                 kv.add_rmsnorm(None, self.x, L["post_norm"], self.h, batch, H, cfg.eps, dt,
                                stream, packed_out=self.packed)
                 kv.gate_up_silu(self.h, L["gate_up_w"], self.act, batch, H, inter, dt,
-                                self.dense_ws, stream, packed=self.packed, packed_x=self.packed)
+                                self.dense_ws, stream, packed=self.packed, packed_x=self.packed,
+                                packed_out=self.act_packed)
                 kv.linear_residual(self.act, L["down_w"], self.x, batch, H, inter, dt,
-                                   self.dense_ws, stream, packed=self.packed)
+                                   self.dense_ws, stream, packed=self.packed,
+                                   packed_x=self.act_packed)
                 # lm_head reads the final norm packed only if it runs on the
                 # MFMA kernel (vocab a multiple of 16)
                 last = l + 1 == cfg.layers

@@ -930,6 +930,8 @@ DENSE_PACKED = 0x100
 # RLSE_PACKED_ROWS: x of a projection (or out of add_rmsnorm) in the packed
 # row order of the MFMA kernel's B operands.
 PACKED_ROWS = 0x200
+# RLSE_PACKED_OUT: gate_up_silu's act written in that order.
+PACKED_OUT = 0x400
 
 
 def _dtp(dtype, packed: bool, packed_x: bool = False) -> int:
@@ -985,10 +987,12 @@ def linear_residual(x, weight, residual, rows: int, out_features: int, in_featur
 
 
 def gate_up_silu(x, w_gate_up, act, rows: int, hidden: int, inter: int, dtype, workspace=None,
-                 stream=None, packed: bool = False, packed_x: bool = False) -> None:
+                 stream=None, packed: bool = False, packed_x: bool = False,
+                 packed_out: bool = False) -> None:
     wp, wb = _ws(workspace)
     _check(load().rlse_gate_up_silu(_ptr(x), _ptr(w_gate_up), _ptr(act), rows, hidden, inter,
-                                    _dtp(dtype, packed, packed_x), wp, wb, _stream(stream)))
+                                    _dtp(dtype, packed, packed_x) |
+                                    (PACKED_OUT if packed_out else 0), wp, wb, _stream(stream)))
 
 
 # --------------------------------------------------------------------------

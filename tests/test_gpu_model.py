@@ -533,6 +533,33 @@ def test_packed_rows_and_weights_give_identical_results(kv, dt, rows):
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("rows", [1, 33, 100])
+def test_packed_act_feeds_down_proj(kv, dt, rows):
+    """gate_up_silu with packed output writes the row-major act's bits in the
+    packed row order; down_proj (K split) reading it packed returns the
+    row-major call's bits."""
+    rng = np.random.default_rng(rows + 11)
+    r = lambda *s: O.round_to(rng.standard_normal(s) / np.sqrt(s[-1]), dt)  # noqa: E731
+    hidden, inter = 1024, 3072
+    x, w, wd = dev(r(rows, hidden), dt), dev(r(2 * inter, hidden), dt), dev(r(hidden, inter), dt)
+    act0 = torch.zeros((rows, inter), dtype=_T[dt], device=DEV)
+    kv.gate_up_silu(x, w, act0, rows, hidden, inter, dt)
+    act1 = torch.zeros(((rows + 15) // 16 * 16, inter), dtype=_T[dt], device=DEV)
+    kv.gate_up_silu(x, w, act1, rows, hidden, inter, dt, packed_out=True)
+    want = _pack_rows(host(act0))
+    np.testing.assert_array_equal(host(act1).reshape(-1)[:want.size], want.reshape(-1))
+    res0 = O.round_to(rng.standard_normal((rows, hidden)), dt)
+    ys = []
+    for a, packed in ((act0, False), (act1, True)):
+        y = dev(res0, dt)
+        ws = _dense_ws(kv, rows, hidden, inter, True)
+        kv.linear_residual(a, wd, y, rows, hidden, inter, dt, ws, packed_x=packed)
+        _assert_clean(ws)
+        ys.append(_bits(y))
+    np.testing.assert_array_equal(ys[0], ys[1])
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows", [1, 33, 100])
 def test_packed_weights_give_identical_results(kv, dt, rows):
     """Every projection over packed weights (RLSE_DENSE_PACKED) returns the
     row-major weight's bits: q/k/v with bias, o/down_proj with and without
