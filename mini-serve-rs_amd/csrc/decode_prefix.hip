@@ -9,8 +9,9 @@
 // O^T += V^T . P^T on 16x16x16 MFMAs with V transposed through LDS). The
 // prefix is cut into NS = prefix_splits(P) slices of about 16 pages, one
 // workgroup per (column tile, KV head, slice), and each wave of a workgroup
-// takes its own pages of the slice. The waves' partial softmax states are
-// combined in LDS (pairwise, in a fixed order) into the slice's state --
+// takes its own pages of the slice. The waves' partial softmax states meet
+// in LDS, where wave t combines accumulator tile t of all waves (in wave
+// order) into the slice's state --
 // acc[D], m, l of each query in the decode's log2 units -- and the decode
 // launch combines the slices' states, in slice order, into each row it
 // finishes; it leaves the prefix out of its page stream. Workgroups are
