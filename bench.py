@@ -125,17 +125,18 @@ def copy_calibration():
     print(json.dumps({"copy_bytes": COPY_BYTES, "dispatches": 3}))
 
 
-def algorithmic_decode_bytes(lens, hq, hkv, d, es, fused):
+def algorithmic_decode_bytes(lens, hq, hkv, d, es, fused, qk_norm=True):
     """HBM bytes one decode launch must move: every attended K and V row once,
     q in and out once, the used block-table entries and the lengths. The fused
     step also reads each sequence's new K/V rows and writes them into the pool
     (2 x B x 2 x Hkv x d elements), reads one cos and one sin row of d/2
-    elements per sequence and the two RMSNorm weights."""
+    elements per sequence and, when the model has q/k norms, the two RMSNorm
+    weights."""
     b = len(lens)
     kv = sum(int(n) * 2 * hkv * d * es for n in lens)
     qo = 2 * b * hq * d * es
     tab = sum(((int(n) + 15) // 16) * 4 for n in lens)
-    app = (2 * b * 2 * hkv * d * es + b * d * es + 2 * d * es) if fused else 0
+    app = (2 * b * 2 * hkv * d * es + b * d * es + (2 * d * es if qk_norm else 0)) if fused else 0
     return kv + qo + tab + 4 * b + app
 
 
@@ -303,27 +304,23 @@ def prefill_cpu_baseline(args, hq, hkv, d, tq, offset):
             "sample": f"{n} KV head(s) of the chunk ({g} query heads each, f32) in {el:.2f} s"}
 
 
-def fork_bench(args):
-    """Prefix fork: one prefix held in refcounted pages of a pool handle (all
-    layers in one allocation, one block id spanning the layers), 64 requests
+def fork_inputs(workload, seed, dev, layers=None):
+    """Every buffer of a prefix-fork workload, resident on dev. One prefix of
+    plen tokens is written into refcounted pages of a pool handle (all layers
+    in one allocation, one block id spanning the layers); 64 requests are
     forked from it by the block manager (full pages shared, the trailing
-    partial page copied on write), each with a private suffix. The fork runs
-    once per request and is timed on its own; one step = one fused decode step
-    per layer for the 64 forked sequences (append of the new token + decode
-    over shared prefix pages and private suffix pages): by default the
-    cascade step (rlse_decode_step_cascade: the shared full pages attended once
-    for the batch, then each sequence's own pages, streamed), with
-    --no-cascade the planned step over every sequence's whole table (prefix
-    pages cacheable, re-read by every row)."""
+    partial page copied on write, timed as fork_ms), each then growing
+    private pages for its suffix of U[lo, hi] cached tokens + the token this
+    step appends. Returns the pool, the host and device block tables, the
+    lengths (keys after the append), each layer's q / new k / new v, the q/k
+    RMSNorm weights and the RoPE tables. layers: how many layers the pool
+    holds (default: all of the workload's)."""
     import numpy as np
     import torch
-
     import rlse_kv as kv
-
-    hq, hkv, d, layers, b, plen, lo, hi, desc = FORK[args.workload]
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    rng = np.random.default_rng(args.seed)
+    hq, hkv, d, n_layers, b, plen, lo, hi, _ = FORK[workload]
+    layers = n_layers if layers is None else layers
+    rng = np.random.default_rng(seed)
     suffix = rng.integers(lo, hi + 1, b).astype(np.int32)
     lens = plen + suffix + 1  # keys after this step's append
     nb = (plen + 15) // 16 + int(sum((int(n) + 15) // 16 - plen // 16 for n in lens)) + 64
@@ -335,7 +332,7 @@ def fork_bench(args):
     bm.allocate("prefix", plen)
     ptable = torch.tensor(bm.block_table("prefix"), dtype=torch.int32, device=dev)
     g = torch.Generator(device=dev)
-    g.manual_seed(args.seed)
+    g.manual_seed(seed)
     pk = torch.randn((layers, hkv, plen, d), generator=g, device=dev, dtype=bf)
     pv = torch.randn((layers, hkv, plen, d), generator=g, device=dev, dtype=bf)
     kv.kv_scatter(pk, pv, k0, v0, stride, layers, ptable, 0, plen, hkv, d, nb, "bf16")
@@ -379,6 +376,39 @@ def fork_bench(args):
     cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, "bf16")
     cos_t = torch.frombuffer(bytearray(cos_b), dtype=torch.int16).to(dev).view(bf)
     sin_t = torch.frombuffer(bytearray(sin_b), dtype=torch.int16).to(dev).view(bf)
+    return {"pool": pool, "block_manager": bm, "lens": lens, "suffix": suffix, "tables": tables,
+            "tables_dev": t_dev, "prefix_table": ptable, "mbps": mbps, "num_blocks": nb,
+            "cow_pairs": src, "fork_ms": fork_ms, "q": q_in, "k_new": k_in, "v_new": v_in,
+            "q_norm": qw, "k_norm": kw, "cos": cos_t, "sin": sin_t, "cos_bytes": cos_b,
+            "sin_bytes": sin_b, "max_pos": max_pos}
+
+
+def fork_bench(args):
+    """Prefix fork: one prefix held in refcounted pages of a pool handle (all
+    layers in one allocation, one block id spanning the layers), 64 requests
+    forked from it by the block manager (full pages shared, the trailing
+    partial page copied on write), each with a private suffix. The fork runs
+    once per request and is timed on its own; one step = one fused decode step
+    per layer for the 64 forked sequences (append of the new token + decode
+    over shared prefix pages and private suffix pages): by default the
+    cascade step (rlse_decode_step_cascade: the shared full pages attended once
+    for the batch, then each sequence's own pages, streamed), with
+    --no-cascade the planned step over every sequence's whole table (prefix
+    pages cacheable, re-read by every row)."""
+    import numpy as np
+    import torch
+
+    import rlse_kv as kv
+
+    hq, hkv, d, layers, b, plen, lo, hi, desc = FORK[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    f = fork_inputs(args.workload, args.seed, dev)
+    pool, lens, tables, mbps, nb = f["pool"], f["lens"], f["tables"], f["mbps"], f["num_blocks"]
+    src, fork_ms, t_dev = f["cow_pairs"], f["fork_ms"], f["tables_dev"]
+    q_in, k_in, v_in, qw, kw = f["q"], f["k_new"], f["v_new"], f["q_norm"], f["k_norm"]
+    cos_t, sin_t, max_pos = f["cos"], f["sin"], f["max_pos"]
+    bf = torch.bfloat16
     lens_dev = torch.from_numpy(lens.astype(np.int32)).to(dev)
     out = torch.empty((b, hq, d), device=dev, dtype=bf)
     ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
@@ -650,6 +680,71 @@ def e2e_cpu_baseline(args, cfg, cached):
                       f"{sub}), f32, in {el:.2f} s"}
 
 
+# Whether the model of each attention workload has per-head q_norm / k_norm
+# (Qwen3 does; Qwen2.5 does not: Config.q_norm is absent for it,
+# src/backends/qwen2.rs:251-260). RoPE applies to every workload.
+WORKLOAD_QK_NORM = {"qwen3": True, "qwen25": False, "qwen3_8b": True}
+
+
+def decode_layout(workload, seed):
+    """Host side of an attention workload: cached lengths U[lo, hi], keys
+    attended = cached + 1 (the token appended this step), and block tables
+    drawing each sequence's pages from one seeded random permutation."""
+    import numpy as np
+    hq, hkv, d, layers, b, lo, hi, _ = WORKLOADS[workload]
+    rng = np.random.default_rng(seed)
+    cached = rng.integers(lo, hi + 1, b).astype(np.int32)
+    lens = cached + 1  # keys attended: cached + the appended token
+    mbps = int(max((int(n) + 15) // 16 for n in lens))
+    need = int(sum((int(n) + 15) // 16 for n in lens))
+    nb = need + 64
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.zeros((b, mbps), np.int32)
+    used = 0
+    for i, n in enumerate(lens):
+        k = (int(n) + 15) // 16
+        tables[i, :k] = perm[used:used + k]
+        used += k
+    return cached, lens, tables, mbps, need, nb
+
+
+def decode_inputs(workload, seed, dev, layers=None):
+    """Every buffer of an attention workload, resident on dev: the layout of
+    decode_layout, a distinct N(0,1) K/V pool per layer, each layer's q and
+    new-token k/v, q/k RMSNorm weights 1 + 0.1 N(0,1) where the model has
+    them (None otherwise) and the bf16 RoPE tables (theta 1e6) for every
+    position a table can hold. layers: how many layers to build (default:
+    all of the workload's; a layer's buffers are drawn together, layer by
+    layer, so the first layers do not depend on it)."""
+    import torch
+    import rlse_kv as kv
+    hq, hkv, d, n_layers, b, _, _, _ = WORKLOADS[workload]
+    n_layers = n_layers if layers is None else layers
+    cached, lens, tables, mbps, need, nb = decode_layout(workload, seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    bf = torch.bfloat16
+    k_pools, v_pools, q_in, k_in, v_in, qw, kw = [], [], [], [], [], [], []
+    for _ in range(n_layers):   # layer by layer: a layer's draws do not depend on n_layers
+        k_pools.append(torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf))
+        v_pools.append(torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf))
+        q_in.append(torch.randn((b, hq, d), generator=g, device=dev, dtype=bf))
+        k_in.append(torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf))
+        v_in.append(torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf))
+        qw.append((1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf))
+        kw.append((1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf))
+    if not WORKLOAD_QK_NORM[workload]:
+        qw = kw = [None] * n_layers
+    max_pos = mbps * 16  # every position the block tables can hold
+    cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, "bf16")
+    cos_t = torch.frombuffer(bytearray(cos_b), dtype=torch.int16).to(dev).view(bf)
+    sin_t = torch.frombuffer(bytearray(sin_b), dtype=torch.int16).to(dev).view(bf)
+    return {"cached": cached, "lens": lens, "tables": tables, "mbps": mbps, "pages": need,
+            "num_blocks": nb, "k_pools": k_pools, "v_pools": v_pools, "q": q_in, "k_new": k_in,
+            "v_new": v_in, "q_norm": qw, "k_norm": kw, "cos": cos_t, "sin": sin_t,
+            "cos_bytes": cos_b, "sin_bytes": sin_b, "max_pos": max_pos}
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -676,36 +771,12 @@ def main():
     hq, hkv, d, layers, b, lo, hi, desc = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    rng = np.random.default_rng(args.seed)
-    cached = rng.integers(lo, hi + 1, b).astype(np.int32)
-    lens = cached + 1  # keys attended: cached + the appended token
-    mbps = int(max((int(n) + 15) // 16 for n in lens))
-    need = int(sum((int(n) + 15) // 16 for n in lens))
-    nb = need + 64
-    perm = rng.permutation(nb).astype(np.int32)
-    tables = np.zeros((b, mbps), np.int32)
-    used = 0
-    for i, n in enumerate(lens):
-        k = (int(n) + 15) // 16
-        tables[i, :k] = perm[used:used + k]
-        used += k
-
-    g = torch.Generator(device=dev)
-    g.manual_seed(args.seed)
+    w = decode_inputs(args.workload, args.seed, dev)
+    lens, cached, tables, mbps, need, nb = (w["lens"], w["cached"], w["tables"], w["mbps"],
+                                            w["pages"], w["num_blocks"])
+    k_pools, v_pools, q_in, k_in, v_in = w["k_pools"], w["v_pools"], w["q"], w["k_new"], w["v_new"]
+    qw, kw, cos_t, sin_t, max_pos = w["q_norm"], w["k_norm"], w["cos"], w["sin"], w["max_pos"]
     bf = torch.bfloat16
-    k_pools = [torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf)
-               for _ in range(layers)]
-    v_pools = [torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf)
-               for _ in range(layers)]
-    q_in = [torch.randn((b, hq, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
-    k_in = [torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
-    v_in = [torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
-    qw = [(1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf) for _ in range(layers)]
-    kw = [(1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf) for _ in range(layers)]
-    max_pos = mbps * 16  # every position the block tables can hold
-    cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, "bf16")
-    cos_t = torch.frombuffer(bytearray(cos_b), dtype=torch.int16).to(dev).view(bf)
-    sin_t = torch.frombuffer(bytearray(sin_b), dtype=torch.int16).to(dev).view(bf)
     t_dev = torch.from_numpy(tables).to(dev)
     pos_dev = torch.from_numpy(cached).to(dev)
     lens_dev = torch.from_numpy(lens).to(dev)
@@ -773,7 +844,8 @@ def main():
         torch.cuda.synchronize()
     spans = [a.elapsed_time(e) for a, e in zip(ev_a, ev_b)]
     avg_ms = float(np.mean(spans)) / (layers if not args.unfused else 1)
-    per_launch = algorithmic_decode_bytes(lens, hq, hkv, d, 2, not args.unfused)
+    per_launch = algorithmic_decode_bytes(lens, hq, hkv, d, 2, not args.unfused,
+                                          WORKLOAD_QK_NORM[args.workload])
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
     ms_per_step = elapsed * 1e3 / args.steps
     traffic, traffic_src = measured_traffic(args.workload, not args.unfused)

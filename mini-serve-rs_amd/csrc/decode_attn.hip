@@ -565,26 +565,23 @@ extern "C" int rlse_workspace_check(void* workspace, rlse_stream_t stream, unsig
   hipStream_t s = as_stream(stream);
   if (workspace) return read_and_clear_ws_flags(workspace, s, flags);
   // The library's own decode workspaces of the current device: the
-  // allocated one and the static scratch, each if a call has used it.
+  // allocated one and the static scratch, each if a call has used it. Each
+  // one's mutex is held until its flags are read and cleared, so a call
+  // that grows the allocated workspace (hipFree, then hipMalloc) cannot free
+  // it between the lookup and the clear.
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
     return fail(RLSE_ERR_INVALID_VALUE, "workspace_check: no current device");
-  void* own[2] = {nullptr, nullptr};
-  {
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    own[0] = g_ws_ptr[dev];
-  }
-  {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    own[1] = g_scratch_ptr[dev];
-  }
   int rc = RLSE_OK;
-  for (void* w : own) {
-    if (!w) continue;
+  auto check_one = [&](std::mutex& mu, void* const* slot) {
+    std::lock_guard<std::mutex> lock(mu);
+    if (!*slot) return;
     unsigned f = 0;
-    const int r = read_and_clear_ws_flags(w, s, &f);
+    const int r = read_and_clear_ws_flags(*slot, s, &f);
     if (flags) *flags |= f;
     if (rc == RLSE_OK || r == RLSE_ERR_DEVICE_TIMEOUT) rc = r ? r : rc;
-  }
+  };
+  check_one(g_ws_mu, &g_ws_ptr[dev]);
+  check_one(g_scratch_mu, &g_scratch_ptr[dev]);
   return rc;
 }

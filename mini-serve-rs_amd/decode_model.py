@@ -208,6 +208,29 @@ class DecodeModel:
         self.lens_in = torch.zeros(B, dtype=torch.int32, device=dev)
         self.graphs = {}
 
+    def check(self, stream=None) -> None:
+        """Synchronises the stream, then reads and clears the sticky device
+        error flags the step's kernels raise: a sequence longer than its
+        block table (its rows come out as zeros) raises TokenLimitExceeded,
+        a split-K merge that gave up waiting (its rows come out as NaN)
+        raises DeviceTimeout -- the device-side failures a step can have,
+        surfaced where the reference returns BackendError for a failed step
+        (src/backends/candle.rs:689-696). step() and replay() do not check
+        on their own (a check synchronises the host with the device): call
+        this after the steps whose results are used -- after each eager
+        step, or after a run of graph replays."""
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        # both workspaces are read and cleared, whichever of them raises
+        errs = []
+        for ws in (self.workspace, self.dense_ws):
+            try:
+                kv.workspace_check(ws, stream)
+            except kv.RlseError as e:
+                errs.append(e)
+        if errs:
+            raise errs[0]
+
     def close(self) -> None:
         if getattr(self, "pool", None) is not None:
             torch.cuda.synchronize(self.device)

@@ -536,3 +536,40 @@ def test_planned_step_equals_unplanned(kv, hq, hkv, d, lens):
         assert torch.equal(pools[0][0].view(torch.int16), pools[i][0].view(torch.int16)), i
         assert torch.equal(pools[0][1].view(torch.int16), pools[i][1].view(torch.int16)), i
     print(f"[planned] hq={hq} hkv={hkv} d={d} B={b}: outputs and pools identical")
+
+
+def test_workspace_check_races_library_workspace_growth(kv):
+    """rlse_workspace_check on the library-owned workspace while another
+    host thread grows it (decode calls with no workspace at growing group
+    sizes: each growth frees and reallocates the buffer). The check holds the
+    workspace's mutex until its read and clear are queued, so it never
+    touches a freed buffer; every call returns OK and no flag is raised."""
+    import threading
+    rng = np.random.default_rng(29)
+    hkv, d, lens = 2, 128, np.array([40, 200, 17], np.int32)
+    cases = []
+    for g in range(1, 9):          # the workspace's records grow with the group size
+        q, kp, vp, tables, _ = make_case(rng, lens, g * hkv, hkv, d, "bf16")
+        cases.append((g, to_dev(q, "bf16"), to_dev(kp, "bf16"), to_dev(vp, "bf16"), tables))
+    errors = []
+
+    def grow():
+        try:
+            for g, q, kp, vp, tables in cases:
+                out = torch.empty_like(q)
+                kv.paged_gqa_decode(q, kp, vp, to_dev(tables), to_dev(lens), out, len(lens),
+                                    g * hkv, hkv, d, tables.shape[1], kp.shape[0],
+                                    1.0 / math.sqrt(d), "bf16")
+                torch.cuda.synchronize()
+        except Exception as e:  # noqa: BLE001 -- reported below
+            errors.append(e)
+
+    t = threading.Thread(target=grow)
+    t.start()
+    checks = 0
+    while t.is_alive() or checks < 20:
+        assert kv.workspace_flags() == 0
+        checks += 1
+    t.join()
+    assert not errors, errors
+    print(f"workspace growth x {len(cases)} with {checks} concurrent checks: clean")

@@ -745,3 +745,31 @@ def test_captured_step_replays_equal_eager_steps(kv):
         assert torch.equal(ke, kg) and torch.equal(ve, vg)
     eager.close()
     graph.close()
+
+
+def test_decode_model_check_raises_token_limit(kv):
+    """DecodeModel.check reads and clears the step's device error flags. A
+    step with a sequence longer than its block table (mbps * 16 tokens)
+    writes zeros for that row and raises RLSE_WS_ERR_LENGTH on the device;
+    check() turns it into TokenLimitExceeded (the reference's
+    EngineError::TokenLimitExceeded), after which the next step is clean."""
+    from decode_model import DecodeModel, ModelConfig
+    dt, arch = "bf16", "qwen3"
+    spec = O.ModelSpec(**SPECS[arch])
+    rng = np.random.default_rng(23)
+    w = O.random_weights(spec, rng, dt)
+    b, mbps, nb = 2, 3, 8
+    tables = build_tables(rng, [mbps * 16] * b, nb, mbps)
+    model = DecodeModel(ModelConfig(**SPECS[arch]), w, dt, nb, b, mbps)
+    t_dev = torch.from_numpy(tables).to(DEV)
+    ids = torch.from_numpy(np.array([3, 4], np.int32)).to(DEV)
+    model.step(ids, t_dev, torch.from_numpy(np.array([5, 9], np.int32)).to(DEV), b)
+    model.check()                                    # a clean step
+    model.step(ids, t_dev, torch.from_numpy(np.array([5, mbps * 16 + 1], np.int32)).to(DEV), b)
+    with pytest.raises(kv.TokenLimitExceeded):
+        model.check()
+    model.check()                                    # the flag was cleared
+    model.step(ids, t_dev, torch.from_numpy(np.array([6, 10], np.int32)).to(DEV), b)
+    model.check()
+    model.close()
+
