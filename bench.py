@@ -50,11 +50,16 @@ METRIC_NAME = {
 }
 # Chunked prefill: (Hq, Hkv, d, chunk tokens, cached tokens before the chunk, description)
 PREFILL = {
-    "qwen3_8b_prefill": (32, 8, 128, 512, 8192,
+    "qwen3_8b_prefill": (32, 8, 128, 512, 8192, "bf16",
                          "Qwen3-8B chunked prefill: 512-token chunk after 8192 cached tokens, "
                          "32q/8kv heads, d=128, causal, bf16, one layer"),
+    "qwen3_8b_prefill_f32": (32, 8, 128, 512, 8192, "f32",
+                             "Qwen3-8B chunked prefill in f32 (the reference CPU path's dtype): "
+                             "512-token chunk after 8192 cached tokens, 32q/8kv heads, d=128, "
+                             "causal, one layer"),
 }
 PEAK_BF16_TFLOPS = 2500.0  # dense MFMA
+PEAK_F32_TFLOPS = 157.3    # dense MFMA, f32 operands
 # Prefix fork: (Hq, Hkv, d, layers, batch, prefix tokens, suffix lo, suffix hi, description)
 FORK = {
     "qwen3_fork": (16, 8, 128, 28, 64, 1024, 64, 512,
@@ -213,7 +218,8 @@ def prefill_bench(args):
 
     import rlse_kv as kv
 
-    hq, hkv, d, tq, offset, desc = PREFILL[args.workload]
+    hq, hkv, d, tq, offset, dt, desc = PREFILL[args.workload]
+    peak = PEAK_F32_TFLOPS if dt == "f32" else PEAK_BF16_TFLOPS
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     L = offset + tq
@@ -223,10 +229,10 @@ def prefill_bench(args):
     table = torch.from_numpy(rng.permutation(nb)[:npages].astype(np.int32)).to(dev)
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed)
-    bf = torch.bfloat16
-    kp = torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf)
-    vp = torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=bf)
-    q = torch.randn((tq, hq, d), generator=g, device=dev, dtype=bf)
+    tdt = torch.float32 if dt == "f32" else torch.bfloat16
+    kp = torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=tdt)
+    vp = torch.randn((nb, hkv, 16, d), generator=g, device=dev, dtype=tdt)
+    q = torch.randn((tq, hq, d), generator=g, device=dev, dtype=tdt)
     out = torch.empty_like(q)
     ws_bytes = kv.prefill_workspace_size(tq, L, hq, hkv, d)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
@@ -234,7 +240,7 @@ def prefill_bench(args):
     scale = 1.0 / math.sqrt(d)
 
     def step():
-        kv.prefill_attn(q, kp, vp, table, L, tq, out, hq, hkv, d, npages, nb, scale, "bf16", ws,
+        kv.prefill_attn(q, kp, vp, table, L, tq, out, hq, hkv, d, npages, nb, scale, dt, ws,
                         ws_bytes, stream)
 
     for _ in range(args.warmup):
@@ -255,17 +261,17 @@ def prefill_bench(args):
     flops = prefill_flops(hq, d, tq, offset)
     achieved = flops / (avg_ms * 1e-3) / 1e12
     result = {
-        "metric": "prefill-attn TFLOP/s (% of dense bf16 MFMA peak) at Qwen3-8B chunk, 1 GPU",
+        "metric": f"prefill-attn TFLOP/s (% of dense {dt} MFMA peak) at Qwen3-8B chunk, 1 GPU",
         "value": flops * args.steps / elapsed / 1e12, "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": elapsed * 1e3 / args.steps, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16",
+        "vs_baseline": None, "dtype": dt,
         "data": "synthetic N(0,1) q/K/V, seeded random page permutation",
         "config": {"workload": desc, "chunk": tq, "cached": offset, "q_heads": hq,
                    "kv_heads": hkv, "head_dim": d, "splits_workspace_bytes": ws_bytes,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": peak,
+                     "unit": "TFLOP/s", "frac": achieved / peak, "traffic": None,
                      "kernel": "prefill_kernel + prefill_merge_kernel (rlse_prefill_attn)",
                      "flops_per_launch": flops, "avg_launch_ms": avg_ms,
                      "timed_launches": n_ev},

@@ -304,8 +304,9 @@ int rlse_decode_step_noalloc(const void* q, const void* k_new, const void* v_new
  * before attending). Query t sees keys 0 .. ctx_len-num_tokens+t of the
  * page list block_table[max_blocks] (ctx_len <= max_blocks*16); keys in
  * pages with ids outside [0, num_blocks) are skipped. out [num_tokens]
- * [num_heads][head_dim]. bf16 and f16 only (MFMA tiles), head_dim 64 or
- * 128. workspace: rlse_prefill_workspace_size bytes (may be 0), or NULL
+ * [num_heads][head_dim]. f32, bf16 or f16 (MFMA tiles: f32 products for
+ * f32, the reference CPU path's dtype), head_dim 64 or 128. workspace:
+ * rlse_prefill_workspace_size bytes (may be 0), or NULL
  * for a library-owned one per device. Calls that share a workspace, the
  * library-owned one included, must be ordered (same stream). */
 int rlse_prefill_workspace_size(int num_tokens, int ctx_len, int num_heads, int num_kv_heads,

@@ -365,6 +365,242 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(PrefillParams p) 
   blk[4 * DB * kPThreads] = make_float4(m, lsum, 0.f, 0.f);
 }
 
+// The same chunked prefill with f32 K/V and queries (the dtype of the
+// reference's CPU path), on v_mfma_f32_32x32x2_f32: lane l holds
+// A[l%32][l/32], B[l/32][l%32] and accumulator element i at
+// [8*(i/4) + 4*(l/32) + i%4][l%32], the layout of the 16-bit kernel's 32x32
+// tiles, so the softmax, the masks, the partial records and the merge are
+// the same. Per 2-wide k step:
+//   S^T += K . Q^T: lane half h contracts dimension h*D/2 + j at step j, so
+//   a lane's query operand is D/2 consecutive elements of its query (held in
+//   registers) and its K operand comes from LDS four steps at a time;
+//   O^T += V^T . P^T: step j pairs the keys the two lane halves hold in
+//   accumulator element j (8*(j/4) + 4h + j%4), so the B operand is the
+//   lane's own probability and the A operand one float of V's key row.
+// K and V rows are staged in LDS as they are (f32), padded by 4 floats so the
+// 16-byte K reads and the V reads of 32 consecutive columns are free of bank
+// conflicts.
+constexpr int kPadF = 4;
+template <int D>
+__global__ __launch_bounds__(kPThreads, 1) void prefill_kernel_f32(PrefillParams p) {
+  constexpr int DB = D / 32;                  // 32-row blocks of O^T
+  constexpr int KH = D / 2;                   // k steps of q.k
+  constexpr int CPR = D / 4;                  // 16-byte chunks per key row
+  constexpr int KPK = kBN * CPR;              // K packets per tile
+  constexpr int KPT = KPK / kPThreads;        // per thread
+  static_assert(KPK % kPThreads == 0, "K tile must split evenly");
+  __shared__ __align__(16) float s_k[2][kBN][D + kPadF];  // K rows
+  __shared__ __align__(16) float s_v[2][kBN][D + kPadF];  // V rows
+  __shared__ int s_valid[2];                               // page-valid bits of the tile
+  __shared__ __align__(16) int s_pages[kMaxSplitPages];    // the split's page ids (-1: invalid)
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int half = lane >> 5, col = lane & 31;
+
+  // XCD-aware work index, as in the 16-bit kernel.
+  const int nwg = gridDim.x;
+  const int b = blockIdx.x;
+  const int wid = (nwg % 8 == 0) ? (b % 8) * (nwg / 8) + b / 8 : b;
+  const int rt = wid % p.row_tiles;
+  const int h = (wid / p.row_tiles) % p.Hkv;
+  const int split = wid / (p.row_tiles * p.Hkv);
+
+  const int G = p.G, Hq = p.Hq, Hkv = p.Hkv;
+  const int rows = p.Tq * G;
+  const int myrow = rt * kBM + wave * 32 + col;
+  const int row_c = myrow < rows ? myrow : rows - 1;
+  const int t = row_c / G, g = row_c - t * G, qh = h * G + g;
+  const int kmax = p.offset + t;
+  const int kmin_wave = p.offset + min(rt * kBM + wave * 32, rows - 1) / G;
+  const int last_row = min(rows - 1, rt * kBM + kBM - 1);
+  const int wg_keys = min(p.L, p.offset + last_row / G + 1);
+  const int k_begin = split * p.split_keys;
+  const int k_end = min(wg_keys, k_begin + p.split_keys);
+
+  const float* __restrict__ qb = reinterpret_cast<const float*>(p.q);
+  const float* __restrict__ kp = reinterpret_cast<const float*>(p.k_pool);
+  const float* __restrict__ vp = reinterpret_cast<const float*>(p.v_pool);
+
+  {
+    const int npg = k_begin < k_end ? (((k_end - k_begin + 15) >> 4) + 3) & ~3 : 0;
+    const int plast = (p.L - 1) >> 4;
+    for (int i = tid; i < npg; i += kPThreads) {
+      const int pi = min((k_begin >> 4) + i, plast);
+      const int id = p.table[pi];
+      s_pages[i] = ((unsigned)id < (unsigned)p.num_blocks) ? id : -1;
+    }
+    __syncthreads();
+  }
+
+  f32x16_t o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+  float m = -INFINITY, lsum = 0.f;
+
+  if (k_begin < k_end) {
+    // Dimensions half*D/2 .. +D/2 of the lane's query.
+    float qreg[KH];
+#pragma unroll
+    for (int j = 0; j < KH; j += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(qb + ((size_t)t * Hq + qh) * D +
+                                                        half * KH + j);
+      qreg[j] = x.x;
+      qreg[j + 1] = x.y;
+      qreg[j + 2] = x.z;
+      qreg[j + 3] = x.w;
+    }
+    const int last_tile = k_begin + ((k_end - 1 - k_begin) / kBN) * kBN;
+    static_assert(kBN == 64, "a tile spans 4 pages");
+    int voff[KPT], pg_of[KPT];
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int pk = tid + u * kPThreads;
+      const int kk = pk / CPR, dc = pk - kk * CPR;
+      voff[u] = (((kk & 15) * D) + dc * 4) * (int)sizeof(float);
+      pg_of[u] = __builtin_amdgcn_readfirstlane(kk >> 4);
+    }
+    u32x4_t kst[KPT], vst[KPT];
+    int4 pid;
+    const size_t tile_elems = (size_t)16 * D;
+    auto load_tile = [&](int kt) __attribute__((always_inline)) {
+      pid = *reinterpret_cast<const int4*>(&s_pages[(kt - k_begin) >> 4]);
+#pragma unroll
+      for (int u = 0; u < KPT; ++u) {
+        const int r = __builtin_amdgcn_readfirstlane(s_pages[((kt - k_begin) >> 4) + pg_of[u]]);
+        const size_t tb = ((size_t)(r < 0 ? 0 : r) * Hkv + h) * tile_elems;
+        const int nrec = r < 0 ? 0 : (int)(tile_elems * sizeof(float));
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kp + tb), 0, nrec,
+                                                          kBufferWord3);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vp + tb), 0, nrec,
+                                                          kBufferWord3);
+        kst[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, voff[u], 0, 0);
+        vst[u] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff[u], 0, 0);
+      }
+    };
+    auto store_tile = [&](int bf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < KPT; ++u) {
+        const int pk = tid + u * kPThreads;
+        const int kk = pk / CPR, dc = pk - kk * CPR;
+        *reinterpret_cast<u32x4_t*>(&s_k[bf][kk][dc * 4]) = kst[u];
+        *reinterpret_cast<u32x4_t*>(&s_v[bf][kk][dc * 4]) = vst[u];
+      }
+      if (tid == 0) {
+        s_valid[bf] = (pid.x >= 0 ? 1 : 0) | (pid.y >= 0 ? 2 : 0) | (pid.z >= 0 ? 4 : 0) |
+                      (pid.w >= 0 ? 8 : 0);
+      }
+    };
+
+    load_tile(k_begin);
+    store_tile(0);
+    __syncthreads();
+    int bf = 0;
+    for (int kt = k_begin;; kt += kBN) {
+      const bool more = kt < last_tile;
+      load_tile(more ? kt + kBN : kt);  // in flight during this tile's math
+      const int vbits = s_valid[bf];
+
+      f32x16_t s[2];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
+#pragma unroll
+      for (int j = 0; j < KH; j += 4)
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+          const float4 a = *reinterpret_cast<const float4*>(&s_k[bf][sb * 32 + col][half * KH + j]);
+          s[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qreg[j], s[sb], 0, 0, 0);
+          s[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, qreg[j + 1], s[sb], 0, 0, 0);
+          s[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qreg[j + 2], s[sb], 0, 0, 0);
+          s[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qreg[j + 3], s[sb], 0, 0, 0);
+        }
+      if (!(kt + kBN - 1 <= kmin_wave && kt + kBN <= k_end && vbits == 15)) {
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kk = sb * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
+            const int ka = kt + kk;
+            if (!(ka <= kmax && ka < k_end && ((vbits >> (kk >> 4)) & 1))) s[sb][i] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sb][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float cand = mx * p.c;
+      if (__any(cand > m + kLazyLog2)) {
+        const float mn = fmaxf(m, cand);
+        const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+        lsum *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        m = mn;
+      }
+      const float nms = m == -INFINITY ? 0.f : -m;
+      float rs = 0.f;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          s[sb][i] = __builtin_amdgcn_exp2f(fmaf(s[sb][i], p.c, nms));
+          rs += s[sb][i];
+        }
+      rs += __shfl_xor(rs, 32, 64);
+      lsum += rs;
+      // O^T += V^T . P^T, step j of key half sb: the lane's half takes key
+      // sb*32 + 8*(j/4) + 4*half + j%4 (its accumulator element j).
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float* vrow = &s_v[bf][sb * 32 + (j >> 2) * 8 + half * 4 + (j & 3)][col];
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[db * 32], s[sb][j], o[db], 0, 0, 0);
+        }
+
+      if (!more) break;
+      store_tile(bf ^ 1);
+      __syncthreads();
+      bf ^= 1;
+    }
+  }
+
+  // Lane holds O^T rows d = 32*db + 8*(i/4) + 4*half + i%4 of its query.
+  if (p.splits == 1) {
+    if (myrow < rows) {
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      float* dst = reinterpret_cast<float*>(p.out) + ((size_t)t * Hq + qh) * D;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4)
+          *reinterpret_cast<float4*>(dst + db * 32 + i4 * 8 + half * 4) =
+              make_float4(o[db][i4 * 4] * inv, o[db][i4 * 4 + 1] * inv, o[db][i4 * 4 + 2] * inv,
+                          o[db][i4 * 4 + 3] * inv);
+    }
+    return;
+  }
+  // Key splits: the partial block in the 16-bit kernel's layout.
+  float4* blk = part_block<D>(p, split, h, rt) + tid;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4)
+      blk[(db * 4 + i4) * kPThreads] =
+          make_float4(o[db][i4 * 4], o[db][i4 * 4 + 1], o[db][i4 * 4 + 2], o[db][i4 * 4 + 3]);
+  blk[4 * DB * kPThreads] = make_float4(m, lsum, 0.f, 0.f);
+}
+
 // Log-sum-exp merge of the key splits. Workgroup (row tile, KV head, q)
 // combines slots 4q..4q+3 of every row: thread tid reads what thread tid of
 // each split stored, so all the loads of kMergeBatch splits are in flight
@@ -427,9 +663,16 @@ __global__ __launch_bounds__(kPThreads) void prefill_merge_kernel(PrefillParams 
     // slot k = (db, i4): dims 32*db + 8*i4 + 4*half .. +3
     const int k = q * KQ + kk;
     const int d0 = (k >> 2) * 32 + (k & 3) * 8 + half * 4;
-    *reinterpret_cast<uint2*>(dst + d0) =
-        make_uint2(Packet<T>::pack2(acc[kk * 4] * inv, acc[kk * 4 + 1] * inv),
-                   Packet<T>::pack2(acc[kk * 4 + 2] * inv, acc[kk * 4 + 3] * inv));
+    if constexpr (sizeof(T) == 4) {
+      *reinterpret_cast<float4*>(dst + d0) = make_float4(acc[kk * 4] * inv,
+                                                         acc[kk * 4 + 1] * inv,
+                                                         acc[kk * 4 + 2] * inv,
+                                                         acc[kk * 4 + 3] * inv);
+    } else {
+      *reinterpret_cast<uint2*>(dst + d0) =
+          make_uint2(Packet<T>::pack2(acc[kk * 4] * inv, acc[kk * 4 + 1] * inv),
+                     Packet<T>::pack2(acc[kk * 4 + 2] * inv, acc[kk * 4 + 3] * inv));
+    }
   }
 }
 
@@ -467,7 +710,10 @@ int plan_prefill(int Tq, int ctx_len, int Hq, int Hkv, int D, PrefillPlan* plan)
 template <typename T, int D>
 int launch_prefill(PrefillParams& pp, hipStream_t stream) {
   const int nwg = pp.row_tiles * pp.Hkv * pp.splits;
-  hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(nwg), dim3(kPThreads), 0, stream, pp);
+  if constexpr (sizeof(T) == 4)
+    hipLaunchKernelGGL((prefill_kernel_f32<D>), dim3(nwg), dim3(kPThreads), 0, stream, pp);
+  else
+    hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(nwg), dim3(kPThreads), 0, stream, pp);
   const int st = launch_status("prefill_kernel");
   if (st || pp.splits == 1) return st;
   hipLaunchKernelGGL((prefill_merge_kernel<T, D>), dim3(pp.row_tiles * pp.Hkv * (D / 32)),
@@ -493,9 +739,8 @@ int validate_prefill(int num_tokens, int ctx_len, int Hq, int Hkv, int D, int mb
                 Hq, Hkv);
   if (D != 64 && D != 128)
     return fail(RLSE_ERR_INVALID_VALUE, "prefill: head_dim %d not in {64, 128}", D);
-  if (dtype != RLSE_DTYPE_BF16 && dtype != RLSE_DTYPE_F16)
-    return fail(RLSE_ERR_INVALID_VALUE, "prefill: dtype %d unsupported (bf16 and f16 only)",
-                dtype);
+  if (dtype != RLSE_DTYPE_BF16 && dtype != RLSE_DTYPE_F16 && dtype != RLSE_DTYPE_F32)
+    return fail(RLSE_ERR_INVALID_VALUE, "prefill: bad dtype %d", dtype);
   if (mbps <= 0 || num_blocks <= 0 || (long long)mbps * 16 < ctx_len)
     return fail(RLSE_ERR_INVALID_VALUE,
                 "prefill: ctx_len %d exceeds the table's %d blocks of 16 (num_blocks %d)",
@@ -582,5 +827,8 @@ extern "C" int rlse_prefill_attn(const void* q, const void* k_pool, const void* 
   const hipStream_t s = as_stream(stream);
   if (dtype == RLSE_DTYPE_BF16)
     return head_dim == 128 ? launch_prefill<bf16, 128>(pp, s) : launch_prefill<bf16, 64>(pp, s);
+  if (dtype == RLSE_DTYPE_F32)
+    return head_dim == 128 ? launch_prefill<float, 128>(pp, s)
+                           : launch_prefill<float, 64>(pp, s);
   return head_dim == 128 ? launch_prefill<f16, 128>(pp, s) : launch_prefill<f16, 64>(pp, s);
 }

@@ -57,13 +57,13 @@ def test_decode_rejects_bad_shapes(kv, args):
     dict(tq=4, L=40, hq=8, hkv=8, d=128, mb=2, dt="bf16"),     # table too short for ctx_len
     dict(tq=4, L=10, hq=12, hkv=8, d=128, mb=1, dt="bf16"),    # Hq not a multiple of Hkv
     dict(tq=4, L=10, hq=8, hkv=8, d=96, mb=1, dt="bf16"),      # unsupported head_dim
-    dict(tq=4, L=10, hq=8, hkv=8, d=128, mb=1, dt="f32"),      # MFMA path: bf16/f16 only
+    dict(tq=4, L=10, hq=8, hkv=8, d=128, mb=1, dt=9),          # no such dtype code
 ])
 def test_prefill_rejects_bad_arguments(kv, case):
     lib = kv.load()
+    dt = kv.DTYPE_NAMES[case["dt"]] if isinstance(case["dt"], str) else case["dt"]
     rc = lib.rlse_prefill_attn(1, 1, 1, 1, case["L"], case["tq"], 1, case["hq"], case["hkv"],
-                               case["d"], case["mb"], 64, 0.088, kv.DTYPE_NAMES[case["dt"]],
-                               None, 0, None)
+                               case["d"], case["mb"], 64, 0.088, dt, None, 0, None)
     assert rc == kv.ERR_INVALID_VALUE, kv.last_error()
 
 
