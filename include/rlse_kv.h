@@ -219,6 +219,9 @@ int rlse_decode_plan(const int32_t* block_tables, const int32_t* seq_lens, int b
  * num_blocks (every layer of a decode step shares them): each wave's page
  * ids then arrive with its first load, its query and append loads go out
  * next and its first pages right after. Results are identical to rlse_decode_step's.
+ * The plan carries a stamp of the step shape it was built for (plain, a
+ * cascade's prefix_pages, prefix groups); a planned launch given a plan of
+ * another shape raises RLSE_WS_ERR_PREFIX in the workspace.
  * flags: RLSE_DECODE_STREAM when no page of the batch is read by more than
  * one row (no sequence shares pages with another -- the caller's block
  * manager knows: no page with a refcount above 1): the pages are then read
@@ -275,6 +278,42 @@ int rlse_decode_step_cascade(const void* q, const void* k_new, const void* v_new
                              size_t workspace_bytes, const void* plan, int flags,
                              int prefix_pages, void* prefix_buf, size_t prefix_bytes,
                              rlse_stream_t stream);
+
+/* Cascade decode step of a mixed batch: several prefix groups and unforked
+ * sequences in one step. The batch the reference decodes in one
+ * step_decode_batch (src/backends/qwen2.rs:628-764) holds sequences restored
+ * from different cached prefixes and sequences with none
+ * (src/backends/candle.rs:437-478, 602-640); here each group's shared pages
+ * are attended once for its members and every other page once for its
+ * sequence. seq_group (device int32 [batch]): the group of each sequence, -1
+ * for none (its whole table is streamed). group_pages (device int32
+ * [num_groups]): the number of leading table entries every member of group
+ * g shares with the group's other members (the same pages, and each
+ * member's new token lies past them), 1 .. min(max_blocks_per_seq, 512).
+ * Members may sit anywhere in the batch. rlse_decode_plan_groups builds the
+ * step's plan (one per step, read by every layer; required), including the
+ * member lists the prefix launch reads; rlse_decode_step_groups then runs
+ * the prefix launch over every group's column tiles and the decode, with
+ * max_group_pages >= every group's pages sizing both and prefix_buf
+ * (rlse_decode_prefix_size with prefix_pages = max_group_pages). 1 <=
+ * num_groups <= 64; bf16/f16 only. Same results as rlse_decode_step_planned
+ * within rounding. A group id or page count out of range, a member whose
+ * leading entries differ from its group's, a new token inside its group's
+ * pages, or a plan built for another step raise RLSE_WS_ERR_PREFIX. */
+int rlse_decode_plan_groups(const int32_t* block_tables, const int32_t* seq_lens,
+                            const int32_t* seq_group, const int32_t* group_pages, int num_groups,
+                            int batch, int num_heads, int num_kv_heads, int max_blocks_per_seq,
+                            int num_blocks, void* plan, size_t plan_bytes, rlse_stream_t stream);
+int rlse_decode_step_groups(const void* q, const void* k_new, const void* v_new,
+                            const void* q_norm_weight, const void* k_norm_weight, float eps,
+                            const void* cos_table, const void* sin_table, int max_pos,
+                            void* k_pool, void* v_pool, const int32_t* block_tables,
+                            const int32_t* seq_lens, void* out, int batch, int num_heads,
+                            int num_kv_heads, int head_dim, int max_blocks_per_seq,
+                            int num_blocks, float scale, int dtype, void* workspace,
+                            size_t workspace_bytes, const void* plan, int flags, int num_groups,
+                            int max_group_pages, void* prefix_buf, size_t prefix_bytes,
+                            rlse_stream_t stream);
 
 /* rlse_decode_step for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -34,11 +34,16 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __rest
                                                                int B, int Hkv, int mbps,
                                                                int num_blocks, int W, int w1,
                                                                int prefix,
+                                                               const int* __restrict__ seq_pre,
+                                                               int stamp,
                                                                int4* __restrict__ plan) {
   extern __shared__ int s_pref[];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  if (wave == 0) block_prefix(seq_lens, B, mbps, s_pref, lane < B ? seq_lens[lane] : 0, prefix);
+  if (wave == 0)
+    block_prefix(seq_lens, B, mbps, s_pref, lane < B ? seq_lens[lane] : 0, prefix, seq_pre,
+                 lane < B ? stream_skip(seq_pre, prefix, lane) : 0);
+  if (blockIdx.x == 0 && tid == 0) const_cast<int*>(plan_tail(plan, W))[0] = stamp;
   __syncthreads();
   const long long w = blockIdx.x;
   const long long total = (long long)Hkv * s_pref[B];
@@ -50,7 +55,8 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __rest
       const long long ghi = range_lo(w + 1, total, we, W, w1);
       const long long wlo = glo + (ghi - glo) * wave / kWaves;
       const long long whi = glo + (ghi - glo) * (wave + 1) / kWaves;
-      d = block_desc(wlo + lane, whi, s_pref, tables, seq_lens, B, Hkv, mbps, num_blocks, prefix);
+      d = block_desc(wlo + lane, whi, s_pref, tables, seq_lens, B, Hkv, mbps, num_blocks, prefix,
+                     seq_pre);
     }
   }
   const size_t at = ((size_t)w * kWaves + wave) * 64 + lane;
@@ -62,6 +68,81 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __rest
     pos = L > 0 ? L - 1 : 0;
   }
   reinterpret_cast<int*>(plan + (size_t)gridDim.x * kWaves * 64)[at] = pos;
+}
+
+// Grouped plan of a cascade step with prefix groups (one workgroup): from
+// seq_group[b] (the prefix group of sequence b, -1 for none) and
+// group_pages[g] (the pages group g's members share), into the plan's tail:
+// each sequence's shared pages (0 for none), the grouped sequences group by
+// group (in batch order within a group), the groups' member and column-tile
+// offsets (G columns per member, 16 per tile) and pages. A group id outside
+// [-1, NG) or a page count outside [1, min(mbps, kMaxPrefixPages)] sets the
+// error word (the prefix launch raises RLSE_WS_ERR_PREFIX) and the sequence,
+// or the group's members, are left unforked.
+__global__ __launch_bounds__(1024) void group_plan_kernel(const int* __restrict__ seq_group,
+                                                          const int* __restrict__ group_pages,
+                                                          int B, int NG, int G, int mbps,
+                                                          int* __restrict__ tail) {
+  __shared__ int s_cnt[kMaxPrefixGroups], s_pages[kMaxPrefixGroups], s_next[kMaxPrefixGroups];
+  __shared__ int s_err;
+  int* seq_pre = tail + kPlanStampWords;
+  int* members = seq_pre + kMaxDecodeBatch;
+  int* grp = members + kMaxDecodeBatch;
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid == 0) s_err = 0;
+  if (tid < NG) {
+    const int pg = group_pages[tid];
+    const bool ok = pg >= 1 && pg <= mbps && pg <= kMaxPrefixPages;
+    s_pages[tid] = ok ? pg : 0;
+    s_cnt[tid] = 0;
+  }
+  __syncthreads();
+  if (tid < NG && s_pages[tid] == 0) atomicOr(&s_err, 1);
+  // A sequence's group, -1 when it has none or its group is invalid.
+  auto group_of_seq = [&](int b) __attribute__((always_inline)) {
+    const int g = seq_group[b];
+    return (g >= 0 && g < NG && s_pages[g] > 0) ? g : -1;
+  };
+  for (int b = tid; b < B; b += 1024) {
+    const int g = seq_group[b];
+    if (g < -1 || g >= NG) atomicOr(&s_err, 2);
+    const int gg = group_of_seq(b);
+    if (gg >= 0) atomicAdd(&s_cnt[gg], 1);
+    seq_pre[b] = gg >= 0 ? s_pages[gg] : 0;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int off = 0, tiles = 0;
+    for (int g = 0; g < NG; ++g) {
+      grp[kGrpOff + g] = off;
+      grp[kGrpTiles + g] = tiles;
+      grp[kGrpPages + g] = s_pages[g];
+      s_next[g] = off;
+      off += s_cnt[g];
+      tiles += (s_cnt[g] * G + 15) / 16;
+    }
+    grp[kGrpOff + NG] = off;
+    grp[kGrpTiles + NG] = tiles;
+    grp[kGrpErr] = s_err;
+  }
+  __syncthreads();
+  // Members in batch order within each group: wave 0 walks the batch 64
+  // sequences at a time; the lanes of one group take consecutive slots.
+  if (tid < 64) {
+    for (int base = 0; base < B; base += 64) {
+      const int b = base + lane;
+      const int g = b < B ? group_of_seq(b) : -1;
+      uint64_t pending = __ballot(g >= 0);
+      while (pending) {
+        const int g0 = __shfl(g, __builtin_ctzll(pending), 64);
+        const uint64_t m = __ballot(g == g0);
+        const int at = s_next[g0];
+        if (g == g0) members[at + __builtin_popcountll(m & ((1ull << lane) - 1))] = b;
+        if (lane == 0) s_next[g0] = at + __builtin_popcountll(m);
+        pending &= ~m;
+      }
+    }
+  }
 }
 
 static int decode_groups(int* W) {
@@ -254,13 +335,16 @@ extern "C" int rlse_decode_plan_size(size_t* bytes) {
   int W = 0;
   const int st = decode_groups(&W);
   if (st) return st;
-  *bytes = (size_t)W * kWaves * 64 * (sizeof(int4) + sizeof(int));
+  *bytes = plan_bytes(W);
   return RLSE_OK;
 }
 
 static int decode_plan_impl(const int32_t* block_tables, const int32_t* seq_lens, int batch,
                             int num_kv_heads, int max_blocks_per_seq, int num_blocks, int prefix,
-                            void* plan, size_t plan_bytes, rlse_stream_t stream) {
+                            void* plan, size_t plan_bytes, rlse_stream_t stream,
+                            const int32_t* seq_group = nullptr,
+                            const int32_t* group_pages = nullptr, int num_groups = 0,
+                            int group_size = 1) {
   if (prefix < 0 || prefix > max_blocks_per_seq || prefix > kMaxPrefixPages)
     return fail(RLSE_ERR_INVALID_VALUE, "decode_plan: prefix_pages %d outside [0, min(%d, %d)]",
                 prefix, max_blocks_per_seq, kMaxPrefixPages);
@@ -279,10 +363,22 @@ static int decode_plan_impl(const int32_t* block_tables, const int32_t* seq_lens
   int W = 0;
   st = decode_groups(&W);
   if (st) return st;
+  int4* pl = reinterpret_cast<int4*>(plan);
+  const int* seq_pre = nullptr;
+  int stamp = plan_stamp(1, prefix);
+  if (num_groups > 0) {
+    int* tail = const_cast<int*>(plan_tail(pl, W));
+    hipLaunchKernelGGL(group_plan_kernel, dim3(1), dim3(1024), 0, as_stream(stream), seq_group,
+                       group_pages, batch, num_groups, group_size, max_blocks_per_seq, tail);
+    st = launch_status("group_plan_kernel");
+    if (st) return st;
+    seq_pre = tail + kPlanStampWords;
+    stamp = plan_stamp(2, num_groups);
+  }
   const size_t lds = (size_t)(batch + 1) * sizeof(int);
   hipLaunchKernelGGL(decode_plan_kernel, dim3(W), dim3(kThreads), lds, as_stream(stream),
                      block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq, num_blocks,
-                     W, kSlot1Weight, prefix, reinterpret_cast<int4*>(plan));
+                     W, kSlot1Weight, prefix, seq_pre, stamp, pl);
   return launch_status("decode_plan_kernel");
 }
 
@@ -299,6 +395,23 @@ extern "C" int rlse_decode_plan_cascade(const int32_t* block_tables, const int32
                                         size_t plan_bytes, rlse_stream_t stream) {
   return decode_plan_impl(block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq,
                           num_blocks, prefix_pages, plan, plan_bytes, stream);
+}
+
+extern "C" int rlse_decode_plan_groups(const int32_t* block_tables, const int32_t* seq_lens,
+                                       const int32_t* seq_group, const int32_t* group_pages,
+                                       int num_groups, int batch, int num_heads,
+                                       int num_kv_heads, int max_blocks_per_seq, int num_blocks,
+                                       void* plan, size_t plan_bytes, rlse_stream_t stream) {
+  if (num_groups < 1 || num_groups > kMaxPrefixGroups)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_plan_groups: num_groups %d outside [1, %d]",
+                num_groups, kMaxPrefixGroups);
+  if (!seq_group || !group_pages)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_plan_groups: null pointer argument");
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_plan_groups: bad head counts");
+  return decode_plan_impl(block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq,
+                          num_blocks, 0, plan, plan_bytes, stream, seq_group, group_pages,
+                          num_groups, num_heads / num_kv_heads);
 }
 
 extern "C" int rlse_decode_prefix_size(int batch, int num_heads, int head_dim,
@@ -322,7 +435,8 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
                                 int num_blocks, float scale, int dtype, void* workspace,
                                 size_t workspace_bytes, const void* plan, int flags,
                                 int prefix, void* prefix_buf, size_t prefix_bytes,
-                                rlse_stream_t stream) {
+                                rlse_stream_t stream, int num_groups = 0,
+                                int max_group_pages = 0) {
   if (flags & ~RLSE_DECODE_STREAM)
     return fail(RLSE_ERR_INVALID_VALUE, "decode_step: unknown flags 0x%x", flags);
   DecodeParams p;
@@ -352,6 +466,24 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
   p.plan = reinterpret_cast<const int4*>(plan);
   const int G = num_heads / num_kv_heads;
   const hipStream_t s = as_stream(stream);
+  p.plan_stamp = num_groups > 0 ? plan_stamp(2, num_groups) : plan_stamp(1, prefix);
+  const int* tail = plan ? plan_tail(p.plan, p.W) : nullptr;
+  if (num_groups > 0) {
+    // Prefix groups: every sequence's shared pages come from the plan, and
+    // the bound max_group_pages sizes the prefix launch and buffer.
+    if (!plan)
+      return fail(RLSE_ERR_INVALID_VALUE, "decode_step_groups: a plan from "
+                                          "rlse_decode_plan_groups is required");
+    if (num_groups > kMaxPrefixGroups)
+      return fail(RLSE_ERR_INVALID_VALUE, "decode_step_groups: num_groups %d > %d", num_groups,
+                  kMaxPrefixGroups);
+    if (max_group_pages < 1 || max_group_pages > max_blocks_per_seq ||
+        max_group_pages > kMaxPrefixPages)
+      return fail(RLSE_ERR_INVALID_VALUE,
+                  "decode_step_groups: max_group_pages %d outside [1, min(%d, %d)]",
+                  max_group_pages, max_blocks_per_seq, kMaxPrefixPages);
+    prefix = max_group_pages;
+  }
   if (prefix > 0) {
     // Cascade step: the shared prefix's partials first, on the same stream.
     if (dtype != RLSE_DTYPE_BF16 && dtype != RLSE_DTYPE_F16)
@@ -386,9 +518,21 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
     pp.prefix = prefix;
     pp.pre = reinterpret_cast<float*>(prefix_buf);
     pp.ws_err = p.ws_err;
+    pp.members = nullptr;
+    pp.grp = nullptr;
+    pp.num_groups = 0;
+    pp.tiles = 0;
+    if (num_groups > 0) {
+      const int* seq_pre = tail + kPlanStampWords;
+      pp.members = seq_pre + kMaxDecodeBatch;
+      pp.grp = pp.members + kMaxDecodeBatch;
+      pp.num_groups = num_groups;
+      pp.tiles = (batch * G + 15) / 16 + num_groups;  // each group adds at most one part tile
+      p.seq_pre = seq_pre;
+    }
     st2 = launch_decode_prefix(dtype, head_dim, G, pp, s);
     if (st2) return st2;
-    p.prefix = prefix;
+    p.prefix = num_groups > 0 ? 0 : prefix;
     p.pre = pp.pre;
     p.pre_slices = prefix_splits(prefix);
     p.pre_stride = (long long)batch * num_heads * prefix_row_floats(head_dim);
@@ -445,6 +589,23 @@ extern "C" int rlse_decode_step_cascade(
                           num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
                           scale, dtype, workspace, workspace_bytes, plan, flags, prefix_pages,
                           prefix_buf, prefix_bytes, stream);
+}
+
+extern "C" int rlse_decode_step_groups(
+    const void* q, const void* k_new, const void* v_new, const void* q_norm_weight,
+    const void* k_norm_weight, float eps, const void* cos_table, const void* sin_table,
+    int max_pos, void* k_pool, void* v_pool, const int32_t* block_tables,
+    const int32_t* seq_lens, void* out, int batch, int num_heads, int num_kv_heads, int head_dim,
+    int max_blocks_per_seq, int num_blocks, float scale, int dtype, void* workspace,
+    size_t workspace_bytes, const void* plan, int flags, int num_groups, int max_group_pages,
+    void* prefix_buf, size_t prefix_bytes, rlse_stream_t stream) {
+  if (num_groups < 1)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_step_groups: num_groups %d < 1", num_groups);
+  return decode_step_impl(q, k_new, v_new, q_norm_weight, k_norm_weight, eps, cos_table,
+                          sin_table, max_pos, k_pool, v_pool, block_tables, seq_lens, out, batch,
+                          num_heads, num_kv_heads, head_dim, max_blocks_per_seq, num_blocks,
+                          scale, dtype, workspace, workspace_bytes, plan, flags, 0, prefix_buf,
+                          prefix_bytes, stream, num_groups, max_group_pages);
 }
 
 static int compat_decode(const void* q, const void* k, const void* v, const int* tables,

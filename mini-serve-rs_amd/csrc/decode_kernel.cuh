@@ -84,19 +84,26 @@ __device__ __forceinline__ int valid_len(int L, int mbps) {
   return (L <= 0 || L > mbps * 16) ? 0 : L;
 }
 
+// Leading table entries of sequence b left out of the page stream: a
+// shared prefix attended separately (cascade step), the same `prefix` for
+// every sequence or, with seq_pre (prefix groups), each sequence's own.
+__device__ __forceinline__ int stream_skip(const int* __restrict__ seq_pre, int prefix, int b) {
+  return seq_pre ? seq_pre[b] : prefix;
+}
+
 // Exclusive prefix of per-sequence block counts into s_pref[0..B] (one wave).
-// first: seq_lens[lane] for lane < B, requested by the caller beforehand.
-// (The first chunk issues no load, so a caller with loads in flight does not
-// wait for them here.) prefix: leading blocks of every sequence left out of
-// the stream (a shared prefix attended separately; 0 = none).
+// first / first_pre: seq_lens[lane] and the lane's skipped entries for
+// lane < B, requested by the caller beforehand. (The first chunk issues no
+// load, so a caller with loads in flight does not wait for them here.)
 __device__ void block_prefix(const int* __restrict__ seq_lens, int B, int mbps, int* s_pref,
-                             int first, int prefix) {
+                             int first, int prefix, const int* __restrict__ seq_pre,
+                             int first_pre) {
   const int lane = threadIdx.x & 63;
   int carry = 0;
-  auto chunk = [&](int base, int len) __attribute__((always_inline)) {
+  auto chunk = [&](int base, int len, int pre) __attribute__((always_inline)) {
     const int b = base + lane;
     int x = b < B ? (valid_len(len, mbps) + 15) >> 4 : 0;
-    x = x > prefix ? x - prefix : 0;
+    x = x > pre ? x - pre : 0;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const int y = __shfl_up(x, o, 64);
@@ -105,9 +112,11 @@ __device__ void block_prefix(const int* __restrict__ seq_lens, int B, int mbps, 
     if (b < B) s_pref[b + 1] = carry + x;
     carry += __shfl(x, 63, 64);
   };
-  chunk(0, first);
-  for (int base = 64; base < B; base += 64)
-    chunk(base, base + lane < B ? seq_lens[base + lane] : 0);
+  chunk(0, first, first_pre);
+  for (int base = 64; base < B; base += 64) {
+    const int b = base + lane < B ? base + lane : B - 1;
+    chunk(base, base + lane < B ? seq_lens[b] : 0, stream_skip(seq_pre, prefix, b));
+  }
   if (lane == 0) s_pref[0] = 0;
 }
 
@@ -162,21 +171,23 @@ __device__ __forceinline__ int locate_seq(const int* s_pref, int B, int Hkv, lon
 // the valid rows in bits 0-7 (0 for a page id outside the pool) with bit 8
 // set on the last block of its row, the (sequence, KV head) row and the
 // row's new-token position. Blocks past the wave's end get {0, 0, -1, 0}.
-// A row's stream starts at table entry `prefix` (block_prefix).
+// A row's stream starts at table entry stream_skip(b) (block_prefix).
 __device__ __forceinline__ int4 block_desc(long long f, long long whi, const int* s_pref,
                                            const int* __restrict__ tables,
                                            const int* __restrict__ seq_lens, int B, int Hkv,
-                                           int mbps, int num_blocks, int prefix) {
+                                           int mbps, int num_blocks, int prefix,
+                                           const int* __restrict__ seq_pre) {
   int4 d = make_int4(0, 0, -1, 0);
   if (f < whi) {
     const int b = locate_seq(s_pref, B, Hkv, f);
     const int nb = s_pref[b + 1] - s_pref[b];
     const long long o = f - (long long)Hkv * s_pref[b];
     const int kvh = (int)(o / nb), blk = (int)(o % nb);
+    const int pre = stream_skip(seq_pre, prefix, b);
     d.z = b * Hkv + kvh;
-    d.x = tables[(size_t)b * mbps + prefix + blk];
+    d.x = tables[(size_t)b * mbps + pre + blk];
     const int L = valid_len(seq_lens[b], mbps);
-    const int nv = L - (prefix + blk) * 16;
+    const int nv = L - (pre + blk) * 16;
     d.y = nv > 16 ? 16 : nv;
     d.w = L - 1;
     if ((unsigned)d.x >= (unsigned)num_blocks)
@@ -241,6 +252,13 @@ struct DecodeParams {
   const float* pre;      // cascade step: pre_slices states over the shared prefix
   int pre_slices;        // (regions pre_stride floats apart), combined in order
   long long pre_stride;
+  // Prefix groups (several shared prefixes and unforked sequences in one
+  // cascade step): the shared pages of each sequence ([B], 0 = none; its
+  // prefix states take prefix_splits of them slices), or null (`prefix` for
+  // every sequence).
+  const int* seq_pre;
+  // The stamp a planned launch expects in its plan (plan_stamp).
+  int plan_stamp;
   // Cascade step: rows finished inside one wave's range park their state
   // here ([B][Hq][prefix_row_floats(D)] floats) and are combined with the
   // prefix states after the wave's stream, all slices' loads at once.
@@ -273,7 +291,43 @@ struct PrefixParams {
   int prefix;
   float* pre;        // prefix_splits(prefix) x [B][Hq][prefix_row_floats(D)] floats
   uint32_t* ws_err;  // sticky flags: RLSE_WS_ERR_PREFIX
+  // Prefix groups (null members: one group, every sequence, `prefix`
+  // pages): the grouped sequences, group by group, and GroupPlan's offsets
+  // and pages (group_plan_kernel); num_groups groups, `prefix` then bounds
+  // every group's pages and tiles the launch's column tiles.
+  const int* members;
+  const int* grp;
+  int num_groups;
+  int tiles;
 };
+// Most prefix groups one grouped cascade step takes.
+constexpr int kMaxPrefixGroups = 64;
+// The grouped plan, after the per-wave descriptors of a plan buffer:
+// seq_pre[kMaxDecodeBatch] (shared pages per sequence), members
+// [kMaxDecodeBatch] (grouped sequences, group by group, in batch order within
+// a group), then grp: member offsets [kMaxPrefixGroups + 1], column-tile
+// offsets [kMaxPrefixGroups + 1], pages [kMaxPrefixGroups], and one word of
+// error bits (a group id or a page count out of range).
+constexpr int kGrpOff = 0, kGrpTiles = kMaxPrefixGroups + 1, kGrpPages = 2 * kGrpTiles,
+              kGrpErr = kGrpPages + kMaxPrefixGroups, kGrpWords = kGrpErr + 1;
+__host__ __device__ constexpr size_t group_plan_words() {
+  return 2 * (size_t)kMaxDecodeBatch + kGrpWords;
+}
+// A plan buffer: the descriptors of the first 64 blocks of every wave
+// (int4), the new-token positions of the 64 rows from each wave's first row
+// (int), then the tail: 64 words whose first is the plan's stamp, and the
+// grouped plan.
+constexpr int kPlanStampWords = 64;
+__host__ __device__ inline const int* plan_tail(const int4* plan, int W) {
+  return reinterpret_cast<const int*>(plan + (size_t)W * kWaves * 64) + (size_t)W * kWaves * 64;
+}
+__host__ __device__ constexpr size_t plan_bytes(int W) {
+  return (size_t)W * kWaves * 64 * (sizeof(int4) + sizeof(int)) +
+         (kPlanStampWords + group_plan_words()) * sizeof(int);
+}
+// The stamp of a plan: mode 1 with the shared prefix's pages (0 for a
+// plain plan), mode 2 with the number of prefix groups.
+__host__ __device__ constexpr int plan_stamp(int mode, int value) { return (mode << 24) | value; }
 // Longest shared prefix a cascade step takes, in pages (8192 tokens).
 constexpr int kMaxPrefixPages = 512;
 // Slices of the prefix attended by separate workgroups (each leaves its own
@@ -472,13 +526,15 @@ struct DecodeLds {
 // once: the lines do not displace the small per-launch data -- plan, tables,
 // queries, records -- from L2); 0 otherwise, so that a page shared by many
 // rows (a forked prefix) is served from the caches after its first read.
-// plan_d, ctr0 and len_t0 were requested by decode_kernel: the wave's plan
-// descriptors (planned modes), its launch counter and seq_lens[tid].
+// plan_d, ctr0, len_t0, pre_t0 and stamp were requested by decode_kernel:
+// the wave's plan descriptors (planned modes), its launch counter,
+// seq_lens[tid], the leading table entries sequence tid leaves out of the
+// stream and the plan's stamp.
 template <typename T, int D, int G, int MODE, int POL>
 __device__ __forceinline__ void decode_body(const DecodeParams& p,
                                             DecodeLds<T, D, G, MODE != kModePlain>& lds,
                                             int* s_pref, int4 plan_d, int plan_pos,
-                                            uint32_t ctr0, int len_t0) {
+                                            uint32_t ctr0, int len_t0, int pre_t0, int stamp) {
   constexpr bool FUSED = MODE != kModePlain;
   constexpr bool PLANNED = MODE >= kModePlanned;
   constexpr bool kMma = decode_mma<T, D, G>();
@@ -653,6 +709,16 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     rope_packets(pos, a_c, a_s);
   };
   if constexpr (PLANNED) {
+    // A plan built for another step shape (another prefix, prefix groups
+    // where none are expected, or the reverse) does not describe this
+    // launch's page stream: nothing of it is used, the launch does no work
+    // (every wave still advances its launch counter) and the error is
+    // flagged, as the caller's.
+    if (__builtin_amdgcn_readfirstlane(stamp) != p.plan_stamp) {
+      if (blockIdx.x == 0 && tid == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
+      end_epoch(next_epoch(ctr0));
+      return;
+    }
     // The plan gives the first row and the appends of the first 64 blocks:
     // their query and append loads go out ahead of the first blocks', so the
     // prologue's math waits for them alone and not behind the launch's first
@@ -668,7 +734,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < kPreIssued; ++k) {
-      if (k == 2 && p.prefix > 0) break;
+      if (k == 2 && p.pre) break;
       const int nv = __builtin_amdgcn_readlane(plan_d.y, k) & 255;
       const int row = __builtin_amdgcn_readlane(plan_d.z, k);
       const int kvh = nv > 0 ? row % Hkv : 0;
@@ -676,7 +742,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
                  nv > 0);
     }
   }
-  if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref, len_t0, p.prefix);
+  if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref, len_t0, p.prefix, p.seq_pre, pre_t0);
   if constexpr (FUSED) {
     if (tid < B) s_len[tid] = valid_len(len_t0, mbps);
     for (int b = tid + kThreads; b < B; b += kThreads) s_len[b] = valid_len(p.seq_lens[b], mbps);
@@ -738,7 +804,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         d = plan_d;
       else
         d = block_desc(wlo + base + lane, whi, s_pref, p.tables, p.seq_lens, B, Hkv, mbps,
-                       p.num_blocks, p.prefix);
+                       p.num_blocks, p.prefix, p.seq_pre);
       d_id = d.x;
       d_nv = d.y;
       d_row = d.z;
@@ -1277,7 +1343,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     if constexpr (PLANNED) issue(b1, 1, false);
     after_pre_issue();
     if constexpr (!PLANNED) issue(b1, 1, true);
-    if constexpr (NBUF == 3) issue(b2, 2, !PLANNED || kPreIssued < 3 || p.prefix > 0);
+    if constexpr (NBUF == 3) issue(b2, 2, !PLANNED || kPreIssued < 3 || p.pre);
     for (int i = 0;;) {
       compute(b0);
       if (++i == nblk) break;
@@ -1317,7 +1383,11 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
                             float(&A)[G][DPL]) __attribute__((always_inline)) {
     constexpr int PF = prefix_row_floats(D);
     const float* pr = p.pre + ((size_t)b * Hq + (size_t)kvh * G) * PF;
-    const int ns = p.pre_slices;
+    int ns = p.pre_slices;
+    if (p.seq_pre) {  // prefix groups: the slices of this sequence's group, none if unforked
+      const int pg = p.seq_pre[b];
+      ns = pg > 0 ? (prefix_splits(pg) < ns ? prefix_splits(pg) : ns) : 0;  // at most the buffer's
+    }
 #pragma unroll 1
     for (int s0 = 0; s0 < ns; s0 += SB) {
       float sm[SB][G], sl[SB][G], sa[SB][G][DPL];
@@ -1561,20 +1631,28 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   // that would wait for it early. The lengths arrive with the descriptors,
   // so the prefix never waits behind the first blocks.
   int4 plan_d = make_int4(0, 0, -1, 0);
-  int plan_pos = 0;
+  int plan_pos = 0, stamp = 0;
   if constexpr (PLANNED) {
     const size_t at = ((size_t)blockIdx.x * kWaves + wave) * 64 + lane;
     plan_d = p.plan[at];
     plan_pos = reinterpret_cast<const int*>(p.plan + (size_t)p.W * kWaves * 64)[at];
+    stamp = plan_tail(p.plan, p.W)[0];
   }
   const uint32_t ctr0 = __hip_atomic_load(p.ws_ctr + (size_t)blockIdx.x * kWaves + wave,
                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int len_t0 = (int)__builtin_amdgcn_raw_buffer_load_b32(
       __builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(p.seq_lens), 0, p.B * 4, kBufferWord3),
       tid * 4, 0, 0);
+  // The lane's skipped table entries for the block prefix's first chunk (a
+  // null seq_pre gets a descriptor of zero records: zeros, no access).
+  const int pre_t0 = p.seq_pre ? (int)__builtin_amdgcn_raw_buffer_load_b32(
+                                     __builtin_amdgcn_make_buffer_rsrc(
+                                         const_cast<int*>(p.seq_pre), 0, p.B * 4, kBufferWord3),
+                                     tid * 4, 0, 0)
+                               : p.prefix;
   (void)lane;
   decode_body<T, D, G, MODE, MODE == kModePlannedStream ? kLoadNonTemporal : 0>(
-      p, lds, s_pref, plan_d, plan_pos, ctr0, len_t0);
+      p, lds, s_pref, plan_d, plan_pos, ctr0, len_t0, pre_t0, stamp);
 }
 
 

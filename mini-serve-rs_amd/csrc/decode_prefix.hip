@@ -52,36 +52,80 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane % LPR, rsub = lane / LPR;
   const int mh = lane & 15, mq = lane >> 4;
-  const int B = p.B, Hkv = p.Hkv, Hq = Hkv * G, ncols = B * G, P = p.prefix;
+  const int B = p.B, Hkv = p.Hkv, Hq = Hkv * G;
+  const bool grouped = p.members != nullptr;
   // Workgroup id -> (slice set ps = h * NS + sp, column tile c): the tiles of
   // one slice set share id % 8, i.e. one XCD (workgroups are dealt to the
-  // XCDs round-robin); ids past the last slice set have no work.
-  const int NS = prefix_splits(P), NC = (ncols + 15) / 16;
+  // XCDs round-robin); ids past the last slice set have no work. With prefix
+  // groups NS and NC are bounds (p.prefix bounds every group's pages, p.tiles
+  // its column tiles) and a workgroup first finds its group: tile c belongs
+  // to group grp, its columns to the group's members, its pages to the
+  // group's first member's table.
+  const int NS = prefix_splits(p.prefix), NC = grouped ? p.tiles : (B * G + 15) / 16;
   const int id = blockIdx.x, xq = id >> 3;
   const int ps = (xq / NC) * 8 + (id & 7), c = xq % NC;
+  if (grouped) {
+    // The groups come from the plan: one built for another step shape (no
+    // member lists, or another group count) is not read; the error is
+    // flagged and the decode launch that follows does nothing either.
+    const int* stamp = p.members - kMaxDecodeBatch - kPlanStampWords;
+    if (__builtin_amdgcn_readfirstlane(stamp[0]) != plan_stamp(2, p.num_groups)) {
+      if (id == 0 && tid == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
+      return;
+    }
+    if (id == 0 && tid == 0 && p.grp[kGrpErr] != 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
+  }
   if (ps >= Hkv * NS) return;
-  const int h = ps / NS, sp = ps - h * NS, c0 = c * 16;
+  const int h = ps / NS, sp = ps - h * NS;
+  int P = p.prefix, ncols = B * G, c0 = c * 16, moff = 0;
+  const int* __restrict__ mem = nullptr;  // grouped: the group's members
+  if (grouped) {
+    if (c >= p.grp[kGrpTiles + p.num_groups]) return;
+    // the group holding tile c: the last g with tiles[g] <= c (lane g reads tiles[g])
+    const int tg = lane < p.num_groups ? p.grp[kGrpTiles + lane] : 0x7fffffff;
+    const int g = 63 - __builtin_clzll(__ballot(tg <= c));
+    P = p.grp[kGrpPages + g];
+    if (P > p.prefix) {  // above the bound that sized the launch and the buffer
+      if (tid == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
+      return;
+    }
+    if (P <= 0 || sp >= prefix_splits(P)) return;
+    moff = p.grp[kGrpOff + g];
+    ncols = (p.grp[kGrpOff + g + 1] - moff) * G;
+    c0 = (c - p.grp[kGrpTiles + g]) * 16;
+    mem = p.members + moff;
+  }
+  const int NSg = prefix_splits(P);
+  // Sequence of column j (one per query head of the sequence); member
+  // indices are clamped into the batch.
+  auto seq_of = [&](int j) __attribute__((always_inline)) {
+    const int b = mem ? mem[j / G] : j / G;
+    return b < 0 ? 0 : (b < B ? b : B - 1);
+  };
+  const int* __restrict__ ptab = p.tables + (size_t)seq_of(0) * p.mbps;  // the group's pages
   const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
   const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
   const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
 
 
   // This wave's pages: slice sp of the prefix, then the wave's share of it.
-  const int PS = (P + NS - 1) / NS;
+  const int PS = (P + NSg - 1) / NSg;
   const int slo = sp * PS < P ? sp * PS : P, shi = slo + PS < P ? slo + PS : P;
   const int per = (shi - slo + kPrefixWaves - 1) / kPrefixWaves;
   const int lo = slo + wave * per < shi ? slo + wave * per : shi;
   const int hi = lo + per < shi ? lo + per : shi;
   // Lane i holds the page id of block lo + i (a wave takes at most 64).
-  const int ids = lo + lane < hi ? p.tables[lo + lane] : 0;
+  const int ids = lo + lane < hi ? ptab[lo + lane] : 0;
   // Wave 1 of each workgroup checks a share of the batch against the
   // contract: every sequence's first P table entries are sequence 0's, and
   // its new token (position L - 1) lies past them. The first sequence's
   // entries are requested here, ahead of the page loads, and compared once
   // those are issued (further sequences, when the batch outnumbers the
-  // workgroups, are read at the end).
+  // workgroups, are read at the end). With prefix groups the workgroups of
+  // slice set 0 check the members of their column tile against the group's
+  // first member, at the end.
   constexpr int kChk = kMaxPrefixPages / 64;
-  const int nwork = Hkv * NS * NC, bchk = ps * NC + c;
+  const int nwork = Hkv * NS * NC, bchk = grouped ? B : ps * NC + c;
   int chk_len = 0, chk_t[kChk], chk_0[kChk];
   bool bad = false;
   if (wave == 1 && bchk < B) {
@@ -104,7 +148,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
   uint4 sq_x = make_uint4(0, 0, 0, 0), sq_c = sq_x, sq_s = sq_x, sq_w = sq_x;
   if (stager) {
     const int jj = qj < ncols ? qj : ncols - 1;
-    const int b = jj / G, g = jj - b * G;
+    const int b = seq_of(jj), g = jj % G;
     sq_x = *reinterpret_cast<const uint4*>(qb + ((size_t)b * Hq + (size_t)h * G + g) * D +
                                            (size_t)col * EPL);
     const int L = valid_len(p.seq_lens[b], p.mbps);
@@ -270,7 +314,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     // The head's sum over its four lanes; M is common to them.
     l = l + __shfl_xor(l, 16, 64);
     l = l + __shfl_xor(l, 32, 64);
-    const int b = j / G, g = j - b * G;
+    const int b = seq_of(j), g = j % G;
     const size_t slice = (size_t)B * Hq * PF;  // floats of one region
     float* dst = p.pre + (size_t)sp * slice + ((size_t)b * Hq + (size_t)h * G + g) * PF;
     *reinterpret_cast<float4*>(dst + 16 * wave + 4 * mq) = make_float4(a[0], a[1], a[2], a[3]);
@@ -285,12 +329,23 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     }
     if (__any(bad) && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
   }
+  if (grouped && wave == 1 && ps == 0) {
+    // the members whose columns fall in this tile, against the group's first
+    for (int m = c0 / G; m * G < c0 + 16 && m * G < ncols; ++m) {
+      const int b = seq_of(m * G);
+      const int L = p.seq_lens[b];
+      bad = bad || L <= 16 * P || L > p.mbps * 16;
+      for (int i = lane; i < P; i += 64) bad = bad || p.tables[(size_t)b * p.mbps + i] != ptab[i];
+    }
+    if (__any(bad) && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
+  }
 }
 
 template <typename T, int D, int G>
 int launch_prefix_t(const PrefixParams& p, hipStream_t s) {
   // 8 ids per group of 8 slice sets and column tile (see the kernel).
-  const int nc = (p.B * G + 15) / 16, nps = p.Hkv * prefix_splits(p.prefix);
+  const int nc = p.members ? p.tiles : (p.B * G + 15) / 16;
+  const int nps = p.Hkv * prefix_splits(p.prefix);
   const unsigned grid = (unsigned)(8 * nc * ((nps + 7) / 8));
   hipLaunchKernelGGL((decode_prefix_kernel<T, D, G>), dim3(grid), dim3(64 * kPrefixWaves), 0, s, p);
   return launch_status("decode_prefix_kernel");

@@ -79,7 +79,7 @@ EXPORTED = (
     "rlse_dense_workspace_size", "rlse_dense_pack", "rlse_decode_plan_size", "rlse_decode_plan",
     "rlse_decode_step_planned", "rlse_workspace_check", "rlse_set_merge_wait_ns",
     "rlse_decode_step_noalloc", "rlse_decode_prefix_size", "rlse_decode_plan_cascade",
-    "rlse_decode_step_cascade",
+    "rlse_decode_step_cascade", "rlse_decode_plan_groups", "rlse_decode_step_groups",
 )
 
 
@@ -196,6 +196,10 @@ _SIGS = {
     "rlse_decode_step_cascade": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp,
                                       _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _i,
                                       _i, _vp, _sz, _vp]),
+    "rlse_decode_plan_groups": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "rlse_decode_step_groups": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp,
+                                     _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _i,
+                                     _i, _i, _vp, _sz, _vp]),
     "rlse_prefill_workspace_size": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz)]),
     "rlse_prefill_attn": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _i, _f, _i, _vp,
                                _sz, _vp]),
@@ -832,6 +836,38 @@ def decode_step_cascade(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: floa
         max_blocks_per_seq, num_blocks, scale, _dt(dtype), _ptr(workspace), workspace_bytes,
         _ptr(plan), DECODE_STREAM if stream_pages else 0, prefix_pages, _ptr(prefix_buf),
         prefix_bytes, _stream(stream)))
+
+
+def decode_plan_groups(block_tables, seq_lens, seq_group, group_pages, num_groups: int,
+                       batch: int, num_heads: int, num_kv_heads: int, max_blocks_per_seq: int,
+                       num_blocks: int, plan, plan_bytes: int, stream=None) -> None:
+    """The plan of a cascade step with prefix groups: seq_group (device int32
+    [batch], -1 = no shared prefix) and group_pages (device int32
+    [num_groups], the leading table entries each group's members share)."""
+    _check(load().rlse_decode_plan_groups(_ptr(block_tables), _ptr(seq_lens), _ptr(seq_group),
+                                          _ptr(group_pages), num_groups, batch, num_heads,
+                                          num_kv_heads, max_blocks_per_seq, num_blocks,
+                                          _ptr(plan), plan_bytes, _stream(stream)))
+
+
+def decode_step_groups(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: float, cos_table,
+                       sin_table, max_pos: int, k_pool, v_pool, block_tables, seq_lens, out,
+                       batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                       max_blocks_per_seq: int, num_blocks: int, scale: float, dtype, plan,
+                       num_groups: int, max_group_pages: int, prefix_buf, prefix_bytes: int,
+                       workspace=None, workspace_bytes: int = 0, stream=None,
+                       stream_pages: bool = False) -> None:
+    """The cascade step of a mixed batch: each prefix group's shared pages
+    attended once for its members, every other page once for its sequence.
+    plan: from decode_plan_groups (required); prefix_buf: decode_prefix_size
+    bytes with prefix_pages = max_group_pages."""
+    _check(load().rlse_decode_step_groups(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(q_norm_weight), _ptr(k_norm_weight), eps,
+        _ptr(cos_table), _ptr(sin_table), max_pos, _ptr(k_pool), _ptr(v_pool),
+        _ptr(block_tables), _ptr(seq_lens), _ptr(out), batch, num_heads, num_kv_heads, head_dim,
+        max_blocks_per_seq, num_blocks, scale, _dt(dtype), _ptr(workspace), workspace_bytes,
+        _ptr(plan), DECODE_STREAM if stream_pages else 0, num_groups, max_group_pages,
+        _ptr(prefix_buf), prefix_bytes, _stream(stream)))
 
 
 def prefill_workspace_size(num_tokens: int, ctx_len: int, num_heads: int, num_kv_heads: int,

@@ -191,3 +191,181 @@ def test_cascade_contract_violations_raise_the_prefix_flag(kv):
                    {"pre_bytes": pre.numel() - 16}, {"dtype": "f32"}):
         with pytest.raises(kv.RlseError):
             step(tables, lens, **kwargs)
+
+
+def _group_batch(rng, groups, n_unforked, hkv, d, seed):
+    """A mixed batch: groups = [(members, shared pages)], each member holding
+    its group's shared pages then private ones (suffix U[1, 300] + the new
+    token), plus n_unforked sequences with private pages only (U[1, 2000]
+    keys); batch positions shuffled so members are scattered."""
+    spec = [(g, pp) for g, (n, pp) in enumerate(groups) for _ in range(n)]
+    spec += [(-1, 0)] * n_unforked
+    order = rng.permutation(len(spec))
+    spec = [spec[i] for i in order]
+    b = len(spec)
+    seq_group = np.array([g for g, _ in spec], np.int32)
+    lens = np.array([16 * pp + int(rng.integers(1, 301)) + 1 if g >= 0 else
+                     int(rng.integers(1, 2001)) for g, pp in spec], np.int32)
+    own = np.array([(int(n) + 15) // 16 - pp for n, (_, pp) in zip(lens, spec)])
+    nb = sum(pp for _, pp in groups) + int(own.sum()) + 5
+    perm = rng.permutation(nb).astype(np.int32)
+    used = 0
+    shared = []
+    for _, pp in groups:
+        shared.append(perm[used:used + pp])
+        used += pp
+    mbps = int(max((int(n) + 15) // 16 for n in lens))
+    tables = np.zeros((b, mbps), np.int32)
+    for i, (g, pp) in enumerate(spec):
+        if g >= 0:
+            tables[i, :pp] = shared[g]
+        tables[i, pp:pp + own[i]] = perm[used:used + own[i]]
+        used += int(own[i])
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(seed)
+    kp = torch.randn((nb, hkv, 16, d), generator=gen, device=DEV).to(BF)
+    vp = torch.randn((nb, hkv, 16, d), generator=gen, device=DEV).to(BF)
+    return seq_group, lens, tables, nb, mbps, kp, vp, gen
+
+
+def test_grouped_cascade_mixed_batch_matches_oracle(kv):
+    """Three prefix groups (5, 17 and 64 shared pages: one, two and four
+    slices) and unforked sequences, members scattered through the batch, in
+    one grouped cascade step (rlse_decode_step_groups, streamed pages): every
+    row against the oracle over its full key range, the outputs against the
+    planned step's (another sum order) and the pool bytes equal to its."""
+    hq, hkv, d = 16, 8, 128
+    rng = np.random.default_rng(91)
+    groups = [(5, 5), (9, 17), (20, 64)]
+    seq_group, lens, tables, nb, mbps, kp, vp, g = _group_batch(rng, groups, 7, hkv, d, 91)
+    b = len(lens)
+    q, kn, vn, qw, kw, max_pos, c_h, s_h, c_d, s_d = _step_inputs(kv, g, BF, b, hq, hkv, d, mbps,
+                                                                  "bf16")
+    print(f"grouped cascade: B={b}, groups {groups}, 7 unforked, keys "
+          f"{int(lens.min())}..{int(lens.max())}", flush=True)
+    t_dev, l_dev = to_dev(tables), to_dev(lens)
+    sg_dev = to_dev(seq_group)
+    gp = np.array([pp for _, pp in groups], np.int32)
+    gp_dev = to_dev(gp)
+    max_pages = int(gp.max())
+    scale = 1.0 / math.sqrt(d)
+    ws = torch.zeros(kv.decode_workspace_size(b, hq, hkv, d), dtype=torch.uint8, device=DEV)
+    plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=DEV)
+    pre = torch.zeros(kv.decode_prefix_size(b, hq, d, max_pages), dtype=torch.uint8, device=DEV)
+    res = {}
+    for name in ("grouped", "grouped_cacheable", "planned"):
+        kp_i, vp_i = kp.clone(), vp.clone()
+        out = torch.full((b, hq, d), 3.0, dtype=BF, device=DEV)
+        args = (q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp_i, vp_i, t_dev, l_dev, out, b, hq,
+                hkv, d, mbps, nb, scale, "bf16")
+        if name == "planned":
+            kv.decode_plan(t_dev, l_dev, b, hkv, mbps, nb, plan, plan.numel())
+            kv.decode_step_planned(*args, plan, ws, ws.numel())
+        else:
+            kv.decode_plan_groups(t_dev, l_dev, sg_dev, gp_dev, len(groups), b, hq, hkv, mbps, nb,
+                                  plan, plan.numel())
+            kv.decode_step_groups(*args, plan, len(groups), max_pages, pre, pre.numel(), ws,
+                                  ws.numel(), stream_pages=name == "grouped")
+        torch.cuda.synchronize()
+        assert kv.workspace_flags(ws) == 0, name
+        res[name] = (_host16(out), _host16(kp_i), _host16(vp_i))
+    out_g, k_g, v_g = res["grouped"]
+    np.testing.assert_array_equal(res["grouped_cacheable"][0], out_g)  # the cache flag: same bits
+    np.testing.assert_array_equal(k_g, res["planned"][1])
+    np.testing.assert_array_equal(v_g, res["planned"][2])
+    mx, rel = err_report(_to_f32(out_g, "bf16"), _to_f32(res["planned"][0], "bf16"))
+    print(f"[grouped vs planned] max_abs={mx:.3e} rel={rel:.3e}")
+    assert mx <= 1e-2
+    got = _to_f32(out_g, "bf16")
+    kf, vf = _to_f32(k_g, "bf16"), _to_f32(v_g, "bf16")
+    qh, qwh = _host16(q), _host16(qw)
+    worst = {}
+    for r in range(b):
+        n = int(lens[r])
+        pos = np.full(hq, n - 1, np.int32)
+        q_ref = O.bf16_bits_to_f32(O.apply_rope_bf16(O.rmsnorm_bf16(qh[r], qwh, 1e-6), pos,
+                                                      c_h, s_h))
+        kc = O.paged_to_contiguous(kf, tables[r], n)
+        vc = O.paged_to_contiguous(vf, tables[r], n)
+        want = O.decode_batch_f32(q_ref[None], kc[None], vc[None], np.array([n], np.int32), scale)
+        mx, _ = err_report(got[r], want[0])
+        key = int(seq_group[r])
+        worst[key] = max(worst.get(key, 0.0), mx)
+        assert np.isfinite(got[r]).all()
+        assert mx <= TOL["bf16"], (r, key, mx)
+    print("grouped cascade: worst max_abs per group (-1 = unforked): " +
+          ", ".join(f"{k}: {v:.3e}" for k, v in sorted(worst.items())))
+
+
+def test_grouped_cascade_contract_and_plan_stamp(kv):
+    """A member whose shared entries differ from its group's, or a group id
+    out of range, raises RLSE_WS_ERR_PREFIX; so does a planned launch given a
+    plan built for another step shape (a plain plan for a cascade step, a
+    cascade plan of another prefix). The next correct step is clean."""
+    hq, hkv, d = 16, 8, 128
+    rng = np.random.default_rng(93)
+    groups = [(3, 4), (4, 9)]
+    seq_group, lens, tables, nb, mbps, kp, vp, g = _group_batch(rng, groups, 2, hkv, d, 93)
+    b = len(lens)
+    q, kn, vn, qw, kw, max_pos, _, _, c_d, s_d = _step_inputs(kv, g, BF, b, hq, hkv, d, mbps,
+                                                              "bf16")
+    ws = torch.zeros(kv.decode_workspace_size(b, hq, hkv, d), dtype=torch.uint8, device=DEV)
+    plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=DEV)
+    pre = torch.zeros(kv.decode_prefix_size(b, hq, d, 9), dtype=torch.uint8, device=DEV)
+    out = torch.empty((b, hq, d), dtype=BF, device=DEV)
+    gp = to_dev(np.array([4, 9], np.int32))
+
+    def grouped(tables_, sg):
+        t_dev, l_dev = to_dev(tables_), to_dev(lens)
+        kv.decode_plan_groups(t_dev, l_dev, to_dev(sg), gp, 2, b, hq, hkv, mbps, nb, plan,
+                              plan.numel())
+        kv.decode_step_groups(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp.clone(), vp.clone(),
+                              t_dev, l_dev, out, b, hq, hkv, d, mbps, nb, 1.0 / math.sqrt(d),
+                              "bf16", plan, 2, 9, pre, pre.numel(), ws, ws.numel())
+        torch.cuda.synchronize()
+        return kv.workspace_flags(ws)
+
+    assert grouped(tables, seq_group) == 0
+    m = int(np.flatnonzero(seq_group == 1)[1])
+    bad_t = tables.copy()
+    bad_t[m, 2] = tables[m, 9]                   # a private page inside group 1's shared range
+    print("grouped contract: member's shared entries differ", flush=True)
+    assert grouped(bad_t, seq_group) == kv.WS_ERR_PREFIX
+    bad_g = seq_group.copy()
+    bad_g[0] = 5                                 # no group 5
+    print("grouped contract: group id out of range", flush=True)
+    assert grouped(tables, bad_g) == kv.WS_ERR_PREFIX
+    assert grouped(tables, seq_group) == 0
+    # a plan of another step shape
+    t_dev, l_dev = to_dev(tables), to_dev(lens)
+    fork_t = tables.copy()
+    fork_t[:, :2] = tables[0, :2]                # two pages shared by the whole batch
+    ft_dev = to_dev(fork_t)
+    pre2 = torch.zeros(kv.decode_prefix_size(b, hq, d, 2), dtype=torch.uint8, device=DEV)
+    for plan_prefix, step_prefix in ((0, 2), (1, 2)):
+        print(f"plan stamp: plan for prefix {plan_prefix}, cascade step of prefix {step_prefix}",
+              flush=True)
+        kv.decode_plan_cascade(ft_dev, l_dev, b, hkv, mbps, nb, plan_prefix, plan, plan.numel())
+        kv.decode_step_cascade(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp.clone(), vp.clone(),
+                               ft_dev, l_dev, out, b, hq, hkv, d, mbps, nb, 1.0 / math.sqrt(d),
+                               "bf16", plan, step_prefix, pre2, pre2.numel(), ws, ws.numel())
+        torch.cuda.synchronize()
+        assert kv.workspace_flags(ws) == kv.WS_ERR_PREFIX
+    print("plan stamp: grouped plan for a plain planned step", flush=True)
+    kv.decode_plan_groups(t_dev, l_dev, to_dev(seq_group), gp, 2, b, hq, hkv, mbps, nb, plan,
+                          plan.numel())
+    kv.decode_step_planned(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp.clone(), vp.clone(),
+                           t_dev, l_dev, out, b, hq, hkv, d, mbps, nb, 1.0 / math.sqrt(d), "bf16",
+                           plan, ws, ws.numel())
+    torch.cuda.synchronize()
+    assert kv.workspace_flags(ws) == kv.WS_ERR_PREFIX
+    assert grouped(tables, seq_group) == 0
+    for kwargs in ({"num_groups": 0}, {"num_groups": 65}, {"max_group_pages": 0},
+                   {"max_group_pages": mbps + 1}, {"dtype": "f32"}):
+        a = dict(num_groups=2, max_group_pages=9, dtype="bf16")
+        a.update(kwargs)
+        with pytest.raises(kv.RlseError):
+            kv.decode_step_groups(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp.clone(),
+                                  vp.clone(), t_dev, l_dev, out, b, hq, hkv, d, mbps, nb,
+                                  1.0 / math.sqrt(d), a["dtype"], plan, a["num_groups"],
+                                  a["max_group_pages"], pre, pre.numel(), ws, ws.numel())
