@@ -72,6 +72,17 @@ FORK = {
                        "suffixes U[64,512] + 1 appended, 16q/8kv heads, d=128, 28 layers, bf16"),
 }
 
+# Mixed batch: sequences forked from several cached prefixes and unforked
+# ones in one decode step: (Hq, Hkv, d, layers, [(members, prefix tokens)],
+# unforked, suffix lo, suffix hi, unforked cached lo, hi, description)
+MIXED = {
+    "qwen3_mixed": (16, 8, 128, 28, [(20, 1024), (20, 512), (8, 2048)], 16, 64, 512, 128, 2048,
+                    "Qwen3-0.6B mixed-batch decode: 64 sequences -- 20 forked from a 1024-token "
+                    "prefix, 20 from a 512-token one, 8 from a 2048-token one (refcounted "
+                    "pages), private suffixes U[64,512] + 1 appended -- and 16 unforked with "
+                    "U[128,2048] cached + 1, batch order shuffled, 16q/8kv heads, d=128, 28 "
+                    "layers, bf16"),
+}
 
 # Whole decode step (every op of step_decode_batch on the device):
 # (model config factory name, batch, len_lo, len_hi, description)
@@ -94,7 +105,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="qwen3",
-                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(FORK) + sorted(E2E))
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(FORK) + sorted(MIXED) +
+                    sorted(E2E))
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -105,9 +117,9 @@ def parse():
                     help="whole-step workloads: launch every op from the host each step "
                          "instead of replaying the step captured as a HIP graph")
     ap.add_argument("--no-cascade", action="store_true",
-                    help="fork workload: decode every sequence's prefix pages in the decode "
-                         "launch (rlse_decode_step_planned) instead of once per batch "
-                         "(rlse_decode_step_cascade)")
+                    help="fork and mixed workloads: decode every sequence's prefix pages in "
+                         "the decode launch (rlse_decode_step_planned) instead of once per "
+                         "batch or group (rlse_decode_step_cascade / rlse_decode_step_groups)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 1 GiB (HBM counter calibration)")
     return ap.parse_args()
@@ -387,6 +399,190 @@ def fork_inputs(workload, seed, dev, layers=None):
             "cow_pairs": src, "fork_ms": fork_ms, "q": q_in, "k_new": k_in, "v_new": v_in,
             "q_norm": qw, "k_norm": kw, "cos": cos_t, "sin": sin_t, "cos_bytes": cos_b,
             "sin_bytes": sin_b, "max_pos": max_pos}
+
+
+def mixed_inputs(workload, seed, dev, layers=None):
+    """Every buffer of a mixed-batch workload, resident on dev: each prefix
+    of the workload written into refcounted pages of one pool handle and
+    forked to its members by the block manager (full pages shared), the
+    unforked sequences with private pages only, every sequence growing
+    private pages for its suffix and the token this step appends; the batch
+    order is a seeded permutation, so group members are scattered. Returns
+    the pool, the tables, the lengths, seq_group (-1 = unforked), the groups'
+    shared pages, each layer's q / new k / new v, the q/k RMSNorm weights and
+    the RoPE tables."""
+    import numpy as np
+    import torch
+    import rlse_kv as kv
+    hq, hkv, d, n_layers, groups, n_free, lo, hi, flo, fhi, _ = MIXED[workload]
+    layers = n_layers if layers is None else layers
+    rng = np.random.default_rng(seed)
+    spec = [(g, plen) for g, (n, plen) in enumerate(groups) for _ in range(n)]
+    spec += [(-1, 0)] * n_free
+    spec = [spec[i] for i in rng.permutation(len(spec))]
+    b = len(spec)
+    lens = np.array([plen + int(rng.integers(lo, hi + 1)) + 1 if g >= 0 else
+                     int(rng.integers(flo, fhi + 1)) + 1 for g, plen in spec], np.int32)
+    nb = sum((plen + 15) // 16 for _, plen in groups) + \
+        int(sum((int(n) + 15) // 16 - plen // 16 for n, (_, plen) in zip(lens, spec))) + 64
+    bf = torch.bfloat16
+    pool = kv.KVPool(layers, nb, hkv, d, "bf16")
+    stride = pool.layer_stride_elems
+    k0, v0 = pool.layer(0)
+    bm = kv.BlockManager(nb)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    for gi, (_, plen) in enumerate(groups):
+        bm.allocate(f"prefix{gi}", plen)
+        ptable = torch.tensor(bm.block_table(f"prefix{gi}"), dtype=torch.int32, device=dev)
+        pk = torch.randn((layers, hkv, plen, d), generator=g, device=dev, dtype=bf)
+        pv = torch.randn((layers, hkv, plen, d), generator=g, device=dev, dtype=bf)
+        kv.kv_scatter(pk, pv, k0, v0, stride, layers, ptable, 0, plen, hkv, d, nb, "bf16")
+        del pk, pv
+    src, dst = [], []
+    for i, (gi, plen) in enumerate(spec):
+        if gi >= 0:
+            for sp, dp in bm.fork(f"prefix{gi}", f"r{i}", plen):
+                src.append(sp)
+                dst.append(dp)
+    if src:
+        kv.kv_copy_blocks(k0, v0, stride, layers, torch.tensor(src, dtype=torch.int32, device=dev),
+                          torch.tensor(dst, dtype=torch.int32, device=dev), len(src), hkv, d, nb,
+                          "bf16")
+    for i, (gi, plen) in enumerate(spec):
+        if gi < 0:
+            bm.allocate(f"r{i}", 0)
+        while len(bm.block_table(f"r{i}")) * 16 < int(lens[i]):
+            bm.allocate_block(f"r{i}")
+    mbps = max(len(bm.block_table(f"r{i}")) for i in range(b))
+    tables = np.zeros((b, mbps), np.int32)
+    for i in range(b):
+        t = bm.block_table(f"r{i}")
+        tables[i, :len(t)] = t
+    t_dev = torch.from_numpy(tables).to(dev)
+    for i, (gi, plen) in enumerate(spec):   # private cached tokens (before the new one)
+        start = plen if gi >= 0 else 0
+        n = int(lens[i]) - 1 - start
+        sk = torch.randn((layers, hkv, n, d), generator=g, device=dev, dtype=bf)
+        sv = torch.randn((layers, hkv, n, d), generator=g, device=dev, dtype=bf)
+        kv.kv_scatter(sk, sv, k0, v0, stride, layers, t_dev[i], start, n, hkv, d, nb, "bf16")
+    q_in = [torch.randn((b, hq, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
+    k_in = [torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
+    v_in = [torch.randn((b, hkv, d), generator=g, device=dev, dtype=bf) for _ in range(layers)]
+    qw = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf)
+    kw = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(bf)
+    max_pos = mbps * 16
+    cos_b, sin_b = kv.rope_tables(1e6, d, max_pos, "bf16")
+    cos_t = torch.frombuffer(bytearray(cos_b), dtype=torch.int16).to(dev).view(bf)
+    sin_t = torch.frombuffer(bytearray(sin_b), dtype=torch.int16).to(dev).view(bf)
+    torch.cuda.synchronize()
+    return {"pool": pool, "lens": lens, "tables": tables, "tables_dev": t_dev, "mbps": mbps,
+            "num_blocks": nb, "seq_group": np.array([gi for gi, _ in spec], np.int32),
+            "group_pages": np.array([plen // 16 for _, plen in groups], np.int32),
+            "prefix_tokens": [plen for _, plen in groups], "q": q_in, "k_new": k_in,
+            "v_new": v_in, "q_norm": qw, "k_norm": kw, "cos": cos_t, "sin": sin_t,
+            "cos_bytes": cos_b, "sin_bytes": sin_b, "max_pos": max_pos}
+
+
+def mixed_bench(args):
+    """Mixed batch: one step = one fused decode step per layer for the whole
+    batch (append of the new token + decode): by default the grouped cascade
+    step (rlse_decode_step_groups: each group's shared pages attended once
+    for its members, every other page streamed), with --no-cascade the
+    planned step over every sequence's whole table (shared pages cacheable,
+    re-read by every member)."""
+    import numpy as np
+    import torch
+
+    import rlse_kv as kv
+
+    hq, hkv, d, layers, groups, _, _, _, _, _, desc = MIXED[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    f = mixed_inputs(args.workload, args.seed, dev)
+    pool, lens, mbps, nb, t_dev = f["pool"], f["lens"], f["mbps"], f["num_blocks"], f["tables_dev"]
+    b = len(lens)
+    lens_dev = torch.from_numpy(lens).to(dev)
+    sg_dev = torch.from_numpy(f["seq_group"]).to(dev)
+    gp_dev = torch.from_numpy(f["group_pages"]).to(dev)
+    ng, max_pages = len(groups), int(f["group_pages"].max())
+    out = torch.empty((b, hq, d), device=dev, dtype=torch.bfloat16)
+    ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    plan_bytes = kv.decode_plan_size()
+    plan = torch.zeros(plan_bytes, dtype=torch.uint8, device=dev)
+    pre_bytes = kv.decode_prefix_size(b, hq, d, max_pages)
+    pre = torch.zeros(pre_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    scale = 1.0 / math.sqrt(d)
+    ptrs = [pool.layer(layer) for layer in range(layers)]
+    cascade = not args.no_cascade
+
+    def step(evs=None):
+        if cascade:
+            kv.decode_plan_groups(t_dev, lens_dev, sg_dev, gp_dev, ng, b, hq, hkv, mbps, nb, plan,
+                                  plan_bytes, stream)
+        else:
+            kv.decode_plan(t_dev, lens_dev, b, hkv, mbps, nb, plan, plan_bytes, stream)
+        if evs is not None:
+            evs[0].record(stream)
+        for layer in range(layers):
+            a = (f["q"][layer], f["k_new"][layer], f["v_new"][layer], f["q_norm"], f["k_norm"],
+                 1e-6, f["cos"], f["sin"], f["max_pos"], ptrs[layer][0], ptrs[layer][1], t_dev,
+                 lens_dev, out, b, hq, hkv, d, mbps, nb, scale, "bf16", plan)
+            if cascade:
+                kv.decode_step_groups(*a, ng, max_pages, pre, pre_bytes, ws, ws_bytes, stream,
+                                      stream_pages=True)
+            else:
+                kv.decode_step_planned(*a, ws, ws_bytes, stream)
+        if evs is not None:
+            evs[1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kv.workspace_check(ws)
+    avg_ms = float(np.mean([a.elapsed_time(z) for a, z in evs])) / layers
+    row = 2 * hkv * d * 2  # K+V bytes of one token
+    extra = 2 * b * hq * d * 2 + sum(((int(n) + 15) // 16) * 4 for n in lens) + 4 * b + \
+        2 * b * row + b * d * 2 + 2 * d * 2
+    shared = sum(f["prefix_tokens"])
+    own = int(sum(int(n) - (f["prefix_tokens"][gi] if gi >= 0 else 0)
+                  for n, gi in zip(lens, f["seq_group"])))
+    compulsory = (shared + own) * row + extra
+    logical = int(sum(int(n) for n in lens)) * row + extra
+    achieved = compulsory / (avg_ms * 1e-3) / 1e9
+    result = {
+        "metric": "mixed-batch decode tokens/sec and compulsory HBM GB/s at Qwen3-0.6B shape, "
+                  "1 GPU",
+        "value": b * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": elapsed * 1e3 / args.steps,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1) prefix/suffix K/V and q, block-manager page placement",
+        "config": {"workload": desc, "batch": b, "layers": layers, "groups": groups,
+                   "mean_keys": float(np.mean(lens)), "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "kernel": ("decode_prefix_kernel (groups) + decode_kernel grouped cascade "
+                                "step (rlse_decode_step_groups)" if cascade else
+                                "decode_kernel planned fused step (rlse_decode_step_planned, "
+                                "cacheable pages)"),
+                     "bytes_per_launch": compulsory, "logical_bytes_per_launch": logical,
+                     "effective_GBps": logical / (avg_ms * 1e-3) / 1e9,
+                     "avg_launch_ms": avg_ms, "timed_launches": args.steps * layers},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args, lens, hq, hkv, d, layers)
+    print(json.dumps(result))
+    pool.close()
 
 
 def fork_bench(args):
@@ -765,6 +961,9 @@ def main():
         return
     if args.workload in FORK:
         fork_bench(args)
+        return
+    if args.workload in MIXED:
+        mixed_bench(args)
         return
     if args.workload in E2E:
         e2e_bench(args)

@@ -250,3 +250,76 @@ def test_decode_model_step_at_model_shape_matches_oracle(kv, factory):
         np.testing.assert_array_equal(g, O.argmax_ref(got))
         ids = g.astype(np.int32)     # teacher-forced into the oracle too
     model.close()
+
+
+def test_grouped_cascade_mixed_bench_inputs_match_oracle(kv):
+    """The mixed-batch bench's inputs (bench.py mixed_inputs, one layer):
+    sequences forked from 1024-, 512- and 2048-token prefixes and unforked
+    ones, scattered through the batch, in one grouped cascade step
+    (rlse_decode_step_groups, streamed): rows of every group and unforked
+    rows against the oracle over their full key range, outputs against the
+    planned step's, the pool bytes equal to its."""
+    workload = "qwen3_mixed"
+    hq, hkv, d, _, groups, _, _, _, _, _, _ = bench.MIXED[workload]
+    f = bench.mixed_inputs(workload, BENCH_SEED, DEV, layers=1)
+    lens, tables, mbps, nb = f["lens"], f["tables"], f["mbps"], f["num_blocks"]
+    sg, gp = f["seq_group"], f["group_pages"]
+    b = len(lens)
+    for g in range(len(groups)):   # members share their group's pages
+        rows = np.flatnonzero(sg == g)
+        assert (tables[rows, :gp[g]] == tables[rows[0], :gp[g]]).all()
+    print(f"mixed: B={b}, groups {groups}, keys {int(lens.min())}..{int(lens.max())}", flush=True)
+    k_ptr, v_ptr = f["pool"].layer(0)
+    c_h = np.frombuffer(f["cos_bytes"], np.uint16).reshape(f["max_pos"], d // 2)
+    s_h = np.frombuffer(f["sin_bytes"], np.uint16).reshape(f["max_pos"], d // 2)
+    t_dev, l_dev = f["tables_dev"], to_dev(lens)
+    scale = 1.0 / math.sqrt(d)
+    ws = torch.zeros(kv.decode_workspace_size(b, hq, hkv, d), dtype=torch.uint8, device=DEV)
+    plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=DEV)
+    pre = torch.zeros(kv.decode_prefix_size(b, hq, d, int(gp.max())), dtype=torch.uint8,
+                      device=DEV)
+    args = (f["q"][0], f["k_new"][0], f["v_new"][0], f["q_norm"], f["k_norm"], 1e-6, f["cos"],
+            f["sin"], f["max_pos"], k_ptr, v_ptr, t_dev, l_dev)
+    outs, seqs = {}, {}
+    for name in ("grouped", "planned"):
+        out = torch.full((b, hq, d), 3.0, dtype=BF, device=DEV)
+        if name == "grouped":
+            kv.decode_plan_groups(t_dev, l_dev, to_dev(sg), to_dev(gp), len(groups), b, hq, hkv,
+                                  mbps, nb, plan, plan.numel())
+            kv.decode_step_groups(*args, out, b, hq, hkv, d, mbps, nb, scale, "bf16", plan,
+                                  len(groups), int(gp.max()), pre, pre.numel(), ws, ws.numel(),
+                                  stream_pages=True)
+        else:
+            kv.decode_plan(t_dev, l_dev, b, hkv, mbps, nb, plan, plan.numel())
+            kv.decode_step_planned(*args, out, b, hq, hkv, d, mbps, nb, scale, "bf16", plan, ws,
+                                   ws.numel())
+        torch.cuda.synchronize()
+        assert kv.workspace_flags(ws) == 0, name
+        outs[name] = O.bf16_bits_to_f32(_host16(out))
+        seqs[name] = [_gather(kv, k_ptr, v_ptr, t_dev[i], int(lens[i]), hkv, d, nb)
+                      for i in range(b)]
+    for i in range(b):
+        np.testing.assert_array_equal(seqs["grouped"][i][0], seqs["planned"][i][0], err_msg=i)
+        np.testing.assert_array_equal(seqs["grouped"][i][1], seqs["planned"][i][1], err_msg=i)
+    mx, rel = err_report(outs["grouped"], outs["planned"])
+    print(f"mixed grouped vs planned: max_abs={mx:.3e} rel={rel:.3e}")
+    assert mx <= 1e-2
+    qh, qwh = _host16(f["q"][0]), _host16(f["q_norm"])
+    rng = np.random.default_rng(13)
+    rows = []
+    for g in list(range(len(groups))) + [-1]:   # three rows of every group and unforked
+        rows += [int(x) for x in rng.choice(np.flatnonzero(sg == g), 3, replace=False)]
+    worst = 0.0
+    for r in rows:
+        n = int(lens[r])
+        q_ref = O.bf16_bits_to_f32(_q_ref(qh[r], qwh, n - 1, c_h, s_h))
+        k_i, v_i = seqs["grouped"][r]
+        want = O.decode_batch_f32(q_ref[None], O.bf16_bits_to_f32(k_i)[None],
+                                  O.bf16_bits_to_f32(v_i)[None], np.array([n], np.int32), scale)
+        mx, _ = err_report(outs["grouped"][r], want[0])
+        worst = max(worst, mx)
+        assert np.isfinite(outs["grouped"][r]).all()
+        assert mx <= TOL["bf16"], (r, int(sg[r]), mx)
+    print(f"mixed grouped: {len(rows)} rows (3 per group and unforked) x {hq} heads within "
+          f"{worst:.3e} of the oracle (bar {TOL['bf16']})")
+    f["pool"].close()
