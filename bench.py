@@ -1083,9 +1083,50 @@ def main():
                                      "one per decode launch, second pass")},
         "cpu_baseline": None,
     }
+    result["read_ceiling"] = read_ceiling(kv, k_pools, v_pools, t_dev, lens_dev, lens, hkv, d,
+                                          mbps, nb, layers, min(args.steps, 50), stream)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args, lens, hq, hkv, d, layers)
     print(json.dumps(result))
+
+
+def read_ceiling(kv, k_pools, v_pools, t_dev, lens_dev, lens, hkv, d, mbps, nb, layers, steps,
+                 stream):
+    """The time a launch of the decode's shape needs just to read the
+    decode's K/V bytes: rlse_kv_checksum (the same page walk, grid and
+    loads, no other work) over every layer's pool with the same tables and
+    lengths, timed like the decode (one event pair around a step's
+    back-to-back launches). Its sums land in a zero-filled buffer per step
+    (the fill outside the event pair)."""
+    import numpy as np
+    import torch
+    b = len(lens)
+    out = torch.zeros((b, hkv, 2), dtype=torch.int32, device=t_dev.device)
+
+    def step():
+        for layer in range(layers):
+            kv.kv_checksum(k_pools[layer], v_pools[layer], t_dev, lens_dev, b, hkv, d, mbps, nb,
+                           "bf16", out, stream)
+
+    for _ in range(3):
+        step()
+    spans = []
+    for _ in range(steps):
+        out.zero_()
+        a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        step()
+        z.record(stream)
+        spans.append((a, z))
+    torch.cuda.synchronize()
+    avg_ms = float(np.mean([a.elapsed_time(z) for a, z in spans])) / layers
+    kv_bytes = sum(int(n) * 2 * hkv * d * 2 for n in lens)
+    read = kv_bytes + sum(((int(n) + 15) // 16) * 4 for n in lens) + 4 * b
+    achieved = read / (avg_ms * 1e-3) / 1e9
+    return {"kernel": "checksum_kernel (rlse_kv_checksum: the decode's page walk, grid and "
+                      "loads, nothing else)",
+            "bytes_per_launch": read, "avg_launch_ms": avg_ms, "achieved": achieved,
+            "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "timed_launches": steps * layers}
 
 
 if __name__ == "__main__":

@@ -124,6 +124,24 @@ int rlse_kv_append(const void* k_new, const void* v_new, void* k_pool, void* v_p
                    int head_dim, int max_blocks_per_seq, int num_blocks, int dtype,
                    rlse_stream_t stream);
 
+/* Checksums of the pool's rows: for every (sequence, KV head) row of the
+ * block tables, the sum mod 2^32 over its attended positions t < seq_lens[b]
+ * and the 32-bit words j of a position's head_dim elements of
+ *     (w ^ (t * 0x9E3779B1 + j * 0x85EBCA77)) * 0xC2B2AE3D,
+ * K then V: ADDED into out [batch][num_kv_heads][2] (zero-fill it first; a
+ * caller may accumulate several layers). Pages whose id lies outside
+ * [0, num_blocks) contribute nothing; a length beyond the table's capacity
+ * counts as 0. No counterpart in the reference, whose tests compare snapshot
+ * buffers byte for byte on the host (src/backends/candle.rs:1281-1292): the
+ * sums compare a pool with its expected contents without copying it back.
+ * The launch walks the pages as the paged decode does and does nothing else,
+ * so its duration is the time a decode launch of that shape needs to read
+ * its K/V bytes. */
+int rlse_kv_checksum(const void* k_pool, const void* v_pool, const int32_t* block_tables,
+                     const int32_t* seq_lens, int batch, int num_kv_heads, int head_dim,
+                     int max_blocks_per_seq, int num_blocks, int dtype, uint32_t* out,
+                     rlse_stream_t stream);
+
 /* Snapshot export: pool pages -> contiguous [num_layers][Hkv][len][head_dim]
  * K and V, the layout of Attention::get_kv_snapshot views and of the
  * cumulative prefix snapshots (src/backends/qwen2.rs:363-371;

@@ -153,6 +153,53 @@ def paged_to_contiguous(pool: np.ndarray, table: np.ndarray, length: int) -> np.
     return out
 
 
+# Checksums of the pool's rows (rlse_kv_checksum): the definition itself,
+# in numpy uint32 arithmetic (every product and sum wraps mod 2^32).
+_MIX_T, _MIX_J, _MIX_M = np.uint32(0x9E3779B1), np.uint32(0x85EBCA77), np.uint32(0xC2B2AE3D)
+
+
+def mix_words(w: np.ndarray, t: np.ndarray, j: np.ndarray) -> np.ndarray:
+    """(w ^ (t * 0x9E3779B1 + j * 0x85EBCA77)) * 0xC2B2AE3D mod 2^32, with
+    t and j broadcast against w."""
+    with np.errstate(over="ignore"):
+        key = (np.asarray(t, np.uint32) * _MIX_T + np.asarray(j, np.uint32) * _MIX_J)
+        return (np.asarray(w, np.uint32) ^ key) * _MIX_M
+
+
+def kv_checksum_ref(k_pool: np.ndarray, v_pool: np.ndarray, tables: np.ndarray,
+                    lens: np.ndarray) -> np.ndarray:
+    """Per (sequence, KV head) row: the sums mod 2^32, over the attended
+    positions t < L (L = 0 for L <= 0 or beyond the table's capacity) and the
+    32-bit words j of a position's head_dim elements, of mix_words(w, t, j)
+    -- K then V, [B][Hkv][2] uint32. Pages whose id lies outside the pool
+    contribute nothing. Pools are [num_blocks][Hkv][16][head_dim] arrays of
+    the dtype's bits (uint16 for bf16, float16, float32)."""
+    nb, hkv = k_pool.shape[:2]
+    kw = np.ascontiguousarray(k_pool).view(np.uint32).reshape(nb, hkv, 16, -1)
+    vw = np.ascontiguousarray(v_pool).view(np.uint32).reshape(nb, hkv, 16, -1)
+    nw = kw.shape[-1]
+    tables = np.asarray(tables, np.int32)
+    b_sz, mbps = tables.shape
+    out = np.zeros((b_sz, hkv, 2), np.uint32)
+    j = np.arange(nw, dtype=np.uint32)[None, None, :]
+    for b in range(b_sz):
+        n = int(lens[b])
+        if n <= 0 or n > 16 * mbps:
+            continue
+        npg = (n + 15) // 16
+        ids = tables[b, :npg]
+        ok = (ids >= 0) & (ids < nb)
+        t = np.arange(npg * 16, dtype=np.uint32)
+        keep = (t < n) & np.repeat(ok, 16)
+        for c, words in ((0, kw), (1, vw)):
+            rows = words[np.where(ok, ids, 0)]                      # [npg, Hkv, 16, nw]
+            rows = rows.transpose(1, 0, 2, 3).reshape(hkv, npg * 16, nw)
+            m = mix_words(rows, t[None, :, None], j)
+            m = np.where(keep[None, :, None], m, np.uint32(0))
+            out[b, :, c] = (m.sum(axis=(1, 2), dtype=np.uint64) & 0xFFFFFFFF).astype(np.uint32)
+    return out
+
+
 def decode_batch_f32(q: np.ndarray, k: np.ndarray, v: np.ndarray, lens: np.ndarray,
                      scale: float, threads: int = 0) -> np.ndarray:
     """q [B, Hq, d]; k, v [B, Hkv, cap, d] f32; returns [B, Hq, d] f32."""

@@ -350,3 +350,86 @@ def test_golden_norm_rope_vectors():
     # reference tables are f32 too), so the bound grows with the position.
     bound = 2.0 * float(g["pos"].max()) * 2.0 ** -24 * float(np.abs(g["x"]).max()) + 1e-5
     np.testing.assert_allclose(y, g["rope_f64"], rtol=0, atol=bound)
+
+
+# ------------------------------------------------------------ checksums ----
+def _mix_py(w, t, j):
+    m = 0xFFFFFFFF
+    return ((w ^ ((t * 0x9E3779B1 + j * 0x85EBCA77) & m)) * 0xC2B2AE3D) & m
+
+
+def test_mix_words_wraps_like_integer_arithmetic():
+    """mix_words in numpy uint32 equals the definition in Python integers
+    reduced mod 2^32, extreme operands included."""
+    rng = np.random.default_rng(3)
+    w = np.concatenate([rng.integers(0, 2**32, 500, dtype=np.uint64),
+                        np.array([0, 1, 2**31, 2**32 - 1], np.uint64)]).astype(np.uint32)
+    t = rng.integers(0, 2**31, w.size).astype(np.uint32)
+    j = rng.integers(0, 64, w.size).astype(np.uint32)
+    got = O.mix_words(w, t, j)
+    want = np.array([_mix_py(int(a), int(b), int(c)) for a, b, c in zip(w, t, j)], np.uint64)
+    np.testing.assert_array_equal(got.astype(np.uint64), want)
+
+
+def _checksum_brute(kp, vp, tables, lens):
+    nb, hkv = kp.shape[:2]
+    kw = kp.view(np.uint32).reshape(nb, hkv, 16, -1)
+    vw = vp.view(np.uint32).reshape(nb, hkv, 16, -1)
+    out = np.zeros((len(lens), hkv, 2), np.uint64)
+    for b, n in enumerate(lens):
+        if n <= 0 or n > 16 * tables.shape[1]:
+            continue
+        for t in range(n):
+            pid = int(tables[b, t // 16])
+            if not 0 <= pid < nb:
+                continue
+            for h in range(hkv):
+                for j in range(kw.shape[-1]):
+                    out[b, h, 0] += _mix_py(int(kw[pid, h, t % 16, j]), t, j)
+                    out[b, h, 1] += _mix_py(int(vw[pid, h, t % 16, j]), t, j)
+    return (out & 0xFFFFFFFF).astype(np.uint32)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_kv_checksum_ref_matches_brute_force(dt):
+    """kv_checksum_ref against a position-by-position loop: ragged lengths,
+    a page id outside the pool (skipped), an empty row and a row longer than
+    its table (both 0)."""
+    rng = np.random.default_rng(5)
+    nb, hkv, d, mbps = 9, 2, 8, 3
+    shape = (nb, hkv, 16, d)
+    if dt == "f32":
+        kp, vp = (rng.standard_normal(shape).astype(np.float32) for _ in range(2))
+    else:
+        kp, vp = (O.f32_to_bf16_bits(rng.standard_normal(shape)) for _ in range(2))
+    tables = np.array([[3, 7, 1], [0, 12, 5], [2, 4, 6], [8, 8, 8]], np.int32)  # 12: not a page
+    lens = np.array([37, 40, 0, 49], np.int32)                                # 49 > 3 * 16
+    got = O.kv_checksum_ref(kp, vp, tables, lens)
+    np.testing.assert_array_equal(got, _checksum_brute(kp, vp, tables, lens))
+    assert (got[2] == 0).all() and (got[3] == 0).all()
+
+
+def test_kv_checksum_ref_sees_attended_bytes_only():
+    """A flipped bit of an attended element changes its row's sum and no
+    other; a flipped bit past the row's length changes nothing; swapping two
+    attended positions' rows changes the sum (the position enters the mix)."""
+    rng = np.random.default_rng(6)
+    nb, hkv, d = 6, 2, 8
+    kp = O.f32_to_bf16_bits(rng.standard_normal((nb, hkv, 16, d)))
+    vp = O.f32_to_bf16_bits(rng.standard_normal((nb, hkv, 16, d)))
+    tables = np.array([[0, 1], [2, 3]], np.int32)
+    lens = np.array([20, 30], np.int32)
+    base = O.kv_checksum_ref(kp, vp, tables, lens)
+    k2 = kp.copy()
+    k2[1, 1, 2, 5] ^= np.uint16(1 << 3)                 # seq 0, head 1, position 18
+    s2 = O.kv_checksum_ref(k2, vp, tables, lens)
+    assert s2[0, 1, 0] != base[0, 1, 0]
+    s2[0, 1, 0] = base[0, 1, 0]
+    np.testing.assert_array_equal(s2, base)
+    v3 = vp.copy()
+    v3[1, 0, 10, 0] ^= np.uint16(1)                      # seq 0 position 26 >= 20
+    np.testing.assert_array_equal(O.kv_checksum_ref(kp, v3, tables, lens), base)
+    k4 = kp.copy()
+    k4[2, 0, [3, 4]] = k4[2, 0, [4, 3]]                  # seq 1, head 0, positions 3 and 4
+    if not np.array_equal(kp[2, 0, 3], kp[2, 0, 4]):
+        assert O.kv_checksum_ref(k4, vp, tables, lens)[1, 0, 0] != base[1, 0, 0]
