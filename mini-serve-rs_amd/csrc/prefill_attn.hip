@@ -50,10 +50,17 @@ constexpr int kPWaves = 8;
 constexpr int kPThreads = 64 * kPWaves;
 constexpr int kBM = 32 * kPWaves;  // rows per workgroup
 constexpr int kBN = 64;            // keys per tile
-// LDS row padding (elements): K rows are read as 16-byte packets, V rows by
-// transposing 8-byte reads; these paddings keep both free of bank conflicts.
+// LDS row padding (elements), for the 64 four-byte banks of the gfx950
+// LDS. K rows are read as 16-byte packets, 16 lanes (16 rows, one column)
+// per cycle: a row stride of 68 words puts the rows 4 banks apart. V rows
+// are read by transposing 8-byte reads, 32 lanes per cycle: 4 rows (keys)
+// times two 16-column blocks of 8 words each; a row stride of 80 words
+// (D = 128) or 48 (D = 64) puts the 4 rows 16 banks apart, so both column
+// blocks of every row have banks of their own. (A stride of 72 words, a
+// padding of 16, put row j's first block on row j-1's second: 2 conflict
+// cycles per read.)
 constexpr int kPadK = 8;
-constexpr int kPadV = 16;
+constexpr int kPadV = 32;
 constexpr int kMinKeysPerSplit = 512;
 constexpr int kMaxSplits = 16;
 constexpr int kMaxSplitPages = 1024;  // page ids of a split staged in LDS (16384 keys)
@@ -377,10 +384,13 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(PrefillParams p) 
 //   O^T += V^T . P^T: step j pairs the keys the two lane halves hold in
 //   accumulator element j (8*(j/4) + 4h + j%4), so the B operand is the
 //   lane's own probability and the A operand one float of V's key row.
-// K and V rows are staged in LDS as they are (f32), padded by 4 floats so the
-// 16-byte K reads and the V reads of 32 consecutive columns are free of bank
-// conflicts.
+// K and V rows are staged in LDS as they are (f32). K rows are read as
+// 16-byte packets, 16 rows per cycle: a stride of D + 4 words puts them 4
+// banks apart. A V read takes 32 consecutive columns of one row in each lane
+// half, the halves four rows apart: a stride of D + 8 words puts those rows
+// 32 banks apart.
 constexpr int kPadF = 4;
+constexpr int kPadFV = 8;
 template <int D>
 __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel_f32(PrefillParams p) {
   constexpr int DB = D / 32;                  // 32-row blocks of O^T
@@ -390,7 +400,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel_f32(PrefillParams
   constexpr int KPT = KPK / kPThreads;        // per thread
   static_assert(KPK % kPThreads == 0, "K tile must split evenly");
   __shared__ __align__(16) float s_k[2][kBN][D + kPadF];  // K rows
-  __shared__ __align__(16) float s_v[2][kBN][D + kPadF];  // V rows
+  __shared__ __align__(16) float s_v[2][kBN][D + kPadFV];  // V rows
   __shared__ int s_valid[2];                               // page-valid bits of the tile
   __shared__ __align__(16) int s_pages[kMaxSplitPages];    // the split's page ids (-1: invalid)
 
