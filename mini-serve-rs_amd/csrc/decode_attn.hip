@@ -84,10 +84,14 @@ __global__ __launch_bounds__(1024) void group_plan_kernel(const int* __restrict_
                                                           int B, int NG, int G, int mbps,
                                                           int* __restrict__ tail) {
   __shared__ int s_cnt[kMaxPrefixGroups], s_pages[kMaxPrefixGroups], s_next[kMaxPrefixGroups];
+  __shared__ int s_first[kMaxPrefixGroups], s_off[kMaxPrefixGroups + 1];
+  __shared__ int s_tiles[kMaxPrefixGroups + 1], s_items[kMaxPrefixGroups + 1];
   __shared__ int s_err;
   int* seq_pre = tail + kPlanStampWords;
   int* members = seq_pre + kMaxDecodeBatch;
   int* grp = members + kMaxDecodeBatch;
+  int4* items = reinterpret_cast<int4*>(grp + kGrpWords);
+  int* item_rep = reinterpret_cast<int*>(items + kMaxGroupItems);
   const int tid = threadIdx.x, lane = tid & 63;
   if (tid == 0) s_err = 0;
   if (tid < NG) {
@@ -95,6 +99,7 @@ __global__ __launch_bounds__(1024) void group_plan_kernel(const int* __restrict_
     const bool ok = pg >= 1 && pg <= mbps && pg <= kMaxPrefixPages;
     s_pages[tid] = ok ? pg : 0;
     s_cnt[tid] = 0;
+    s_first[tid] = B;
   }
   __syncthreads();
   if (tid < NG && s_pages[tid] == 0) atomicOr(&s_err, 1);
@@ -107,25 +112,43 @@ __global__ __launch_bounds__(1024) void group_plan_kernel(const int* __restrict_
     const int g = seq_group[b];
     if (g < -1 || g >= NG) atomicOr(&s_err, 2);
     const int gg = group_of_seq(b);
-    if (gg >= 0) atomicAdd(&s_cnt[gg], 1);
+    if (gg >= 0) {
+      atomicAdd(&s_cnt[gg], 1);
+      atomicMin(&s_first[gg], b);
+    }
     seq_pre[b] = gg >= 0 ? s_pages[gg] : 0;
   }
   __syncthreads();
   if (tid == 0) {
-    int off = 0, tiles = 0;
+    int off = 0, tiles = 0, nitems = 0;
     for (int g = 0; g < NG; ++g) {
       grp[kGrpOff + g] = off;
       grp[kGrpTiles + g] = tiles;
       grp[kGrpPages + g] = s_pages[g];
-      s_next[g] = off;
+      s_next[g] = s_off[g] = off;
+      s_tiles[g] = tiles;
+      s_items[g] = nitems;
+      const int nt = (s_cnt[g] * G + 15) / 16;
       off += s_cnt[g];
-      tiles += (s_cnt[g] * G + 15) / 16;
+      tiles += nt;
+      nitems += nt * (s_cnt[g] > 0 ? prefix_splits(s_pages[g]) : 0);
     }
-    grp[kGrpOff + NG] = off;
-    grp[kGrpTiles + NG] = tiles;
+    grp[kGrpOff + NG] = s_off[NG] = off;
+    grp[kGrpTiles + NG] = s_tiles[NG] = tiles;
+    s_items[NG] = nitems;
     grp[kGrpErr] = s_err;
+    grp[kGrpItems] = nitems;
   }
   __syncthreads();
+  // The prefix launch's work items, slice-major within each group.
+  for (int j = tid; j < s_items[NG]; j += 1024) {
+    int g = 0;
+    for (int k = 1; k < NG; ++k) g = s_items[k] <= j ? k : g;  // the last group starting at or before j
+    const int nt = s_tiles[g + 1] - s_tiles[g], r = j - s_items[g];
+    const int sp = r / nt, t = r - sp * nt;
+    items[j] = make_int4(s_pages[g], t * 16, s_off[g], s_cnt[g]);
+    item_rep[j] = s_first[g] | (sp << 16);
+  }
   // Members in batch order within each group: wave 0 walks the batch 64
   // sequences at a time; the lanes of one group take consecutive slots.
   if (tid < 64) {
@@ -373,7 +396,7 @@ static int decode_plan_impl(const int32_t* block_tables, const int32_t* seq_lens
     st = launch_status("group_plan_kernel");
     if (st) return st;
     seq_pre = tail + kPlanStampWords;
-    stamp = plan_stamp(2, num_groups);
+    stamp = group_stamp(num_groups, group_size);
   }
   const size_t lds = (size_t)(batch + 1) * sizeof(int);
   hipLaunchKernelGGL(decode_plan_kernel, dim3(W), dim3(kThreads), lds, as_stream(stream),
@@ -407,8 +430,9 @@ extern "C" int rlse_decode_plan_groups(const int32_t* block_tables, const int32_
                 num_groups, kMaxPrefixGroups);
   if (!seq_group || !group_pages)
     return fail(RLSE_ERR_INVALID_VALUE, "decode_plan_groups: null pointer argument");
-  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
-    return fail(RLSE_ERR_INVALID_VALUE, "decode_plan_groups: bad head counts");
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+      num_heads / num_kv_heads > 8)
+    return fail(RLSE_ERR_INVALID_VALUE, "decode_plan_groups: bad head counts (group size <= 8)");
   return decode_plan_impl(block_tables, seq_lens, batch, num_kv_heads, max_blocks_per_seq,
                           num_blocks, 0, plan, plan_bytes, stream, seq_group, group_pages,
                           num_groups, num_heads / num_kv_heads);
@@ -466,7 +490,7 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
   p.plan = reinterpret_cast<const int4*>(plan);
   const int G = num_heads / num_kv_heads;
   const hipStream_t s = as_stream(stream);
-  p.plan_stamp = num_groups > 0 ? plan_stamp(2, num_groups) : plan_stamp(1, prefix);
+  p.plan_stamp = num_groups > 0 ? group_stamp(num_groups, G) : plan_stamp(1, prefix);
   const int* tail = plan ? plan_tail(p.plan, p.W) : nullptr;
   if (num_groups > 0) {
     // Prefix groups: every sequence's shared pages come from the plan, and

@@ -292,9 +292,10 @@ struct PrefixParams {
   float* pre;        // prefix_splits(prefix) x [B][Hq][prefix_row_floats(D)] floats
   uint32_t* ws_err;  // sticky flags: RLSE_WS_ERR_PREFIX
   // Prefix groups (null members: one group, every sequence, `prefix`
-  // pages): the grouped sequences, group by group, and GroupPlan's offsets
-  // and pages (group_plan_kernel); num_groups groups, `prefix` then bounds
-  // every group's pages and tiles the launch's column tiles.
+  // pages): the grouped sequences, group by group, then the grouped plan's
+  // offsets, pages and column tiles (group_plan_kernel); num_groups groups,
+  // `prefix` then bounds every group's pages and tiles the launch's column
+  // tiles.
   const int* members;
   const int* grp;
   int num_groups;
@@ -306,12 +307,27 @@ constexpr int kMaxPrefixGroups = 64;
 // seq_pre[kMaxDecodeBatch] (shared pages per sequence), members
 // [kMaxDecodeBatch] (grouped sequences, group by group, in batch order within
 // a group), then grp: member offsets [kMaxPrefixGroups + 1], column-tile
-// offsets [kMaxPrefixGroups + 1], pages [kMaxPrefixGroups], and one word of
-// error bits (a group id or a page count out of range).
+// offsets [kMaxPrefixGroups + 1], pages [kMaxPrefixGroups], one word of error
+// bits (a group id or a page count out of range) and the number of work
+// items, padded to 16 bytes; then the work items of the prefix launch. An
+// item is one (column tile, prefix slice) of a group -- G columns per member,
+// 16 per tile, prefix_splits(pages) slices -- in group order, slice-major
+// within a group: {pages, the tile's first column within its group, the
+// group's member offset, its member count} and, after all of those, the
+// group's first member (whose table rows hold the pages) | slice << 16. A
+// prefix workgroup reads its item's two entries, the count and the stamp in
+// one round of loads, and no other word of the plan before it requests page
+// ids.
 constexpr int kGrpOff = 0, kGrpTiles = kMaxPrefixGroups + 1, kGrpPages = 2 * kGrpTiles,
-              kGrpErr = kGrpPages + kMaxPrefixGroups, kGrpWords = kGrpErr + 1;
+              kGrpErr = kGrpPages + kMaxPrefixGroups, kGrpItems = kGrpErr + 1,
+              kGrpWords = (kGrpItems + 1 + 3) & ~3;
+// Column tiles a grouped prefix launch may have (every member's G <= 8
+// columns, one part tile per group), and its work items (at most 8 slices a
+// tile).
+constexpr int kMaxGroupTiles = kMaxDecodeBatch * 8 / 16 + kMaxPrefixGroups;
+constexpr int kMaxGroupItems = 8 * kMaxGroupTiles;
 __host__ __device__ constexpr size_t group_plan_words() {
-  return 2 * (size_t)kMaxDecodeBatch + kGrpWords;
+  return 2 * (size_t)kMaxDecodeBatch + kGrpWords + 5 * (size_t)kMaxGroupItems;
 }
 // A plan buffer: the descriptors of the first 64 blocks of every wave
 // (int4), the new-token positions of the 64 rows from each wave's first row
@@ -326,8 +342,12 @@ __host__ __device__ constexpr size_t plan_bytes(int W) {
          (kPlanStampWords + group_plan_words()) * sizeof(int);
 }
 // The stamp of a plan: mode 1 with the shared prefix's pages (0 for a
-// plain plan), mode 2 with the number of prefix groups.
+// plain plan), mode 2 with the number of prefix groups and the query heads
+// per KV head (the grouped plan's column tiles depend on both).
 __host__ __device__ constexpr int plan_stamp(int mode, int value) { return (mode << 24) | value; }
+__host__ __device__ constexpr int group_stamp(int num_groups, int G) {
+  return plan_stamp(2, num_groups | (G << 8));
+}
 // Longest shared prefix a cascade step takes, in pages (8192 tokens).
 constexpr int kMaxPrefixPages = 512;
 // Slices of the prefix attended by separate workgroups (each leaves its own

@@ -54,46 +54,68 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
   const int mh = lane & 15, mq = lane >> 4;
   const int B = p.B, Hkv = p.Hkv, Hq = Hkv * G;
   const bool grouped = p.members != nullptr;
-  // Workgroup id -> (slice set ps = h * NS + sp, column tile c): the tiles of
-  // one slice set share id % 8, i.e. one XCD (workgroups are dealt to the
-  // XCDs round-robin); ids past the last slice set have no work. With prefix
-  // groups NS and NC are bounds (p.prefix bounds every group's pages, p.tiles
-  // its column tiles) and a workgroup first finds its group: tile c belongs
-  // to group grp, its columns to the group's members, its pages to the
-  // group's first member's table.
+  // Workgroup id -> (KV head h, prefix slice sp, column tile c). One prefix:
+  // slice set ps = sp * Hkv + h and tile c, where the tiles of one slice set
+  // share id % 8, i.e. one XCD (workgroups are dealt to the XCDs
+  // round-robin), and heads run fastest in ps, so that with Hkv a multiple
+  // of 8 an XCD takes every slice of its heads; ids past the last slice set
+  // have no work. Prefix groups: id = j * Hkv + h, where item j of the plan
+  // names the group's tile and slice. The items are dense, so the ids with
+  // work come first and are dispatched first, one workgroup a CU while they
+  // last; the launch is sized by bounds (p.prefix bounds every group's
+  // pages, p.tiles its column tiles) and the ids past the plan's items have
+  // no work.
   const int NS = prefix_splits(p.prefix), NC = grouped ? p.tiles : (B * G + 15) / 16;
-  const int id = blockIdx.x, xq = id >> 3;
-  const int ps = (xq / NC) * 8 + (id & 7), c = xq % NC;
+  const int id = blockIdx.x;
+  int h, sp, ps = 0, c = 0;
+  int P = p.prefix, ncols = B * G, c0 = 0, first = 0;
+  const int* __restrict__ mem = nullptr;  // grouped: the group's members
   if (grouped) {
-    // The groups come from the plan: one built for another step shape (no
-    // member lists, or another group count) is not read; the error is
-    // flagged and the decode launch that follows does nothing either.
-    const int* stamp = p.members - kMaxDecodeBatch - kPlanStampWords;
-    if (__builtin_amdgcn_readfirstlane(stamp[0]) != plan_stamp(2, p.num_groups)) {
+    // One round of loads: the item's entries, the plan's item count, stamp
+    // and error word (and, in workgroup 0, every group's pages). A plan built
+    // for another step shape (no items, another group count or group size)
+    // is not used: the error is flagged and the decode launch that follows
+    // does nothing either. Every entry is clamped into the batch, so no plan
+    // makes an access leave its buffers.
+    const int j = id / Hkv;
+    h = id - j * Hkv;
+    if (j >= kMaxGroupItems) return;
+    const int* tail = p.members - kMaxDecodeBatch - kPlanStampWords;
+    const int4* items = reinterpret_cast<const int4*>(p.grp + kGrpWords);
+    const int4 te = items[j];
+    const int rep = reinterpret_cast<const int*>(items + kMaxGroupItems)[j];
+    const int stamp = tail[0], err = p.grp[kGrpErr], nitems = p.grp[kGrpItems];
+    const int gpages = id == 0 && lane < p.num_groups ? p.grp[kGrpPages + lane] : 0;
+    if (__builtin_amdgcn_readfirstlane(stamp) != group_stamp(p.num_groups, G)) {
       if (id == 0 && tid == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
       return;
     }
-    if (id == 0 && tid == 0 && p.grp[kGrpErr] != 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
-  }
-  if (ps >= Hkv * NS) return;
-  const int h = ps / NS, sp = ps - h * NS;
-  int P = p.prefix, ncols = B * G, c0 = c * 16, moff = 0;
-  const int* __restrict__ mem = nullptr;  // grouped: the group's members
-  if (grouped) {
-    if (c >= p.grp[kGrpTiles + p.num_groups]) return;
-    // the group holding tile c: the last g with tiles[g] <= c (lane g reads tiles[g])
-    const int tg = lane < p.num_groups ? p.grp[kGrpTiles + lane] : 0x7fffffff;
-    const int g = 63 - __builtin_clzll(__ballot(tg <= c));
-    P = p.grp[kGrpPages + g];
-    if (P > p.prefix) {  // above the bound that sized the launch and the buffer
-      if (tid == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
-      return;
+    if (id == 0 && wave == 0) {
+      // a group above the bound that sized the launch and the buffer, or
+      // the plan's own error bits
+      if (__any(gpages > p.prefix) && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
+      if (err != 0 && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
     }
-    if (P <= 0 || sp >= prefix_splits(P)) return;
-    moff = p.grp[kGrpOff + g];
-    ncols = (p.grp[kGrpOff + g + 1] - moff) * G;
-    c0 = (c - p.grp[kGrpTiles + g]) * 16;
+    if (j >= __builtin_amdgcn_readfirstlane(nitems)) return;
+    P = __builtin_amdgcn_readfirstlane(te.x);
+    const int r = __builtin_amdgcn_readfirstlane(rep);
+    sp = r >> 16;
+    if (P <= 0 || P > p.prefix || sp >= prefix_splits(P)) return;
+    const int moff = min(max(__builtin_amdgcn_readfirstlane(te.z), 0), B);
+    const int n_g = min(__builtin_amdgcn_readfirstlane(te.w), B - moff);
+    c0 = __builtin_amdgcn_readfirstlane(te.y);
+    if (n_g <= 0 || c0 < 0 || c0 >= n_g * G) return;
+    ncols = n_g * G;
+    first = min(max(r & 0xffff, 0), B - 1);
     mem = p.members + moff;
+  } else {
+    const int xq = id >> 3;
+    ps = (xq / NC) * 8 + (id & 7);
+    c = xq % NC;
+    if (ps >= Hkv * NS) return;
+    sp = ps / Hkv;
+    h = ps - sp * Hkv;
+    c0 = c * 16;
   }
   const int NSg = prefix_splits(P);
   // Sequence of column j (one per query head of the sequence); member
@@ -102,7 +124,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     const int b = mem ? mem[j / G] : j / G;
     return b < 0 ? 0 : (b < B ? b : B - 1);
   };
-  const int* __restrict__ ptab = p.tables + (size_t)seq_of(0) * p.mbps;  // the group's pages
+  const int* __restrict__ ptab = p.tables + (size_t)first * p.mbps;  // the group's pages
   const T* __restrict__ qb = reinterpret_cast<const T*>(p.q);
   const T* __restrict__ kp = reinterpret_cast<const T*>(p.k_pool);
   const T* __restrict__ vp = reinterpret_cast<const T*>(p.v_pool);
@@ -117,24 +139,35 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
   // Lane i holds the page id of block lo + i (a wave takes at most 64).
   const int ids = lo + lane < hi ? ptab[lo + lane] : 0;
   // Wave 1 of each workgroup checks a share of the batch against the
-  // contract: every sequence's first P table entries are sequence 0's, and
-  // its new token (position L - 1) lies past them. The first sequence's
-  // entries are requested here, ahead of the page loads, and compared once
-  // those are issued (further sequences, when the batch outnumbers the
-  // workgroups, are read at the end). With prefix groups the workgroups of
-  // slice set 0 check the members of their column tile against the group's
-  // first member, at the end.
+  // contract: every sequence's first P table entries are the group's first
+  // sequence's (sequence 0's without groups), and its new token (position
+  // L - 1) lies past them. The share is every nwork-th of slots [k0, kend):
+  // sequences, or with prefix groups the group's members whose columns fall
+  // in this tile, dealt over the tile's workgroups. The first slot's entries
+  // are requested here, ahead of the page loads, and compared once those are
+  // issued; further slots, when there are more than workgroups, are read at
+  // the end.
   constexpr int kChk = kMaxPrefixPages / 64;
-  const int nwork = Hkv * NS * NC, bchk = grouped ? B : ps * NC + c;
+  int k0, kend, nwork;
+  if (grouped) {
+    k0 = c0 / G + h * NSg + sp;
+    kend = min((c0 + 15) / G + 1, ncols / G);
+    nwork = Hkv * NSg;
+  } else {
+    k0 = ps * NC + c;
+    kend = B;
+    nwork = Hkv * NS * NC;
+  }
   int chk_len = 0, chk_t[kChk], chk_0[kChk];
   bool bad = false;
-  if (wave == 1 && bchk < B) {
-    chk_len = p.seq_lens[bchk];
+  if (wave == 1 && k0 < kend) {
+    const int b = seq_of(k0 * G);
+    chk_len = p.seq_lens[b];
 #pragma unroll
     for (int k = 0; k < kChk; ++k) {
       const int i = lane + 64 * k;
-      chk_t[k] = i < P ? p.tables[(size_t)bchk * p.mbps + i] : 0;
-      chk_0[k] = i < P ? p.tables[i] : 0;
+      chk_t[k] = i < P ? p.tables[(size_t)b * p.mbps + i] : 0;
+      chk_0[k] = i < P ? ptab[i] : 0;
     }
   }
 
@@ -204,7 +237,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     load(b0, lo);
     load(b1, lo + 1);
     load(b2, lo + 2);
-    if (wave == 1 && bchk < B) {
+    if (wave == 1 && k0 < kend) {
       bad = chk_len <= 16 * P || chk_len > p.mbps * 16;
 #pragma unroll
       for (int k = 0; k < kChk; ++k) bad = bad || chk_t[k] != chk_0[k];
@@ -320,19 +353,9 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     *reinterpret_cast<float4*>(dst + 16 * wave + 4 * mq) = make_float4(a[0], a[1], a[2], a[3]);
     if (wave == 0 && mq == 0) *reinterpret_cast<float2*>(dst + D) = make_float2(M, l);
   }
-  if (wave == 1 && bchk < B) {
-    for (int b = bchk + nwork; b < B; b += nwork) {
-      const int L = p.seq_lens[b];
-      bad = bad || L <= 16 * P || L > p.mbps * 16;
-      for (int i = lane; i < P; i += 64)
-        bad = bad || p.tables[(size_t)b * p.mbps + i] != p.tables[i];
-    }
-    if (__any(bad) && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
-  }
-  if (grouped && wave == 1 && ps == 0) {
-    // the members whose columns fall in this tile, against the group's first
-    for (int m = c0 / G; m * G < c0 + 16 && m * G < ncols; ++m) {
-      const int b = seq_of(m * G);
+  if (wave == 1 && k0 < kend) {
+    for (int k = k0 + nwork; k < kend; k += nwork) {
+      const int b = seq_of(k * G);
       const int L = p.seq_lens[b];
       bad = bad || L <= 16 * P || L > p.mbps * 16;
       for (int i = lane; i < P; i += 64) bad = bad || p.tables[(size_t)b * p.mbps + i] != ptab[i];
@@ -343,10 +366,11 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
 
 template <typename T, int D, int G>
 int launch_prefix_t(const PrefixParams& p, hipStream_t s) {
-  // 8 ids per group of 8 slice sets and column tile (see the kernel).
-  const int nc = p.members ? p.tiles : (p.B * G + 15) / 16;
+  // One prefix: 8 ids per group of 8 slice sets and column tile; prefix
+  // groups: Hkv ids per work item the bounds allow (see the kernel).
   const int nps = p.Hkv * prefix_splits(p.prefix);
-  const unsigned grid = (unsigned)(8 * nc * ((nps + 7) / 8));
+  const unsigned grid = p.members ? (unsigned)(nps * p.tiles)
+                                  : (unsigned)(8 * ((p.B * G + 15) / 16) * ((nps + 7) / 8));
   hipLaunchKernelGGL((decode_prefix_kernel<T, D, G>), dim3(grid), dim3(64 * kPrefixWaves), 0, s, p);
   return launch_status("decode_prefix_kernel");
 }

@@ -301,7 +301,8 @@ def test_grouped_cascade_contract_and_plan_stamp(kv):
     """A member whose shared entries differ from its group's, or a group id
     out of range, raises RLSE_WS_ERR_PREFIX; so does a planned launch given a
     plan built for another step shape (a plain plan for a cascade step, a
-    cascade plan of another prefix). The next correct step is clean."""
+    cascade plan of another prefix, a grouped plan of another group size).
+    The next correct step is clean."""
     hq, hkv, d = 16, 8, 128
     rng = np.random.default_rng(93)
     groups = [(3, 4), (4, 9)]
@@ -357,6 +358,15 @@ def test_grouped_cascade_contract_and_plan_stamp(kv):
     kv.decode_step_planned(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp.clone(), vp.clone(),
                            t_dev, l_dev, out, b, hq, hkv, d, mbps, nb, 1.0 / math.sqrt(d), "bf16",
                            plan, ws, ws.numel())
+    torch.cuda.synchronize()
+    assert kv.workspace_flags(ws) == kv.WS_ERR_PREFIX
+    assert grouped(tables, seq_group) == 0
+    print("plan stamp: grouped plan of group size 1 for a step of group size 2", flush=True)
+    kv.decode_plan_groups(t_dev, l_dev, to_dev(seq_group), gp, 2, b, hkv, hkv, mbps, nb, plan,
+                          plan.numel())
+    kv.decode_step_groups(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp.clone(), vp.clone(),
+                          t_dev, l_dev, out, b, hq, hkv, d, mbps, nb, 1.0 / math.sqrt(d), "bf16",
+                          plan, 2, 9, pre, pre.numel(), ws, ws.numel())
     torch.cuda.synchronize()
     assert kv.workspace_flags(ws) == kv.WS_ERR_PREFIX
     assert grouped(tables, seq_group) == 0
