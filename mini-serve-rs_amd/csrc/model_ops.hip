@@ -383,7 +383,11 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
   constexpr int kRecWords = FT * RT * 256;
   __shared__ float red[kDenseWaves][FT][RT][256];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform (a scalar register): the k-step bounds below derive from
+  // it, and a bound the compiler takes for a per-lane value puts the
+  // unrolled steps' MFMAs under an exec mask instead of a branch -- steps
+  // past the wave's last then fed their stale operands into the sums.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int fi = lane & 15;
   const int g = lane >> 4;
   const int K = p.K;

@@ -217,7 +217,8 @@ DENSE_CTR = 2048   # launch counters of a K-split workspace (512 workgroups x 4 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("rows", ROWS)
-@pytest.mark.parametrize("hidden,nq,nkv,bias", [(1024, 2048, 1024, False), (896, 896, 128, True)])
+@pytest.mark.parametrize("hidden,nq,nkv,bias", [(1024, 2048, 1024, False), (896, 896, 128, True),
+                                               (256, 512, 128, False)])
 def test_qkv_proj_matches_three_linears(kv, dt, rows, hidden, nq, nkv, bias):
     rng = np.random.default_rng(rows * 7 + hidden)
     x = O.round_to(rng.standard_normal((rows, hidden)), dt)
@@ -238,8 +239,11 @@ def test_qkv_proj_matches_three_linears(kv, dt, rows, hidden, nq, nkv, bias):
 @pytest.mark.parametrize("rows", ROWS)
 @pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("n_out,n_in", [(1024, 2048), (1024, 3072), (896, 4864), (64, 160),
-                                        (8192, 128)])
+                                        (8192, 128), (1024, 256), (2048, 256)])
 def test_linear_residual_matches_oracle(kv, dt, rows, split, n_out, n_in):
+    """(1024, 256) and (2048, 256) split K into slices of one 32-wide step
+    per wave (a regression case: the steps past a wave's own once ran under
+    an exec mask and fed stale operands into the sums)."""
     rng = np.random.default_rng(rows + n_in)
     x = O.round_to(rng.standard_normal((rows, n_in)), dt)
     w = O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt)
