@@ -466,7 +466,6 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
 #pragma unroll
     for (int j = 0; j < U; ++j) {
       if (s + j < s_end) {
-        const int off = 32 * (s + j);
 #pragma unroll
         for (int f = 0; f < FT; ++f)
           a[j][f] = *reinterpret_cast<const u32x4_t*>(wr[f] + (size_t)wstep * (s + j));
@@ -1033,7 +1032,6 @@ extern "C" int rlse_qkv_proj(const void* x, const void* w_qkv, const void* b_qkv
                              rlse_stream_t stream) {
   DenseParams flags{};
   take_packed(dtype, flags);
-  const bool packed = flags.packed || flags.xpacked;
   const void* outs[3] = {q, k, v};
   int rc = check_dense("qkv_proj", dtype, rows, hidden, x, w_qkv, outs, 3);
   if (rc || rows == 0) return rc;
@@ -1070,7 +1068,6 @@ extern "C" int rlse_linear_residual(const void* x, const void* weight, void* res
                                     rlse_stream_t stream) {
   DenseParams flags{};
   take_packed(dtype, flags);
-  const bool packed = flags.packed || flags.xpacked;
   const void* outs[1] = {residual};
   int rc = check_dense("linear_residual", dtype, rows, in_features, x, weight, outs, 1);
   if (rc || rows == 0) return rc;
@@ -1099,7 +1096,6 @@ extern "C" int rlse_gate_up_silu(const void* x, const void* w_gate_up, void* act
                                  size_t workspace_bytes, rlse_stream_t stream) {
   DenseParams flags{};
   take_packed(dtype, flags);
-  const bool packed = flags.packed || flags.xpacked;
   const void* outs[1] = {act};
   int rc = check_dense("gate_up_silu", dtype, rows, hidden, x, w_gate_up, outs, 1);
   if (rc || rows == 0) return rc;

@@ -228,20 +228,22 @@ def _group_batch(rng, groups, n_unforked, hkv, d, seed):
     return seq_group, lens, tables, nb, mbps, kp, vp, gen
 
 
-def test_grouped_cascade_mixed_batch_matches_oracle(kv):
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (14, 2, 64), (32, 8, 128), (8, 8, 64)])
+def test_grouped_cascade_mixed_batch_matches_oracle(kv, hq, hkv, d):
     """Three prefix groups (5, 17 and 64 shared pages: one, two and four
     slices) and unforked sequences, members scattered through the batch, in
     one grouped cascade step (rlse_decode_step_groups, streamed pages): every
     row against the oracle over its full key range, the outputs against the
-    planned step's (another sum order) and the pool bytes equal to its."""
-    hq, hkv, d = 16, 8, 128
-    rng = np.random.default_rng(91)
+    planned step's (another sum order) and the pool bytes equal to its. Group
+    sizes G = 2, 7, 4 and 1: with G = 7 a member's columns straddle the
+    16-column tiles, with G = 1 a tile holds 16 members."""
+    rng = np.random.default_rng(91 + hq + d)
     groups = [(5, 5), (9, 17), (20, 64)]
     seq_group, lens, tables, nb, mbps, kp, vp, g = _group_batch(rng, groups, 7, hkv, d, 91)
     b = len(lens)
     q, kn, vn, qw, kw, max_pos, c_h, s_h, c_d, s_d = _step_inputs(kv, g, BF, b, hq, hkv, d, mbps,
                                                                   "bf16")
-    print(f"grouped cascade: B={b}, groups {groups}, 7 unforked, keys "
+    print(f"grouped cascade: Hq={hq} Hkv={hkv} d={d} B={b}, groups {groups}, 7 unforked, keys "
           f"{int(lens.min())}..{int(lens.max())}", flush=True)
     t_dev, l_dev = to_dev(tables), to_dev(lens)
     sg_dev = to_dev(seq_group)
