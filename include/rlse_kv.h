@@ -310,14 +310,17 @@ int rlse_decode_step_cascade(const void* q, const void* k_new, const void* v_new
  * member's new token lies past them), 1 .. min(max_blocks_per_seq, 512).
  * Members may sit anywhere in the batch. rlse_decode_plan_groups builds the
  * step's plan (one per step, read by every layer; required), including the
- * member lists the prefix launch reads; rlse_decode_step_groups then runs
- * the prefix launch over every group's column tiles and the decode, with
+ * member lists and the prefix launch's work items (one per group column
+ * tile and prefix slice); rlse_decode_step_groups then runs the prefix
+ * launch over those items and the decode, with
  * max_group_pages >= every group's pages sizing both and prefix_buf
  * (rlse_decode_prefix_size with prefix_pages = max_group_pages). 1 <=
- * num_groups <= 64; bf16/f16 only. Same results as rlse_decode_step_planned
- * within rounding. A group id or page count out of range, a member whose
- * leading entries differ from its group's, a new token inside its group's
- * pages, or a plan built for another step raise RLSE_WS_ERR_PREFIX. */
+ * num_groups <= 64; num_heads / num_kv_heads <= 8; bf16/f16 only. Same
+ * results as rlse_decode_step_planned within rounding. A group id or page
+ * count out of range, a member whose leading entries differ from its
+ * group's, a new token inside its group's pages, or a plan built for
+ * another step shape (another group count or group size included) raise
+ * RLSE_WS_ERR_PREFIX. */
 int rlse_decode_plan_groups(const int32_t* block_tables, const int32_t* seq_lens,
                             const int32_t* seq_group, const int32_t* group_pages, int num_groups,
                             int batch, int num_heads, int num_kv_heads, int max_blocks_per_seq,
