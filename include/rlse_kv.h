@@ -476,10 +476,11 @@ int rlse_argmax(const void* logits, int32_t* out, int rows, int vocab, int dtype
 /* Linear (q/k/v/o_proj, gate/up/down_proj, lm_head; qwen2.rs:233-252,
  * 153-158): y[rows][out] = x[rows][in] . W[out][in]^T with f32
  * accumulation, rounded once; bias (may be NULL) added after, rounded
- * again, as Candle's broadcast_add after the matmul. bf16/f16 with at most
- * 64 rows (a decode step's batch), in a multiple of 32 and out a multiple of
- * 16 run on the MFMA kernel of the three calls below; other shapes and f32
- * go through rocBLAS gemm_ex. */
+ * again, as Candle's broadcast_add after the matmul. At most 64 rows (a
+ * decode step's batch) with out a multiple of 16 run on the MFMA kernel of
+ * the three calls below: bf16/f16 with in a multiple of 32, f32 (on f32
+ * MFMAs) with in a multiple of 16 and 16-byte aligned buffers; other shapes
+ * (prefill-sized products among them) go through rocBLAS gemm_ex. */
 int rlse_linear(const void* x, const void* weight, const void* bias, void* y, int rows,
                 int out_features, int in_features, int dtype, rlse_stream_t stream);
 /* Packed weights (no counterpart in the reference, which multiplies its

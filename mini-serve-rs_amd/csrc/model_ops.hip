@@ -321,6 +321,26 @@ struct Mma16<f16> {
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
   }
 };
+// f32 (the reference CPU path's dtype): a 16-byte operand load holds four
+// floats, so a k step spans 16 elements, lane l holding elements
+// 4*(l/16) .. +3 of its row. v_mfma_f32_16x16x4_f32 number m takes each
+// lane's element m, for A and B alike: its four k indices are 4g + m over
+// the lane groups g, and the four products cover the step. The accumulator
+// layout is the 16-bit products' (lane l: D[4*(l/16) + v][l%16]).
+template <>
+struct Mma16<float> {
+  static __device__ __forceinline__ f32x4_t run(u32x4_t a, u32x4_t b, f32x4_t c) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[m]), __uint_as_float(b[m]), c, 0,
+                                               0, 0);
+    return c;
+  }
+};
+// Elements of one k step (four lanes groups' 16-byte loads) and of one
+// lane's load.
+template <typename T>
+__host__ __device__ constexpr int dense_step_elems() { return 64 / (int)sizeof(T); }
 
 enum : int { kEpiStore = 0, kEpiQkv = 1, kEpiResidual = 2, kEpiSiluMul = 3 };
 
@@ -357,23 +377,35 @@ constexpr int kDenseHeaderWords = 64;
 
 template <typename T>
 __device__ __forceinline__ void load4(const T* p, float* v) {
-  const uint2 u = *reinterpret_cast<const uint2*>(p);
-  const uint4 q = make_uint4(u.x, u.y, 0, 0);
-  float t[8];
-  Packet<T>::unpack(q, t);
+  if constexpr (sizeof(T) == 4) {
+    const float4 u = *reinterpret_cast<const float4*>(p);
+    v[0] = u.x;
+    v[1] = u.y;
+    v[2] = u.z;
+    v[3] = u.w;
+  } else {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    const uint4 q = make_uint4(u.x, u.y, 0, 0);
+    float t[8];
+    Packet<T>::unpack(q, t);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = t[e];
+    for (int e = 0; e < 4; ++e) v[e] = t[e];
+  }
 }
 
 template <typename T>
 __device__ __forceinline__ void store4(T* p, const float* v) {
-  *reinterpret_cast<uint2*>(p) = make_uint2(Packet<T>::pack2(v[0], v[1]),
-                                            Packet<T>::pack2(v[2], v[3]));
+  if constexpr (sizeof(T) == 4)
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  else
+    *reinterpret_cast<uint2*>(p) = make_uint2(Packet<T>::pack2(v[0], v[1]),
+                                              Packet<T>::pack2(v[2], v[3]));
 }
 
 template <typename T, int RT, int FT, int EPI>
 __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParams p) {
   constexpr int U = FT == 1 ? 8 : 4;
+  constexpr int SE = dense_step_elems<T>();  // elements of a k step (packed: 16-bit only)
   // An epilogue item is the four consecutive features one lane slot holds
   // (4*(slot/16).. of batch row slot%16); kEpiSiluMul pairs slot s (gate
   // features) with slot s+32 (the matching up features) in one item.
@@ -419,9 +451,9 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
     // Packed weights: tile t's operands of k step s are 64 lanes x 16
     // bytes at ((t * K/32 + s) * 64 + lane) * 8, one contiguous KiB per load.
     wr[f] = p.packed ? (const T*)p.w + ((size_t)tile * (K >> 5) * 64 + lane) * 8
-                     : (const T*)p.w + (size_t)row * K + 8 * g;
+                     : (const T*)p.w + (size_t)row * K + (SE / 4) * g;
   }
-  const int wstep = p.packed ? 512 : 32;  // weight elements between k steps
+  const int wstep = p.packed ? 512 : SE;  // weight elements between k steps
   // x: row-major (rows past the batch read its last row), or packed rows:
   // row tile t's operands of k step s at ((t * K/32 + s) * 64 + lane) * 8
   // (the packed buffer holds whole 16-row tiles).
@@ -429,8 +461,8 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
 #pragma unroll
   for (int t = 0; t < RT; ++t)
     xr[t] = p.xpacked ? (const T*)p.x + ((size_t)t * (K >> 5) * 64 + lane) * 8
-                      : (const T*)p.x + (size_t)min(16 * t + fi, p.rows - 1) * K + 8 * g;
-  const int xstep = p.xpacked ? 512 : 32;  // x elements between k steps
+                      : (const T*)p.x + (size_t)min(16 * t + fi, p.rows - 1) * K + (SE / 4) * g;
+  const int xstep = p.xpacked ? 512 : SE;  // x elements between k steps
   f32x4_t acc[FT][RT];
 #pragma unroll
   for (int f = 0; f < FT; ++f)
@@ -457,7 +489,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
       if (p.bias) load4<T>((const T*)p.bias + n, pre[k]);
   }
 
-  const int S = K >> 5;
+  const int S = K / SE;
   const int slice_end = (ks + 1) * S / KS;
   const int s_begin = ks * S / KS + wave * p.steps;
   const int s_end = min(slice_end, s_begin + p.steps);
@@ -689,7 +721,7 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
   const bool wide = ft == 4;
   const int groups = tiles / ft;
   const int ks = p.ws_rec ? dense_split(groups, p.K) : 1;
-  const int steps_total = p.K / 32;
+  const int steps_total = p.K / dense_step_elems<T>();
   const int slice = (steps_total + ks - 1) / ks;
   p.ksplit = ks;
   p.steps = (slice + kDenseWaves - 1) / kDenseWaves;
@@ -965,12 +997,30 @@ extern "C" int rlse_linear(const void* x, const void* weight, const void* bias, 
   const bool mfma = (dtype == RLSE_DTYPE_BF16 || dtype == RLSE_DTYPE_F16) &&
                     in_features % 32 == 0 && out_features % 16 == 0 && aligned(x, 16) &&
                     aligned(weight, 16) && aligned(y, 8) && (!bias || aligned(bias, 8));
+  // f32 at decode shapes: the same kernel on f32 MFMAs (16-element k steps,
+  // 16-byte output and bias packets).
+  const bool mfma32 = dtype == RLSE_DTYPE_F32 && !packed && rows <= kDenseMaxRows &&
+                      in_features % 16 == 0 && out_features % 16 == 0 && aligned(x, 16) &&
+                      aligned(weight, 16) && aligned(y, 16) && (!bias || aligned(bias, 16));
+  if (mfma32) {
+    DenseParams p{};
+    p.x = x;
+    p.w = weight;
+    p.bias = bias;
+    p.out0 = y;
+    p.rows = rows;
+    p.K = in_features;
+    p.N = out_features;
+    return launch_dense<float, kEpiStore>(p, in_features, out_features, 0, 0, 0, s);
+  }
   if (packed && !mfma)
     return fail(RLSE_ERR_INVALID_VALUE,
                 "linear: packed weights or rows need bf16/f16, in_features %% 32 == 0, "
                 "out_features %% 16 == 0 and aligned buffers");
-  // Decode-shaped products (a few rows, bf16/f16) run on the MFMA kernel, as
-  // do products over packed weights (64 rows at a time).
+  // Decode-shaped products (a few rows) run on the MFMA kernel, as do
+  // products over packed weights (64 rows at a time); larger unpacked
+  // products (prefill-sized, one weight read serving many rows) are plain
+  // library GEMMs.
   if (mfma && (rows <= kDenseMaxRows || packed)) {
     DenseParams p{};
     p.x = x;

@@ -101,8 +101,12 @@ def test_silu_mul_matches_oracle(kv, dt):
 @pytest.mark.parametrize("dt", O.DTYPES)
 @pytest.mark.parametrize("rows,n_out,n_in,bias", [(1, 2048, 1024, False), (32, 3072, 1024, True),
                                                   (33, 896, 4864, False), (64, 1000, 128, True),
-                                                  (40, 8192, 256, True)])   # two tiles per group
+                                                  (40, 8192, 256, True),    # two tiles per group
+                                                  (17, 64, 48, True)])      # f32: three 16-wide k steps
 def test_linear_matches_oracle(kv, dt, rows, n_out, n_in, bias):
+    """Decode-shaped products run on the MFMA kernel: bf16/f16 with in % 32,
+    f32 (16-element k steps on f32 MFMAs) with in % 16, outputs a multiple of
+    16; others (1000 outputs, 48 inputs at 16 bits) go to the library GEMM."""
     rng = np.random.default_rng(rows + n_out)
     x = O.round_to(rng.standard_normal((rows, n_in)), dt)
     w = O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt)
