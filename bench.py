@@ -122,6 +122,10 @@ def parse():
                          "batch or group (rlse_decode_step_cascade / rlse_decode_step_groups)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 1 GiB (HBM counter calibration)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="attention workloads: per-phase timeline of the last decode launch of "
+                         "one step, from the measurement build (make -C mini-serve-rs_amd/csrc "
+                         "timeline), as one JSON line instead of the bench line")
     return ap.parse_args()
 
 
@@ -956,6 +960,9 @@ def main():
         print(f"bench.py measures one GPU only (the library has no multi-GPU path); "
               f"got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
+    if args.timeline:
+        timeline_bench(args)
+        return
     if args.workload in PREFILL:
         prefill_bench(args)
         return
@@ -1084,18 +1091,124 @@ def main():
         "cpu_baseline": None,
     }
     result["read_ceiling"] = read_ceiling(kv, k_pools, v_pools, t_dev, lens_dev, lens, hkv, d,
-                                          mbps, nb, layers, min(args.steps, 50), stream)
+                                          mbps, nb, layers, min(args.steps, 50), stream,
+                                          None if args.unfused else plan)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args, lens, hq, hkv, d, layers)
     print(json.dumps(result))
 
 
+TIMELINE_POINTS = ["entry", "plan arrived", "first pages requested", "prologue barrier passed",
+                   "prologue done", "first page computed", "streaming loop ended", "finished"]
+
+
+def timeline_bench(args):
+    """Per-phase timeline of a decode launch: the measurement build of the
+    library (librlse_kv_timeline.so, RLSE_DECODE_TIMELINE) stamps the wall
+    clock (100 MHz) in every wave at the points of TIMELINE_POINTS. After
+    `warmup` steps of the workload (plan + one planned streamed launch per
+    layer, as the bench times them), the stamps are cleared, one more step
+    runs, and the last layer's launch is read back: for every point, the
+    spread over the waves of each workgroup slot (slot 0: the first
+    workgroup dispatched to a compute unit, 1: the second), in us from the
+    launch's first entry, and each phase's duration per wave."""
+    import ctypes
+    lib = os.path.join(ROOT, "mini-serve-rs_amd", "librlse_kv_timeline.so")
+    if not os.path.exists(lib):
+        print("bench.py --timeline needs the measurement build: "
+              "make -C mini-serve-rs_amd/csrc timeline", file=sys.stderr)
+        sys.exit(2)
+    if args.workload not in WORKLOADS:
+        print(f"--timeline covers the attention workloads {sorted(WORKLOADS)}", file=sys.stderr)
+        sys.exit(2)
+    os.environ["RLSE_KV_LIB"] = lib
+    import numpy as np
+    import torch
+    import rlse_kv as kv
+    hq, hkv, d, layers, b, _, _, desc = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = decode_inputs(args.workload, args.seed, dev)
+    t_dev = torch.from_numpy(w["tables"]).to(dev)
+    lens_dev = torch.from_numpy(w["lens"]).to(dev)
+    out = torch.empty((b, hq, d), device=dev, dtype=torch.bfloat16)
+    ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    plan_bytes = kv.decode_plan_size()
+    plan = torch.zeros(plan_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    lib_h = kv.load()
+    fn = lib_h.rlse_decode_timeline
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+
+    def step():
+        kv.decode_plan(t_dev, lens_dev, b, hkv, w["mbps"], w["num_blocks"], plan, plan_bytes,
+                       stream)
+        for layer in range(layers):
+            kv.decode_step_planned(w["q"][layer], w["k_new"][layer], w["v_new"][layer],
+                                   w["q_norm"][layer], w["k_norm"][layer], 1e-6, w["cos"],
+                                   w["sin"], w["max_pos"], w["k_pools"][layer],
+                                   w["v_pools"][layer], t_dev, lens_dev, out, b, hq, hkv, d,
+                                   w["mbps"], w["num_blocks"], 1.0 / math.sqrt(d), "bf16", plan,
+                                   ws, ws_bytes, stream, stream_pages=True)
+
+    for _ in range(max(args.warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    n_words = 8192 * len(TIMELINE_POINTS)
+    buf = np.zeros(n_words, np.uint64)
+    h_stream = ctypes.c_void_p(stream.cuda_stream)
+    if fn(None, 0, 1, h_stream) != 0:
+        raise RuntimeError("rlse_decode_timeline (clear) failed")
+    step()
+    torch.cuda.synchronize()
+    if fn(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes, 0, h_stream) != 0:
+        raise RuntimeError("rlse_decode_timeline (read) failed")
+    n_pts = len(TIMELINE_POINTS)
+    stamps = buf.reshape(-1, n_pts).astype(np.int64)
+    waves = int(np.nonzero(stamps[:, 0])[0].max()) + 1
+    stamps = stamps[:waves]
+    groups = waves // 4
+    t0 = stamps[stamps[:, 0] > 0, 0].min()
+    rel = np.where(stamps > 0, (stamps - t0) * 0.01, np.nan)  # us
+    slot = (np.arange(waves) // 4) >= groups // 2
+
+    def spread(x):
+        x = x[~np.isnan(x)]
+        if not len(x):
+            return None
+        return {"n": int(len(x)), "min": round(float(x.min()), 2),
+                "p10": round(float(np.percentile(x, 10)), 2),
+                "median": round(float(np.median(x)), 2),
+                "p90": round(float(np.percentile(x, 90)), 2), "max": round(float(x.max()), 2)}
+
+    points = {}
+    for k, name in enumerate(TIMELINE_POINTS):
+        points[name] = {"slot0": spread(rel[~slot, k]), "slot1": spread(rel[slot, k])}
+    phases = {}
+    for k in range(1, n_pts):
+        phases[f"{TIMELINE_POINTS[k - 1]} -> {TIMELINE_POINTS[k]}"] = spread(rel[:, k] -
+                                                                             rel[:, k - 1])
+    merge_wave = np.arange(waves) % 4 == 0
+    result = {"timeline": args.workload, "workload": desc, "launch_span_us":
+              round(float(np.nanmax(rel[:, n_pts - 1])), 2), "waves": waves,
+              "workgroups": groups, "points_us": points, "phases_us": phases,
+              "finish_by_wave_index": {f"wave{i}": spread(rel[np.arange(waves) % 4 == i,
+                                                              n_pts - 1]) for i in range(4)},
+              "loop_end_to_finish_wave0": spread(rel[merge_wave, n_pts - 1] -
+                                                         rel[merge_wave, n_pts - 2])}
+    print(json.dumps(result))
+
+
 def read_ceiling(kv, k_pools, v_pools, t_dev, lens_dev, lens, hkv, d, mbps, nb, layers, steps,
-                 stream):
+                 stream, plan=None):
     """The time a launch of the decode's shape needs just to read the
-    decode's K/V bytes: rlse_kv_checksum (the same page walk, grid and
-    loads, no other work) over every layer's pool with the same tables and
-    lengths, timed like the decode (one event pair around a step's
+    decode's K/V bytes: rlse_kv_checksum (the decode's grid and page split,
+    one page in flight per wave, no other work; with the decode's plan,
+    rlse_kv_checksum_planned: each wave's first page requested from the plan,
+    as the planned decode does) over every layer's pool with the same tables
+    and lengths, timed like the decode (one event pair around a step's
     back-to-back launches). Its sums land in a zero-filled buffer per step
     (the fill outside the event pair)."""
     import numpy as np
@@ -1106,7 +1219,7 @@ def read_ceiling(kv, k_pools, v_pools, t_dev, lens_dev, lens, hkv, d, mbps, nb, 
     def step():
         for layer in range(layers):
             kv.kv_checksum(k_pools[layer], v_pools[layer], t_dev, lens_dev, b, hkv, d, mbps, nb,
-                           "bf16", out, stream)
+                           "bf16", out, stream, plan=plan)
 
     for _ in range(3):
         step()
@@ -1123,8 +1236,9 @@ def read_ceiling(kv, k_pools, v_pools, t_dev, lens_dev, lens, hkv, d, mbps, nb, 
     kv_bytes = sum(int(n) * 2 * hkv * d * 2 for n in lens)
     read = kv_bytes + sum(((int(n) + 15) // 16) * 4 for n in lens) + 4 * b
     achieved = read / (avg_ms * 1e-3) / 1e9
-    return {"kernel": "checksum_kernel (rlse_kv_checksum: the decode's page walk, grid and "
-                      "loads, nothing else)",
+    return {"kernel": ("checksum_kernel (rlse_kv_checksum%s: the decode's grid and page split, "
+                       "one page in flight per wave, nothing else)"
+                       % ("_planned, the decode's plan" if plan is not None else "")),
             "bytes_per_launch": read, "avg_launch_ms": avg_ms, "achieved": achieved,
             "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "timed_launches": steps * layers}
 

@@ -134,13 +134,25 @@ int rlse_kv_append(const void* k_new, const void* v_new, void* k_pool, void* v_p
  * counts as 0. No counterpart in the reference, whose tests compare snapshot
  * buffers byte for byte on the host (src/backends/candle.rs:1281-1292): the
  * sums compare a pool with its expected contents without copying it back.
- * The launch walks the pages as the paged decode does and does nothing else,
- * so its duration is the time a decode launch of that shape needs to read
- * its K/V bytes. */
+ * The launch splits the pages as the paged decode does, one page in flight
+ * per wave, and does nothing else, so its duration is the time a decode
+ * launch of that shape needs to read its K/V bytes. */
 int rlse_kv_checksum(const void* k_pool, const void* v_pool, const int32_t* block_tables,
                      const int32_t* seq_lens, int batch, int num_kv_heads, int head_dim,
                      int max_blocks_per_seq, int num_blocks, int dtype, uint32_t* out,
                      rlse_stream_t stream);
+
+/* The same sums, each wave's first page requested from plan (rlse_decode_plan
+ * of the same tables and lengths, 16-byte aligned) before the launch builds
+ * its block prefix, as a planned decode launch does: the read ceiling of
+ * rlse_decode_step_planned. A plan of another step shape (a cascade or
+ * grouped plan) is ignored and the walk builds its own descriptors; the
+ * sums are the same either way. No counterpart in the reference. */
+int rlse_kv_checksum_planned(const void* k_pool, const void* v_pool,
+                             const int32_t* block_tables, const int32_t* seq_lens, int batch,
+                             int num_kv_heads, int head_dim, int max_blocks_per_seq,
+                             int num_blocks, int dtype, const void* plan, uint32_t* out,
+                             rlse_stream_t stream);
 
 /* Snapshot export: pool pages -> contiguous [num_layers][Hkv][len][head_dim]
  * K and V, the layout of Attention::get_kv_snapshot views and of the

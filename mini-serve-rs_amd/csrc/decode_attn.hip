@@ -279,6 +279,42 @@ extern "C" int rlse_decode_workspace_size(int batch, int num_heads, int num_kv_h
 // Validates the shared decode arguments and fills p (workspace included).
 // With a library-owned workspace, `lock` holds its mutex on return; the
 // caller keeps it until the launch is queued.
+#ifdef RLSE_DECODE_TIMELINE
+// Measurement build: one timeline buffer per device, allocated and cleared
+// on first use; every decode launch stamps it (see kTimelinePoints).
+static unsigned long long* g_tl_ptr[64] = {nullptr};
+static std::mutex g_tl_mu;
+static unsigned long long* timeline_buffer() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_tl_mu);
+  if (!g_tl_ptr[dev]) {
+    const size_t bytes = (size_t)kTimelineMaxWaves * kTimelinePoints * sizeof(unsigned long long);
+    void* ptr = nullptr;
+    if (hipMalloc(&ptr, bytes) != hipSuccess) return nullptr;
+    if (hipMemset(ptr, 0, bytes) != hipSuccess) return nullptr;
+    g_tl_ptr[dev] = reinterpret_cast<unsigned long long*>(ptr);
+  }
+  return g_tl_ptr[dev];
+}
+
+// Copies the current device's timeline (kTimelineMaxWaves x kTimelinePoints
+// stamps, 100 MHz wall clock, 0 = not stamped since the last clear) into
+// host (bytes at most) after the stream's work, then clears it when clear
+// is nonzero. Exported by the measurement build only.
+extern "C" int rlse_decode_timeline(void* host, size_t bytes, int clear, rlse_stream_t stream) {
+  unsigned long long* tl = timeline_buffer();
+  if (!tl) return fail(RLSE_ERR_INVALID_VALUE, "decode_timeline: no timeline buffer");
+  const size_t all = (size_t)kTimelineMaxWaves * kTimelinePoints * sizeof(unsigned long long);
+  hipStream_t s = as_stream(stream);
+  hipError_t e = hipSuccess;
+  if (host) e = hipMemcpyAsync(host, tl, bytes < all ? bytes : all, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess && clear) e = hipMemsetAsync(tl, 0, all, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return e == hipSuccess ? RLSE_OK : fail((int)e, "decode_timeline: copy or clear failed");
+}
+#endif
+
 static int prepare_decode(DecodeParams& p, std::unique_lock<std::mutex>& lock, const void* q,
                           const void* k_pool, const void* v_pool, const int32_t* block_tables,
                           const int32_t* seq_lens, void* out, int batch, int num_heads,
@@ -334,6 +370,9 @@ static int prepare_decode(DecodeParams& p, std::unique_lock<std::mutex>& lock, c
   p.W = W;
   p.w1 = kSlot1Weight;
   p.c = scale * 1.4426950408889634f;
+#ifdef RLSE_DECODE_TIMELINE
+  p.timeline = timeline_buffer();
+#endif
   return RLSE_OK;
 }
 

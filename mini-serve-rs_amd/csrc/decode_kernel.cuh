@@ -66,6 +66,32 @@ enum : int { kModePlain = 0, kModeFused = 1, kModePlanned = 2, kModePlannedStrea
 // than this many powers of two.
 constexpr float kLazyLog2 = 8.f;
 
+// Per-phase timeline of a launch, in the measurement build only (`make
+// timeline` defines RLSE_DECODE_TIMELINE; the library then exports
+// rlse_decode_timeline): lane 0 of every wave stores the wall clock (100 MHz
+// ticks) at kTimelinePoints points of its launch into
+// p.timeline[(block * kWaves + wave) * kTimelinePoints + point]:
+//   0 entry, 1 plan arrived (planned), 2 first pages requested (planned),
+//   3 prologue barrier passed, 4 prologue done (queries staged, appends
+//   stored), 5 first page computed, 6 streaming loop ended, 7 finished
+//   (merges and publications included).
+// Points a wave does not reach keep the previous value (the buffer is
+// cleared by the caller). Other builds compile no stamp.
+constexpr int kTimelinePoints = 8;
+constexpr int kTimelineMaxWaves = 8192;
+#ifdef RLSE_DECODE_TIMELINE
+#define RLSE_TL(k)                                                                        \
+  do {                                                                                    \
+    if (p.timeline && (threadIdx.x & 63) == 0)                                            \
+      p.timeline[((size_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * kTimelinePoints + \
+                 (k)] = wall_clock64();                                                   \
+  } while (0)
+#else
+#define RLSE_TL(k) \
+  do {             \
+  } while (0)
+#endif
+
 template <typename T, int D>
 struct DecodeShape {
   static constexpr int ES = sizeof(T);
@@ -263,6 +289,9 @@ struct DecodeParams {
   // here ([B][Hq][prefix_row_floats(D)] floats) and are combined with the
   // prefix states after the wave's stream, all slices' loads at once.
   float* pre_own;
+#ifdef RLSE_DECODE_TIMELINE
+  unsigned long long* timeline;  // [waves][kTimelinePoints] wall-clock stamps
+#endif
 };
 
 // Floats per (sequence, query head) of a prefix partial: acc[D], m, l, and
@@ -739,6 +768,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       end_epoch(next_epoch(ctr0));
       return;
     }
+    RLSE_TL(1);
     // The plan gives the first row and the appends of the first 64 blocks:
     // their query and append loads go out ahead of the first blocks', so the
     // prologue's math waits for them alone and not behind the launch's first
@@ -761,6 +791,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       load_pages(k == 0 ? b0 : (k == 1 ? b1 : b2), __builtin_amdgcn_readlane(plan_d.x, k), kvh,
                  nv > 0);
     }
+    RLSE_TL(2);
   }
   if (wave == 0) block_prefix(p.seq_lens, B, mbps, s_pref, len_t0, p.prefix, p.seq_pre, pre_t0);
   if constexpr (FUSED) {
@@ -769,6 +800,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   }
   if (tid < NPART) s_part_row[tid] = -1;
   __syncthreads();
+  RLSE_TL(3);
   const long long w = blockIdx.x;
   if (w == 0) {  // rows without keys and invalid rows produce zeros
     for (int b = 0; b < B; ++b) {
@@ -1362,10 +1394,14 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     issue(b0, 0, !PLANNED);
     if constexpr (PLANNED) issue(b1, 1, false);
     after_pre_issue();
+    RLSE_TL(4);
     if constexpr (!PLANNED) issue(b1, 1, true);
     if constexpr (NBUF == 3) issue(b2, 2, !PLANNED || kPreIssued < 3 || p.pre);
     for (int i = 0;;) {
       compute(b0);
+#ifdef RLSE_DECODE_TIMELINE
+      if (i == 0) RLSE_TL(5);
+#endif
       if (++i == nblk) break;
       issue(b0, i + NBUF - 1, true);
       compute(b1);
@@ -1378,6 +1414,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       }
     }
     finalize();
+    RLSE_TL(6);
   }
   __syncthreads();
 
@@ -1633,6 +1670,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       }
     }
   }
+  RLSE_TL(7);
   end_epoch(ep);
 }
 
@@ -1650,6 +1688,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   // load over the B lengths, so no exec-masked branch and no copy at a join
   // that would wait for it early. The lengths arrive with the descriptors,
   // so the prefix never waits behind the first blocks.
+  RLSE_TL(0);
   int4 plan_d = make_int4(0, 0, -1, 0);
   int plan_pos = 0, stamp = 0;
   if constexpr (PLANNED) {

@@ -80,7 +80,7 @@ EXPORTED = (
     "rlse_decode_step_planned", "rlse_workspace_check", "rlse_set_merge_wait_ns",
     "rlse_decode_step_noalloc", "rlse_decode_prefix_size", "rlse_decode_plan_cascade",
     "rlse_decode_step_cascade", "rlse_decode_plan_groups", "rlse_decode_step_groups",
-    "rlse_kv_checksum",
+    "rlse_kv_checksum", "rlse_kv_checksum_planned",
 )
 
 
@@ -199,6 +199,8 @@ _SIGS = {
                                       _i, _vp, _sz, _vp]),
     "rlse_decode_plan_groups": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "rlse_kv_checksum": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp]),
+    "rlse_kv_checksum_planned": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp,
+                                      _vp]),
     "rlse_decode_step_groups": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp, _vp,
                                      _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _i,
                                      _i, _i, _vp, _sz, _vp]),
@@ -842,13 +844,21 @@ def decode_step_cascade(q, k_new, v_new, q_norm_weight, k_norm_weight, eps: floa
 
 def kv_checksum(k_pool, v_pool, block_tables, seq_lens, batch: int, num_kv_heads: int,
                 head_dim: int, max_blocks_per_seq: int, num_blocks: int, dtype, out,
-                stream=None) -> None:
+                stream=None, plan=None) -> None:
     """Adds every (sequence, KV head) row's K and V checksums into out
-    (device int32/uint32 [batch][num_kv_heads][2], zero-filled by the caller)."""
-    _check(load().rlse_kv_checksum(_ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
-                                   _ptr(seq_lens), batch, num_kv_heads, head_dim,
-                                   max_blocks_per_seq, num_blocks, _dt(dtype), _ptr(out),
-                                   _stream(stream)))
+    (device int32/uint32 [batch][num_kv_heads][2], zero-filled by the caller).
+    plan: a decode plan of the same tables and lengths (rlse_kv_checksum_planned:
+    each wave's first page requested from it, as a planned decode does)."""
+    if plan is None:
+        _check(load().rlse_kv_checksum(_ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
+                                       _ptr(seq_lens), batch, num_kv_heads, head_dim,
+                                       max_blocks_per_seq, num_blocks, _dt(dtype), _ptr(out),
+                                       _stream(stream)))
+        return
+    _check(load().rlse_kv_checksum_planned(_ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
+                                           _ptr(seq_lens), batch, num_kv_heads, head_dim,
+                                           max_blocks_per_seq, num_blocks, _dt(dtype), _ptr(plan),
+                                           _ptr(out), _stream(stream)))
 
 
 def decode_plan_groups(block_tables, seq_lens, seq_group, group_pages, num_groups: int,

@@ -1,4 +1,5 @@
-"""Pool checksums (rlse_kv_checksum) on the GPU against the oracle's
+"""Pool checksums (rlse_kv_checksum, and rlse_kv_checksum_planned with a
+decode plan) on the GPU against the oracle's
 definition, and the append checked through them at full size.
 
 The checksum of a (sequence, KV head) row is the sum mod 2^32, over its
@@ -37,11 +38,20 @@ def _host_bits(t):
         np.uint16 if t.dtype == torch.bfloat16 else np.float16)
 
 
-def _device_sums(kv, kp, vp, tables, lens, hkv, d, nb, dtype, reps=1):
+def _device_sums(kv, kp, vp, tables, lens, hkv, d, nb, dtype, reps=1, plan=None):
+    """The device sums; plan: None (rlse_kv_checksum), "plan" (a decode plan
+    of the same tables and lengths: rlse_kv_checksum_planned) or "zeros" (a
+    zero-filled plan buffer, whose stamp is no plain plan's: ignored)."""
     out = torch.zeros((len(lens), hkv, 2), dtype=torch.int32, device=DEV)
     t_dev, l_dev = to_dev(tables), to_dev(np.asarray(lens, np.int32))
+    pl = None
+    if plan is not None:
+        pl = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=DEV)
+        if plan == "plan":
+            kv.decode_plan(t_dev, l_dev, len(lens), hkv, tables.shape[1], nb, pl, pl.numel())
     for _ in range(reps):
-        kv.kv_checksum(kp, vp, t_dev, l_dev, len(lens), hkv, d, tables.shape[1], nb, dtype, out)
+        kv.kv_checksum(kp, vp, t_dev, l_dev, len(lens), hkv, d, tables.shape[1], nb, dtype, out,
+                       plan=pl)
     torch.cuda.synchronize()
     return out.cpu().numpy().view(np.uint32)
 
@@ -69,6 +79,12 @@ def test_checksums_match_oracle(kv, dtype, hkv, d):
     twice = _device_sums(kv, to_dev(kp, dtype), to_dev(vp, dtype), tables, lens, hkv, d, nb,
                          dtype, reps=2)
     np.testing.assert_array_equal(twice, (2 * want.astype(np.uint64) & 0xFFFFFFFF).astype(np.uint32))
+    # The planned walk (first pages from a decode plan) and a plan of no
+    # plain step's shape (ignored) give the same sums.
+    for plan in ("plan", "zeros"):
+        got = _device_sums(kv, to_dev(kp, dtype), to_dev(vp, dtype), tables, lens, hkv, d, nb,
+                           dtype, plan=plan)
+        np.testing.assert_array_equal(got, want, err_msg=f"plan={plan}")
 
 
 def test_full_batch_append_through_checksums(kv):
@@ -84,8 +100,11 @@ def test_full_batch_append_through_checksums(kv):
     kp, vp = w["k_pools"][0], w["v_pools"][0]
     kp0, vp0 = _host_bits(kp), _host_bits(vp)
     print(f"full batch: {w['pages']} pages, {kp.numel() * 4 / 1e6:.0f} MB of K/V", flush=True)
+    before = O.kv_checksum_ref(kp0, vp0, tables, lens)
     np.testing.assert_array_equal(_device_sums(kv, kp, vp, tables, lens, hkv, d, nb, "bf16"),
-                                  O.kv_checksum_ref(kp0, vp0, tables, lens))
+                                  before)
+    np.testing.assert_array_equal(
+        _device_sums(kv, kp, vp, tables, lens, hkv, d, nb, "bf16", plan="plan"), before)
     t_dev, l_dev = to_dev(tables), to_dev(lens)
     out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=DEV)
     ws = torch.zeros(kv.decode_workspace_size(b, hq, hkv, d), dtype=torch.uint8, device=DEV)
@@ -107,5 +126,7 @@ def test_full_batch_append_through_checksums(kv):
         kp0[blk, :, slot] = O.apply_rope_bf16(kn, np.full(hkv, pos, np.int32), c_h, s_h)
         vp0[blk, :, slot] = vnh[i]
     got = _device_sums(kv, kp, vp, tables, lens, hkv, d, nb, "bf16")
+    np.testing.assert_array_equal(got, O.kv_checksum_ref(kp0, vp0, tables, lens))
+    got = _device_sums(kv, kp, vp, tables, lens, hkv, d, nb, "bf16", plan="plan")
     np.testing.assert_array_equal(got, O.kv_checksum_ref(kp0, vp0, tables, lens))
     print(f"full batch: {b * hkv} rows' K and V sums equal the expected pool's after the append")
