@@ -68,28 +68,25 @@ constexpr float kLazyLog2 = 8.f;
 
 // Per-phase timeline of a launch, in the measurement build only (`make
 // timeline` defines RLSE_DECODE_TIMELINE; the library then exports
-// rlse_decode_timeline): lane 0 of every wave stores the wall clock (100 MHz
-// ticks) at kTimelinePoints points of its launch into
-// p.timeline[(block * kWaves + wave) * kTimelinePoints + point]:
+// rlse_decode_timeline): every wave reads the wall clock (100 MHz ticks) at
+// kTimelinePoints points of its launch into registers, and lane 0 stores them
+// once, when the wave has finished, at p.timeline[(block * kWaves + wave) *
+// kTimelinePoints + point] -- a store per point would wait behind the loads
+// in flight and move the points after it. The points:
 //   0 entry, 1 plan arrived (planned), 2 first pages requested (planned),
 //   3 prologue barrier passed, 4 prologue done (queries staged, appends
 //   stored), 5 first page computed, 6 streaming loop ended, 7 finished
 //   (merges and publications included).
-// Points a wave does not reach keep the previous value (the buffer is
-// cleared by the caller). Other builds compile no stamp.
+// A point a wave does not reach reads 0. Other builds compile no stamp.
 constexpr int kTimelinePoints = 8;
 constexpr int kTimelineMaxWaves = 8192;
+struct TimelineStamps {
+  unsigned long long t[kTimelinePoints];
+};
 #ifdef RLSE_DECODE_TIMELINE
-#define RLSE_TL(k)                                                                        \
-  do {                                                                                    \
-    if (p.timeline && (threadIdx.x & 63) == 0)                                            \
-      p.timeline[((size_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * kTimelinePoints + \
-                 (k)] = wall_clock64();                                                   \
-  } while (0)
+#define RLSE_TL(k) (tl.t[k] = wall_clock64())
 #else
-#define RLSE_TL(k) \
-  do {             \
-  } while (0)
+#define RLSE_TL(k) ((void)0)
 #endif
 
 template <typename T, int D>
@@ -583,7 +580,8 @@ template <typename T, int D, int G, int MODE, int POL>
 __device__ __forceinline__ void decode_body(const DecodeParams& p,
                                             DecodeLds<T, D, G, MODE != kModePlain>& lds,
                                             int* s_pref, int4 plan_d, int plan_pos,
-                                            uint32_t ctr0, int len_t0, int pre_t0, int stamp) {
+                                            uint32_t ctr0, int len_t0, int pre_t0, int stamp,
+                                            TimelineStamps& tl) {
   constexpr bool FUSED = MODE != kModePlain;
   constexpr bool PLANNED = MODE >= kModePlanned;
   constexpr bool kMma = decode_mma<T, D, G>();
@@ -1670,7 +1668,6 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       }
     }
   }
-  RLSE_TL(7);
   end_epoch(ep);
 }
 
@@ -1688,6 +1685,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   // load over the B lengths, so no exec-masked branch and no copy at a join
   // that would wait for it early. The lengths arrive with the descriptors,
   // so the prefix never waits behind the first blocks.
+  TimelineStamps tl = {};
   RLSE_TL(0);
   int4 plan_d = make_int4(0, 0, -1, 0);
   int plan_pos = 0, stamp = 0;
@@ -1711,7 +1709,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
                                : p.prefix;
   (void)lane;
   decode_body<T, D, G, MODE, MODE == kModePlannedStream ? kLoadNonTemporal : 0>(
-      p, lds, s_pref, plan_d, plan_pos, ctr0, len_t0, pre_t0, stamp);
+      p, lds, s_pref, plan_d, plan_pos, ctr0, len_t0, pre_t0, stamp, tl);
+#ifdef RLSE_DECODE_TIMELINE
+  RLSE_TL(7);
+  if (p.timeline && lane == 0) {
+    unsigned long long* dst =
+        p.timeline + ((size_t)blockIdx.x * kWaves + wave) * kTimelinePoints;
+#pragma unroll
+    for (int k = 0; k < kTimelinePoints; ++k) dst[k] = tl.t[k];
+  }
+#endif
 }
 
 
