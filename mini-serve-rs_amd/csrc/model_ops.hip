@@ -369,6 +369,9 @@ struct DenseParams {
 constexpr int kDenseWaves = 4;
 constexpr int kDenseMaxRows = 64;
 constexpr int kDenseMaxSplit = 8;
+// Most K slices run inside one workgroup (kDenseWaves waves each; 1024
+// threads at most).
+constexpr int kDenseMaxInner = 4;
 // Launch counters of a K-split workspace: one per wave of the largest split
 // grid. A split grid has fewer than 512 workgroups: an output is split only
 // when it has fewer than 256 tile groups, into ceil(256 / groups) slices.
@@ -402,8 +405,15 @@ __device__ __forceinline__ void store4(T* p, const float* v) {
                                               Packet<T>::pack2(v[2], v[3]));
 }
 
-template <typename T, int RT, int FT, int EPI>
-__global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParams p) {
+// KV > 1: the K split runs inside the workgroup instead of across
+// workgroups -- KV slices of kDenseWaves waves each, every wave on the k
+// steps it would have in the split grid, their sums added in LDS in the
+// order the split grid's merge adds its records (the waves of a slice in
+// order, then the slices in order), so the results are the split grid's to
+// the bit. No records, no launch counters, no second round trip to memory.
+template <typename T, int RT, int FT, int EPI, int KV = 1>
+__global__ __launch_bounds__(64 * kDenseWaves * KV) void dense_rows_kernel(DenseParams p) {
+  constexpr int WV = kDenseWaves * KV;  // waves per workgroup
   constexpr int U = FT == 1 ? 8 : 4;
   constexpr int SE = dense_step_elems<T>();  // elements of a k step (packed: 16-bit only)
   // An epilogue item is the four consecutive features one lane slot holds
@@ -411,9 +421,9 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
   // features) with slot s+32 (the matching up features) in one item.
   constexpr int kPair = EPI == kEpiSiluMul ? 2 : 1;
   constexpr int kItems = FT * RT * 64 / kPair;
-  constexpr int kItemsPerThread = (kItems + 64 * kDenseWaves - 1) / (64 * kDenseWaves);
+  constexpr int kItemsPerThread = (kItems + 64 * WV - 1) / (64 * WV);
   constexpr int kRecWords = FT * RT * 256;
-  __shared__ float red[kDenseWaves][FT][RT][256];
+  __shared__ float red[WV][FT][RT][256];
   const int lane = threadIdx.x & 63;
   // Wave-uniform (a scalar register): the k-step bounds below derive from
   // it, and a bound the compiler takes for a per-lane value puts the
@@ -475,7 +485,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
   float pre[kItemsPerThread][4];
 #pragma unroll
   for (int k = 0; k < kItemsPerThread; ++k) {
-    const int it = threadIdx.x + k * 64 * kDenseWaves;
+    const int it = threadIdx.x + k * 64 * WV;
     const int l2 = it & (64 / kPair - 1);
     const int ft = it / (64 / kPair);
     const int t = ft % RT, f = ft / RT;
@@ -490,8 +500,13 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
   }
 
   const int S = K / SE;
-  const int slice_end = (ks + 1) * S / KS;
-  const int s_begin = ks * S / KS + wave * p.steps;
+  // The wave's k steps: slice sl of NS (a workgroup of the split grid, or a
+  // slice of this workgroup's waves), its ws-th share.
+  const int NS = KV > 1 ? KV : KS;
+  const int sl = KV > 1 ? wave / kDenseWaves : ks;
+  const int ws = KV > 1 ? wave % kDenseWaves : wave;
+  const int slice_end = (sl + 1) * S / NS;
+  const int s_begin = sl * S / NS + ws * p.steps;
   const int s_end = min(slice_end, s_begin + p.steps);
   for (int s = s_begin; s < s_end; s += U) {
     u32x4_t a[U][FT], b[U][RT];
@@ -528,7 +543,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
   float v[kItemsPerThread][kPair][4];
 #pragma unroll
   for (int k = 0; k < kItemsPerThread; ++k) {
-    const int it = threadIdx.x + k * 64 * kDenseWaves;
+    const int it = threadIdx.x + k * 64 * WV;
     if (it < kItems) {
       const int l2 = it & (64 / kPair - 1);
       const int ft = it / (64 / kPair);
@@ -537,9 +552,15 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
       for (int q = 0; q < kPair; ++q)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float x = red[0][f][t][(l2 + 32 * q) * 4 + e];
+          float x = 0.f;
 #pragma unroll
-          for (int w = 1; w < kDenseWaves; ++w) x += red[w][f][t][(l2 + 32 * q) * 4 + e];
+          for (int c = 0; c < KV; ++c) {
+            float y = red[c * kDenseWaves][f][t][(l2 + 32 * q) * 4 + e];
+#pragma unroll
+            for (int w = 1; w < kDenseWaves; ++w)
+              y += red[c * kDenseWaves + w][f][t][(l2 + 32 * q) * 4 + e];
+            x = c == 0 ? y : x + y;
+          }
           v[k][q][e] = x;
         }
     }
@@ -555,7 +576,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
     if (ks < KS - 1) {
 #pragma unroll
       for (int k = 0; k < kItemsPerThread; ++k) {
-        const int it = threadIdx.x + k * 64 * kDenseWaves;
+        const int it = threadIdx.x + k * 64 * WV;
         if (it < kItems)
 #pragma unroll
           for (int j = 0; j < kWords; ++j) st_tagged(word_ptr(ks, it, j), ep, v[k][j >> 2][j & 3]);
@@ -569,7 +590,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
     const unsigned long long t0 = wall_clock64();
 #pragma unroll
     for (int k = 0; k < kItemsPerThread; ++k) {
-      const int it = threadIdx.x + k * 64 * kDenseWaves;
+      const int it = threadIdx.x + k * 64 * WV;
       if (it >= kItems) continue;
       uint64_t r[kDenseMaxSplit - 1][kWords];
 #pragma unroll
@@ -614,7 +635,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_rows_kernel(DenseParam
 
 #pragma unroll
   for (int k = 0; k < kItemsPerThread; ++k) {
-    const int it = threadIdx.x + k * 64 * kDenseWaves;
+    const int it = threadIdx.x + k * 64 * WV;
     if (it >= kItems) continue;
     const int l2 = it & (64 / kPair - 1);
     const int ft = it / (64 / kPair);
@@ -721,9 +742,18 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
   const bool wide = ft == 4;
   const int groups = tiles / ft;
   const int ks = p.ws_rec ? dense_split(groups, p.K) : 1;
+  // A split of one-tile groups over at most 32 rows runs inside the
+  // workgroup (KV slices of kDenseWaves waves, at most kDenseMaxInner of
+  // them): the split grid's k steps and sums, without its records. (With
+  // more rows, or with the SwiGLU epilogue's paired items, a 16-wave
+  // workgroup's 128 registers per lane would spill.)
+  const int kv_inner = (ks > 1 && ft == 1 && total_rows <= 32 && EPI != kEpiSiluMul)
+                           ? std::min(ks, kDenseMaxInner)
+                           : 1;
+  const int ns = kv_inner > 1 ? kv_inner : ks;
   const int steps_total = p.K / dense_step_elems<T>();
-  const int slice = (steps_total + ks - 1) / ks;
-  p.ksplit = ks;
+  const int slice = (steps_total + ns - 1) / ns;
+  p.ksplit = kv_inner > 1 ? 1 : ks;
   p.steps = (slice + kDenseWaves - 1) / kDenseWaves;
   const char* base0 = (const char*)p.out0;
   const char* base1 = (const char*)p.out1;
@@ -737,15 +767,27 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
     q.out1 = base1 ? (void*)(base1 + (size_t)r0 * o1_stride * sizeof(T)) : nullptr;
     q.out2 = base2 ? (void*)(base2 + (size_t)r0 * o2_stride * sizeof(T)) : nullptr;
     const int rt = (q.rows + 15) / 16;
-    if (ks > 1 && dense_ws_fixed_words() + (size_t)groups * (ks - 1) * ft * rt * 256 * 2 >
-                      ws_words)
+    if (q.ksplit > 1 && dense_ws_fixed_words() + (size_t)groups * (ks - 1) * ft * rt * 256 * 2 >
+                            ws_words)
       return fail(RLSE_ERR_INVALID_VALUE, "dense: workspace too small");
-    if (ks > 1 && groups * ks * kDenseWaves > kDenseCtrWords)
+    if (q.ksplit > 1 && groups * ks * kDenseWaves > kDenseCtrWords)
       return fail(RLSE_ERR_INVALID_VALUE, "dense: K-split grid larger than its counters");
     const dim3 block(64 * kDenseWaves);
-    const dim3 grid(groups * ks);
+    const dim3 grid(groups * q.ksplit);
     auto run = [&](auto rt_c) {
       constexpr int RT = decltype(rt_c)::value;
+      if constexpr (RT <= 2 && EPI != kEpiSiluMul) {
+        if (kv_inner > 1) {
+          const dim3 big(64 * kDenseWaves * kv_inner);
+          if (kv_inner == 2)
+            hipLaunchKernelGGL((dense_rows_kernel<T, RT, 1, EPI, 2>), grid, big, 0, s, q);
+          else if (kv_inner == 3)
+            hipLaunchKernelGGL((dense_rows_kernel<T, RT, 1, EPI, 3>), grid, big, 0, s, q);
+          else
+            hipLaunchKernelGGL((dense_rows_kernel<T, RT, 1, EPI, 4>), grid, big, 0, s, q);
+          return;
+        }
+      }
       if constexpr (EPI == kEpiStore) {
         if (wide) {
           hipLaunchKernelGGL((dense_rows_kernel<T, RT, 4, EPI>), grid, block, 0, s, q);
