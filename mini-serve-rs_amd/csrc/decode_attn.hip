@@ -43,8 +43,44 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __rest
   if (wave == 0)
     block_prefix(seq_lens, B, mbps, s_pref, lane < B ? seq_lens[lane] : 0, prefix, seq_pre,
                  lane < B ? stream_skip(seq_pre, prefix, lane) : 0);
-  if (blockIdx.x == 0 && tid == 0) const_cast<int*>(plan_tail(plan, W))[0] = stamp;
+  __shared__ int s_bad;
+  if (blockIdx.x == 0 && tid == 0) s_bad = 0;
   __syncthreads();
+  if (blockIdx.x == 0) {
+    // The one-prefix cascade contract, once for every layer of the step:
+    // every sequence's first `prefix` table entries are sequence 0's, and
+    // its length L has its new token past them and within its table
+    // (16 prefix < L <= 16 mbps). The B x prefix entries are dealt over the
+    // threads, four independent loads in flight per thread. (Prefix groups
+    // are checked by the grouped plan.)
+    bool bad = false;
+    if (prefix > 0 && !seq_pre) {
+      for (int b = tid; b < B; b += kThreads) {
+        const int L = seq_lens[b];
+        bad |= L <= 16 * prefix || L > 16 * mbps;
+      }
+      const int n = B * prefix;
+      for (int e0 = tid; e0 < n; e0 += 4 * kThreads) {
+        int a[4], z[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = e0 + u * kThreads < n ? e0 + u * kThreads : e0;
+          const int b = e / prefix, i = e - b * prefix;
+          a[u] = tables[(size_t)b * mbps + i];
+          z[u] = tables[i];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bad |= a[u] != z[u];
+      }
+    }
+    if (__any(bad) && lane == 0) atomicOr(&s_bad, 1);
+  }
+  __syncthreads();
+  if (blockIdx.x == 0 && tid == 0) {
+    int* tail = const_cast<int*>(plan_tail(plan, W));
+    tail[0] = stamp;
+    tail[kPlanContractWord] = s_bad;
+  }
   const long long w = blockIdx.x;
   const long long total = (long long)Hkv * s_pref[B];
   int4 d = make_int4(0, 0, -1, 0);
@@ -78,9 +114,13 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(const int* __rest
 // offsets (G columns per member, 16 per tile) and pages. A group id outside
 // [-1, NG) or a page count outside [1, min(mbps, kMaxPrefixPages)] sets the
 // error word (the prefix launch raises RLSE_WS_ERR_PREFIX) and the sequence,
-// or the group's members, are left unforked.
+// or the group's members, are left unforked. So does a member that breaks
+// its group's contract (error bit 4): its first P table entries must be the
+// group's first member's and its length L within 16 P < L <= 16 mbps.
 __global__ __launch_bounds__(1024) void group_plan_kernel(const int* __restrict__ seq_group,
                                                           const int* __restrict__ group_pages,
+                                                          const int* __restrict__ tables,
+                                                          const int* __restrict__ seq_lens,
                                                           int B, int NG, int G, int mbps,
                                                           int* __restrict__ tail) {
   __shared__ int s_cnt[kMaxPrefixGroups], s_pages[kMaxPrefixGroups], s_next[kMaxPrefixGroups];
@@ -117,6 +157,44 @@ __global__ __launch_bounds__(1024) void group_plan_kernel(const int* __restrict_
       atomicMin(&s_first[gg], b);
     }
     seq_pre[b] = gg >= 0 ? s_pages[gg] : 0;
+  }
+  __syncthreads();
+  {
+    // Each member against its group's first member: thread t takes
+    // sequences t, t + 1024, ... (its length) and, for the table entries,
+    // the members of four consecutive sequences at a time one entry column
+    // per wave lane group -- independent loads, several in flight.
+    bool bad = false;
+    for (int b = tid; b < B; b += 1024) {
+      const int gg = group_of_seq(b);
+      if (gg < 0) continue;
+      const int L = seq_lens[b], P = s_pages[gg];
+      bad |= L <= 16 * P || L > 16 * mbps;
+    }
+    const int wave = tid >> 6;
+    for (int b0 = 4 * wave; b0 < B; b0 += 4 * (1024 / 64)) {
+      int P[4], f[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int gg = b0 + u < B ? group_of_seq(b0 + u) : -1;
+        P[u] = gg >= 0 ? s_pages[gg] : 0;
+        f[u] = gg >= 0 ? s_first[gg] : 0;
+      }
+      const int pmax = max(max(P[0], P[1]), max(P[2], P[3]));
+      for (int i = lane; i < pmax; i += 64) {
+        int a[4], z[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int ii = i < P[u] ? i : 0;
+          const int bb = i < P[u] ? b0 + u : f[u];
+          a[u] = tables[(size_t)bb * mbps + ii];
+          z[u] = tables[(size_t)f[u] * mbps + ii];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bad |= a[u] != z[u];
+      }
+    }
+    if (__any(bad) && lane == 0) atomicOr(&s_err, 4);
   }
   __syncthreads();
   if (tid == 0) {
@@ -431,7 +509,8 @@ static int decode_plan_impl(const int32_t* block_tables, const int32_t* seq_lens
   if (num_groups > 0) {
     int* tail = const_cast<int*>(plan_tail(pl, W));
     hipLaunchKernelGGL(group_plan_kernel, dim3(1), dim3(1024), 0, as_stream(stream), seq_group,
-                       group_pages, batch, num_groups, group_size, max_blocks_per_seq, tail);
+                       group_pages, block_tables, seq_lens, batch, num_groups, group_size,
+                       max_blocks_per_seq, tail);
     st = launch_status("group_plan_kernel");
     if (st) return st;
     seq_pre = tail + kPlanStampWords;
@@ -585,6 +664,10 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
     pp.grp = nullptr;
     pp.num_groups = 0;
     pp.tiles = 0;
+    // A planned one-prefix step reads the plan's verdict on its contract.
+    pp.contract = (plan && num_groups == 0)
+                      ? plan_tail(reinterpret_cast<const int4*>(plan), p.W) + kPlanContractWord
+                      : nullptr;
     if (num_groups > 0) {
       const int* seq_pre = tail + kPlanStampWords;
       pp.members = seq_pre + kMaxDecodeBatch;

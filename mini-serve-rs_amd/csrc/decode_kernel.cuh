@@ -326,6 +326,10 @@ struct PrefixParams {
   const int* grp;
   int num_groups;
   int tiles;
+  // Planned one-prefix step: the plan's verdict on the cascade contract
+  // (kPlanContractWord, nonzero: violated), checked once per step by the
+  // plan; null: the launch checks the tables and lengths itself.
+  const int* contract;
 };
 // Most prefix groups one grouped cascade step takes.
 constexpr int kMaxPrefixGroups = 64;
@@ -360,6 +364,10 @@ __host__ __device__ constexpr size_t group_plan_words() {
 // (int), then the tail: 64 words whose first is the plan's stamp, and the
 // grouped plan.
 constexpr int kPlanStampWords = 64;
+// Tail word 1: the one-prefix cascade contract's verdict (0: every
+// sequence's first `prefix` table entries are sequence 0's and its new token
+// lies past them; 1: some sequence breaks it), written by the plan.
+constexpr int kPlanContractWord = 1;
 __host__ __device__ inline const int* plan_tail(const int4* plan, int W) {
   return reinterpret_cast<const int*>(plan + (size_t)W * kWaves * 64) + (size_t)W * kWaves * 64;
 }

@@ -32,7 +32,9 @@ namespace {
 constexpr int kPrefixWaves = 8;
 static_assert(kMaxPrefixPages <= 64 * kPrefixWaves, "a wave holds the page ids of 64 blocks");
 
-template <typename T, int D, int G>
+// SELF_CHECK: the launch checks the one-prefix contract itself (a step
+// without a plan); planned steps take the plan's verdict.
+template <typename T, int D, int G, bool SELF_CHECK>
 __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(PrefixParams p) {
   using S = DecodeShape<T, D>;
   constexpr int EPL = S::EPL, LPR = S::LPR, RPL = S::RPL, NR = S::NR;
@@ -138,29 +140,23 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
   const int hi = lo + per < shi ? lo + per : shi;
   // Lane i holds the page id of block lo + i (a wave takes at most 64).
   const int ids = lo + lane < hi ? ptab[lo + lane] : 0;
-  // Wave 1 of each workgroup checks a share of the batch against the
-  // contract: every sequence's first P table entries are the group's first
-  // sequence's (sequence 0's without groups), and its new token (position
-  // L - 1) lies past them. The share is every nwork-th of slots [k0, kend):
-  // sequences, or with prefix groups the group's members whose columns fall
-  // in this tile, dealt over the tile's workgroups. The first slot's entries
-  // are requested here, ahead of the page loads, and compared once those are
-  // issued; further slots, when there are more than workgroups, are read at
-  // the end.
+  // The contract: every sequence's first P table entries are the group's
+  // first sequence's (sequence 0's without groups), and its new token
+  // (position L - 1) lies past them. A plan checks it once per step (the
+  // grouped plan's error word, read above; a one-prefix plan's verdict word,
+  // read here by workgroup 0 and acted on at its end). Without a plan, wave 1
+  // of each workgroup checks a share of the batch: every nwork-th of
+  // sequences [k0, B), dealt over the workgroups. The first sequence's
+  // entries are requested here, ahead of the page loads, and compared once
+  // those are issued; further ones, when there are more sequences than
+  // workgroups, are read at the end.
   constexpr int kChk = kMaxPrefixPages / 64;
-  int k0, kend, nwork;
-  if (grouped) {
-    k0 = c0 / G + h * NSg + sp;
-    kend = min((c0 + 15) / G + 1, ncols / G);
-    nwork = Hkv * NSg;
-  } else {
-    k0 = ps * NC + c;
-    kend = B;
-    nwork = Hkv * NS * NC;
-  }
+  constexpr bool self_check = SELF_CHECK;
+  const int k0 = ps * NC + c, kend = B, nwork = Hkv * NS * NC;
+  const int verdict = !grouped && p.contract && id == 0 && wave == 1 ? *p.contract : 0;
   int chk_len = 0, chk_t[kChk], chk_0[kChk];
   bool bad = false;
-  if (wave == 1 && k0 < kend) {
+  if (self_check && wave == 1 && k0 < kend) {
     const int b = seq_of(k0 * G);
     chk_len = p.seq_lens[b];
 #pragma unroll
@@ -237,7 +233,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     load(b0, lo);
     load(b1, lo + 1);
     load(b2, lo + 2);
-    if (wave == 1 && k0 < kend) {
+    if (self_check && wave == 1 && k0 < kend) {
       bad = chk_len <= 16 * P || chk_len > p.mbps * 16;
 #pragma unroll
       for (int k = 0; k < kChk; ++k) bad = bad || chk_t[k] != chk_0[k];
@@ -353,7 +349,8 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     *reinterpret_cast<float4*>(dst + 16 * wave + 4 * mq) = make_float4(a[0], a[1], a[2], a[3]);
     if (wave == 0 && mq == 0) *reinterpret_cast<float2*>(dst + D) = make_float2(M, l);
   }
-  if (wave == 1 && k0 < kend) {
+  if (verdict != 0 && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
+  if (self_check && wave == 1 && k0 < kend) {
     for (int k = k0 + nwork; k < kend; k += nwork) {
       const int b = seq_of(k * G);
       const int L = p.seq_lens[b];
@@ -366,12 +363,20 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
 
 template <typename T, int D, int G>
 int launch_prefix_t(const PrefixParams& p, hipStream_t s) {
+  // Grouped steps are checked by the grouped plan, planned one-prefix steps
+  // by the plan (its verdict word): only a step without a plan checks here.
+  const bool self_check = !p.members && !p.contract;
   // One prefix: 8 ids per group of 8 slice sets and column tile; prefix
   // groups: Hkv ids per work item the bounds allow (see the kernel).
   const int nps = p.Hkv * prefix_splits(p.prefix);
   const unsigned grid = p.members ? (unsigned)(nps * p.tiles)
                                   : (unsigned)(8 * ((p.B * G + 15) / 16) * ((nps + 7) / 8));
-  hipLaunchKernelGGL((decode_prefix_kernel<T, D, G>), dim3(grid), dim3(64 * kPrefixWaves), 0, s, p);
+  if (self_check)
+    hipLaunchKernelGGL((decode_prefix_kernel<T, D, G, true>), dim3(grid), dim3(64 * kPrefixWaves),
+                       0, s, p);
+  else
+    hipLaunchKernelGGL((decode_prefix_kernel<T, D, G, false>), dim3(grid),
+                       dim3(64 * kPrefixWaves), 0, s, p);
   return launch_status("decode_prefix_kernel");
 }
 

@@ -191,6 +191,24 @@ def test_cascade_contract_violations_raise_the_prefix_flag(kv):
                    {"pre_bytes": pre.numel() - 16}, {"dtype": "f32"}):
         with pytest.raises(kv.RlseError):
             step(tables, lens, **kwargs)
+    # Planned steps: the plan checks the contract once (its verdict word),
+    # the step's prefix launch raises the flag from it.
+    plan = torch.zeros(kv.decode_plan_size(), dtype=torch.uint8, device=DEV)
+
+    def planned(tables_, lens_):
+        t_dev, l_dev = to_dev(tables_), to_dev(lens_)
+        kv.decode_plan_cascade(t_dev, l_dev, b, hkv, mbps, nb, pp, plan, plan.numel())
+        kv.decode_step_cascade(q, kn, vn, qw, kw, 1e-6, c_d, s_d, max_pos, kp.clone(), vp.clone(),
+                               t_dev, l_dev, out, b, hq, hkv, d, mbps, nb, 1.0 / math.sqrt(d),
+                               "bf16", plan, pp, pre, pre.numel(), ws, ws.numel())
+        torch.cuda.synchronize()
+        return kv.workspace_flags(ws)
+
+    print("cascade contract, planned steps", flush=True)
+    assert planned(tables, lens) == 0
+    assert planned(bad_t, lens) == kv.WS_ERR_PREFIX
+    assert planned(tables, bad_l) == kv.WS_ERR_PREFIX
+    assert planned(tables, lens) == 0    # a clean plan after a violating one
 
 
 def _group_batch(rng, groups, n_unforked, hkv, d, seed):
