@@ -291,7 +291,9 @@ int rlse_decode_step_planned(const void* q, const void* k_new, const void* v_new
  * query heads, in a launch ahead of the decode launch; the decode combines
  * the slices' states into each row. A batch that breaks the contract
  * raises RLSE_WS_ERR_PREFIX in the workspace; its outputs are then not its
- * attention. */
+ * attention. With a plan the contract is checked once, by
+ * rlse_decode_plan_cascade (the plan carries its verdict), instead of by
+ * every layer's launch. */
 int rlse_decode_prefix_size(int batch, int num_heads, int head_dim, int prefix_pages,
                             size_t* bytes);
 int rlse_decode_plan_cascade(const int32_t* block_tables, const int32_t* seq_lens, int batch,
