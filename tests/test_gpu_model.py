@@ -243,11 +243,14 @@ def test_qkv_proj_matches_three_linears(kv, dt, rows, hidden, nq, nkv, bias):
 @pytest.mark.parametrize("rows", ROWS)
 @pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("n_out,n_in", [(1024, 2048), (1024, 3072), (896, 4864), (64, 160),
-                                        (8192, 128), (1024, 256), (2048, 256)])
+                                        (8192, 128), (1024, 256), (2048, 256), (1536, 1024)])
 def test_linear_residual_matches_oracle(kv, dt, rows, split, n_out, n_in):
     """(1024, 256) and (2048, 256) split K into slices of one 32-wide step
     per wave (a regression case: the steps past a wave's own once ran under
-    an exec mask and fed stale operands into the sums)."""
+    an exec mask and fed stale operands into the sums). Up to 32 rows the
+    split runs inside the workgroup: (1024, 256) and (2048, 256) in 2
+    slices, (1536, 1024) in 3, (1024, 2048/3072) in 4, (896, 4864) in 4 of
+    its 5; more rows take the split grid."""
     rng = np.random.default_rng(rows + n_in)
     x = O.round_to(rng.standard_normal((rows, n_in)), dt)
     w = O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt)
@@ -260,11 +263,13 @@ def test_linear_residual_matches_oracle(kv, dt, rows, split, n_out, n_in):
     rel_check(f"linear_residual rows={rows} {n_out}x{n_in} split={split}", host(rd), want, dt)
 
 
-def test_k_split_is_deterministic_and_equals_unsplit_closely(kv):
+@pytest.mark.parametrize("rows", [32, 64])
+def test_k_split_is_deterministic_and_equals_unsplit_closely(kv, rows):
     """The merged K slices add in slice order: repeated calls give the same
-    bits; the split and unsplit sums differ only by rounding order."""
+    bits; the split and unsplit sums differ only by rounding order. 32 rows:
+    the split inside the workgroup; 64: the split grid."""
     rng = np.random.default_rng(31)
-    rows, n_out, n_in, dt = 32, 1024, 3072, "bf16"
+    n_out, n_in, dt = 1024, 3072, "bf16"
     x = dev(O.round_to(rng.standard_normal((rows, n_in)), dt), dt)
     w = dev(O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt), dt)
     wk = _dense_ws(kv, rows, n_out, n_in, True)
@@ -282,14 +287,38 @@ def test_k_split_is_deterministic_and_equals_unsplit_closely(kv):
         kv.linear_residual(x, w, r, rows, n_out, n_in, dt, wk[:64])
 
 
-def test_k_split_ignores_stale_records_and_reports_timeouts(kv):
+def test_inner_k_split_equals_split_grid_bit_for_bit(kv):
+    """A K split inside the workgroup (up to 32 rows) gives its rows the
+    bits the split grid (more rows) gives them: the same k steps per wave,
+    the waves' and slices' sums added in the same order. The first 32 rows
+    of a 33-row call (split grid) equal a 32-row call (inner split), for 2,
+    3 and 4 slices."""
+    rng = np.random.default_rng(35)
+    dt = "bf16"
+    for n_out, n_in in ((1024, 256), (1536, 1024), (1024, 3072)):
+        x = O.round_to(rng.standard_normal((33, n_in)), dt)
+        w = dev(O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt), dt)
+        r = O.round_to(2 * rng.standard_normal((33, n_out)), dt)
+        wk = _dense_ws(kv, 33, n_out, n_in, True)
+        r33, r32 = dev(r, dt), dev(r[:32], dt)
+        kv.linear_residual(dev(x, dt), w, r33, 33, n_out, n_in, dt, wk)
+        kv.linear_residual(dev(x[:32], dt), w, r32, 32, n_out, n_in, dt, wk)
+        _assert_clean(wk)
+        print(f"inner split vs split grid: {n_out}x{n_in}", flush=True)
+        np.testing.assert_array_equal(host(r32), host(r33)[:32])
+
+
+@pytest.mark.parametrize("rows", [32, 64])
+def test_k_split_ignores_stale_records_and_reports_timeouts(kv, rows):
     """K-split records carry their launch's epoch: records planted with other
     tags between calls (the previous call's epoch, later ones) are never
     summed. With the merge's wait bound forced to zero from the host, a
     merge that gives up writes NaN and raises RLSE_WS_ERR_MERGE_TIMEOUT;
-    every kernel ends normally and the next calls are exact again."""
+    every kernel ends normally and the next calls are exact again. (At 32
+    rows the split runs inside the workgroup: no records, nothing to time
+    out; the planted records must still never reach the sums.)"""
     rng = np.random.default_rng(32)
-    rows, n_out, n_in, dt = 32, 1024, 3072, "bf16"
+    n_out, n_in, dt = 1024, 3072, "bf16"
     x = dev(O.round_to(rng.standard_normal((rows, n_in)), dt), dt)
     w = dev(O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt), dt)
     r0 = dev(O.round_to(rng.standard_normal((rows, n_out)), dt), dt)
