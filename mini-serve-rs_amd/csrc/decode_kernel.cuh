@@ -396,21 +396,6 @@ __host__ __device__ constexpr int prefix_regions(int prefix) { return prefix_spl
 
 int launch_decode_prefix(int dtype, int D, int G, const PrefixParams& p, hipStream_t s);
 
-// Combines (m, l, a) with (mo, lo, ao), all in log2 units; -inf maxima mean
-// "empty" and never produce NaN. The sums are written as one fma over a
-// product rounded on its own, so every instantiation rounds them alike
-// (left to contraction, x*sa + y*sb may fuse either product).
-__device__ __forceinline__ void lse_combine(float& m, float& l, float& a, float mo, float lo,
-                                            float ao) {
-  const float M = fmaxf(m, mo);
-  const float Ms = (M == -INFINITY) ? 0.f : M;
-  const float sa = __builtin_amdgcn_exp2f(m - Ms);
-  const float sb = __builtin_amdgcn_exp2f(mo - Ms);
-  l = fmaf(l, sa, mul_rn(lo, sb));
-  a = fmaf(a, sa, mul_rn(ao, sb));
-  m = M;
-}
-
 template <typename T, int D>
 struct Buf {
   uint4 k[DecodeShape<T, D>::NR];
@@ -599,8 +584,8 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   constexpr int NPART = 2 * kWaves;
   constexpr int DPL = (D + 63) / 64;  // output dims per lane in the row epilogue
   constexpr int QR = q_stage_rows<T, D, G>();
-  // Partial records loaded per batch in a merge: G*DPL + 1 words per lane each.
-  constexpr int MC = 64 / (G * DPL + 1) > 8 ? 8 : (64 / (G * DPL + 1) < 2 ? 2 : 64 / (G * DPL + 1));
+  // Partial records loaded per batch in a merge: G*DPL + 2 words per lane each.
+  constexpr int MC = 64 / (G * DPL + 2) > 8 ? 8 : (64 / (G * DPL + 2) < 2 ? 2 : 64 / (G * DPL + 2));
   // Register buffers per wave: while one block is computed, NBUF - 1 are in
   // flight. The matrix-core decode (16-bit K/V) takes three: the bytes in
   // flight then also cover the stretches in which the compute unit's other
@@ -1438,12 +1423,42 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   // group to group. Every slot's row is read once (lane j < NPART holds slot
   // j's), so the pieces of a row are found with one ballot and their LDS
   // reads issued together.
+  // Epilogue softmax states: head g's running max and sum sit in lane g
+  // (hm, hl; lanes past G hold values that are never read), its
+  // accumulators in A[g][k] (dimension lane + 64k) of every lane.
+  // combine_heads folds a piece (pm, pl in the heads' lanes, pa) into them,
+  // all in log2 units: M = max(m, mo), scales sa = 2^(m - M) and
+  // sb = 2^(mo - M) (M = 0 when both are -inf, so empty states never give
+  // NaN), l = l*sa + lo*sb and a = a*sa + ao*sb. The scales are computed
+  // once, in the heads' own lanes, and read back per head for the
+  // accumulators: one exponential pair per piece instead of one per head
+  // and output dimension in every lane, on the wave's critical path at the
+  // end of the launch. The sums are one fma over a product rounded on its
+  // own, so every instantiation rounds them alike (left to contraction,
+  // x*sa + y*sb may fuse either product).
+  const int hj = lane < G ? lane : 0;  // the head a lane's hm, hl belong to
+  auto combine_heads = [&](float& hm, float& hl, float(&A)[G][DPL], float pm, float pl,
+                           const float(&pa)[G][DPL]) __attribute__((always_inline)) {
+    const float mx = fmaxf(hm, pm);
+    const float ms = (mx == -INFINITY) ? 0.f : mx;
+    const float sa = __builtin_amdgcn_exp2f(hm - ms);
+    const float sb = __builtin_amdgcn_exp2f(pm - ms);
+    hl = fmaf(hl, sa, mul_rn(pl, sb));
+    hm = mx;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float ag = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sa), g));
+      const float bg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sb), g));
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) A[g][k] = fmaf(A[g][k], ag, mul_rn(pa[g][k], bg));
+    }
+  };
   // Cascade step: combines the prefix slices' states of row (b, kvh) into
-  // (M, Ls, A) in slice order, the loads of SB slices in flight at once
+  // (hm, hl, A) in slice order, the loads of SB slices in flight at once
   // (a slice index past the last reloads the first of the batch, unused).
   constexpr int SB = 32 / (G * DPL) < 1 ? 1 : (32 / (G * DPL) > 8 ? 8 : 32 / (G * DPL));
-  auto combine_prefix = [&](int b, int kvh, float(&M)[G][DPL], float(&Ls)[G][DPL],
-                            float(&A)[G][DPL]) __attribute__((always_inline)) {
+  auto combine_prefix = [&](int b, int kvh, float& hm, float& hl, float(&A)[G][DPL])
+      __attribute__((always_inline)) {
     constexpr int PF = prefix_row_floats(D);
     const float* pr = p.pre + ((size_t)b * Hq + (size_t)kvh * G) * PF;
     int ns = p.pre_slices;
@@ -1453,46 +1468,39 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     }
 #pragma unroll 1
     for (int s0 = 0; s0 < ns; s0 += SB) {
-      float sm[SB][G], sl[SB][G], sa[SB][G][DPL];
+      float sm[SB], sl[SB], sa[SB][G][DPL];
 #pragma unroll
       for (int i = 0; i < SB; ++i) {
         const float* r = pr + (size_t)(s0 + i < ns ? s0 + i : s0) * (size_t)p.pre_stride;
+        sm[i] = r[hj * PF + D];
+        sl[i] = r[hj * PF + D + 1];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          sm[i][g] = r[g * PF + D];
-          sl[i][g] = r[g * PF + D + 1];
+        for (int g = 0; g < G; ++g)
 #pragma unroll
           for (int k = 0; k < DPL; ++k)
             sa[i][g][k] = lane + 64 * k < D ? r[g * PF + lane + 64 * k] : 0.f;
-        }
       }
 #pragma unroll
       for (int i = 0; i < SB; ++i)
-        if (s0 + i < ns) {
-#pragma unroll
-          for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int k = 0; k < DPL; ++k)
-              if (lane + 64 * k < D)
-                lse_combine(M[g][k], Ls[g][k], A[g][k], sm[i][g], sl[i][g], sa[i][g][k]);
-        }
+        if (s0 + i < ns) combine_heads(hm, hl, A, sm[i], sl[i], sa[i]);
     }
   };
   // Output of a finished row (NaN if a partial did not arrive within the
   // wait bound).
-  auto write_row = [&](int b, int kvh, bool ok, const float(&Ls)[G][DPL],
-                       const float(&A)[G][DPL]) __attribute__((always_inline)) {
+  auto write_row = [&](int b, int kvh, bool ok, float hl, const float(&A)[G][DPL])
+      __attribute__((always_inline)) {
+    const float inv = hl > 0.f ? 1.f / hl : 0.f;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g) {
+      const float ig = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), g));
 #pragma unroll
       for (int k = 0; k < DPL; ++k) {
         const int d = lane + 64 * k;
-        if (d < D) {
-          const float inv = Ls[g][k] > 0.f ? 1.f / Ls[g][k] : 0.f;
+        if (d < D)
           ob[((size_t)b * Hq + (size_t)kvh * G + g) * D + d] =
-              Elem<T>::from_f32(ok ? A[g][k] * inv : __builtin_nanf(""));
-        }
+              Elem<T>::from_f32(ok ? A[g][k] * ig : __builtin_nanf(""));
       }
+    }
   };
   const int prow = lane < NPART ? s_part_row[lane] : -1;
 #pragma unroll 1
@@ -1504,45 +1512,35 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     const bool merge = R < glo && R + nb <= ghi;  // only ever wave 0's slot 0 in wave 0
     if (merge ? wave != 0 : (R + nb > whi && whi < ghi)) continue;
     const int b = row / Hkv, kvh = row - b * Hkv;
-    float M[G][DPL], Ls[G][DPL], A[G][DPL];
+    float hm = -INFINITY, hl = 0.f, A[G][DPL];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int k = 0; k < DPL; ++k) {
-        M[g][k] = -INFINITY;
-        Ls[g][k] = 0.f;
-        A[g][k] = 0.f;
-      }
+      for (int k = 0; k < DPL; ++k) A[g][k] = 0.f;
     // Slots holding pieces of the row: this wave's slot s and, in the waves
     // below it (every wave when merging), the slot naming the same row. A
     // row's pieces sit in consecutive waves, at most one slot per wave.
     const int top = merge ? kWaves - 1 : wave;
     const uint64_t hit = __ballot(lane < 2 * top + 2 && prow == row &&
                                   ((lane >> 1) != wave || (lane & 1) == s));
-    float pm[kWaves][G], pl[kWaves][G], pa[kWaves][G][DPL];
+    float pm[kWaves], pl[kWaves], pa[kWaves][G][DPL];
 #pragma unroll
     for (int wv = 0; wv < kWaves; ++wv) {
       const int slot = 2 * wv + (int)((hit >> (2 * wv + 1)) & 1);
+      pm[wv] = s_part[slot][hj][D];
+      pl[wv] = s_part[slot][hj][D + 1];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        pm[wv][g] = s_part[slot][g][D];
-        pl[wv][g] = s_part[slot][g][D + 1];
+      for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int k = 0; k < DPL; ++k) {
           const int d = lane + 64 * k;
           pa[wv][g][k] = d < D ? s_part[slot][g][d] : 0.f;
         }
-      }
     }
 #pragma unroll
     for (int wv = kWaves - 1; wv >= 0; --wv) {
       if (((hit >> (2 * wv)) & 3) == 0) continue;
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int k = 0; k < DPL; ++k)
-          if (lane + 64 * k < D)
-            lse_combine(M[g][k], Ls[g][k], A[g][k], pm[wv][g], pl[wv][g], pa[wv][g][k]);
+      combine_heads(hm, hl, A, pm[wv], pl[wv], pa[wv]);
     }
     if (R + nb > ghi) {
       // The row continues in a later group: publish this group's piece
@@ -1555,15 +1553,11 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
           const int d = lane + 64 * k;
           if (d < D) st_tagged(rec + (size_t)g * D + d, ep, A[g][k]);
         }
-      // m and l of every head (the same in every lane): lane j < 2G stores
-      // word G*D + j, m[j] then l[j - G].
-      float ml = 0.f;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        ml = lane == g ? M[g][0] : ml;
-        ml = lane == G + g ? Ls[g][0] : ml;
+      // m then l of every head: lane g < G stores words G*D + g and G*D + G + g.
+      if (lane < G) {
+        st_tagged(rec + G * D + lane, ep, hm);
+        st_tagged(rec + G * D + G + lane, ep, hl);
       }
-      if (lane < 2 * G) st_tagged(rec + G * D + lane, ep, ml);
       continue;
     }
     bool ok = true;
@@ -1584,10 +1578,10 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         return wall_clock64() - t0 > p.wait_ticks;
       };
       // Records are loaded MC at a time, each as G*DPL words of acc per lane
-      // plus one word of m/l per lane j < 2G, and loaded again (after a
-      // short sleep) until every word carries this launch's epoch.
+      // plus the m and l words of head j in lane j < G, and loaded again
+      // (after a short sleep) until every word carries this launch's epoch.
       for (int c = 0; c < np && ok; c += MC) {
-        uint64_t mt[MC], av[MC][G][DPL];
+        uint64_t mm[MC], ml[MC], av[MC][G][DPL];
         for (int attempt = 0;; ++attempt) {
           if (attempt > 0) {
             if (timed_out()) {
@@ -1600,7 +1594,8 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
 #pragma unroll
           for (int i = 0; i < MC; ++i) {  // issue the batch's loads together
             if (c + i >= np) {
-              mt[i] = fill;
+              mm[i] = fill;
+              ml[i] = fill;
 #pragma unroll
               for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -1608,7 +1603,8 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
               continue;
             }
             const uint64_t* r = record(c + i);
-            mt[i] = lane < 2 * G ? ld_tagged(r + G * D + lane) : fill;
+            mm[i] = lane < G ? ld_tagged(r + G * D + lane) : fill;
+            ml[i] = lane < G ? ld_tagged(r + G * D + G + lane) : fill;
 #pragma unroll
             for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -1620,7 +1616,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
           bool ready = true;
 #pragma unroll
           for (int i = 0; i < MC; ++i) {
-            ready = ready && tag_is(mt[i], ep);
+            ready = ready && tag_is(mm[i], ep) && tag_is(ml[i], ep);
 #pragma unroll
             for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -1632,21 +1628,18 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
 #pragma unroll
         for (int i = 0; i < MC; ++i)
           if (c + i < np) {
-            const int mlw = (int)(uint32_t)mt[i];
+            float ra[G][DPL];
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-              const float mo = __int_as_float(__builtin_amdgcn_readlane(mlw, g));
-              const float lo_ = __int_as_float(__builtin_amdgcn_readlane(mlw, G + g));
+            for (int g = 0; g < G; ++g)
 #pragma unroll
-              for (int k = 0; k < DPL; ++k)
-                lse_combine(M[g][k], Ls[g][k], A[g][k], mo, lo_, tag_value(av[i][g][k]));
-            }
+              for (int k = 0; k < DPL; ++k) ra[g][k] = tag_value(av[i][g][k]);
+            combine_heads(hm, hl, A, tag_value(mm[i]), tag_value(ml[i]), ra);
           }
       }
       if (!ok && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_MERGE_TIMEOUT);
     }
-    if (p.pre) combine_prefix(b, kvh, M, Ls, A);  // cascade step
-    write_row(b, kvh, ok, Ls, A);
+    if (p.pre) combine_prefix(b, kvh, hm, hl, A);  // cascade step
+    write_row(b, kvh, ok, hl, A);
   }
   if constexpr (kMma) {
     // Cascade step: the rows this wave finished inside its range, their
@@ -1660,19 +1653,17 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
         row_extent(row, R, nb);
         if (nb == 0) continue;  // no keys of its own: written by group 0
         const int b = row / Hkv, kvh = row - b * Hkv;
-        float M[G][DPL], Ls[G][DPL], A[G][DPL];
         const float* own = p.pre_own + ((size_t)b * Hq + (size_t)kvh * G) * PF;
+        float hm = own[hj * PF + D], hl = own[hj * PF + D + 1], A[G][DPL];
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
           for (int k = 0; k < DPL; ++k) {
             const int d = lane + 64 * k;
-            M[g][k] = own[g * PF + D];
-            Ls[g][k] = own[g * PF + D + 1];
             A[g][k] = d < D ? own[g * PF + d] : 0.f;
           }
-        combine_prefix(b, kvh, M, Ls, A);
-        write_row(b, kvh, true, Ls, A);
+        combine_prefix(b, kvh, hm, hl, A);
+        write_row(b, kvh, true, hl, A);
       }
     }
   }
