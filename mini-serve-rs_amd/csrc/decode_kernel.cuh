@@ -1407,6 +1407,19 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     finalize();
     RLSE_TL(6);
   }
+  // A row that began in earlier groups and ends in this one is finished by
+  // wave 0 (its slot 0 row), which merges the records of groups wa .. w-1;
+  // group wa used record slot 0 only if its range starts exactly at the row
+  // start. Found before the barrier (two 64-bit divisions), so the wave's
+  // wait there covers them.
+  long long wa = 0;
+  int np = 0;
+  bool wa_slot1 = false;
+  if (wave == 0 && part_row0 >= 0 && part_R0 < glo && part_R0 + part_nb0 <= ghi) {
+    wa = group_of(part_R0, total, we, p.W, p.w1);
+    np = (int)(w - wa);
+    wa_slot1 = range_lo(wa, total, we, p.W, p.w1) != part_R0;
+  }
   __syncthreads();
 
   // Rows this group holds in pieces. A row that started in an earlier group
@@ -1562,13 +1575,10 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     }
     bool ok = true;
     if (R < glo) {
-      // The row's last block is in this group: combine the pieces of the
-      // earlier groups wa .. w-1 with this one's, each record once all of its
-      // words carry this launch's epoch. Group wa used slot 0 only if its
-      // range starts exactly at the row start.
-      const long long wa = group_of(R, total, we, p.W, p.w1);
-      const int np = (int)(w - wa);
-      const bool wa_slot1 = range_lo(wa, total, we, p.W, p.w1) != R;
+      // The row's last block is in this group (wave 0's slot 0 row, whose
+      // wa, np and wa_slot1 were found before the barrier): combine the
+      // pieces of the earlier groups with this one's, each record once all
+      // of its words carry this launch's epoch.
       auto record = [&](int j) __attribute__((always_inline)) {
         const int slot = (j == 0 && wa_slot1) ? 1 : 0;
         return p.ws_rec + ((size_t)(wa + j) * 2 + slot) * (size_t)REC;
