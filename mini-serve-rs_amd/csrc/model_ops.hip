@@ -414,14 +414,16 @@ __device__ __forceinline__ void store4(T* p, const float* v) {
 template <typename T, int RT, int FT, int EPI, int KV = 1>
 __global__ __launch_bounds__(64 * kDenseWaves * KV) void dense_rows_kernel(DenseParams p) {
   constexpr int WV = kDenseWaves * KV;  // waves per workgroup
-  if (gridDim.y > 1) {
-    // Row tiles split over the grid's rows: this workgroup takes the RT
-    // row tiles from 16 * RT * blockIdx.y on (row-major output).
-    const int r0 = 16 * RT * (int)blockIdx.y;
-    p.x = p.xpacked ? (const void*)((const T*)p.x + (size_t)(r0 >> 4) * (p.K >> 5) * 512)
-                    : (const void*)((const T*)p.x + (size_t)r0 * p.K);
-    p.out0 = (void*)((T*)p.out0 + (size_t)r0 * p.N);
-    p.rows = min(16 * RT, p.rows - r0);
+  if constexpr (KV > 1 && RT == 1 && EPI == kEpiResidual) {
+    // Row tiles split over the grid's rows (the launcher does so only for
+    // these instantiations): this workgroup takes row tile blockIdx.y.
+    if (gridDim.y > 1) {
+      const int r0 = 16 * (int)blockIdx.y;
+      p.x = p.xpacked ? (const void*)((const T*)p.x + (size_t)(r0 >> 4) * (p.K >> 5) * 512)
+                      : (const void*)((const T*)p.x + (size_t)r0 * p.K);
+      p.out0 = (void*)((T*)p.out0 + (size_t)r0 * p.N);
+      p.rows = min(16, p.rows - r0);
+    }
   }
   constexpr int U = FT == 1 ? 8 : 4;
   constexpr int SE = dense_step_elems<T>();  // elements of a k step (packed: 16-bit only)
