@@ -753,12 +753,16 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
   const bool wide = ft == 4;
   const int groups = tiles / ft;
   const int ks = p.ws_rec ? dense_split(groups, p.K) : 1;
-  // A split of one-tile groups over at most 32 rows runs inside the
-  // workgroup (KV slices of kDenseWaves waves, at most kDenseMaxInner of
-  // them): the split grid's k steps and sums, without its records. (With
-  // more rows, or with the SwiGLU epilogue's paired items, a 16-wave
-  // workgroup's 128 registers per lane would spill.)
-  const int kv_inner = (ks > 1 && ft == 1 && total_rows <= 32 && EPI != kEpiSiluMul)
+  // A split of one-tile groups runs inside the workgroup (KV slices of
+  // kDenseWaves waves, at most kDenseMaxInner of them): the split grid's k
+  // steps and sums, without its records, for up to 32 rows -- and for a
+  // residual projection at any row count, each 16-row tile on its own
+  // workgroup row (grid rows; one row tile per workgroup keeps the 16-wave
+  // workgroup within its registers). With more rows, or with the SwiGLU
+  // epilogue's paired items, the other epilogues keep the split grid (a
+  // 16-wave workgroup's 128 registers per lane would spill).
+  const int kv_inner = (ks > 1 && ft == 1 && EPI != kEpiSiluMul &&
+                        (total_rows <= 32 || EPI == kEpiResidual))
                            ? std::min(ks, kDenseMaxInner)
                            : 1;
   const int ns = kv_inner > 1 ? kv_inner : ks;
@@ -787,16 +791,18 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
     const dim3 grid(groups * q.ksplit);
     auto run = [&](auto rt_c) {
       constexpr int RT = decltype(rt_c)::value;
-      if constexpr (RT <= 2 && EPI != kEpiSiluMul) {
+      if constexpr ((RT <= 2 || EPI == kEpiResidual) && EPI != kEpiSiluMul) {
         if (kv_inner > 1) {
-          // A residual projection's two row tiles go to two workgroups (grid
-          // rows): each streams the tile group's weights (the second from
-          // L2/MALL) but only half the batch's activations, which are most
-          // of a workgroup's bytes, and twice the compute units take part.
-          // Same k steps and sums per row, so the same bits. Measured,
-          // 32 rows x hidden 1024: o_proj 7.3 -> 5.4 us, down_proj 7.9 ->
-          // 6.4 us with cold weights.
-          constexpr int RTL = (RT == 2 && EPI == kEpiResidual) ? 1 : RT;
+          // A residual projection's row tiles go to separate workgroups
+          // (grid rows): each streams the tile group's weights (the others
+          // from L2/MALL) but only its 16 rows of the batch's activations,
+          // which are most of a workgroup's bytes, and more compute units
+          // take part. Same k steps and sums per row, so the same bits.
+          // Measured with cold weights, 32 rows x hidden 1024: o_proj
+          // 7.3 -> 5.4 us, down_proj 7.9 -> 6.4 us; at 64 rows (hidden 896)
+          // it replaces the split grid's records and the whole step goes
+          // 2.11 -> 1.84 ms.
+          constexpr int RTL = EPI == kEpiResidual ? 1 : RT;
           const dim3 g(grid.x, RT / RTL);
           const dim3 big(64 * kDenseWaves * kv_inner);
           if (kv_inner == 2)

@@ -247,10 +247,10 @@ def test_qkv_proj_matches_three_linears(kv, dt, rows, hidden, nq, nkv, bias):
 def test_linear_residual_matches_oracle(kv, dt, rows, split, n_out, n_in):
     """(1024, 256) and (2048, 256) split K into slices of one 32-wide step
     per wave (a regression case: the steps past a wave's own once ran under
-    an exec mask and fed stale operands into the sums). Up to 32 rows the
-    split runs inside the workgroup: (1024, 256) and (2048, 256) in 2
-    slices, (1536, 1024) in 3, (1024, 2048/3072) in 4, (896, 4864) in 4 of
-    its 5; more rows take the split grid."""
+    an exec mask and fed stale operands into the sums). The split runs
+    inside the workgroup, each 16-row tile on its own workgroup row:
+    (1024, 256) and (2048, 256) in 2 slices, (1536, 1024) in 3,
+    (1024, 2048/3072) in 4, (896, 4864) in 4 of its 5."""
     rng = np.random.default_rng(rows + n_in)
     x = O.round_to(rng.standard_normal((rows, n_in)), dt)
     w = O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt)
@@ -263,11 +263,28 @@ def test_linear_residual_matches_oracle(kv, dt, rows, split, n_out, n_in):
     rel_check(f"linear_residual rows={rows} {n_out}x{n_in} split={split}", host(rd), want, dt)
 
 
-@pytest.mark.parametrize("rows", [32, 64])
-def test_k_split_is_deterministic_and_equals_unsplit_closely(kv, rows):
+# K-split projections of 1024 outputs over 3072 inputs (4 slices): "residual"
+# is linear_residual (the split inside the workgroup, row tiles on grid
+# rows), "qkv" a q/k/v projection of 512 + 2 x 256 features (the split
+# inside the workgroup up to 32 rows, the split grid and its records past).
+def _split_call(kv, kind, x, w, r, rows, wk):
+    dt = "bf16"
+    if kind == "residual":
+        kv.linear_residual(x, w, r, rows, 1024, 3072, dt, wk)
+    else:
+        q, k, v = r[:, :512], r[:, 512:768], r[:, 768:]
+        outs = [torch.empty((rows, n), dtype=torch.bfloat16, device=DEV) for n in (512, 256, 256)]
+        kv.qkv_proj(x, w, None, *outs, rows, 3072, 512, 256, dt, wk)
+        for dst, o in zip((q, k, v), outs):
+            dst.copy_(o)
+
+
+@pytest.mark.parametrize("kind,rows", [("residual", 32), ("residual", 64), ("qkv", 64)])
+def test_k_split_is_deterministic_and_equals_unsplit_closely(kv, kind, rows):
     """The merged K slices add in slice order: repeated calls give the same
-    bits; the split and unsplit sums differ only by rounding order. 32 rows:
-    the split inside the workgroup; 64: the split grid."""
+    bits; the split and unsplit sums differ only by rounding order (the
+    split inside the workgroup at 32 and 64 residual rows, the split grid
+    for the 64-row q/k/v projection)."""
     rng = np.random.default_rng(31)
     n_out, n_in, dt = 1024, 3072, "bf16"
     x = dev(O.round_to(rng.standard_normal((rows, n_in)), dt), dt)
@@ -277,46 +294,63 @@ def test_k_split_is_deterministic_and_equals_unsplit_closely(kv, rows):
     outs = []
     for use in (True, True, True, False):
         r = torch.zeros((rows, n_out), dtype=torch.bfloat16, device=DEV)
-        kv.linear_residual(x, w, r, rows, n_out, n_in, dt, wk if use else None)
+        _split_call(kv, kind, x, w, r, rows, wk if use else None)
         outs.append(host(r))
     np.testing.assert_array_equal(outs[0], outs[1])
     np.testing.assert_array_equal(outs[0], outs[2])
     assert np.abs(outs[0] - outs[3]).max() <= 2 * ULP[dt] * np.abs(outs[3]).max()
     _assert_clean(wk)
-    with pytest.raises(kv.RlseError):        # a workspace too small is refused
-        kv.linear_residual(x, w, r, rows, n_out, n_in, dt, wk[:64])
+    if kind == "qkv":
+        with pytest.raises(kv.RlseError):    # a workspace too small is refused
+            _split_call(kv, kind, x, w, r, rows, wk[:64])
 
 
 def test_inner_k_split_equals_split_grid_bit_for_bit(kv):
-    """A K split inside the workgroup (up to 32 rows) gives its rows the
-    bits the split grid (more rows) gives them: the same k steps per wave,
-    the waves' and slices' sums added in the same order. The first 32 rows
-    of a 33-row call (split grid) equal a 32-row call (inner split), for 2,
-    3 and 4 slices."""
+    """A K split inside the workgroup gives its rows the bits the split grid
+    gives them: the same k steps per wave, the waves' and slices' sums added
+    in the same order. A q/k/v projection takes the inner split up to 32
+    rows and the split grid past: the first 32 rows of a 33-row call equal
+    a 32-row call, for 2, 3 and 4 slices. A residual projection splits its
+    row tiles over grid rows at any row count: its first 32 rows of a
+    64-row call equal a 32-row call."""
     rng = np.random.default_rng(35)
     dt = "bf16"
-    for n_out, n_in in ((1024, 256), (1536, 1024), (1024, 3072)):
-        x = O.round_to(rng.standard_normal((33, n_in)), dt)
-        w = dev(O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt), dt)
-        r = O.round_to(2 * rng.standard_normal((33, n_out)), dt)
-        wk = _dense_ws(kv, 33, n_out, n_in, True)
-        r33, r32 = dev(r, dt), dev(r[:32], dt)
-        kv.linear_residual(dev(x, dt), w, r33, 33, n_out, n_in, dt, wk)
-        kv.linear_residual(dev(x[:32], dt), w, r32, 32, n_out, n_in, dt, wk)
+    for hidden, nq, nkv in ((256, 512, 256), (1024, 1024, 256), (3072, 512, 256)):
+        n_out = nq + 2 * nkv
+        x = O.round_to(rng.standard_normal((33, hidden)), dt)
+        w = dev(O.round_to(rng.standard_normal((n_out, hidden)) / np.sqrt(hidden), dt), dt)
+        wk = _dense_ws(kv, 33, n_out, hidden, True)
+        got = {}
+        for rows in (33, 32):
+            outs = [torch.empty((rows, n), dtype=torch.bfloat16, device=DEV) for n in (nq, nkv, nkv)]
+            kv.qkv_proj(dev(x[:rows], dt), w, None, *outs, rows, hidden, nq, nkv, dt, wk)
+            got[rows] = [host(o) for o in outs]
         _assert_clean(wk)
-        print(f"inner split vs split grid: {n_out}x{n_in}", flush=True)
-        np.testing.assert_array_equal(host(r32), host(r33)[:32])
+        print(f"inner split vs split grid: q/k/v {n_out}x{hidden}", flush=True)
+        for a, b in zip(got[32], got[33]):
+            np.testing.assert_array_equal(a, b[:32])
+    n_out, n_in = 1024, 3072
+    x = O.round_to(rng.standard_normal((64, n_in)), dt)
+    w = dev(O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt), dt)
+    r = O.round_to(2 * rng.standard_normal((64, n_out)), dt)
+    wk = _dense_ws(kv, 64, n_out, n_in, True)
+    r64, r32 = dev(r, dt), dev(r[:32], dt)
+    kv.linear_residual(dev(x, dt), w, r64, 64, n_out, n_in, dt, wk)
+    kv.linear_residual(dev(x[:32], dt), w, r32, 32, n_out, n_in, dt, wk)
+    _assert_clean(wk)
+    np.testing.assert_array_equal(host(r32), host(r64)[:32])
 
 
-@pytest.mark.parametrize("rows", [32, 64])
-def test_k_split_ignores_stale_records_and_reports_timeouts(kv, rows):
+@pytest.mark.parametrize("kind,rows", [("residual", 32), ("qkv", 64)])
+def test_k_split_ignores_stale_records_and_reports_timeouts(kv, kind, rows):
     """K-split records carry their launch's epoch: records planted with other
     tags between calls (the previous call's epoch, later ones) are never
     summed. With the merge's wait bound forced to zero from the host, a
     merge that gives up writes NaN and raises RLSE_WS_ERR_MERGE_TIMEOUT;
-    every kernel ends normally and the next calls are exact again. (At 32
-    rows the split runs inside the workgroup: no records, nothing to time
-    out; the planted records must still never reach the sums.)"""
+    every kernel ends normally and the next calls are exact again. (The
+    residual projection splits inside the workgroup: no records, nothing to
+    time out; the planted records must still never reach the sums. The
+    64-row q/k/v projection takes the split grid.)"""
     rng = np.random.default_rng(32)
     n_out, n_in, dt = 1024, 3072, "bf16"
     x = dev(O.round_to(rng.standard_normal((rows, n_in)), dt), dt)
@@ -326,7 +360,7 @@ def test_k_split_ignores_stale_records_and_reports_timeouts(kv, rows):
 
     def call():
         r = r0.clone()
-        kv.linear_residual(x, w, r, rows, n_out, n_in, dt, wk)
+        _split_call(kv, kind, x, w, r, rows, wk)
         return host(r)
 
     ref = call()
@@ -348,7 +382,7 @@ def test_k_split_ignores_stale_records_and_reports_timeouts(kv, rows):
         kv.set_merge_wait_ns(100_000_000)
     flags = kv.workspace_flags(wk)
     bad = np.isnan(got)
-    print(f"dense timeout: flags={flags} NaN outputs={int(bad.sum())}", flush=True)
+    print(f"dense timeout ({kind}): flags={flags} NaN outputs={int(bad.sum())}", flush=True)
     assert bool(flags & kv.WS_ERR_MERGE_TIMEOUT) == bool(bad.any())
     np.testing.assert_array_equal(got[~bad], ref[~bad])
     for rep_ in range(2):
