@@ -414,14 +414,20 @@ __device__ __forceinline__ void store4(T* p, const float* v) {
 template <typename T, int RT, int FT, int EPI, int KV = 1>
 __global__ __launch_bounds__(64 * kDenseWaves * KV) void dense_rows_kernel(DenseParams p) {
   constexpr int WV = kDenseWaves * KV;  // waves per workgroup
-  if constexpr (KV > 1 && RT == 1 && EPI == kEpiResidual) {
+  if constexpr (KV > 1 && RT == 1 && (EPI == kEpiResidual || EPI == kEpiQkv)) {
     // Row tiles split over the grid's rows (the launcher does so only for
     // these instantiations): this workgroup takes row tile blockIdx.y.
     if (gridDim.y > 1) {
       const int r0 = 16 * (int)blockIdx.y;
       p.x = p.xpacked ? (const void*)((const T*)p.x + (size_t)(r0 >> 4) * (p.K >> 5) * 512)
                       : (const void*)((const T*)p.x + (size_t)r0 * p.K);
-      p.out0 = (void*)((T*)p.out0 + (size_t)r0 * p.N);
+      if constexpr (EPI == kEpiQkv) {
+        p.out0 = (void*)((T*)p.out0 + (size_t)r0 * p.n1);
+        p.out1 = (void*)((T*)p.out1 + (size_t)r0 * (p.n2 - p.n1));
+        p.out2 = (void*)((T*)p.out2 + (size_t)r0 * (p.N - p.n2));
+      } else {
+        p.out0 = (void*)((T*)p.out0 + (size_t)r0 * p.N);
+      }
       p.rows = min(16, p.rows - r0);
     }
   }
@@ -755,16 +761,17 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
   const int ks = p.ws_rec ? dense_split(groups, p.K) : 1;
   // A split of one-tile groups runs inside the workgroup (KV slices of
   // kDenseWaves waves, at most kDenseMaxInner of them): the split grid's k
-  // steps and sums, without its records, for up to 32 rows -- and for a
-  // residual projection at any row count, each 16-row tile on its own
-  // workgroup row (grid rows; one row tile per workgroup keeps the 16-wave
-  // workgroup within its registers). With more rows, or with the SwiGLU
-  // epilogue's paired items, the other epilogues keep the split grid (a
-  // 16-wave workgroup's 128 registers per lane would spill).
-  const int kv_inner = (ks > 1 && ft == 1 && EPI != kEpiSiluMul &&
-                        (total_rows <= 32 || EPI == kEpiResidual))
-                           ? std::min(ks, kDenseMaxInner)
-                           : 1;
+  // steps and sums, without its records. The residual and q/k/v
+  // projections put each 16-row tile on its own workgroup row (grid rows;
+  // one row tile per workgroup keeps the 16-wave workgroup within its
+  // registers at any row count); plain stores do so up to 32 rows. The
+  // SwiGLU epilogue's paired items would spill a 16-wave workgroup's 128
+  // registers per lane, so it keeps the split grid.
+  const int kv_inner =
+      (ks > 1 && ft == 1 && EPI != kEpiSiluMul &&
+       (total_rows <= 32 || EPI == kEpiResidual || EPI == kEpiQkv))
+          ? std::min(ks, kDenseMaxInner)
+          : 1;
   const int ns = kv_inner > 1 ? kv_inner : ks;
   const int steps_total = p.K / dense_step_elems<T>();
   const int slice = (steps_total + ns - 1) / ns;
@@ -791,18 +798,18 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
     const dim3 grid(groups * q.ksplit);
     auto run = [&](auto rt_c) {
       constexpr int RT = decltype(rt_c)::value;
-      if constexpr ((RT <= 2 || EPI == kEpiResidual) && EPI != kEpiSiluMul) {
+      if constexpr ((RT <= 2 || EPI == kEpiResidual || EPI == kEpiQkv) && EPI != kEpiSiluMul) {
         if (kv_inner > 1) {
-          // A residual projection's row tiles go to separate workgroups
-          // (grid rows): each streams the tile group's weights (the others
-          // from L2/MALL) but only its 16 rows of the batch's activations,
-          // which are most of a workgroup's bytes, and more compute units
-          // take part. Same k steps and sums per row, so the same bits.
-          // Measured with cold weights, 32 rows x hidden 1024: o_proj
-          // 7.3 -> 5.4 us, down_proj 7.9 -> 6.4 us; at 64 rows (hidden 896)
-          // it replaces the split grid's records and the whole step goes
-          // 2.11 -> 1.84 ms.
-          constexpr int RTL = EPI == kEpiResidual ? 1 : RT;
+          // A residual or q/k/v projection's row tiles go to separate
+          // workgroups (grid rows): each streams the tile group's weights
+          // (the others from L2/MALL) but only its 16 rows of the batch's
+          // activations, which are most of a workgroup's bytes, and more
+          // compute units take part. Same k steps and sums per row, so the
+          // same bits. Measured with cold weights, 32 rows x hidden 1024:
+          // o_proj 7.3 -> 5.4 us, down_proj 7.9 -> 6.4 us; at 64 rows
+          // (hidden 896) it replaces the split grid's records and the
+          // whole step goes 2.11 -> 1.84 ms.
+          constexpr int RTL = (EPI == kEpiResidual || EPI == kEpiQkv) ? 1 : RT;
           const dim3 g(grid.x, RT / RTL);
           const dim3 big(64 * kDenseWaves * kv_inner);
           if (kv_inner == 2)

@@ -263,85 +263,94 @@ def test_linear_residual_matches_oracle(kv, dt, rows, split, n_out, n_in):
     rel_check(f"linear_residual rows={rows} {n_out}x{n_in} split={split}", host(rd), want, dt)
 
 
-# K-split projections of 1024 outputs over 3072 inputs (4 slices): "residual"
-# is linear_residual (the split inside the workgroup, row tiles on grid
-# rows), "qkv" a q/k/v projection of 512 + 2 x 256 features (the split
-# inside the workgroup up to 32 rows, the split grid and its records past).
-def _split_call(kv, kind, x, w, r, rows, wk):
+# K-split projections over 3072 inputs, 64 output tiles (4 slices):
+# "residual" is linear_residual and "qkv" a q/k/v projection of
+# 512 + 2 x 256 features (both split inside the workgroup, row tiles on grid
+# rows), "gate_up" the SwiGLU projection of 2 x 512 features (the split grid
+# and its records). Returns the call's output on the host.
+_SPLIT_OUT = {"residual": 1024, "qkv": 1024, "gate_up": 512}
+
+
+def _split_call(kv, kind, x, w, r0, rows, wk):
     dt = "bf16"
     if kind == "residual":
+        r = r0.clone()
         kv.linear_residual(x, w, r, rows, 1024, 3072, dt, wk)
-    else:
-        q, k, v = r[:, :512], r[:, 512:768], r[:, 768:]
+        return host(r)
+    if kind == "qkv":
         outs = [torch.empty((rows, n), dtype=torch.bfloat16, device=DEV) for n in (512, 256, 256)]
         kv.qkv_proj(x, w, None, *outs, rows, 3072, 512, 256, dt, wk)
-        for dst, o in zip((q, k, v), outs):
-            dst.copy_(o)
+        return np.concatenate([host(o) for o in outs], axis=1)
+    act = torch.empty((rows, 512), dtype=torch.bfloat16, device=DEV)
+    kv.gate_up_silu(x, w, act, rows, 3072, 512, dt, wk)
+    return host(act)
 
 
-@pytest.mark.parametrize("kind,rows", [("residual", 32), ("residual", 64), ("qkv", 64)])
+def _split_inputs(rng, rows, dt="bf16"):
+    x = dev(O.round_to(rng.standard_normal((rows, 3072)), dt), dt)
+    w = dev(O.round_to(rng.standard_normal((1024, 3072)) / np.sqrt(3072), dt), dt)
+    r0 = dev(O.round_to(rng.standard_normal((rows, 1024)), dt), dt)
+    return x, w, r0
+
+
+@pytest.mark.parametrize("kind,rows", [("residual", 32), ("residual", 64), ("qkv", 64),
+                                       ("gate_up", 64)])
 def test_k_split_is_deterministic_and_equals_unsplit_closely(kv, kind, rows):
     """The merged K slices add in slice order: repeated calls give the same
     bits; the split and unsplit sums differ only by rounding order (the
-    split inside the workgroup at 32 and 64 residual rows, the split grid
-    for the 64-row q/k/v projection)."""
+    split inside the workgroup for the residual and q/k/v projections, the
+    split grid for SwiGLU)."""
     rng = np.random.default_rng(31)
-    n_out, n_in, dt = 1024, 3072, "bf16"
-    x = dev(O.round_to(rng.standard_normal((rows, n_in)), dt), dt)
-    w = dev(O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt), dt)
-    wk = _dense_ws(kv, rows, n_out, n_in, True)
+    dt = "bf16"
+    x, w, r0 = _split_inputs(rng, rows)
+    wk = _dense_ws(kv, rows, 1024, 3072, True)
     assert wk.numel() > 4                    # this shape splits K
-    outs = []
-    for use in (True, True, True, False):
-        r = torch.zeros((rows, n_out), dtype=torch.bfloat16, device=DEV)
-        _split_call(kv, kind, x, w, r, rows, wk if use else None)
-        outs.append(host(r))
+    outs = [_split_call(kv, kind, x, w, r0, rows, wk if use else None)
+            for use in (True, True, True, False)]
     np.testing.assert_array_equal(outs[0], outs[1])
     np.testing.assert_array_equal(outs[0], outs[2])
-    assert np.abs(outs[0] - outs[3]).max() <= 2 * ULP[dt] * np.abs(outs[3]).max()
+    # SwiGLU rounds gate and up before silu(gate) * up: an ulp of either
+    # moves the product by up to a few ulps of the largest output
+    bar = (8 if kind == "gate_up" else 2) * ULP[dt]
+    assert np.abs(outs[0] - outs[3]).max() <= bar * np.abs(outs[3]).max()
     _assert_clean(wk)
-    if kind == "qkv":
+    if kind == "gate_up":
         with pytest.raises(kv.RlseError):    # a workspace too small is refused
-            _split_call(kv, kind, x, w, r, rows, wk[:64])
+            _split_call(kv, kind, x, w, r0, rows, wk[:64])
 
 
-def test_inner_k_split_equals_split_grid_bit_for_bit(kv):
-    """A K split inside the workgroup gives its rows the bits the split grid
-    gives them: the same k steps per wave, the waves' and slices' sums added
-    in the same order. A q/k/v projection takes the inner split up to 32
-    rows and the split grid past: the first 32 rows of a 33-row call equal
-    a 32-row call, for 2, 3 and 4 slices. A residual projection splits its
-    row tiles over grid rows at any row count: its first 32 rows of a
-    64-row call equal a 32-row call."""
+def test_split_results_do_not_depend_on_the_row_count(kv):
+    """A row's outputs are the same bits whatever other rows share the call:
+    the residual and q/k/v projections (the split inside the workgroup, one
+    row tile per workgroup row) at 32, 33 and 64 rows, and SwiGLU (the split
+    grid) at 32 and 33 rows, for 2, 3 and 4 slices of q/k/v."""
     rng = np.random.default_rng(35)
     dt = "bf16"
     for hidden, nq, nkv in ((256, 512, 256), (1024, 1024, 256), (3072, 512, 256)):
         n_out = nq + 2 * nkv
-        x = O.round_to(rng.standard_normal((33, hidden)), dt)
+        x = O.round_to(rng.standard_normal((64, hidden)), dt)
         w = dev(O.round_to(rng.standard_normal((n_out, hidden)) / np.sqrt(hidden), dt), dt)
-        wk = _dense_ws(kv, 33, n_out, hidden, True)
+        wk = _dense_ws(kv, 64, n_out, hidden, True)
         got = {}
-        for rows in (33, 32):
+        for rows in (64, 33, 32):
             outs = [torch.empty((rows, n), dtype=torch.bfloat16, device=DEV) for n in (nq, nkv, nkv)]
             kv.qkv_proj(dev(x[:rows], dt), w, None, *outs, rows, hidden, nq, nkv, dt, wk)
             got[rows] = [host(o) for o in outs]
         _assert_clean(wk)
-        print(f"inner split vs split grid: q/k/v {n_out}x{hidden}", flush=True)
-        for a, b in zip(got[32], got[33]):
-            np.testing.assert_array_equal(a, b[:32])
-    n_out, n_in = 1024, 3072
-    x = O.round_to(rng.standard_normal((64, n_in)), dt)
-    w = dev(O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt), dt)
-    r = O.round_to(2 * rng.standard_normal((64, n_out)), dt)
-    wk = _dense_ws(kv, 64, n_out, n_in, True)
-    r64, r32 = dev(r, dt), dev(r[:32], dt)
-    kv.linear_residual(dev(x, dt), w, r64, 64, n_out, n_in, dt, wk)
-    kv.linear_residual(dev(x[:32], dt), w, r32, 32, n_out, n_in, dt, wk)
-    _assert_clean(wk)
-    np.testing.assert_array_equal(host(r32), host(r64)[:32])
+        print(f"row-count independence: q/k/v {n_out}x{hidden}", flush=True)
+        for rows in (64, 33):
+            for a, b in zip(got[32], got[rows]):
+                np.testing.assert_array_equal(a, b[:32])
+    x, w, r0 = _split_inputs(rng, 64)
+    wk = _dense_ws(kv, 64, 1024, 3072, True)
+    for kind, counts in (("residual", (64, 33, 32)), ("gate_up", (33, 32))):
+        got = {rows: _split_call(kv, kind, x[:rows], w, r0[:rows], rows, wk) for rows in counts}
+        _assert_clean(wk)
+        for rows in counts[:-1]:
+            np.testing.assert_array_equal(got[32], got[rows][:32])
 
 
-@pytest.mark.parametrize("kind,rows", [("residual", 32), ("qkv", 64)])
+@pytest.mark.parametrize("kind,rows", [("residual", 32), ("gate_up", 64)])
 def test_k_split_ignores_stale_records_and_reports_timeouts(kv, kind, rows):
     """K-split records carry their launch's epoch: records planted with other
     tags between calls (the previous call's epoch, later ones) are never
@@ -349,19 +358,15 @@ def test_k_split_ignores_stale_records_and_reports_timeouts(kv, kind, rows):
     merge that gives up writes NaN and raises RLSE_WS_ERR_MERGE_TIMEOUT;
     every kernel ends normally and the next calls are exact again. (The
     residual projection splits inside the workgroup: no records, nothing to
-    time out; the planted records must still never reach the sums. The
-    64-row q/k/v projection takes the split grid.)"""
+    time out; the planted records must still never reach the sums. SwiGLU
+    takes the split grid.)"""
     rng = np.random.default_rng(32)
-    n_out, n_in, dt = 1024, 3072, "bf16"
-    x = dev(O.round_to(rng.standard_normal((rows, n_in)), dt), dt)
-    w = dev(O.round_to(rng.standard_normal((n_out, n_in)) / np.sqrt(n_in), dt), dt)
-    r0 = dev(O.round_to(rng.standard_normal((rows, n_out)), dt), dt)
-    wk = _dense_ws(kv, rows, n_out, n_in, True)
+    dt = "bf16"
+    x, w, r0 = _split_inputs(rng, rows)
+    wk = _dense_ws(kv, rows, 1024, 3072, True)
 
     def call():
-        r = r0.clone()
-        _split_call(kv, kind, x, w, r, rows, wk)
-        return host(r)
+        return _split_call(kv, kind, x, w, r0, rows, wk)
 
     ref = call()
     _assert_clean(wk)
