@@ -1099,7 +1099,8 @@ def main():
 
 
 TIMELINE_POINTS = ["entry", "plan arrived", "first pages requested", "prologue barrier passed",
-                   "prologue done", "first page computed", "streaming loop ended", "finished"]
+                   "prologue done", "first page computed", "streaming loop ended",
+                   "group barrier passed", "own pieces combined", "records arrived", "finished"]
 
 
 def timeline_bench(args):
@@ -1186,18 +1187,36 @@ def timeline_bench(args):
     points = {}
     for k, name in enumerate(TIMELINE_POINTS):
         points[name] = {"slot0": spread(rel[~slot, k]), "slot1": spread(rel[slot, k])}
+    P = {name: k for k, name in enumerate(TIMELINE_POINTS)}
+    fin, loop_end = P["finished"], P["streaming loop ended"]
+    # Phases up to the epilogue's barrier in order, then the epilogue's:
+    # waves combining pieces of a row, the merging waves (records of earlier
+    # groups), and the waves that publish or write without records.
+    pairs = [(k - 1, k, None) for k in range(1, P["group barrier passed"] + 1)]
+    merging = ~np.isnan(rel[:, P["records arrived"]])
+    combining = ~np.isnan(rel[:, P["own pieces combined"]])
+    pairs += [(P["group barrier passed"], P["own pieces combined"], None),
+              (P["own pieces combined"], P["records arrived"], "merging waves"),
+              (P["records arrived"], fin, "merging waves"),
+              (P["own pieces combined"], fin, "publishing or writing waves"),
+              (loop_end, fin, None)]
     phases = {}
-    for k in range(1, n_pts):
-        phases[f"{TIMELINE_POINTS[k - 1]} -> {TIMELINE_POINTS[k]}"] = spread(rel[:, k] -
-                                                                             rel[:, k - 1])
-    merge_wave = np.arange(waves) % 4 == 0
+    for a, b, who in pairs:
+        sel = merging if who == "merging waves" else (combining & ~merging if who else
+                                                      np.ones(waves, bool))
+        name = f"{TIMELINE_POINTS[a]} -> {TIMELINE_POINTS[b]}" + (f" ({who})" if who else "")
+        phases[name] = spread(rel[sel, b] - rel[sel, a])
+    last = int(np.nanargmax(rel[:, fin]))
     result = {"timeline": args.workload, "workload": desc, "launch_span_us":
-              round(float(np.nanmax(rel[:, n_pts - 1])), 2), "waves": waves,
+              round(float(np.nanmax(rel[:, fin])), 2), "waves": waves,
               "workgroups": groups, "points_us": points, "phases_us": phases,
-              "finish_by_wave_index": {f"wave{i}": spread(rel[np.arange(waves) % 4 == i,
-                                                              n_pts - 1]) for i in range(4)},
-              "loop_end_to_finish_wave0": spread(rel[merge_wave, n_pts - 1] -
-                                                         rel[merge_wave, n_pts - 2])}
+              "last_loop_end_us": round(float(np.nanmax(rel[:, loop_end])), 2),
+              "last_finisher": {"wave": last, "workgroup": last // 4, "wave_in_group": last % 4,
+                                "points_us": {n: (None if np.isnan(rel[last, k]) else
+                                                  round(float(rel[last, k]), 2))
+                                              for k, n in enumerate(TIMELINE_POINTS)}},
+              "finish_by_wave_index": {f"wave{i}": spread(rel[np.arange(waves) % 4 == i, fin])
+                                       for i in range(4)}}
     print(json.dumps(result))
 
 

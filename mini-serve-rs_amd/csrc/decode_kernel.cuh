@@ -75,10 +75,14 @@ constexpr float kLazyLog2 = 8.f;
 // in flight and move the points after it. The points:
 //   0 entry, 1 plan arrived (planned), 2 first pages requested (planned),
 //   3 prologue barrier passed, 4 prologue done (queries staged, appends
-//   stored), 5 first page computed, 6 streaming loop ended, 7 finished
-//   (merges and publications included).
+//   stored), 5 first page computed, 6 streaming loop ended, 7 group
+//   barrier passed (the epilogue's), 8 the group's own pieces of a row
+//   combined (waves that finish or publish a row held in pieces; the last
+//   such row), 9 earlier groups' records arrived and combined (the merging
+//   wave), 10 finished (outputs, publications and the launch counter
+//   stored).
 // A point a wave does not reach reads 0. Other builds compile no stamp.
-constexpr int kTimelinePoints = 8;
+constexpr int kTimelinePoints = 11;
 constexpr int kTimelineMaxWaves = 8192;
 struct TimelineStamps {
   unsigned long long t[kTimelinePoints];
@@ -1421,6 +1425,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     wa_slot1 = range_lo(wa, total, we, p.W, p.w1) != part_R0;
   }
   __syncthreads();
+  RLSE_TL(7);
 
   // Rows this group holds in pieces. A row that started in an earlier group
   // and ends in this one is finished by wave 0, which merges the partials of
@@ -1555,6 +1560,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       if (((hit >> (2 * wv)) & 3) == 0) continue;
       combine_heads(hm, hl, A, pm[wv], pl[wv], pa[wv]);
     }
+    RLSE_TL(8);
     if (R + nb > ghi) {
       // The row continues in a later group: publish this group's piece
       // (slot 0 = the group's first segment, 1 = a later one) and leave.
@@ -1647,6 +1653,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
           }
       }
       if (!ok && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_MERGE_TIMEOUT);
+      RLSE_TL(9);
     }
     if (p.pre) combine_prefix(b, kvh, hm, hl, A);  // cascade step
     write_row(b, kvh, ok, hl, A);
@@ -1720,7 +1727,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   decode_body<T, D, G, MODE, MODE == kModePlannedStream ? kLoadNonTemporal : 0>(
       p, lds, s_pref, plan_d, plan_pos, ctr0, len_t0, pre_t0, stamp, tl);
 #ifdef RLSE_DECODE_TIMELINE
-  RLSE_TL(7);
+  RLSE_TL(10);
   if (p.timeline && lane == 0) {
     unsigned long long* dst =
         p.timeline + ((size_t)blockIdx.x * kWaves + wave) * kTimelinePoints;
