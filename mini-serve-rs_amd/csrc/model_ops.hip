@@ -805,10 +805,10 @@ int launch_dense(DenseParams p, size_t x_stride, size_t o0_stride, size_t o1_str
           // (the others from L2/MALL) but only its 16 rows of the batch's
           // activations, which are most of a workgroup's bytes, and more
           // compute units take part. Same k steps and sums per row, so the
-          // same bits. Measured with cold weights, 32 rows x hidden 1024:
-          // o_proj 7.3 -> 5.4 us, down_proj 7.9 -> 6.4 us; at 64 rows
-          // (hidden 896) it replaces the split grid's records and the
-          // whole step goes 2.11 -> 1.84 ms.
+          // same bits. Measured in the whole decode step: o_proj and
+          // down_proj 8.05 -> 6.14 us at 32 rows x hidden 1024; at 64 rows
+          // x hidden 896, where it replaces the split grid's records, 11.86
+          // -> 6.46 us, and q/k/v 8.96 -> 6.27 us.
           constexpr int RTL = (EPI == kEpiResidual || EPI == kEpiQkv) ? 1 : RT;
           const dim3 g(grid.x, RT / RTL);
           const dim3 big(64 * kDenseWaves * kv_inner);
