@@ -16,7 +16,11 @@ second), the decode kernel's achieved HBM bandwidth against the 8 TB/s peak
 (algorithmic bytes per launch / HIP-event time per launch), and the oracle's
 CPU time on a bounded sample of the same workload.
 
-  python bench.py [--steps K] [--warmup W] [--workload qwen3|qwen25]
+  python bench.py [--steps K] [--warmup W] [--workload NAME]
+
+Other attention workloads: qwen25 (Qwen2.5-0.5B, G=7, d=64), qwen25_7b
+(Qwen2.5-7B, G=7, d=128), qwen3_8b (long context); prefix forks, mixed
+batches, chunked prefill and whole decode steps (see --help).
 """
 import argparse
 import json
@@ -41,12 +45,16 @@ WORKLOADS = {
     "qwen3_8b": (32, 8, 128, 1, 128, 8192, 32768,
                  "Qwen3-8B long-context decode: 32q/8kv heads, d=128, 1 layer, B=128, "
                  "cached U[8192,32768] + 1 appended, bf16, 16-token pages"),
+    "qwen25_7b": (28, 4, 128, 28, 32, 128, 2048,
+                  "Qwen2.5-7B batched decode: 28q/4kv heads (G=7), d=128, 28 layers, B=32, "
+                  "cached U[128,2048] + 1 appended, bf16, 16-token pages"),
 }
 METRIC_NAME = {
     "qwen3": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen3-0.6B shape, 1 GPU",
     "qwen25": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen2.5-0.5B shape, 1 GPU",
     "qwen3_8b": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen3-8B long-context "
                 "shape, 1 GPU",
+    "qwen25_7b": "decode-attn HBM GB/s (% of peak) + attn tokens/sec at Qwen2.5-7B shape, 1 GPU",
 }
 # Chunked prefill: (Hq, Hkv, d, chunk tokens, cached tokens before the chunk, description)
 PREFILL = {
@@ -889,7 +897,7 @@ def e2e_cpu_baseline(args, cfg, cached):
 # Whether the model of each attention workload has per-head q_norm / k_norm
 # (Qwen3 does; Qwen2.5 does not: Config.q_norm is absent for it,
 # src/backends/qwen2.rs:251-260). RoPE applies to every workload.
-WORKLOAD_QK_NORM = {"qwen3": True, "qwen25": False, "qwen3_8b": True}
+WORKLOAD_QK_NORM = {"qwen3": True, "qwen25": False, "qwen3_8b": True, "qwen25_7b": False}
 
 
 def decode_layout(workload, seed):

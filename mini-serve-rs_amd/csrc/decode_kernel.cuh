@@ -588,8 +588,10 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
   constexpr int NPART = 2 * kWaves;
   constexpr int DPL = (D + 63) / 64;  // output dims per lane in the row epilogue
   constexpr int QR = q_stage_rows<T, D, G>();
-  // Partial records loaded per batch in a merge: G*DPL + 2 words per lane each.
-  constexpr int MC = 64 / (G * DPL + 2) > 8 ? 8 : (64 / (G * DPL + 2) < 2 ? 2 : 64 / (G * DPL + 2));
+  // Partial records loaded per batch in a merge: G*DPL + 2 words per lane
+  // each, about 48 words (96 VGPRs) a batch -- at 64 words the batch's
+  // registers cost the d = 128, G = 7 kernel its second wave per SIMD.
+  constexpr int MC = 48 / (G * DPL + 2) > 8 ? 8 : (48 / (G * DPL + 2) < 2 ? 2 : 48 / (G * DPL + 2));
   // Register buffers per wave: while one block is computed, NBUF - 1 are in
   // flight. The matrix-core decode (16-bit K/V) takes three: the bytes in
   // flight then also cover the stretches in which the compute unit's other
