@@ -64,7 +64,7 @@ def _gather(kv, k_ptr, v_ptr, table_row, n, hkv, d, nb):
     return _host16(ko)[0], _host16(vo)[0]
 
 
-@pytest.mark.parametrize("workload", ["qwen3", "qwen25"])
+@pytest.mark.parametrize("workload", ["qwen3", "qwen25", "qwen25_7b"])
 def test_bench_planned_stream_step_matches_oracle(kv, workload):
     hq, hkv, d, _, b, _, _, _ = bench.WORKLOADS[workload]
     w = bench.decode_inputs(workload, BENCH_SEED, DEV, layers=1)
