@@ -1111,90 +1111,31 @@ TIMELINE_POINTS = ["entry", "plan arrived", "first pages requested", "prologue b
                    "group barrier passed", "own pieces combined", "records arrived", "finished"]
 
 
-def timeline_bench(args):
-    """Per-phase timeline of a decode launch: the measurement build of the
-    library (librlse_kv_timeline.so, RLSE_DECODE_TIMELINE) stamps the wall
-    clock (100 MHz) in every wave at the points of TIMELINE_POINTS. After
-    `warmup` steps of the workload (plan + one planned streamed launch per
-    layer, as the bench times them), the stamps are cleared, one more step
-    runs, and the last layer's launch is read back: for every point, the
-    spread over the waves of each workgroup slot (slot 0: the first
-    workgroup dispatched to a compute unit, 1: the second), in us from the
-    launch's first entry, and each phase's duration per wave."""
-    import ctypes
-    lib = os.path.join(ROOT, "mini-serve-rs_amd", "librlse_kv_timeline.so")
-    if not os.path.exists(lib):
-        print("bench.py --timeline needs the measurement build: "
-              "make -C mini-serve-rs_amd/csrc timeline", file=sys.stderr)
-        sys.exit(2)
-    if args.workload not in WORKLOADS:
-        print(f"--timeline covers the attention workloads {sorted(WORKLOADS)}", file=sys.stderr)
-        sys.exit(2)
-    os.environ["RLSE_KV_LIB"] = lib
-    import numpy as np
-    import torch
-    import rlse_kv as kv
-    hq, hkv, d, layers, b, _, _, desc = WORKLOADS[args.workload]
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    w = decode_inputs(args.workload, args.seed, dev)
-    t_dev = torch.from_numpy(w["tables"]).to(dev)
-    lens_dev = torch.from_numpy(w["lens"]).to(dev)
-    out = torch.empty((b, hq, d), device=dev, dtype=torch.bfloat16)
-    ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
-    plan_bytes = kv.decode_plan_size()
-    plan = torch.zeros(plan_bytes, dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream()
-    lib_h = kv.load()
-    fn = lib_h.rlse_decode_timeline
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
-    fn.restype = ctypes.c_int
+PREFIX_TIMELINE_POINTS = ["entry", "page ids and query loads issued", "first blocks requested",
+                          "queries staged", "first block computed", "loop ended",
+                          "waves' states combined", "slice state stored", "finished"]
 
-    def step():
-        kv.decode_plan(t_dev, lens_dev, b, hkv, w["mbps"], w["num_blocks"], plan, plan_bytes,
-                       stream)
-        for layer in range(layers):
-            kv.decode_step_planned(w["q"][layer], w["k_new"][layer], w["v_new"][layer],
-                                   w["q_norm"][layer], w["k_norm"][layer], 1e-6, w["cos"],
-                                   w["sin"], w["max_pos"], w["k_pools"][layer],
-                                   w["v_pools"][layer], t_dev, lens_dev, out, b, hq, hkv, d,
-                                   w["mbps"], w["num_blocks"], 1.0 / math.sqrt(d), "bf16", plan,
-                                   ws, ws_bytes, stream, stream_pages=True)
 
-    for _ in range(max(args.warmup, 1)):
-        step()
-    torch.cuda.synchronize()
-    n_words = 8192 * len(TIMELINE_POINTS)
-    buf = np.zeros(n_words, np.uint64)
-    h_stream = ctypes.c_void_p(stream.cuda_stream)
-    if fn(None, 0, 1, h_stream) != 0:
-        raise RuntimeError("rlse_decode_timeline (clear) failed")
-    step()
-    torch.cuda.synchronize()
-    if fn(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes, 0, h_stream) != 0:
-        raise RuntimeError("rlse_decode_timeline (read) failed")
-    n_pts = len(TIMELINE_POINTS)
-    stamps = buf.reshape(-1, n_pts).astype(np.int64)
+def _spread(np, x):
+    x = x[~np.isnan(x)]
+    if not len(x):
+        return None
+    return {"n": int(len(x)), "min": round(float(x.min()), 2),
+            "p10": round(float(np.percentile(x, 10)), 2),
+            "median": round(float(np.median(x)), 2),
+            "p90": round(float(np.percentile(x, 90)), 2), "max": round(float(x.max()), 2)}
+
+
+def _decode_timeline(np, stamps, t0):
+    """Summary of the decode launch's stamps (TIMELINE_POINTS, four waves a
+    workgroup, two workgroups a compute unit), times in us from t0."""
     waves = int(np.nonzero(stamps[:, 0])[0].max()) + 1
     stamps = stamps[:waves]
     groups = waves // 4
-    t0 = stamps[stamps[:, 0] > 0, 0].min()
     rel = np.where(stamps > 0, (stamps - t0) * 0.01, np.nan)  # us
     slot = (np.arange(waves) // 4) >= groups // 2
-
-    def spread(x):
-        x = x[~np.isnan(x)]
-        if not len(x):
-            return None
-        return {"n": int(len(x)), "min": round(float(x.min()), 2),
-                "p10": round(float(np.percentile(x, 10)), 2),
-                "median": round(float(np.median(x)), 2),
-                "p90": round(float(np.percentile(x, 90)), 2), "max": round(float(x.max()), 2)}
-
-    points = {}
-    for k, name in enumerate(TIMELINE_POINTS):
-        points[name] = {"slot0": spread(rel[~slot, k]), "slot1": spread(rel[slot, k])}
+    points = {name: {"slot0": _spread(np, rel[~slot, k]), "slot1": _spread(np, rel[slot, k])}
+              for k, name in enumerate(TIMELINE_POINTS)}
     P = {name: k for k, name in enumerate(TIMELINE_POINTS)}
     fin, loop_end = P["finished"], P["streaming loop ended"]
     # Phases up to the epilogue's barrier in order, then the epilogue's:
@@ -1213,18 +1154,153 @@ def timeline_bench(args):
         sel = merging if who == "merging waves" else (combining & ~merging if who else
                                                       np.ones(waves, bool))
         name = f"{TIMELINE_POINTS[a]} -> {TIMELINE_POINTS[b]}" + (f" ({who})" if who else "")
-        phases[name] = spread(rel[sel, b] - rel[sel, a])
+        phases[name] = _spread(np, rel[sel, b] - rel[sel, a])
     last = int(np.nanargmax(rel[:, fin]))
-    result = {"timeline": args.workload, "workload": desc, "launch_span_us":
-              round(float(np.nanmax(rel[:, fin])), 2), "waves": waves,
-              "workgroups": groups, "points_us": points, "phases_us": phases,
-              "last_loop_end_us": round(float(np.nanmax(rel[:, loop_end])), 2),
-              "last_finisher": {"wave": last, "workgroup": last // 4, "wave_in_group": last % 4,
-                                "points_us": {n: (None if np.isnan(rel[last, k]) else
-                                                  round(float(rel[last, k]), 2))
-                                              for k, n in enumerate(TIMELINE_POINTS)}},
-              "finish_by_wave_index": {f"wave{i}": spread(rel[np.arange(waves) % 4 == i, fin])
-                                       for i in range(4)}}
+    return {"launch_span_us": round(float(np.nanmax(rel[:, fin]) -
+                                          np.nanmin(rel[:, P["entry"]])), 2),
+            "waves": waves, "workgroups": groups, "points_us": points, "phases_us": phases,
+            "last_loop_end_us": round(float(np.nanmax(rel[:, loop_end])), 2),
+            "last_finisher": {"wave": last, "workgroup": last // 4, "wave_in_group": last % 4,
+                              "points_us": {n: (None if np.isnan(rel[last, k]) else
+                                                round(float(rel[last, k]), 2))
+                                            for k, n in enumerate(TIMELINE_POINTS)}},
+            "finish_by_wave_index": {f"wave{i}": _spread(np, rel[np.arange(waves) % 4 == i, fin])
+                                     for i in range(4)}}
+
+
+def _prefix_timeline(np, stamps):
+    """Summary of the cascade prefix launch's stamps (PREFIX_TIMELINE_POINTS,
+    eight waves a workgroup; waves without pages have none), times in us
+    from the launch's first entry."""
+    have = stamps[:, 0] > 0
+    waves = int(np.nonzero(have)[0].max()) + 1
+    stamps = stamps[:waves]
+    t0 = stamps[stamps[:, 0] > 0, 0].min()
+    rel = np.where(stamps > 0, (stamps - t0) * 0.01, np.nan)
+    n = len(PREFIX_TIMELINE_POINTS)
+    points = {name: _spread(np, rel[:, k]) for k, name in enumerate(PREFIX_TIMELINE_POINTS)}
+    phases = {}
+    for k in range(1, n):
+        a = k - 1
+        if k == 5:   # waves without blocks have no "first block computed"
+            a = 3
+            phases[f"{PREFIX_TIMELINE_POINTS[3]} -> {PREFIX_TIMELINE_POINTS[4]}"] = _spread(
+                np, rel[:, 4] - rel[:, 3])
+            phases[f"{PREFIX_TIMELINE_POINTS[4]} -> {PREFIX_TIMELINE_POINTS[5]}"] = _spread(
+                np, rel[:, 5] - rel[:, 4])
+            continue
+        if k == 4:
+            continue
+        phases[f"{PREFIX_TIMELINE_POINTS[a]} -> {PREFIX_TIMELINE_POINTS[k]}"] = _spread(
+            np, rel[:, k] - rel[:, a])
+    last = int(np.nanargmax(rel[:, n - 1]))
+    return {"launch_span_us": round(float(np.nanmax(rel[:, n - 1])), 2),
+            "waves_with_stamps": int((~np.isnan(rel[:, 0])).sum()),
+            "workgroups": (waves + 7) // 8, "points_us": points, "phases_us": phases,
+            "last_finisher": {"wave": last, "workgroup": last // 8, "wave_in_group": last % 8,
+                              "points_us": {nm: (None if np.isnan(rel[last, k]) else
+                                                 round(float(rel[last, k]), 2))
+                                            for k, nm in enumerate(PREFIX_TIMELINE_POINTS)}}}
+
+
+def timeline_bench(args):
+    """Per-phase timeline of a decode launch: the measurement build of the
+    library (librlse_kv_timeline.so, RLSE_DECODE_TIMELINE) stamps the wall
+    clock (100 MHz) in every wave at the points of TIMELINE_POINTS. After
+    `warmup` steps of the workload (plan + one planned streamed launch per
+    layer, as the bench times them), the stamps are cleared, one more step
+    runs, and the last layer's launch is read back: for every point, the
+    spread over the waves of each workgroup slot (slot 0: the first
+    workgroup dispatched to a compute unit, 1: the second), in us from the
+    launch's first entry, and each phase's duration per wave. A prefix-fork
+    workload runs its cascade step (plan + prefix launch + decode launch per
+    layer) and also reports the prefix launch's points
+    (PREFIX_TIMELINE_POINTS), with the decode's times from the same origin
+    as the prefix's first entry."""
+    import ctypes
+    lib = os.path.join(ROOT, "mini-serve-rs_amd", "librlse_kv_timeline.so")
+    if not os.path.exists(lib):
+        print("bench.py --timeline needs the measurement build: "
+              "make -C mini-serve-rs_amd/csrc timeline", file=sys.stderr)
+        sys.exit(2)
+    if args.workload not in WORKLOADS and args.workload not in FORK:
+        print(f"--timeline covers the attention workloads {sorted(WORKLOADS)} and the prefix "
+              f"forks {sorted(FORK)}", file=sys.stderr)
+        sys.exit(2)
+    os.environ["RLSE_KV_LIB"] = lib
+    import numpy as np
+    import torch
+    import rlse_kv as kv
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    plan_bytes = kv.decode_plan_size()
+    plan = torch.zeros(plan_bytes, dtype=torch.uint8, device=dev)
+    fork = args.workload in FORK
+    if fork:
+        hq, hkv, d, layers, b, plen, _, _, desc = FORK[args.workload]
+        f = fork_inputs(args.workload, args.seed, dev)
+        t_dev, mbps, nb = f["tables_dev"], f["mbps"], f["num_blocks"]
+        lens_dev = torch.from_numpy(f["lens"].astype(np.int32)).to(dev)
+        shared = plen // 16
+        pre_bytes = kv.decode_prefix_size(b, hq, d, shared)
+        pre = torch.zeros(pre_bytes, dtype=torch.uint8, device=dev)
+        ptrs = [f["pool"].layer(layer) for layer in range(layers)]
+    else:
+        hq, hkv, d, layers, b, _, _, desc = WORKLOADS[args.workload]
+        w = decode_inputs(args.workload, args.seed, dev)
+        t_dev = torch.from_numpy(w["tables"]).to(dev)
+        lens_dev = torch.from_numpy(w["lens"]).to(dev)
+        mbps, nb = w["mbps"], w["num_blocks"]
+    out = torch.empty((b, hq, d), device=dev, dtype=torch.bfloat16)
+    ws_bytes = kv.decode_workspace_size(b, hq, hkv, d)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    lib_h = kv.load()
+    fn = lib_h.rlse_decode_timeline
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+
+    def step():
+        if fork:
+            kv.decode_plan_cascade(t_dev, lens_dev, b, hkv, mbps, nb, shared, plan, plan_bytes,
+                                   stream)
+            for layer in range(layers):
+                kv.decode_step_cascade(f["q"][layer], f["k_new"][layer], f["v_new"][layer],
+                                       f["q_norm"], f["k_norm"], 1e-6, f["cos"], f["sin"],
+                                       f["max_pos"], ptrs[layer][0], ptrs[layer][1], t_dev,
+                                       lens_dev, out, b, hq, hkv, d, mbps, nb,
+                                       1.0 / math.sqrt(d), "bf16", plan, shared, pre, pre_bytes,
+                                       ws, ws_bytes, stream, stream_pages=True)
+            return
+        kv.decode_plan(t_dev, lens_dev, b, hkv, mbps, nb, plan, plan_bytes, stream)
+        for layer in range(layers):
+            kv.decode_step_planned(w["q"][layer], w["k_new"][layer], w["v_new"][layer],
+                                   w["q_norm"][layer], w["k_norm"][layer], 1e-6, w["cos"],
+                                   w["sin"], w["max_pos"], w["k_pools"][layer],
+                                   w["v_pools"][layer], t_dev, lens_dev, out, b, hq, hkv, d,
+                                   mbps, nb, 1.0 / math.sqrt(d), "bf16", plan, ws, ws_bytes,
+                                   stream, stream_pages=True)
+
+    for _ in range(max(args.warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    n_dec = 8192 * len(TIMELINE_POINTS)
+    buf = np.zeros(n_dec + 8192 * len(PREFIX_TIMELINE_POINTS), np.uint64)
+    h_stream = ctypes.c_void_p(stream.cuda_stream)
+    if fn(None, 0, 1, h_stream) != 0:
+        raise RuntimeError("rlse_decode_timeline (clear) failed")
+    step()
+    torch.cuda.synchronize()
+    if fn(buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes, 0, h_stream) != 0:
+        raise RuntimeError("rlse_decode_timeline (read) failed")
+    dec = buf[:n_dec].reshape(-1, len(TIMELINE_POINTS)).astype(np.int64)
+    result = {"timeline": args.workload, "workload": desc}
+    t0 = dec[dec[:, 0] > 0, 0].min()
+    if fork:
+        pst = buf[n_dec:].reshape(-1, len(PREFIX_TIMELINE_POINTS)).astype(np.int64)
+        result["prefix"] = _prefix_timeline(np, pst)
+        t0 = pst[pst[:, 0] > 0, 0].min()   # the decode's times from the prefix's first entry
+    result.update(_decode_timeline(np, dec, t0))
     print(json.dumps(result))
 
 

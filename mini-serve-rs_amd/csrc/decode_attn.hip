@@ -367,7 +367,8 @@ static unsigned long long* timeline_buffer() {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
   std::lock_guard<std::mutex> lock(g_tl_mu);
   if (!g_tl_ptr[dev]) {
-    const size_t bytes = (size_t)kTimelineMaxWaves * kTimelinePoints * sizeof(unsigned long long);
+    const size_t bytes = (size_t)kTimelineMaxWaves * (kTimelinePoints + kPrefixTimelinePoints) *
+                         sizeof(unsigned long long);
     void* ptr = nullptr;
     if (hipMalloc(&ptr, bytes) != hipSuccess) return nullptr;
     if (hipMemset(ptr, 0, bytes) != hipSuccess) return nullptr;
@@ -377,13 +378,16 @@ static unsigned long long* timeline_buffer() {
 }
 
 // Copies the current device's timeline (kTimelineMaxWaves x kTimelinePoints
-// stamps, 100 MHz wall clock, 0 = not stamped since the last clear) into
-// host (bytes at most) after the stream's work, then clears it when clear
-// is nonzero. Exported by the measurement build only.
+// stamps of the decode launches, then kTimelineMaxWaves x
+// kPrefixTimelinePoints of the prefix launches; 100 MHz wall clock, 0 = not
+// stamped since the last clear) into host (bytes at most) after the
+// stream's work, then clears it when clear is nonzero. Exported by the
+// measurement build only.
 extern "C" int rlse_decode_timeline(void* host, size_t bytes, int clear, rlse_stream_t stream) {
   unsigned long long* tl = timeline_buffer();
   if (!tl) return fail(RLSE_ERR_INVALID_VALUE, "decode_timeline: no timeline buffer");
-  const size_t all = (size_t)kTimelineMaxWaves * kTimelinePoints * sizeof(unsigned long long);
+  const size_t all = (size_t)kTimelineMaxWaves * (kTimelinePoints + kPrefixTimelinePoints) *
+                     sizeof(unsigned long long);
   hipStream_t s = as_stream(stream);
   hipError_t e = hipSuccess;
   if (host) e = hipMemcpyAsync(host, tl, bytes < all ? bytes : all, hipMemcpyDeviceToHost, s);
@@ -668,6 +672,9 @@ static int decode_step_impl(const void* q, const void* k_new, const void* v_new,
     pp.contract = (plan && num_groups == 0)
                       ? plan_tail(reinterpret_cast<const int4*>(plan), p.W) + kPlanContractWord
                       : nullptr;
+#ifdef RLSE_DECODE_TIMELINE
+    pp.timeline = p.timeline ? p.timeline + (size_t)kTimelineMaxWaves * kTimelinePoints : nullptr;
+#endif
     if (num_groups > 0) {
       const int* seq_pre = tail + kPlanStampWords;
       pp.members = seq_pre + kMaxDecodeBatch;

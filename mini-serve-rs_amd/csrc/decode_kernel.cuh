@@ -84,6 +84,15 @@ constexpr float kLazyLog2 = 8.f;
 // A point a wave does not reach reads 0. Other builds compile no stamp.
 constexpr int kTimelinePoints = 11;
 constexpr int kTimelineMaxWaves = 8192;
+// The cascade step's prefix launch stamps its own region, after the
+// decode's: kPrefixTimelinePoints per wave, at
+// [kTimelineMaxWaves * kTimelinePoints + (block * 8 + wave) * points]:
+//   0 entry, 1 page ids and query loads issued, 2 first blocks requested,
+//   3 queries staged (normed, roped, in LDS behind the barrier), 4 first
+//   block computed, 5 loop ended, 6 waves' states combined (behind the
+//   second barrier), 7 slice state stored, 8 finished (the contract check
+//   included). Waves with no work leave their row at 0.
+constexpr int kPrefixTimelinePoints = 9;
 struct TimelineStamps {
   unsigned long long t[kTimelinePoints];
 };
@@ -334,6 +343,9 @@ struct PrefixParams {
   // (kPlanContractWord, nonzero: violated), checked once per step by the
   // plan; null: the launch checks the tables and lengths itself.
   const int* contract;
+#ifdef RLSE_DECODE_TIMELINE
+  unsigned long long* timeline;  // the prefix launch's region of the timeline buffer
+#endif
 };
 // Most prefix groups one grouped cascade step takes.
 constexpr int kMaxPrefixGroups = 64;

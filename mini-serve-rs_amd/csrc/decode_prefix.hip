@@ -32,6 +32,14 @@ namespace {
 constexpr int kPrefixWaves = 8;
 static_assert(kMaxPrefixPages <= 64 * kPrefixWaves, "a wave holds the page ids of 64 blocks");
 
+// Measurement build: the wall clock at the points of kPrefixTimelinePoints,
+// kept in registers and stored by lane 0 when the wave has finished.
+#ifdef RLSE_DECODE_TIMELINE
+#define RLSE_PTL(k) (ptl[k] = wall_clock64())
+#else
+#define RLSE_PTL(k) ((void)0)
+#endif
+
 // SELF_CHECK: the launch checks the one-prefix contract itself (a step
 // without a plan); planned steps take the plan's verdict.
 template <typename T, int D, int G, bool SELF_CHECK>
@@ -50,6 +58,10 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
   };
   __shared__ Lds lds;
 
+#ifdef RLSE_DECODE_TIMELINE
+  unsigned long long ptl[kPrefixTimelinePoints] = {};
+#endif
+  RLSE_PTL(0);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane % LPR, rsub = lane / LPR;
@@ -188,6 +200,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     const T* wp = reinterpret_cast<const T*>(p.qw ? p.qw : p.q);
     sq_w = *reinterpret_cast<const uint4*>(wp + col * EPL);
   }
+  RLSE_PTL(1);
 
   uint4 qv[NR];
   float m1 = -INFINITY, l1 = 0.f, nms1 = 0.f, thr1 = -INFINITY;
@@ -233,6 +246,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     load(b0, lo);
     load(b1, lo + 1);
     load(b2, lo + 2);
+    RLSE_PTL(2);
     if (self_check && wave == 1 && k0 < kend) {
       bad = chk_len <= 16 * P || chk_len > p.mbps * 16;
 #pragma unroll
@@ -249,6 +263,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     consume(sq_s);
     consume(sq_w);
     __syncthreads();
+    RLSE_PTL(3);
 #pragma unroll
     for (int r = 0; r < NR; ++r) qv[r] = lds.q[mh][4 * r + mq];
     // The decode's block math (decode_body, matrix-core path) on one block.
@@ -298,6 +313,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     // Blocks i + 1 and i + 2 in flight while block i is computed.
     for (int i = lo; i < hi;) {
       compute(b0);
+      if (i == lo) RLSE_PTL(4);
       if (++i == hi) break;
       load(b0, i + 2);
       compute(b1);
@@ -308,6 +324,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
       load(b2, i + 2);
     }
   }
+  RLSE_PTL(5);
 
   // Every wave parks its partial in LDS (the V blocks are dead here); after
   // one barrier wave t combines accumulator tile t of all waves, in wave
@@ -323,6 +340,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
       for (int i = 0; i < 4; ++i) dst[2 + 4 * t + i][lane] = macc[t][i];
   }
   __syncthreads();
+  RLSE_PTL(6);
   const int j = c0 + mh;
   if (wave < NT && j < ncols) {
     float pm[kPrefixWaves], M = -INFINITY;
@@ -349,6 +367,7 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     *reinterpret_cast<float4*>(dst + 16 * wave + 4 * mq) = make_float4(a[0], a[1], a[2], a[3]);
     if (wave == 0 && mq == 0) *reinterpret_cast<float2*>(dst + D) = make_float2(M, l);
   }
+  RLSE_PTL(7);
   if (verdict != 0 && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
   if (self_check && wave == 1 && k0 < kend) {
     for (int k = k0 + nwork; k < kend; k += nwork) {
@@ -359,6 +378,15 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
     }
     if (__any(bad) && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_PREFIX);
   }
+#ifdef RLSE_DECODE_TIMELINE
+  RLSE_PTL(8);
+  const size_t tw = (size_t)blockIdx.x * kPrefixWaves + wave;
+  if (p.timeline && lane == 0 && tw < (size_t)kTimelineMaxWaves) {
+    unsigned long long* dstt = p.timeline + tw * kPrefixTimelinePoints;
+#pragma unroll
+    for (int k = 0; k < kPrefixTimelinePoints; ++k) dstt[k] = ptl[k];
+  }
+#endif
 }
 
 template <typename T, int D, int G>
