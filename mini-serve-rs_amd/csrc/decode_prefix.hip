@@ -242,30 +242,28 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
         bf.v[r] = make_uint4(vx.x, vx.y, vx.z, vx.w);
       }
     };
-    PBuf b0, b1, b2;
-    load(b0, lo);
-    load(b1, lo + 1);
-    load(b2, lo + 2);
-    RLSE_PTL(2);
-    if (self_check && wave == 1 && k0 < kend) {
-      bad = chk_len <= 16 * P || chk_len > p.mbps * 16;
+    // The queries' math, then the barrier that publishes them, between the
+    // first blocks' requests and their math.
+    auto stage = [&]() __attribute__((always_inline)) {
+      if (self_check && wave == 1 && k0 < kend) {
+        bad = chk_len <= 16 * P || chk_len > p.mbps * 16;
 #pragma unroll
-      for (int k = 0; k < kChk; ++k) bad = bad || chk_t[k] != chk_0[k];
-    }
-    // The queries' math, then the barrier that publishes them.
-    if (stager) {
-      const uint4 y = norm_rope_packet<T, D>(sq_x, p.qw != nullptr, sq_w, p.inv_d, p.eps, sq_c,
-                                             sq_s, col);
-      lds.q[it][col] = qj < ncols ? y : make_uint4(0, 0, 0, 0);
-    }
-    consume(sq_x);
-    consume(sq_c);
-    consume(sq_s);
-    consume(sq_w);
-    __syncthreads();
-    RLSE_PTL(3);
+        for (int k = 0; k < kChk; ++k) bad = bad || chk_t[k] != chk_0[k];
+      }
+      if (stager) {
+        const uint4 y = norm_rope_packet<T, D>(sq_x, p.qw != nullptr, sq_w, p.inv_d, p.eps, sq_c,
+                                               sq_s, col);
+        lds.q[it][col] = qj < ncols ? y : make_uint4(0, 0, 0, 0);
+      }
+      consume(sq_x);
+      consume(sq_c);
+      consume(sq_s);
+      consume(sq_w);
+      __syncthreads();
+      RLSE_PTL(3);
 #pragma unroll
-    for (int r = 0; r < NR; ++r) qv[r] = lds.q[mh][4 * r + mq];
+      for (int r = 0; r < NR; ++r) qv[r] = lds.q[mh][4 * r + mq];
+    };
     // The decode's block math (decode_body, matrix-core path) on one block.
     auto compute = [&](const PBuf& bf) __attribute__((always_inline)) {
       const int nv = bf.nv;
@@ -310,18 +308,41 @@ __global__ __launch_bounds__(64 * kPrefixWaves) void decode_prefix_kernel(Prefix
         macc[t] = Mma16<T>::k16(a, pp, macc[t]);
       }
     };
-    // Blocks i + 1 and i + 2 in flight while block i is computed.
-    for (int i = lo; i < hi;) {
-      compute(b0);
-      if (i == lo) RLSE_PTL(4);
-      if (++i == hi) break;
-      load(b0, i + 2);
-      compute(b1);
-      if (++i == hi) break;
-      load(b1, i + 2);
-      compute(b2);
-      if (++i == hi) break;
-      load(b2, i + 2);
+    PBuf b0, b1;
+    if (per <= 2) {
+      // At most two blocks a wave (per is the workgroup's share, so every
+      // wave takes this branch or none does): both requested up front and
+      // no third buffer, whose zero-size loads would still pass through the
+      // compute unit's address unit ahead of the real ones.
+      load(b0, lo);
+      load(b1, lo + 1);
+      RLSE_PTL(2);
+      stage();
+      if (lo < hi) {
+        compute(b0);
+        RLSE_PTL(4);
+        if (lo + 1 < hi) compute(b1);
+      }
+    } else {
+      PBuf b2;
+      load(b0, lo);
+      load(b1, lo + 1);
+      load(b2, lo + 2);
+      RLSE_PTL(2);
+      stage();
+      // Blocks i + 1 and i + 2 in flight while block i is computed.
+      for (int i = lo; i < hi;) {
+        compute(b0);
+        if (i == lo) RLSE_PTL(4);
+        if (++i == hi) break;
+        load(b0, i + 2);
+        compute(b1);
+        if (++i == hi) break;
+        load(b1, i + 2);
+        compute(b2);
+        if (++i == hi) break;
+        load(b2, i + 2);
+      }
     }
   }
   RLSE_PTL(5);
