@@ -1549,6 +1549,12 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int k = 0; k < DPL; ++k) A[g][k] = 0.f;
+    // Cascade step: a row finished here starts from its prefix slices'
+    // states (written by the prefix launch, so ready from the launch's
+    // start): their round trip then runs under the LDS reads of the pieces
+    // and, for a merged row, under the wait for the earlier groups'
+    // records. A published piece leaves them to the row's finisher.
+    if (p.pre && R + nb <= ghi) combine_prefix(b, kvh, hm, hl, A);
     // Slots holding pieces of the row: this wave's slot s and, in the waves
     // below it (every wave when merging), the slot naming the same row. A
     // row's pieces sit in consecutive waves, at most one slot per wave.
@@ -1669,7 +1675,6 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p,
       if (!ok && lane == 0) ws_raise(p.ws_err, RLSE_WS_ERR_MERGE_TIMEOUT);
       RLSE_TL(9);
     }
-    if (p.pre) combine_prefix(b, kvh, hm, hl, A);  // cascade step
     write_row(b, kvh, ok, hl, A);
   }
   if constexpr (kMma) {
